@@ -1,0 +1,180 @@
+/*
+ * ovfq.h — C ABI of libovfq, the MI355X (gfx950) GGUF quantized-linear library.
+ *
+ * Drop-in device backing for Overfit's CPU quantized projections. Reference paths are relative to the
+ * reference root; RT/ = Sources/Main/LanguageModels/Runtime/, LD/ = Sources/Main/LanguageModels/Loading/.
+ *
+ * Conventions (kept from the reference, RT/Q4KDotKernel.cs:77-97, :957-976):
+ *  - Every entry point validates its arguments BEFORE any device work and returns a status code instead of
+ *    throwing: OVFQ_ERR_NULL ~ ArgumentNullException, OVFQ_ERR_SIZE ~ ArgumentException,
+ *    OVFQ_ERR_RANGE ~ ArgumentOutOfRangeException. ovfq_last_error() gives the message (per thread).
+ *  - Outputs are overwritten, never accumulated. A NULL bias means "no bias" (the reference's empty span).
+ *  - Weights are immutable after creation; they are copied to HBM once, in their native GGUF layout
+ *    (Q4_K 144-byte and Q6_K 210-byte super-blocks, output-major), or as the reference's resident Q8_0 planes
+ *    (int8 quants + f32 scales, RT/Q8Weight.cs:21-75).
+ *  - Host-pointer entry points (no suffix) are synchronous, like the reference's calls: they return after the
+ *    output is written, and never retain a host pointer.
+ *  - Entry points with the _dev suffix take device pointers and enqueue on the context's stream (see
+ *    ovfq_ctx_set_stream); they return once the work is enqueued. Call ovfq_ctx_synchronize() to wait.
+ *  - Thread safety: any number of host threads may call into one context; calls are serialised by a
+ *    per-context lock and run in order on the context's stream (the reference calls Project concurrently from
+ *    its head-parallel workers, RT/CachedMultiHeadAttention.cs:280, :876-907).
+ */
+#ifndef OVFQ_H
+#define OVFQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OVFQ_API __attribute__((visibility("default")))
+
+/* Status codes. */
+#define OVFQ_OK 0
+#define OVFQ_ERR_NULL (-1)  /* a required pointer was NULL                */
+#define OVFQ_ERR_SIZE (-2)  /* a size or shape is inconsistent            */
+#define OVFQ_ERR_RANGE (-3) /* a count is zero/negative or an index is out of range */
+#define OVFQ_ERR_TYPE (-4)  /* unsupported weight type for this entry point */
+#define OVFQ_ERR_HIP (-10)  /* the HIP runtime reported an error          */
+
+/* Weight formats (numbered as ggml's type ids). */
+#define OVFQ_TYPE_Q8_0 8
+#define OVFQ_TYPE_Q4_K 12
+#define OVFQ_TYPE_Q6_K 14
+
+/* Block geometry. */
+#define OVFQ_QK 256          /* elements per K-quant super-block (RT/Q4KWeight.cs:26) */
+#define OVFQ_Q4K_BYTES 144   /* RT/Q4KWeight.cs:29 */
+#define OVFQ_Q6K_BYTES 210   /* RT/Q6KWeight.cs SuperBlockBytes */
+#define OVFQ_Q8_BLOCK 32     /* RT/Q8DotKernel.cs:34 */
+#define OVFQ_GROUP 16        /* Q8_K bsum group (RT/Q4KDotKernel.cs:47) */
+
+typedef struct ovfq_ctx ovfq_ctx;
+typedef struct ovfq_weight ovfq_weight;
+
+/* ------------------------------------------------------------------------------------------------ context */
+
+/* Creates a context on HIP device `device` with its own (default-priority) stream. New; the reference has
+ * no device context. */
+OVFQ_API int ovfq_ctx_create(int device, ovfq_ctx** out);
+OVFQ_API int ovfq_ctx_destroy(ovfq_ctx* ctx);
+/* Makes the context enqueue its work on `stream` (a hipStream_t; NULL is the device's null stream). Work
+ * already queued on the previous stream is waited for first. */
+OVFQ_API int ovfq_ctx_set_stream(ovfq_ctx* ctx, void* stream);
+/* Returns the context to its own stream. */
+OVFQ_API int ovfq_ctx_reset_stream(ovfq_ctx* ctx);
+OVFQ_API int ovfq_ctx_synchronize(ovfq_ctx* ctx);
+/* Message for the last non-zero status returned on the calling thread ("" if none). */
+OVFQ_API const char* ovfq_last_error(void);
+/* Library version string. */
+OVFQ_API const char* ovfq_version(void);
+
+/* ------------------------------------------------------------------------------------------------ weights */
+
+/* Replaces the constructors Q4KWeight(ReadOnlyMemory<byte> blocks, int inputSize, int outputSize)
+ * (RT/Q4KWeight.cs:44-66) and Q6KWeight(...) (RT/Q6KWeight.cs:47): `blocks` holds output_size rows of
+ * input_size/256 super-blocks (host memory, e.g. a slice of a memory-mapped GGUF file); `nbytes` is the
+ * region length and must be >= the expected size. For Q8_0 (Q8Weight(sbyte[] quants, float[] scales, int
+ * inputSize, int outputSize), RT/Q8Weight.cs:23-50) `blocks` is the int8 quant plane [out*in] and `q8_scales`
+ * the f32 scale plane [out*in/32]; `nbytes` is the quant plane length. The bytes are copied once to HBM. */
+OVFQ_API int ovfq_weight_create(ovfq_ctx* ctx, int type, const void* blocks, size_t nbytes,
+                                const float* q8_scales, int input_size, int output_size, ovfq_weight** out);
+/* As ovfq_weight_create, but `blocks` / `q8_scales` are device pointers (device-to-device copy). */
+OVFQ_API int ovfq_weight_create_from_device(ovfq_ctx* ctx, int type, const void* blocks, size_t nbytes,
+                                            const float* q8_scales, int input_size, int output_size,
+                                            ovfq_weight** out);
+OVFQ_API int ovfq_weight_destroy(ovfq_weight* w);
+/* Shape/format query (InputSize / OutputSize / ByteCount of the weight classes). Any out pointer may be NULL.
+ * `device_blocks` receives the HBM address of the resident blocks (the quant plane for Q8_0). */
+OVFQ_API int ovfq_weight_info(const ovfq_weight* w, int* type, int* input_size, int* output_size,
+                              size_t* byte_count, const void** device_blocks);
+
+/* DecodeRow (RT/Q4KWeight.cs:121-138, RT/Q6KWeight.cs DecodeRow, RT/Q8Weight.cs:81-106): dequantises output
+ * row `row` into dst[input_size] (F32, e.g. an embedding lookup). */
+OVFQ_API int ovfq_weight_decode_row(ovfq_ctx* ctx, const ovfq_weight* w, int row, float* dst);
+OVFQ_API int ovfq_weight_decode_row_dev(ovfq_ctx* ctx, const ovfq_weight* w, int row, float* dst_dev);
+
+/* ------------------------------------------------------------------------------ activation quantisation */
+
+/* Q4KDotKernel.QuantizeActivationQ8K (RT/Q4KDotKernel.cs:71-136), applied to `rows` rows of length k
+ * (k % 256 == 0): quants[rows*k] int8, scales[rows*k/256] f32, bsums[rows*k/16] int16 — the reference's
+ * caller-owned scratch layout. Bit-exact to the reference. */
+OVFQ_API int ovfq_quantize_q8k(ovfq_ctx* ctx, const float* x, int rows, int k, int8_t* quants, float* scales,
+                               int16_t* bsums);
+OVFQ_API int ovfq_quantize_q8k_dev(ovfq_ctx* ctx, const float* x, int rows, int k, int8_t* quants,
+                                   float* scales, int16_t* bsums);
+/* Q8DotKernel.Quantize (RT/Q8DotKernel.cs:42-91) row by row (k % 32 == 0): quants[rows*k], scales[rows*k/32]. */
+OVFQ_API int ovfq_quantize_q8_0(ovfq_ctx* ctx, const float* x, int rows, int k, int8_t* quants, float* scales);
+OVFQ_API int ovfq_quantize_q8_0_dev(ovfq_ctx* ctx, const float* x, int rows, int k, int8_t* quants,
+                                    float* scales);
+
+/* ------------------------------------------------------------------------------------------- projections */
+
+/* y[rows][out] = (bias +) x[rows][in] @ W^T.
+ *  rows == 1 replaces Q4KDotKernel.Project / ProjectParallel (RT/Q4KDotKernel.cs:414-552),
+ *  Q6KDotKernel.Project / ProjectParallel (RT/Q6KDotKernel.cs:245-381) and Q8DotKernel.Project /
+ *  ProjectParallel (RT/Q8DotKernel.cs:155-330);
+ *  rows >= 2 replaces ProjectBatched / ProjectBatchedWeightStationary (RT/Q4KDotKernel.cs:681-955,
+ *  RT/Q6KDotKernel.cs:403-510, RT/Q8DotKernel.cs:352-445) and BatchedQuantProjection.Dispatch
+ *  (RT/BatchedQuantProjection.cs:26-87). The activation is quantised on the device (Q8_K for Q4_K/Q6_K,
+ *  Q8_0 for Q8_0), exactly as the reference does. */
+OVFQ_API int ovfq_project(ovfq_ctx* ctx, const ovfq_weight* w, const float* x, int rows, const float* bias,
+                          float* y);
+OVFQ_API int ovfq_project_dev(ovfq_ctx* ctx, const ovfq_weight* w, const float* x, int rows,
+                              const float* bias, float* y);
+
+/* Q4KDotKernel.ProjectPreQuantized (RT/Q4KDotKernel.cs:445-476) / Q6KDotKernel.ProjectPreQuantized
+ * (RT/Q6KDotKernel.cs:274-305), for `rows` rows of an already-quantised Q8_K activation in the layout
+ * ovfq_quantize_q8k writes. For Q8_0 weights pass the Q8_0 activation scales in `scales` and NULL bsums. */
+OVFQ_API int ovfq_project_prequantized(ovfq_ctx* ctx, const ovfq_weight* w, const int8_t* quants,
+                                       const float* scales, const int16_t* bsums, int rows, const float* bias,
+                                       float* y);
+OVFQ_API int ovfq_project_prequantized_dev(ovfq_ctx* ctx, const ovfq_weight* w, const int8_t* quants,
+                                           const float* scales, const int16_t* bsums, int rows,
+                                           const float* bias, float* y);
+
+/* Q4KDotKernel.ProjectGateUpParallel (RT/Q4KDotKernel.cs:563-645): one activation quantisation, gate and up
+ * in one launch; no bias. gate and up must have equal shapes. Any K-quant/Q8_0 type is accepted as long as
+ * both weights share it. */
+OVFQ_API int ovfq_project_gate_up(ovfq_ctx* ctx, const ovfq_weight* gate, const ovfq_weight* up,
+                                  const float* x, float* gate_out, float* up_out);
+OVFQ_API int ovfq_project_gate_up_dev(ovfq_ctx* ctx, const ovfq_weight* gate, const ovfq_weight* up,
+                                      const float* x, float* gate_out, float* up_out);
+
+/* Several projections of the SAME activation in one launch (the generalisation of gate/up that the
+ * attention block's shared quantised hidden row needs, RT/CachedMultiHeadAttention.cs:196-207): weights[i]
+ * share input_size and type; ys[i] receives rows x output_size_i; biases may be NULL or hold NULL entries.
+ * At most 4 weights. rows == 1 only. */
+OVFQ_API int ovfq_project_multi_dev(ovfq_ctx* ctx, int count, const ovfq_weight* const* weights,
+                                    const float* x, const float* const* biases, float* const* ys);
+
+/* ovfq_project_multi_dev from an already-quantised Q8_K activation (one row): the attention block quantises
+ * its hidden row once and runs every head's projection against it with ProjectPreQuantized
+ * (RT/CachedMultiHeadAttention.cs:196-207, RT/Q4KDotKernel.cs:445-476); here all of them run in one launch.
+ * K-quant weights only; at most 4. */
+OVFQ_API int ovfq_project_multi_prequantized_dev(ovfq_ctx* ctx, int count, const ovfq_weight* const* weights,
+                                                 const int8_t* quants, const float* scales, const int16_t* bsums,
+                                                 const float* const* biases, float* const* ys);
+
+/* ---------------------------------------------------------------------------------- weight quantisation */
+
+/* GgmlQuant.QuantizeQ4_K (LD/GgmlQuant.cs:132-161): output-major f32 [out][in] (in % 256 == 0) -> Q4_K
+ * bytes [out][in/256][144], bit-exact to the reference encoder. Device pointers. */
+OVFQ_API int ovfq_quantize_weight_q4k_dev(ovfq_ctx* ctx, const float* w, int input_size, int output_size,
+                                          uint8_t* dst);
+/* Q6_K encoder (no reference counterpart: the reference reads Q6_K but cannot write it). Plain absmax per
+ * 16-element sub-block under one fp16 super-scale; decodes with GgmlDequant.DecodeQ6_KBlock
+ * (LD/GgmlDequant.cs:143-209). Device pointers. */
+OVFQ_API int ovfq_quantize_weight_q6k_dev(ovfq_ctx* ctx, const float* w, int input_size, int output_size,
+                                          uint8_t* dst);
+/* Q8Weight.QuantizeRows (RT/Q8Weight.cs:115-175): device pointers. */
+OVFQ_API int ovfq_quantize_weight_q8_0_dev(ovfq_ctx* ctx, const float* w, int input_size, int output_size,
+                                           int8_t* quants, float* scales);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* OVFQ_H */

@@ -1,0 +1,624 @@
+// api.cpp — the C ABI of libovfq (declared in include/ovfq.h).
+//
+// Host responsibilities: argument validation before any device work (the reference throws before work,
+// RT/Q4KDotKernel.cs:77-97), weight residency in HBM, activation quantisation scratch, staging of host
+// buffers for the synchronous entry points, and dispatch to the kernels in quant.hip / project.hip.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "../../include/ovfq.h"
+#include "ovfq_launch.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int ok() {
+    g_last_error.clear();
+    return OVFQ_OK;
+}
+
+#define HIP_TRY(expr)                                                                                  \
+    do {                                                                                               \
+        hipError_t _e = (expr);                                                                        \
+        if (_e != hipSuccess) return fail(OVFQ_ERR_HIP, "%s failed: %s", #expr, hipGetErrorString(_e)); \
+    } while (0)
+
+// A growable device buffer owned by a context.
+struct DevBuf {
+    void* p = nullptr;
+    size_t cap = 0;
+};
+
+}  // namespace
+
+struct ovfq_ctx {
+    int device = 0;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    std::mutex mu;
+    // Activation quantisation scratch (Q8_K / Q8_0) and host-call staging.
+    DevBuf act_q, act_s, act_b, x_stage, y_stage, y2_stage, bias_stage;
+};
+
+struct ovfq_weight {
+    ovfq_ctx* ctx = nullptr;
+    int type = 0;
+    int in = 0;
+    int out = 0;
+    void* blocks = nullptr;  // Q4_K/Q6_K blocks or Q8_0 quant plane
+    float* scales = nullptr; // Q8_0 scale plane
+    size_t nbytes = 0;       // resident bytes (blocks + scales)
+};
+
+namespace {
+
+// Grows `b` to at least `bytes`, waiting for queued work that may still read the old buffer.
+int ensure(ovfq_ctx* c, DevBuf& b, size_t bytes) {
+    if (b.cap >= bytes) return OVFQ_OK;
+    if (b.p) {
+        HIP_TRY(hipStreamSynchronize(c->stream));
+        HIP_TRY(hipFree(b.p));
+        b.p = nullptr;
+        b.cap = 0;
+    }
+    size_t cap = bytes < 4096 ? 4096 : bytes;
+    cap = (cap + 255) & ~size_t(255);
+    HIP_TRY(hipMalloc(&b.p, cap));
+    b.cap = cap;
+    return OVFQ_OK;
+}
+
+bool valid_type(int t) { return t == OVFQ_TYPE_Q4_K || t == OVFQ_TYPE_Q6_K || t == OVFQ_TYPE_Q8_0; }
+
+size_t block_bytes_per_row(int type, int in) {
+    if (type == OVFQ_TYPE_Q4_K) return (size_t)(in / OVFQ_QK) * OVFQ_Q4K_BYTES;
+    if (type == OVFQ_TYPE_Q6_K) return (size_t)(in / OVFQ_QK) * OVFQ_Q6K_BYTES;
+    return (size_t)in;  // Q8_0 quant plane
+}
+
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+// Shape checks of the weight constructors (RT/Q4KWeight.cs:46-62, RT/Q8Weight.cs:25-42).
+int check_weight_shape(int type, int in, int out) {
+    if (!valid_type(type)) return fail(OVFQ_ERR_TYPE, "unsupported weight type %d", type);
+    if (in <= 0) return fail(OVFQ_ERR_RANGE, "inputSize (%d) must be positive", in);
+    if (out <= 0) return fail(OVFQ_ERR_RANGE, "outputSize (%d) must be positive", out);
+    if (type == OVFQ_TYPE_Q8_0) {
+        if (in % OVFQ_Q8_BLOCK) return fail(OVFQ_ERR_SIZE, "inputSize (%d) must be a multiple of 32", in);
+        if (in / OVFQ_Q8_BLOCK > 4000) return fail(OVFQ_ERR_SIZE, "Q8_0 inputSize (%d) above 128000", in);
+    } else if (in % OVFQ_QK) {
+        return fail(OVFQ_ERR_SIZE, "inputSize (%d) must be a multiple of 256", in);
+    }
+    if ((int64_t)in * out > (int64_t)1 << 40) return fail(OVFQ_ERR_SIZE, "weight too large");
+    return OVFQ_OK;
+}
+
+int weight_create(ovfq_ctx* ctx, int type, const void* blocks, size_t nbytes, const float* q8_scales, int in,
+                  int out, ovfq_weight** res, hipMemcpyKind kind) {
+    if (!ctx) return fail(OVFQ_ERR_NULL, "ctx is NULL");
+    if (!blocks) return fail(OVFQ_ERR_NULL, "blocks is NULL");
+    if (!res) return fail(OVFQ_ERR_NULL, "out is NULL");
+    int rc = check_weight_shape(type, in, out);
+    if (rc) return rc;
+    const size_t expected = block_bytes_per_row(type, in) * (size_t)out;
+    if (nbytes < expected)
+        return fail(OVFQ_ERR_SIZE, "blocks region (%zu B) is smaller than the expected %zu B", nbytes, expected);
+    if (type == OVFQ_TYPE_Q8_0 && !q8_scales) return fail(OVFQ_ERR_NULL, "Q8_0 weight needs a scale plane");
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    HIP_TRY(hipSetDevice(ctx->device));
+    ovfq_weight* w = new ovfq_weight();
+    w->ctx = ctx;
+    w->type = type;
+    w->in = in;
+    w->out = out;
+    hipError_t e = hipMalloc(&w->blocks, expected);
+    if (e != hipSuccess) {
+        delete w;
+        return fail(OVFQ_ERR_HIP, "hipMalloc(%zu) failed: %s", expected, hipGetErrorString(e));
+    }
+    e = hipMemcpyAsync(w->blocks, blocks, expected, kind, ctx->stream);
+    size_t scale_bytes = 0;
+    if (e == hipSuccess && type == OVFQ_TYPE_Q8_0) {
+        scale_bytes = (size_t)out * (in / OVFQ_Q8_BLOCK) * sizeof(float);
+        e = hipMalloc(&w->scales, scale_bytes);
+        if (e == hipSuccess) e = hipMemcpyAsync(w->scales, q8_scales, scale_bytes, kind, ctx->stream);
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        if (w->blocks) (void)hipFree(w->blocks);
+        if (w->scales) (void)hipFree(w->scales);
+        delete w;
+        return fail(OVFQ_ERR_HIP, "weight upload failed: %s", hipGetErrorString(e));
+    }
+    w->nbytes = expected + scale_bytes;
+    *res = w;
+    return ok();
+}
+
+// Quantises `rows` activation rows of length `in` for weight type `type` into the context scratch.
+int quantize_into_scratch(ovfq_ctx* c, int type, const float* x_dev, int rows, int in, ovfq::ActQ* act) {
+    const size_t n = (size_t)rows * in;
+    int rc = ensure(c, c->act_q, n);
+    if (rc) return rc;
+    if (type == OVFQ_TYPE_Q8_0) {
+        rc = ensure(c, c->act_s, n / 32 * sizeof(float));
+        if (rc) return rc;
+        HIP_TRY(ovfq::launch_quantize_q8_0(x_dev, (int64_t)(n / 32), (int8_t*)c->act_q.p, (float*)c->act_s.p,
+                                           c->stream));
+        *act = ovfq::ActQ{(const int8_t*)c->act_q.p, (const float*)c->act_s.p, nullptr};
+    } else {
+        rc = ensure(c, c->act_s, n / 256 * sizeof(float));
+        if (rc) return rc;
+        rc = ensure(c, c->act_b, n / 16 * sizeof(int16_t));
+        if (rc) return rc;
+        HIP_TRY(ovfq::launch_quantize_q8k(x_dev, (int64_t)(n / 256), (int8_t*)c->act_q.p, (float*)c->act_s.p,
+                                          (int16_t*)c->act_b.p, c->stream));
+        *act = ovfq::ActQ{(const int8_t*)c->act_q.p, (const float*)c->act_s.p, (const int16_t*)c->act_b.p};
+    }
+    return OVFQ_OK;
+}
+
+int launch_projection(ovfq_ctx* c, const ovfq_weight* const* ws, int count, const float* const* biases,
+                      float* const* ys, int rows, ovfq::ActQ act) {
+    ovfq::ProjJob jobs[ovfq::kMaxJobs];
+    for (int i = 0; i < count; i++) {
+        jobs[i].w = static_cast<const uint8_t*>(ws[i]->blocks);
+        jobs[i].ws = ws[i]->scales;
+        jobs[i].bias = biases ? biases[i] : nullptr;
+        jobs[i].y = ys[i];
+        jobs[i].n_rows = ws[i]->out;
+    }
+    const int type = ws[0]->type;
+    const int in = ws[0]->in;
+    if (type == OVFQ_TYPE_Q8_0) {
+        HIP_TRY(ovfq::launch_project_q8_0(jobs, count, in, rows, act, c->stream));
+    } else {
+        HIP_TRY(ovfq::launch_project_kquant(type, jobs, count, in, rows, act, c->stream));
+    }
+    return OVFQ_OK;
+}
+
+int check_weight(const ovfq_ctx* ctx, const ovfq_weight* w) {
+    if (!w) return fail(OVFQ_ERR_NULL, "weight is NULL");
+    if (w->ctx != ctx) return fail(OVFQ_ERR_SIZE, "weight belongs to another context");
+    return OVFQ_OK;
+}
+
+int check_rows(int rows) {
+    if (rows <= 0) return fail(OVFQ_ERR_RANGE, "rows (%d) must be positive", rows);
+    if (rows > 65536) return fail(OVFQ_ERR_RANGE, "rows (%d) above 65536", rows);
+    return OVFQ_OK;
+}
+
+// Device pointers handed to the _dev entry points must keep the kernels' 4-byte (quants/bsums) alignment.
+int check_dev_align(const void* p, const char* name) {
+    if (p && !aligned(p, 4)) return fail(OVFQ_ERR_SIZE, "%s must be 4-byte aligned", name);
+    return OVFQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* ovfq_last_error(void) { return g_last_error.c_str(); }
+
+const char* ovfq_version(void) { return "ovfq 0.1 (gfx950)"; }
+
+int ovfq_ctx_create(int device, ovfq_ctx** out) {
+    if (!out) return fail(OVFQ_ERR_NULL, "out is NULL");
+    int n = 0;
+    HIP_TRY(hipGetDeviceCount(&n));
+    if (device < 0 || device >= n) return fail(OVFQ_ERR_RANGE, "device %d out of range (%d devices)", device, n);
+    HIP_TRY(hipSetDevice(device));
+    ovfq_ctx* c = new ovfq_ctx();
+    c->device = device;
+    hipError_t e = hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete c;
+        return fail(OVFQ_ERR_HIP, "hipStreamCreate failed: %s", hipGetErrorString(e));
+    }
+    c->stream = c->own_stream;
+    *out = c;
+    return ok();
+}
+
+int ovfq_ctx_destroy(ovfq_ctx* c) {
+    if (!c) return fail(OVFQ_ERR_NULL, "ctx is NULL");
+    {
+        std::lock_guard<std::mutex> lk(c->mu);
+        (void)hipSetDevice(c->device);
+        (void)hipStreamSynchronize(c->stream);
+        DevBuf* bufs[] = {&c->act_q, &c->act_s, &c->act_b, &c->x_stage, &c->y_stage, &c->y2_stage, &c->bias_stage};
+        for (DevBuf* b : bufs)
+            if (b->p) (void)hipFree(b->p);
+        if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
+    }
+    delete c;
+    return ok();
+}
+
+int ovfq_ctx_set_stream(ovfq_ctx* c, void* stream) {
+    if (!c) return fail(OVFQ_ERR_NULL, "ctx is NULL");
+    std::lock_guard<std::mutex> lk(c->mu);
+    HIP_TRY(hipSetDevice(c->device));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    c->stream = static_cast<hipStream_t>(stream);
+    return ok();
+}
+
+int ovfq_ctx_reset_stream(ovfq_ctx* c) {
+    if (!c) return fail(OVFQ_ERR_NULL, "ctx is NULL");
+    std::lock_guard<std::mutex> lk(c->mu);
+    HIP_TRY(hipSetDevice(c->device));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    c->stream = c->own_stream;
+    return ok();
+}
+
+int ovfq_ctx_synchronize(ovfq_ctx* c) {
+    if (!c) return fail(OVFQ_ERR_NULL, "ctx is NULL");
+    std::lock_guard<std::mutex> lk(c->mu);
+    HIP_TRY(hipSetDevice(c->device));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    return ok();
+}
+
+int ovfq_weight_create(ovfq_ctx* ctx, int type, const void* blocks, size_t nbytes, const float* q8_scales,
+                       int input_size, int output_size, ovfq_weight** out) {
+    return weight_create(ctx, type, blocks, nbytes, q8_scales, input_size, output_size, out,
+                         hipMemcpyHostToDevice);
+}
+
+int ovfq_weight_create_from_device(ovfq_ctx* ctx, int type, const void* blocks, size_t nbytes,
+                                   const float* q8_scales, int input_size, int output_size, ovfq_weight** out) {
+    return weight_create(ctx, type, blocks, nbytes, q8_scales, input_size, output_size, out,
+                         hipMemcpyDeviceToDevice);
+}
+
+int ovfq_weight_destroy(ovfq_weight* w) {
+    if (!w) return fail(OVFQ_ERR_NULL, "weight is NULL");
+    {
+        std::lock_guard<std::mutex> lk(w->ctx->mu);
+        (void)hipSetDevice(w->ctx->device);
+        (void)hipStreamSynchronize(w->ctx->stream);
+        if (w->blocks) (void)hipFree(w->blocks);
+        if (w->scales) (void)hipFree(w->scales);
+    }
+    delete w;
+    return ok();
+}
+
+int ovfq_weight_info(const ovfq_weight* w, int* type, int* input_size, int* output_size, size_t* byte_count,
+                     const void** device_blocks) {
+    if (!w) return fail(OVFQ_ERR_NULL, "weight is NULL");
+    if (type) *type = w->type;
+    if (input_size) *input_size = w->in;
+    if (output_size) *output_size = w->out;
+    if (byte_count) *byte_count = w->nbytes;
+    if (device_blocks) *device_blocks = w->blocks;
+    return ok();
+}
+
+static int decode_row_impl(ovfq_ctx* ctx, const ovfq_weight* w, int row, float* dst, bool host) {
+    if (!ctx) return fail(OVFQ_ERR_NULL, "ctx is NULL");
+    int rc = check_weight(ctx, w);
+    if (rc) return rc;
+    if (!dst) return fail(OVFQ_ERR_NULL, "dst is NULL");
+    if (row < 0 || row >= w->out) return fail(OVFQ_ERR_RANGE, "row %d out of range [0, %d)", row, w->out);
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    HIP_TRY(hipSetDevice(ctx->device));
+    float* d = dst;
+    if (host) {
+        rc = ensure(ctx, ctx->y_stage, (size_t)w->in * 4);
+        if (rc) return rc;
+        d = (float*)ctx->y_stage.p;
+    }
+    HIP_TRY(ovfq::launch_decode_row(w->type, w->blocks, w->scales, w->in, row, d, ctx->stream));
+    if (host) {
+        HIP_TRY(hipMemcpyAsync(dst, d, (size_t)w->in * 4, hipMemcpyDeviceToHost, ctx->stream));
+        HIP_TRY(hipStreamSynchronize(ctx->stream));
+    }
+    return ok();
+}
+
+int ovfq_weight_decode_row(ovfq_ctx* ctx, const ovfq_weight* w, int row, float* dst) {
+    return decode_row_impl(ctx, w, row, dst, true);
+}
+
+int ovfq_weight_decode_row_dev(ovfq_ctx* ctx, const ovfq_weight* w, int row, float* dst) {
+    return decode_row_impl(ctx, w, row, dst, false);
+}
+
+// ---------------------------------------------------------------------------------------- quantisation
+
+static int quantize_impl(ovfq_ctx* ctx, bool k_quant, const float* x, int rows, int k, int8_t* q, float* s,
+                         int16_t* b, bool host) {
+    if (!ctx) return fail(OVFQ_ERR_NULL, "ctx is NULL");
+    if (!x || !q || !s || (k_quant && !b)) return fail(OVFQ_ERR_NULL, "a source or scratch pointer is NULL");
+    int rc = check_rows(rows);
+    if (rc) return rc;
+    const int blk = k_quant ? OVFQ_QK : OVFQ_Q8_BLOCK;
+    if (k <= 0 || k % blk)
+        return fail(OVFQ_ERR_SIZE, "Source length (%d) must be a multiple of %d.", k, blk);
+    if (!host) {
+        if ((rc = check_dev_align(x, "x")) || (rc = check_dev_align(q, "quants")) ||
+            (rc = check_dev_align(s, "scales")) || (rc = check_dev_align(b, "bsums")))
+            return rc;
+    }
+    const size_t n = (size_t)rows * k;
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    HIP_TRY(hipSetDevice(ctx->device));
+    const float* xd = x;
+    int8_t* qd = q;
+    float* sd = s;
+    int16_t* bd = b;
+    if (host) {
+        if ((rc = ensure(ctx, ctx->x_stage, n * 4))) return rc;
+        if ((rc = ensure(ctx, ctx->y_stage, n))) return rc;
+        if ((rc = ensure(ctx, ctx->y2_stage, n / blk * 4))) return rc;
+        if (k_quant && (rc = ensure(ctx, ctx->bias_stage, n / 16 * 2))) return rc;
+        HIP_TRY(hipMemcpyAsync(ctx->x_stage.p, x, n * 4, hipMemcpyHostToDevice, ctx->stream));
+        xd = (const float*)ctx->x_stage.p;
+        qd = (int8_t*)ctx->y_stage.p;
+        sd = (float*)ctx->y2_stage.p;
+        bd = (int16_t*)ctx->bias_stage.p;
+    }
+    if (k_quant) {
+        HIP_TRY(ovfq::launch_quantize_q8k(xd, (int64_t)(n / OVFQ_QK), qd, sd, bd, ctx->stream));
+    } else {
+        HIP_TRY(ovfq::launch_quantize_q8_0(xd, (int64_t)(n / OVFQ_Q8_BLOCK), qd, sd, ctx->stream));
+    }
+    if (host) {
+        HIP_TRY(hipMemcpyAsync(q, qd, n, hipMemcpyDeviceToHost, ctx->stream));
+        HIP_TRY(hipMemcpyAsync(s, sd, n / blk * 4, hipMemcpyDeviceToHost, ctx->stream));
+        if (k_quant) HIP_TRY(hipMemcpyAsync(b, bd, n / 16 * 2, hipMemcpyDeviceToHost, ctx->stream));
+        HIP_TRY(hipStreamSynchronize(ctx->stream));
+    }
+    return ok();
+}
+
+int ovfq_quantize_q8k(ovfq_ctx* ctx, const float* x, int rows, int k, int8_t* q, float* s, int16_t* b) {
+    return quantize_impl(ctx, true, x, rows, k, q, s, b, true);
+}
+int ovfq_quantize_q8k_dev(ovfq_ctx* ctx, const float* x, int rows, int k, int8_t* q, float* s, int16_t* b) {
+    return quantize_impl(ctx, true, x, rows, k, q, s, b, false);
+}
+int ovfq_quantize_q8_0(ovfq_ctx* ctx, const float* x, int rows, int k, int8_t* q, float* s) {
+    return quantize_impl(ctx, false, x, rows, k, q, s, nullptr, true);
+}
+int ovfq_quantize_q8_0_dev(ovfq_ctx* ctx, const float* x, int rows, int k, int8_t* q, float* s) {
+    return quantize_impl(ctx, false, x, rows, k, q, s, nullptr, false);
+}
+
+// ---------------------------------------------------------------------------------------- projections
+
+// Shared body of the fused (same activation) projections: count weights, one quantisation, one launch.
+static int project_impl(ovfq_ctx* ctx, int count, const ovfq_weight* const* ws, const float* x, int rows,
+                        const float* const* biases, float* const* ys, bool host) {
+    if (!ctx) return fail(OVFQ_ERR_NULL, "ctx is NULL");
+    if (count < 1 || count > ovfq::kMaxJobs) return fail(OVFQ_ERR_RANGE, "count (%d) must be in [1, 4]", count);
+    if (!ws || !ys) return fail(OVFQ_ERR_NULL, "weights / outputs array is NULL");
+    if (!x) return fail(OVFQ_ERR_NULL, "input is NULL");
+    int rc = check_rows(rows);
+    if (rc) return rc;
+    for (int i = 0; i < count; i++) {
+        if ((rc = check_weight(ctx, ws[i]))) return rc;
+        if (!ys[i]) return fail(OVFQ_ERR_NULL, "output %d is NULL", i);
+        if (ws[i]->type != ws[0]->type) return fail(OVFQ_ERR_TYPE, "fused weights must share a type");
+        if (ws[i]->in != ws[0]->in) return fail(OVFQ_ERR_SIZE, "fused weights must share inputSize");
+        if (!host && (rc = check_dev_align(ys[i], "output"))) return rc;
+    }
+    if (!host && (rc = check_dev_align(x, "input"))) return rc;
+    const int in = ws[0]->in;
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    HIP_TRY(hipSetDevice(ctx->device));
+    const float* xd = x;
+    const float* bd[ovfq::kMaxJobs] = {nullptr, nullptr, nullptr, nullptr};
+    float* yd[ovfq::kMaxJobs];
+    size_t y_off[ovfq::kMaxJobs];
+    if (host) {
+        size_t ytotal = 0, btotal = 0;
+        for (int i = 0; i < count; i++) {
+            y_off[i] = ytotal;
+            ytotal += (size_t)rows * ws[i]->out;
+            if (biases && biases[i]) btotal += ws[i]->out;
+        }
+        if ((rc = ensure(ctx, ctx->x_stage, (size_t)rows * in * 4))) return rc;
+        if ((rc = ensure(ctx, ctx->y_stage, ytotal * 4))) return rc;
+        if (btotal && (rc = ensure(ctx, ctx->bias_stage, btotal * 4))) return rc;
+        HIP_TRY(hipMemcpyAsync(ctx->x_stage.p, x, (size_t)rows * in * 4, hipMemcpyHostToDevice, ctx->stream));
+        xd = (const float*)ctx->x_stage.p;
+        size_t boff = 0;
+        for (int i = 0; i < count; i++) {
+            yd[i] = (float*)ctx->y_stage.p + y_off[i];
+            if (biases && biases[i]) {
+                float* bdst = (float*)ctx->bias_stage.p + boff;
+                HIP_TRY(hipMemcpyAsync(bdst, biases[i], (size_t)ws[i]->out * 4, hipMemcpyHostToDevice, ctx->stream));
+                bd[i] = bdst;
+                boff += ws[i]->out;
+            }
+        }
+    } else {
+        for (int i = 0; i < count; i++) {
+            yd[i] = ys[i];
+            bd[i] = biases ? biases[i] : nullptr;
+        }
+    }
+    ovfq::ActQ act;
+    if ((rc = quantize_into_scratch(ctx, ws[0]->type, xd, rows, in, &act))) return rc;
+    if ((rc = launch_projection(ctx, ws, count, bd, yd, rows, act))) return rc;
+    if (host) {
+        for (int i = 0; i < count; i++) {
+            HIP_TRY(hipMemcpyAsync(ys[i], yd[i], (size_t)rows * ws[i]->out * 4, hipMemcpyDeviceToHost, ctx->stream));
+        }
+        HIP_TRY(hipStreamSynchronize(ctx->stream));
+    }
+    return ok();
+}
+
+int ovfq_project(ovfq_ctx* ctx, const ovfq_weight* w, const float* x, int rows, const float* bias, float* y) {
+    const float* biases[1] = {bias};
+    float* ys[1] = {y};
+    return project_impl(ctx, 1, &w, x, rows, biases, ys, true);
+}
+
+int ovfq_project_dev(ovfq_ctx* ctx, const ovfq_weight* w, const float* x, int rows, const float* bias,
+                     float* y) {
+    const float* biases[1] = {bias};
+    float* ys[1] = {y};
+    return project_impl(ctx, 1, &w, x, rows, biases, ys, false);
+}
+
+int ovfq_project_gate_up(ovfq_ctx* ctx, const ovfq_weight* gate, const ovfq_weight* up, const float* x,
+                         float* gate_out, float* up_out) {
+    if (gate && up && (gate->out != up->out || gate->in != up->in))
+        return fail(OVFQ_ERR_SIZE, "gate and up must have the same shape");
+    const ovfq_weight* ws[2] = {gate, up};
+    float* ys[2] = {gate_out, up_out};
+    return project_impl(ctx, 2, ws, x, 1, nullptr, ys, true);
+}
+
+int ovfq_project_gate_up_dev(ovfq_ctx* ctx, const ovfq_weight* gate, const ovfq_weight* up, const float* x,
+                             float* gate_out, float* up_out) {
+    if (gate && up && (gate->out != up->out || gate->in != up->in))
+        return fail(OVFQ_ERR_SIZE, "gate and up must have the same shape");
+    const ovfq_weight* ws[2] = {gate, up};
+    float* ys[2] = {gate_out, up_out};
+    return project_impl(ctx, 2, ws, x, 1, nullptr, ys, false);
+}
+
+int ovfq_project_multi_dev(ovfq_ctx* ctx, int count, const ovfq_weight* const* weights, const float* x,
+                           const float* const* biases, float* const* ys) {
+    return project_impl(ctx, count, weights, x, 1, biases, ys, false);
+}
+
+static int prequant_impl(ovfq_ctx* ctx, const ovfq_weight* w, const int8_t* q, const float* s, const int16_t* b,
+                         int rows, const float* bias, float* y, bool host) {
+    if (!ctx) return fail(OVFQ_ERR_NULL, "ctx is NULL");
+    int rc = check_weight(ctx, w);
+    if (rc) return rc;
+    const bool kq = w->type != OVFQ_TYPE_Q8_0;
+    if (!q || !s || (kq && !b) || !y) return fail(OVFQ_ERR_NULL, "activation scratch or output is NULL");
+    if ((rc = check_rows(rows))) return rc;
+    if (!host) {
+        if ((rc = check_dev_align(q, "quants")) || (rc = check_dev_align(s, "scales")) ||
+            (rc = check_dev_align(b, "bsums")) || (rc = check_dev_align(y, "output")))
+            return rc;
+    }
+    const size_t n = (size_t)rows * w->in;
+    const int blk = kq ? OVFQ_QK : OVFQ_Q8_BLOCK;
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    HIP_TRY(hipSetDevice(ctx->device));
+    ovfq::ActQ act{q, s, b};
+    const float* bd = bias;
+    float* yd = y;
+    if (host) {
+        if ((rc = ensure(ctx, ctx->act_q, n))) return rc;
+        if ((rc = ensure(ctx, ctx->act_s, n / blk * 4))) return rc;
+        if (kq && (rc = ensure(ctx, ctx->act_b, n / 16 * 2))) return rc;
+        if ((rc = ensure(ctx, ctx->y_stage, (size_t)rows * w->out * 4))) return rc;
+        if (bias && (rc = ensure(ctx, ctx->bias_stage, (size_t)w->out * 4))) return rc;
+        HIP_TRY(hipMemcpyAsync(ctx->act_q.p, q, n, hipMemcpyHostToDevice, ctx->stream));
+        HIP_TRY(hipMemcpyAsync(ctx->act_s.p, s, n / blk * 4, hipMemcpyHostToDevice, ctx->stream));
+        if (kq) HIP_TRY(hipMemcpyAsync(ctx->act_b.p, b, n / 16 * 2, hipMemcpyHostToDevice, ctx->stream));
+        if (bias) {
+            HIP_TRY(hipMemcpyAsync(ctx->bias_stage.p, bias, (size_t)w->out * 4, hipMemcpyHostToDevice, ctx->stream));
+            bd = (const float*)ctx->bias_stage.p;
+        }
+        act = ovfq::ActQ{(const int8_t*)ctx->act_q.p, (const float*)ctx->act_s.p,
+                         kq ? (const int16_t*)ctx->act_b.p : nullptr};
+        yd = (float*)ctx->y_stage.p;
+    }
+    const ovfq_weight* ws[1] = {w};
+    const float* bs[1] = {bd};
+    float* ys[1] = {yd};
+    if ((rc = launch_projection(ctx, ws, 1, bs, ys, rows, act))) return rc;
+    if (host) {
+        HIP_TRY(hipMemcpyAsync(y, yd, (size_t)rows * w->out * 4, hipMemcpyDeviceToHost, ctx->stream));
+        HIP_TRY(hipStreamSynchronize(ctx->stream));
+    }
+    return ok();
+}
+
+int ovfq_project_prequantized(ovfq_ctx* ctx, const ovfq_weight* w, const int8_t* q, const float* s,
+                              const int16_t* b, int rows, const float* bias, float* y) {
+    return prequant_impl(ctx, w, q, s, b, rows, bias, y, true);
+}
+
+int ovfq_project_prequantized_dev(ovfq_ctx* ctx, const ovfq_weight* w, const int8_t* q, const float* s,
+                                  const int16_t* b, int rows, const float* bias, float* y) {
+    return prequant_impl(ctx, w, q, s, b, rows, bias, y, false);
+}
+
+int ovfq_project_multi_prequantized_dev(ovfq_ctx* ctx, int count, const ovfq_weight* const* ws, const int8_t* q,
+                                        const float* s, const int16_t* b, const float* const* biases,
+                                        float* const* ys) {
+    if (!ctx) return fail(OVFQ_ERR_NULL, "ctx is NULL");
+    if (count < 1 || count > ovfq::kMaxJobs) return fail(OVFQ_ERR_RANGE, "count (%d) must be in [1, 4]", count);
+    if (!ws || !ys) return fail(OVFQ_ERR_NULL, "weights / outputs array is NULL");
+    if (!q || !s || !b) return fail(OVFQ_ERR_NULL, "activation is NULL");
+    int rc;
+    for (int i = 0; i < count; i++) {
+        if ((rc = check_weight(ctx, ws[i]))) return rc;
+        if (!ys[i]) return fail(OVFQ_ERR_NULL, "output %d is NULL", i);
+        if (ws[i]->type == OVFQ_TYPE_Q8_0) return fail(OVFQ_ERR_TYPE, "Q8_K activations need K-quant weights");
+        if (ws[i]->type != ws[0]->type) return fail(OVFQ_ERR_TYPE, "fused weights must share a type");
+        if (ws[i]->in != ws[0]->in) return fail(OVFQ_ERR_SIZE, "fused weights must share inputSize");
+        if ((rc = check_dev_align(ys[i], "output"))) return rc;
+    }
+    if ((rc = check_dev_align(q, "quants")) || (rc = check_dev_align(s, "scales")) || (rc = check_dev_align(b, "bsums")))
+        return rc;
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    HIP_TRY(hipSetDevice(ctx->device));
+    if ((rc = launch_projection(ctx, ws, count, biases, ys, 1, ovfq::ActQ{q, s, b}))) return rc;
+    return ok();
+}
+
+// ---------------------------------------------------------------------------------------- weight encoders
+
+static int encode_impl(ovfq_ctx* ctx, int type, const float* w, int in, int out, void* dst, float* scales) {
+    if (!ctx) return fail(OVFQ_ERR_NULL, "ctx is NULL");
+    if (!w || !dst || (type == OVFQ_TYPE_Q8_0 && !scales)) return fail(OVFQ_ERR_NULL, "source or destination is NULL");
+    int rc = check_weight_shape(type, in, out);
+    if (rc) return rc;
+    if ((rc = check_dev_align(w, "weights")) || (rc = check_dev_align(dst, "dst"))) return rc;
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    HIP_TRY(hipSetDevice(ctx->device));
+    const int64_t n = (int64_t)in * out;
+    if (type == OVFQ_TYPE_Q4_K) {
+        HIP_TRY(ovfq::launch_encode_q4k(w, n / OVFQ_QK, (uint8_t*)dst, ctx->stream));
+    } else if (type == OVFQ_TYPE_Q6_K) {
+        HIP_TRY(ovfq::launch_encode_q6k(w, n / OVFQ_QK, (uint8_t*)dst, ctx->stream));
+    } else {
+        HIP_TRY(ovfq::launch_quantize_q8_0(w, n / OVFQ_Q8_BLOCK, (int8_t*)dst, scales, ctx->stream));
+    }
+    return ok();
+}
+
+int ovfq_quantize_weight_q4k_dev(ovfq_ctx* ctx, const float* w, int in, int out, uint8_t* dst) {
+    return encode_impl(ctx, OVFQ_TYPE_Q4_K, w, in, out, dst, nullptr);
+}
+int ovfq_quantize_weight_q6k_dev(ovfq_ctx* ctx, const float* w, int in, int out, uint8_t* dst) {
+    return encode_impl(ctx, OVFQ_TYPE_Q6_K, w, in, out, dst, nullptr);
+}
+int ovfq_quantize_weight_q8_0_dev(ovfq_ctx* ctx, const float* w, int in, int out, int8_t* q, float* s) {
+    return encode_impl(ctx, OVFQ_TYPE_Q8_0, w, in, out, q, s);
+}
+
+}  // extern "C"

@@ -1,0 +1,42 @@
+// ovfq_launch.h — host-side launchers for the ovfq kernels (internal to libovfq).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ovfq {
+
+constexpr int kMaxJobs = 4;
+
+// One output matrix of a (possibly fused) projection launch. Every job of a launch shares the activation.
+struct ProjJob {
+    const uint8_t* w;   // Q4_K / Q6_K blocks, or the Q8_0 int8 quant plane
+    const float* ws;    // Q8_0 f32 scale plane (NULL for K-quants)
+    const float* bias;  // may be NULL
+    float* y;           // [rows][n_rows]
+    int n_rows;         // output size of this matrix
+};
+
+// Q8_K activation (RT/Q4KDotKernel.cs:64-136 layout) or Q8_0 activation (bsums == NULL).
+struct ActQ {
+    const int8_t* q;
+    const float* s;
+    const int16_t* b;
+};
+
+hipError_t launch_quantize_q8k(const float* x, int64_t n_blocks, int8_t* q, float* s, int16_t* b, hipStream_t st);
+hipError_t launch_quantize_q8_0(const float* x, int64_t n_blocks, int8_t* q, float* s, hipStream_t st);
+
+// type: 12 (Q4_K) or 14 (Q6_K). `in` % 256 == 0. rows = activation rows (M).
+hipError_t launch_project_kquant(int type, const ProjJob* jobs, int njobs, int in, int rows, ActQ act,
+                                 hipStream_t st);
+hipError_t launch_project_q8_0(const ProjJob* jobs, int njobs, int in, int rows, ActQ act, hipStream_t st);
+
+hipError_t launch_encode_q4k(const float* w, int64_t n_blocks, uint8_t* dst, hipStream_t st);
+hipError_t launch_encode_q6k(const float* w, int64_t n_blocks, uint8_t* dst, hipStream_t st);
+
+// Row dequantisation (type 8/12/14). For Q8_0, `blocks` is the quant plane and `scales` the scale plane.
+hipError_t launch_decode_row(int type, const void* blocks, const float* scales, int in, int row, float* dst,
+                             hipStream_t st);
+
+}  // namespace ovfq

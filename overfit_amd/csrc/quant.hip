@@ -1,0 +1,302 @@
+// quant.hip — on-device quantisers: the Q8_K / Q8_0 activation quantisers every projection starts with,
+// the Q4_K / Q6_K weight encoders, and the row decoders.
+//
+// All of them are bit-exact restatements of the reference's scalar code: per-operation IEEE binary32
+// (the library is built with -ffp-contract=off, and fp32 division / reciprocal are the correctly rounded
+// ones), rintf for MathF.Round (round half to even), integer fp32 -> fp16 conversion with ties to even.
+#include "ovfq_device.h"
+#include "ovfq_launch.h"
+
+namespace ovfq {
+
+// ------------------------------------------------------------------------------------------ Q8_K activation
+// Q4KDotKernel.QuantizeActivationQ8K (RT/Q4KDotKernel.cs:71-136): one wave per 256-element super-block, four
+// consecutive elements per lane. absMax is a max (exact in any order); scale = absMax / 127f; inverse =
+// scale > 0 ? 1f / scale : 0f; q = clamp(rint(x * inverse), -127, 127); bsums[g] = sum of the 16 quants of
+// group g (four lanes).
+__global__ __launch_bounds__(256) void quantize_q8k_kernel(const float* __restrict__ x, int64_t n_blocks,
+                                                            int8_t* __restrict__ q, float* __restrict__ s,
+                                                            int16_t* __restrict__ bs) {
+    const int64_t blk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (blk >= n_blocks) return;
+    const int lane = threadIdx.x & 63;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(x + blk * kQK, kQK * 4);
+    const u32x4 raw = ld4(xr, lane * 16);
+    const float v0 = __builtin_bit_cast(float, raw.x), v1 = __builtin_bit_cast(float, raw.y);
+    const float v2 = __builtin_bit_cast(float, raw.z), v3 = __builtin_bit_cast(float, raw.w);
+    float am = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) am = fmaxf(am, __shfl_xor(am, off, 64));
+    const float scale = am / 127.0f;
+    const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+    const int q0 = (int)fminf(fmaxf(rintf(v0 * inv), -127.0f), 127.0f);
+    const int q1 = (int)fminf(fmaxf(rintf(v1 * inv), -127.0f), 127.0f);
+    const int q2 = (int)fminf(fmaxf(rintf(v2 * inv), -127.0f), 127.0f);
+    const int q3 = (int)fminf(fmaxf(rintf(v3 * inv), -127.0f), 127.0f);
+    const uint32_t packed = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) |
+                            ((uint32_t)(q3 & 0xff) << 24);
+    reinterpret_cast<uint32_t*>(q + blk * kQK)[lane] = packed;
+    const int gsum = quad_sum(q0 + q1 + q2 + q3);
+    if ((lane & 3) == 0) bs[blk * 16 + (lane >> 2)] = (int16_t)gsum;
+    if (lane == 0) s[blk] = scale;
+}
+
+// ------------------------------------------------------------------------------------------ Q8_0 activation
+// Q8DotKernel.Quantize (RT/Q8DotKernel.cs:42-91): 32-element blocks, eight lanes per block.
+__global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float* __restrict__ x, int64_t n_blocks,
+                                                             int8_t* __restrict__ q, float* __restrict__ s) {
+    const int64_t blk = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 3;
+    if (blk >= n_blocks) return;
+    const int sub = threadIdx.x & 7;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(x + blk * 32, 32 * 4);
+    const u32x4 raw = ld4(xr, sub * 16);
+    const float v0 = __builtin_bit_cast(float, raw.x), v1 = __builtin_bit_cast(float, raw.y);
+    const float v2 = __builtin_bit_cast(float, raw.z), v3 = __builtin_bit_cast(float, raw.w);
+    float am = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
+    am = fmaxf(am, __shfl_xor(am, 1, 64));
+    am = fmaxf(am, __shfl_xor(am, 2, 64));
+    am = fmaxf(am, __shfl_xor(am, 4, 64));
+    const float scale = am / 127.0f;
+    const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+    const int q0 = (int)fminf(fmaxf(rintf(v0 * inv), -127.0f), 127.0f);
+    const int q1 = (int)fminf(fmaxf(rintf(v1 * inv), -127.0f), 127.0f);
+    const int q2 = (int)fminf(fmaxf(rintf(v2 * inv), -127.0f), 127.0f);
+    const int q3 = (int)fminf(fmaxf(rintf(v3 * inv), -127.0f), 127.0f);
+    const uint32_t packed = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) |
+                            ((uint32_t)(q3 & 0xff) << 24);
+    reinterpret_cast<uint32_t*>(q + blk * 32)[sub] = packed;
+    if (sub == 0) s[blk] = scale;
+}
+
+// ------------------------------------------------------------------------------------------ Q4_K encoder
+// GgmlQuant.EncodeQ4_KBlock (LD/GgmlQuant.cs:31-126): one thread per 256-element super-block.
+__global__ __launch_bounds__(256) void encode_q4k_kernel(const float* __restrict__ w, int64_t n_blocks,
+                                                          uint8_t* __restrict__ dst) {
+    const int64_t blk = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (blk >= n_blocks) return;
+    const float* src = w + blk * kQK;
+    float sub_scale[8], sub_min[8];
+    for (int j = 0; j < 8; j++) {
+        float lo = __builtin_inff(), hi = -__builtin_inff();
+        for (int e = 0; e < 32; e++) {
+            const float v = src[j * 32 + e];
+            if (v < lo) lo = v;
+            if (v > hi) hi = v;
+        }
+        if (lo > 0.0f) lo = 0.0f;
+        sub_scale[j] = (hi - lo) / 15.0f;
+        sub_min[j] = -lo;
+    }
+    float max_scale = 0.0f, max_min = 0.0f;
+    for (int j = 0; j < 8; j++) {
+        if (sub_scale[j] > max_scale) max_scale = sub_scale[j];
+        if (sub_min[j] > max_min) max_min = sub_min[j];
+    }
+    const float inv_scale = max_scale > 0.0f ? 63.0f / max_scale : 0.0f;
+    const float inv_min = max_min > 0.0f ? 63.0f / max_min : 0.0f;
+    uint32_t sc[8], m[8];
+    for (int j = 0; j < 8; j++) {
+        const int a = (int)rintf(inv_scale * sub_scale[j]);
+        const int c = (int)rintf(inv_min * sub_min[j]);
+        sc[j] = (uint32_t)(a < 63 ? a : 63);
+        m[j] = (uint32_t)(c < 63 ? c : 63);
+    }
+    const float d = max_scale / 63.0f;
+    const float dmin = max_min / 63.0f;
+    uint32_t* out = reinterpret_cast<uint32_t*>(dst + blk * kQ4KBytes);
+    out[0] = (uint32_t)float_to_half_rne(d) | ((uint32_t)float_to_half_rne(dmin) << 16);
+    // PackScalesMins (LD/GgmlQuant.cs:164-172), four bytes per 32-bit word.
+    uint32_t p0 = 0, p1 = 0, p2 = 0;
+    for (int j = 0; j < 4; j++) {
+        p0 |= ((sc[j] & 0x3f) | ((sc[j + 4] >> 4) << 6)) << (8 * j);
+        p1 |= ((m[j] & 0x3f) | ((m[j + 4] >> 4) << 6)) << (8 * j);
+        p2 |= ((sc[j + 4] & 0x0f) | ((m[j + 4] & 0x0f) << 4)) << (8 * j);
+    }
+    out[1] = p0;
+    out[2] = p1;
+    out[3] = p2;
+    // Nibbles from the float d / dmin (LD/GgmlQuant.cs:108-116): qs[32p+e] = q[64p+e] | q[64p+32+e] << 4.
+    for (int p = 0; p < 4; p++) {
+        const float es_lo = d * (float)sc[2 * p], em_lo = dmin * (float)m[2 * p];
+        const float es_hi = d * (float)sc[2 * p + 1], em_hi = dmin * (float)m[2 * p + 1];
+        for (int e4 = 0; e4 < 32; e4 += 4) {
+            uint32_t word = 0;
+            for (int k = 0; k < 4; k++) {
+                const int e = e4 + k;
+                int l0 = es_lo > 0.0f ? (int)rintf((src[64 * p + e] + em_lo) / es_lo) : 0;
+                int l1 = es_hi > 0.0f ? (int)rintf((src[64 * p + 32 + e] + em_hi) / es_hi) : 0;
+                l0 = l0 < 0 ? 0 : (l0 > 15 ? 15 : l0);
+                l1 = l1 < 0 ? 0 : (l1 > 15 ? 15 : l1);
+                word |= (uint32_t)(l0 | (l1 << 4)) << (8 * k);
+            }
+            out[4 + (32 * p + e4) / 4] = word;
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------ Q6_K encoder
+// The build's own Q6_K encoder (the reference has none): the signed value of largest magnitude in each
+// 16-element sub-block maps to q = -32; one fp16 super-scale d = 1 / (-128 / largest sub-scale) carries 16
+// int8 sub-scales; quants are rint(x / (fp16(d) * sc)) clamped to [-32, 31], stored +32. The byte layout is
+// the inverse of GgmlDequant.DecodeQ6_KBlock (LD/GgmlDequant.cs:143-209).
+__global__ __launch_bounds__(256) void encode_q6k_kernel(const float* __restrict__ w, int64_t n_blocks,
+                                                          uint8_t* __restrict__ dst) {
+    const int64_t blk = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (blk >= n_blocks) return;
+    const float* src = w + blk * kQK;
+    uint8_t* out = dst + blk * kQ6KBytes;  // 210-byte stride: 2-byte aligned, so store 16-bit halves
+    float sub_scale[16];
+    float max_abs_scale = 0.0f, max_scale = 0.0f;
+    for (int s = 0; s < 16; s++) {
+        float amax = 0.0f, vmax = 0.0f;
+        for (int e = 0; e < 16; e++) {
+            const float v = src[s * 16 + e];
+            const float a = fabsf(v);
+            if (a > amax) {
+                amax = a;
+                vmax = v;
+            }
+        }
+        sub_scale[s] = amax > 0.0f ? vmax / -32.0f : 0.0f;
+        const float as = fabsf(sub_scale[s]);
+        if (as > max_abs_scale) {
+            max_abs_scale = as;
+            max_scale = sub_scale[s];
+        }
+    }
+    uint16_t* o16 = reinterpret_cast<uint16_t*>(out);
+    if (max_abs_scale == 0.0f) {
+        for (int i = 0; i < kQ6KBytes / 2; i++) o16[i] = 0;
+        return;
+    }
+    const float iscale = -128.0f / max_scale;
+    const float d = 1.0f / iscale;
+    const uint16_t dh = float_to_half_rne(d);
+    const float dd = half_bits_to_float(dh);
+    int sc[16];
+    for (int s = 0; s < 16; s++) {
+        const int v = (int)rintf(iscale * sub_scale[s]);
+        sc[s] = v < 127 ? v : 127;
+    }
+    for (int i = 0; i < 8; i++) {
+        o16[96 + i] = (uint16_t)((uint32_t)(sc[2 * i] & 0xff) | ((uint32_t)(sc[2 * i + 1] & 0xff) << 8));
+    }
+    o16[104] = dh;
+    auto quant = [&](int i) -> int {
+        const float ds = dd * (float)sc[i >> 4];
+        int l = 0;
+        if (ds != 0.0f) {
+            l = (int)rintf(src[i] / ds);
+            l = l < -32 ? -32 : (l > 31 ? 31 : l);
+        }
+        return l + 32;
+    };
+    for (int h = 0; h < 2; h++) {
+        for (int l = 0; l < 32; l += 2) {
+            uint32_t qlA = 0, qlB = 0, qh = 0;
+            for (int k = 0; k < 2; k++) {
+                const int q1 = quant(128 * h + l + k), q2 = quant(128 * h + 32 + l + k);
+                const int q3 = quant(128 * h + 64 + l + k), q4 = quant(128 * h + 96 + l + k);
+                qlA |= (uint32_t)((q1 & 0x0f) | ((q3 & 0x0f) << 4)) << (8 * k);
+                qlB |= (uint32_t)((q2 & 0x0f) | ((q4 & 0x0f) << 4)) << (8 * k);
+                qh |= (uint32_t)((q1 >> 4) | ((q2 >> 4) << 2) | ((q3 >> 4) << 4) | ((q4 >> 4) << 6)) << (8 * k);
+            }
+            o16[(64 * h + l) / 2] = (uint16_t)qlA;
+            o16[(64 * h + 32 + l) / 2] = (uint16_t)qlB;
+            o16[(128 + 32 * h + l) / 2] = (uint16_t)qh;
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------ row decode
+// GgmlDequant.DecodeQ4_KBlock (LD/GgmlDequant.cs:95-141) over one output row: one thread per element.
+__global__ __launch_bounds__(256) void decode_row_q4k_kernel(const uint8_t* __restrict__ row, float* __restrict__ dst) {
+    const uint8_t* b = row + (size_t)blockIdx.x * kQ4KBytes;
+    const int i = threadIdx.x;
+    const int p = i >> 6, hi = (i >> 5) & 1, e = i & 31;
+    const float d = half_bits_to_float((uint16_t)(b[0] | (b[1] << 8)));
+    const float dmin = half_bits_to_float((uint16_t)(b[2] | (b[3] << 8)));
+    const uint8_t* q = b + 4;
+    const int j = 2 * p + hi;
+    int sc, m;
+    if (j < 4) {
+        sc = q[j] & 63;
+        m = q[j + 4] & 63;
+    } else {
+        sc = (q[j + 4] & 0x0f) | ((q[j - 4] >> 6) << 4);
+        m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+    const int packed = b[16 + 32 * p + e];
+    const int nib = hi ? (packed >> 4) : (packed & 0x0f);
+    const float scale = d * (float)sc;
+    const float mn = dmin * (float)m;
+    dst[(size_t)blockIdx.x * kQK + i] = scale * (float)nib - mn;
+}
+
+// GgmlDequant.DecodeQ6_KBlock (LD/GgmlDequant.cs:143-209): dst = d * s * (q - 32).
+__global__ __launch_bounds__(256) void decode_row_q6k_kernel(const uint8_t* __restrict__ row, float* __restrict__ dst) {
+    const uint8_t* b = row + (size_t)blockIdx.x * kQ6KBytes;
+    const int i = threadIdx.x;
+    const int h = i >> 7, r = i & 127, grp = r >> 5, l = r & 31;
+    const int qlb = b[64 * h + l + ((grp & 1) ? 32 : 0)];
+    const int nib = (grp >= 2) ? (qlb >> 4) : (qlb & 0x0f);
+    const int hb = (b[128 + 32 * h + l] >> (2 * grp)) & 3;
+    const int q = nib | (hb << 4);
+    const int s = (int8_t)b[192 + 8 * h + (l >> 4) + 2 * grp];
+    const float d = half_bits_to_float((uint16_t)(b[208] | (b[209] << 8)));
+    dst[(size_t)blockIdx.x * kQK + i] = d * (float)s * (float)(q - 32);
+}
+
+// Q8Weight.DecodeRow (RT/Q8Weight.cs:81-106): dst[i] = scale[block] * quant[i].
+__global__ __launch_bounds__(256) void decode_row_q8_0_kernel(const int8_t* __restrict__ q, const float* __restrict__ s,
+                                                              int n, float* __restrict__ dst) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    dst[i] = s[i >> 5] * (float)q[i];
+}
+
+// ------------------------------------------------------------------------------------------ launchers
+
+hipError_t launch_quantize_q8k(const float* x, int64_t n_blocks, int8_t* q, float* s, int16_t* b, hipStream_t st) {
+    if (n_blocks <= 0) return hipSuccess;
+    const int64_t grid = (n_blocks + 3) / 4;
+    hipLaunchKernelGGL(quantize_q8k_kernel, dim3((unsigned)grid), dim3(256), 0, st, x, n_blocks, q, s, b);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_q8_0(const float* x, int64_t n_blocks, int8_t* q, float* s, hipStream_t st) {
+    if (n_blocks <= 0) return hipSuccess;
+    const int64_t grid = (n_blocks * 8 + 255) / 256;
+    hipLaunchKernelGGL(quantize_q8_0_kernel, dim3((unsigned)grid), dim3(256), 0, st, x, n_blocks, q, s);
+    return hipGetLastError();
+}
+
+hipError_t launch_encode_q4k(const float* w, int64_t n_blocks, uint8_t* dst, hipStream_t st) {
+    if (n_blocks <= 0) return hipSuccess;
+    hipLaunchKernelGGL(encode_q4k_kernel, dim3((unsigned)((n_blocks + 255) / 256)), dim3(256), 0, st, w, n_blocks, dst);
+    return hipGetLastError();
+}
+
+hipError_t launch_encode_q6k(const float* w, int64_t n_blocks, uint8_t* dst, hipStream_t st) {
+    if (n_blocks <= 0) return hipSuccess;
+    hipLaunchKernelGGL(encode_q6k_kernel, dim3((unsigned)((n_blocks + 255) / 256)), dim3(256), 0, st, w, n_blocks, dst);
+    return hipGetLastError();
+}
+
+hipError_t launch_decode_row(int type, const void* blocks, const float* scales, int in, int row, float* dst,
+                             hipStream_t st) {
+    if (type == 12) {
+        const uint8_t* r = static_cast<const uint8_t*>(blocks) + (size_t)row * (in / kQK) * kQ4KBytes;
+        hipLaunchKernelGGL(decode_row_q4k_kernel, dim3(in / kQK), dim3(256), 0, st, r, dst);
+    } else if (type == 14) {
+        const uint8_t* r = static_cast<const uint8_t*>(blocks) + (size_t)row * (in / kQK) * kQ6KBytes;
+        hipLaunchKernelGGL(decode_row_q6k_kernel, dim3(in / kQK), dim3(256), 0, st, r, dst);
+    } else {
+        const int8_t* q = static_cast<const int8_t*>(blocks) + (size_t)row * in;
+        const float* s = scales + (size_t)row * (in / 32);
+        hipLaunchKernelGGL(decode_row_q8_0_kernel, dim3((in + 255) / 256), dim3(256), 0, st, q, s, in, dst);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace ovfq

@@ -1,0 +1,154 @@
+"""Device context and buffer plumbing for the ctypes binding.
+
+Buffers may be numpy arrays / bytes (host memory: the synchronous C entry points are used) or torch tensors
+on the GPU (device memory: the asynchronous ``_dev`` entry points are used, on the context's stream, which
+is bound to torch's default stream so that torch work and library work are ordered). One call never mixes
+host and device buffers.
+"""
+import ctypes
+import threading
+
+import numpy as np
+
+from . import _lib
+from .errors import OverfitArgumentError, OverfitArgumentNullError, raise_for_status
+
+try:  # torch is plumbing for device memory only
+    import torch
+except Exception:  # pragma: no cover - torch is present in this image
+    torch = None
+
+_NP_OF_TORCH = {}
+if torch is not None:
+    _NP_OF_TORCH = {
+        torch.int8: np.int8,
+        torch.uint8: np.uint8,
+        torch.int16: np.int16,
+        torch.float32: np.float32,
+        torch.int32: np.int32,
+    }
+
+
+class Buf:
+    """A validated view of a caller buffer: address, element count, and where it lives."""
+
+    __slots__ = ("ptr", "size", "device", "obj")
+
+    def __init__(self, ptr, size, device, obj):
+        self.ptr = ptr
+        self.size = size
+        self.device = device
+        self.obj = obj
+
+
+def as_buf(x, dtype, name, allow_none=False):
+    """Wrap `x` (numpy / bytes / torch tensor) as a Buf of element type `dtype`. None -> None if allowed."""
+    if x is None:
+        if allow_none:
+            return None
+        raise OverfitArgumentNullError(f"{name} is None")
+    dtype = np.dtype(dtype)
+    if torch is not None and isinstance(x, torch.Tensor):
+        if _NP_OF_TORCH.get(x.dtype) is not dtype.type:
+            raise OverfitArgumentError(f"{name} must have dtype {dtype}, got {x.dtype}")
+        if not x.is_contiguous():
+            raise OverfitArgumentError(f"{name} must be contiguous")
+        return Buf(x.data_ptr(), x.numel(), x.is_cuda, x)
+    if isinstance(x, (bytes, bytearray, memoryview)):
+        x = np.frombuffer(x, dtype=np.uint8)
+        if dtype != np.uint8:
+            x = x.view(dtype)
+    if not isinstance(x, np.ndarray):
+        raise OverfitArgumentError(f"{name} must be a numpy array or a torch tensor")
+    if x.dtype != dtype:
+        raise OverfitArgumentError(f"{name} must have dtype {dtype}, got {x.dtype}")
+    if not x.flags["C_CONTIGUOUS"]:
+        raise OverfitArgumentError(f"{name} must be C-contiguous")
+    return Buf(x.ctypes.data, x.size, False, x)
+
+
+def same_side(*bufs):
+    """True if every non-None buffer is on the device, False if all are host; raises on a mix."""
+    sides = {b.device for b in bufs if b is not None}
+    if len(sides) > 1:
+        raise OverfitArgumentError("host and device buffers cannot be mixed in one call")
+    return sides.pop() if sides else False
+
+
+def is_empty(b):
+    return b is None or b.size == 0
+
+
+class Context:
+    """One libovfq context (a device plus the stream its work runs on)."""
+
+    def __init__(self, device: int = 0, bind_torch_stream: bool = True):
+        self.lib = _lib.load()
+        h = ctypes.c_void_p()
+        raise_for_status(self.lib.ovfq_ctx_create(device, ctypes.byref(h)), self.lib)
+        self.handle = h
+        self.device = device
+        if bind_torch_stream and torch is not None:
+            self.set_stream(torch.cuda.current_stream(device).cuda_stream)
+
+    def check(self, rc):
+        raise_for_status(rc, self.lib)
+
+    def set_stream(self, stream_handle):
+        self.check(self.lib.ovfq_ctx_set_stream(self.handle, ctypes.c_void_p(stream_handle or None)))
+
+    def synchronize(self):
+        self.check(self.lib.ovfq_ctx_synchronize(self.handle))
+
+    def close(self):
+        if self.handle:
+            self.lib.ovfq_ctx_destroy(self.handle)
+            self.handle = None
+
+    # ---------------------------------------------------------------- device-pointer conveniences
+
+    def quantize_q8k_dev(self, x, rows, k, q, s, b):
+        self.check(self.lib.ovfq_quantize_q8k_dev(self.handle, x.data_ptr(), rows, k, q.data_ptr(), s.data_ptr(),
+                                                  b.data_ptr()))
+
+    def project_dev(self, weight, x, y, bias=None, rows=1):
+        self.check(self.lib.ovfq_project_dev(self.handle, weight.handle, x.data_ptr(), rows,
+                                             None if bias is None else bias.data_ptr(), y.data_ptr()))
+
+    def project_multi_dev(self, weights, x, ys, biases=None):
+        n = len(weights)
+        W = (ctypes.c_void_p * n)(*[w.handle.value for w in weights])
+        Y = (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys])
+        B = None
+        if biases is not None:
+            B = (ctypes.c_void_p * n)(*[None if b is None else b.data_ptr() for b in biases])
+        self.check(self.lib.ovfq_project_multi_dev(self.handle, n, W, x.data_ptr(), B, Y))
+
+    def project_multi_prequantized_dev(self, weights, q, s, b, ys, biases=None):
+        n = len(weights)
+        W = (ctypes.c_void_p * n)(*[w.handle.value for w in weights])
+        Y = (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys])
+        B = None
+        if biases is not None:
+            B = (ctypes.c_void_p * n)(*[None if x is None else x.data_ptr() for x in biases])
+        self.check(self.lib.ovfq_project_multi_prequantized_dev(self.handle, n, W, q.data_ptr(), s.data_ptr(),
+                                                                b.data_ptr(), B, Y))
+
+    def project_prequantized_dev(self, weight, q, s, b, y, rows=1, bias=None):
+        self.check(self.lib.ovfq_project_prequantized_dev(
+            self.handle, weight.handle, q.data_ptr(), s.data_ptr(), None if b is None else b.data_ptr(), rows,
+            None if bias is None else bias.data_ptr(), y.data_ptr()))
+
+
+_default = {}
+_default_lock = threading.Lock()
+
+
+def default_context(device: int = 0) -> Context:
+    """The process-wide context for `device` (created on first use, bound to torch's default stream)."""
+    with _default_lock:
+        ctx = _default.get(device)
+        if ctx is None:
+            ctx = Context(device)
+            _default[device] = ctx
+        return ctx

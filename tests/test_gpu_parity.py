@@ -1,0 +1,343 @@
+"""Parity of the device path (libovfq through its C ABI) with the oracle on identical seeded inputs.
+
+The bar is bit-exactness everywhere: integer dequant and block integer dots are exact by construction, and
+the fp32 tail and the per-row super-block sum are evaluated in the reference's order, so every output float
+must equal the oracle's. The north-star tolerance (max relative error 1e-3, cosine >= 0.99999) is reported
+alongside as the outer bound.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from qdata import normal, random_q4k_blocks, random_q6k_blocks, set_subnormal_scales
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+ov = pytest.importorskip("overfit_amd")
+
+DEV = "cuda:0"
+
+
+def case(*what):
+    print("[case]", *what, flush=True, file=sys.stderr)
+
+
+def north_star(y, ref):
+    y64, r64 = y.astype(np.float64).ravel(), ref.astype(np.float64).ravel()
+    denom = np.maximum(np.abs(r64), 1e-30)
+    rel = float(np.max(np.abs(y64 - r64) / denom)) if r64.size else 0.0
+    cos = float(np.dot(y64, r64) / (np.linalg.norm(y64) * np.linalg.norm(r64) + 1e-300))
+    return rel, cos
+
+
+def assert_bit_exact(y, ref, what):
+    y = np.asarray(y, np.float32).reshape(ref.shape)
+    if not np.array_equal(y.view(np.uint32), ref.astype(np.float32).view(np.uint32)):
+        rel, cos = north_star(y, ref)
+        bad = int(np.count_nonzero(y.view(np.uint32) != ref.astype(np.float32).view(np.uint32)))
+        pytest.fail(f"{what}: {bad}/{y.size} outputs differ from the oracle (max rel {rel:.3e}, cos {cos:.8f})")
+
+
+def t(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    return ov.default_context()
+
+
+# ------------------------------------------------------------------------------------------------ quantizers
+
+@pytest.mark.parametrize("rows,k", [(1, 256), (3, 4096), (2, 14336), (7, 512)])
+def test_quantize_q8k_bit_exact(orc, ctx, rows, k):
+    case("quantize_q8k", rows, k)
+    rng = np.random.default_rng(rows * 1000 + k)
+    x = normal(rng, (rows, k))
+    x[0, :256] = 0.0                                    # all-zero block -> scale 0, quants 0
+    if k >= 512:
+        x[0, 256:512] = 0.0
+        x[0, 256] = 127.0
+        x[0, 257:265] = [2.5, 3.5, -2.5, -3.5, 0.5, -0.5, 1.5, 126.5]  # ties to even
+    if rows > 1:
+        x[1] *= 1e-30                                   # tiny values
+    q, s, b = (torch.empty(rows * k, dtype=torch.int8, device=DEV),
+               torch.empty(rows * k // 256, dtype=torch.float32, device=DEV),
+               torch.empty(rows * k // 16, dtype=torch.int16, device=DEV))
+    ctx.quantize_q8k_dev(t(x), rows, k, q, s, b)
+    rq, rd, rb = orc.quantize_q8k(x)
+    torch.cuda.synchronize()
+    assert np.array_equal(q.cpu().numpy(), rq.reshape(-1))
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), rd.reshape(-1).view(np.uint32))
+    assert np.array_equal(b.cpu().numpy(), rb.reshape(-1))
+
+
+def test_quantize_q8k_host_api_and_mirror(orc):
+    case("QuantizeActivationQ8K host")
+    rng = np.random.default_rng(5)
+    x = normal(rng, 1024)
+    q, s, b = np.zeros(1024, np.int8), np.zeros(4, np.float32), np.zeros(64, np.int16)
+    ov.Q4KDotKernel.QuantizeActivationQ8K(x, q, s, b)
+    rq, rd, rb = orc.quantize_q8k(x)
+    assert np.array_equal(q, rq[0]) and np.array_equal(s, rd[0]) and np.array_equal(b, rb[0])
+
+
+@pytest.mark.parametrize("k", [32, 128, 4096])
+def test_quantize_q8_0_bit_exact(orc, k):
+    case("quantize_q8_0", k)
+    rng = np.random.default_rng(k)
+    x = normal(rng, (3, k))
+    x[1, :32] = 0.0
+    q, s = np.zeros(3 * k, np.int8), np.zeros(3 * k // 32, np.float32)
+    for r in range(3):
+        ov.Q8DotKernel.Quantize(x[r], q[r * k:(r + 1) * k], s[r * k // 32:(r + 1) * k // 32])
+    rq, rs = orc.quantize_q8_0(x)
+    assert np.array_equal(q, rq.reshape(-1)) and np.array_equal(s, rs.reshape(-1))
+
+
+# ------------------------------------------------------------------------------------------------ encoders
+
+@pytest.mark.parametrize("fmt", ["q4k", "q6k"])
+@pytest.mark.parametrize("n,k", [(8, 512), (64, 4096), (3, 14336)])
+def test_weight_encoder_bit_exact(orc, fmt, n, k):
+    case("encode", fmt, n, k)
+    rng = np.random.default_rng(n * 7 + k)
+    w = normal(rng, (n, k), 0.02)
+    w[0, :256] = 0.37                    # constant block (GgmlQuantTests.cs:88-108)
+    w[1, :256] = 0.0                     # zero block
+    w[2 % n, 256:512] = -np.abs(w[2 % n, 256:512])  # all-negative block (lo < 0, hi < 0)
+    ref = orc.quantize_q4k(w) if fmt == "q4k" else orc.quantize_q6k(w)
+    got = ov.quantize_weight(t(w), ov.TYPE_Q4_K if fmt == "q4k" else ov.TYPE_Q6_K)
+    torch.cuda.synchronize()
+    assert np.array_equal(got.cpu().numpy(), ref.reshape(-1))
+
+
+def test_q8_0_weight_quantize_rows(orc):
+    case("Q8Weight.QuantizeRows")
+    rng = np.random.default_rng(3)
+    w = normal(rng, (50, 256), 0.05)
+    q, s = ov.quantize_weight(t(w), ov.TYPE_Q8_0)
+    rq, rs = orc.q8_quantize_rows(w)
+    torch.cuda.synchronize()
+    assert np.array_equal(q.cpu().numpy(), rq.reshape(-1)) and np.array_equal(s.cpu().numpy(), rs.reshape(-1))
+
+
+# ------------------------------------------------------------------------------------------------ projections
+
+KQ_SHAPES = [(256, 1), (256, 7), (512, 96), (1024, 33), (4096, 129), (4096, 1024), (14336, 65), (3072, 4099)]
+
+
+def _kq_blocks(rng, fmt, n, k):
+    if fmt == "q4k":
+        return set_subnormal_scales(random_q4k_blocks(rng, n * (k // 256))).reshape(n, -1)
+    return set_subnormal_scales(random_q6k_blocks(rng, n * (k // 256)), q6=True).reshape(n, -1)
+
+
+@pytest.mark.parametrize("fmt", ["q4k", "q6k"])
+@pytest.mark.parametrize("k,n", KQ_SHAPES)
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_kquant_project_bit_exact(orc, ctx, fmt, k, n, with_bias):
+    case("project", fmt, k, n, with_bias)
+    rng = np.random.default_rng(k * 31 + n + with_bias)
+    blocks = _kq_blocks(rng, fmt, n, k)
+    x = normal(rng, k)
+    bias = normal(rng, n) if with_bias else None
+    W = ov.Q4KWeight if fmt == "q4k" else ov.Q6KWeight
+    w = W(blocks, k, n)
+    ref = (orc.q4k_project if fmt == "q4k" else orc.q6k_project)(x, blocks, k, n, bias)
+    # device pointers
+    yd = ov.project(w, t(x), None if bias is None else t(bias))
+    torch.cuda.synchronize()
+    assert_bit_exact(yd.cpu().numpy(), ref, f"{fmt} {k}x{n} device")
+    # host pointers (synchronous entry point)
+    assert_bit_exact(ov.project(w, x, bias), ref, f"{fmt} {k}x{n} host")
+
+
+@pytest.mark.parametrize("fmt", ["q4k", "q6k"])
+@pytest.mark.parametrize("rows", [2, 3, 16, 17, 70])
+def test_kquant_batched_bit_exact(orc, fmt, rows):
+    case("batched", fmt, rows)
+    rng = np.random.default_rng(rows * 13)
+    k, n = 1024, 96
+    blocks = _kq_blocks(rng, fmt, n, k)
+    x = normal(rng, (rows, k))
+    bias = normal(rng, n)
+    w = (ov.Q4KWeight if fmt == "q4k" else ov.Q6KWeight)(blocks, k, n)
+    ref = (orc.q4k_project_batched if fmt == "q4k" else orc.q6k_project_batched)(x, rows, blocks, k, n, bias)
+    if fmt == "q4k":
+        assert np.array_equal(ref, orc.q4k_project_batched_ws(x, rows, blocks, k, n, bias))
+    y = ov.project(w, x, bias, rows=rows).reshape(rows, n)
+    assert_bit_exact(y, ref, f"{fmt} batched rows={rows}")
+
+
+@pytest.mark.parametrize("k,n", [(32, 5), (128, 4096), (4096, 300), (14336, 40)])
+@pytest.mark.parametrize("rows", [1, 3])
+def test_q8_0_project_bit_exact(orc, k, n, rows):
+    case("q8_0 project", k, n, rows)
+    rng = np.random.default_rng(k + n + rows)
+    wq, ws = orc.q8_quantize_rows(normal(rng, (n, k), 0.05))
+    wq[0, :32] = -128                               # GGUF Q8_0 weights may hold -128
+    x = normal(rng, (rows, k))
+    bias = normal(rng, n)
+    w = ov.Q8Weight(wq, ws, k, n)
+    ref = orc.q8_project_batched(x, rows, wq, ws, k, n, bias)
+    if rows == 1:
+        assert np.array_equal(ref[0], orc.q8_project(x[0], wq, ws, k, n, bias))
+    y = ov.project(w, x, bias, rows=rows).reshape(rows, n)
+    assert_bit_exact(y, ref, f"q8_0 {k}x{n} rows={rows}")
+
+
+def test_gate_up_and_multi_projection(orc, ctx):
+    case("gate_up / multi")
+    rng = np.random.default_rng(77)
+    k, n = 2048, 300
+    g = _kq_blocks(rng, "q4k", n, k)
+    u = _kq_blocks(rng, "q4k", n, k)
+    x = normal(rng, k)
+    wg, wu = ov.Q4KWeight(g, k, n), ov.Q4KWeight(u, k, n)
+    rg, ru = orc.q4k_project_gate_up(x, g, u, k, n)
+    go, uo = ov.project_gate_up(wg, wu, x)
+    assert_bit_exact(go, rg, "gate (host)")
+    assert_bit_exact(uo, ru, "up (host)")
+    go, uo = ov.project_gate_up(wg, wu, t(x))
+    torch.cuda.synchronize()
+    assert_bit_exact(go.cpu().numpy(), rg, "gate (device)")
+    assert_bit_exact(uo.cpu().numpy(), ru, "up (device)")
+    # q/k/v-style fused launch with different row counts and a bias on one of them
+    n2 = 77
+    v = _kq_blocks(rng, "q4k", n2, k)
+    wv = ov.Q4KWeight(v, k, n2)
+    bias_v = normal(rng, n2)
+    ys = [torch.empty(n, device=DEV), torch.empty(n, device=DEV), torch.empty(n2, device=DEV)]
+    ctx.project_multi_dev([wg, wu, wv], t(x), ys, [None, None, t(bias_v)])
+    torch.cuda.synchronize()
+    assert_bit_exact(ys[0].cpu().numpy(), rg, "multi gate")
+    assert_bit_exact(ys[1].cpu().numpy(), ru, "multi up")
+    assert_bit_exact(ys[2].cpu().numpy(), orc.q4k_project(x, v, k, n2, bias_v), "multi v")
+
+
+def test_reference_mirror_api_host_and_device(orc):
+    case("Q4KDotKernel / Q6KDotKernel / Q8DotKernel mirror")
+    rng = np.random.default_rng(9)
+    k, n = 512, 96
+    blocks = _kq_blocks(rng, "q4k", n, k)
+    w = ov.Q4KWeight(blocks, k, n)
+    x = (rng.random(k) * 2 - 1).astype(np.float32)
+    bias = normal(rng, n)
+    y = np.zeros(n, np.float32)
+    q, s, b = np.zeros(k, np.int8), np.zeros(2, np.float32), np.zeros(32, np.int16)
+    ov.Q4KDotKernel.Project(x, w, bias, y, q, s, b)
+    ref = orc.q4k_project(x, blocks, k, n, bias)
+    assert_bit_exact(y, ref, "Q4KDotKernel.Project")
+    rq, rd, rb = orc.quantize_q8k(x)
+    assert np.array_equal(q, rq[0]) and np.array_equal(b, rb[0])  # caller scratch holds the Q8_K form
+    y2 = np.zeros(n, np.float32)
+    ov.Q4KDotKernel.ProjectPreQuantized(w, bias, y2, q, s, b)
+    assert_bit_exact(y2, ref, "ProjectPreQuantized")
+    yd = torch.zeros(n, device=DEV)
+    ov.Q4KDotKernel.ProjectParallel(t(x), w, t(bias), yd, torch.zeros(k, dtype=torch.int8, device=DEV),
+                                    torch.zeros(2, device=DEV), torch.zeros(32, dtype=torch.int16, device=DEV))
+    torch.cuda.synchronize()
+    assert_bit_exact(yd.cpu().numpy(), ref, "ProjectParallel (device)")
+    # Dot of one block
+    blk = blocks[0, :144].copy()
+    got = ov.Q4KDotKernel.Dot(blk, rq[0, :256], float(rd[0, 0]), rb[0, :16])
+    assert np.float32(got) == np.float32(orc.lib().orc_q4k_dot(orc.P(blk), orc.P(rq[0]), float(rd[0, 0]), orc.P(rb[0])))
+    # errors raised before work, like the reference's argument exceptions
+    with pytest.raises(ov.OverfitArgumentError):
+        ov.Q4KDotKernel.Project(x, w, bias[:5], y, q, s, b)
+    with pytest.raises(ov.OverfitArgumentError):
+        ov.Q4KDotKernel.Project(x[:100], w, None, y, q, s, b)
+    with pytest.raises(ov.OverfitArgumentOutOfRangeError):
+        ov.Q4KDotKernel.ProjectBatched(x, 0, w, None, y, q, s, b)
+    with pytest.raises(ov.OverfitArgumentNullError):
+        ov.Q4KDotKernel.Project(x, None, None, y, q, s, b)
+    # Q6_K and Q8 mirrors
+    b6 = _kq_blocks(rng, "q6k", n, k)
+    w6 = ov.Q6KWeight(b6, k, n)
+    ov.Q6KDotKernel.Project(x, w6, None, y, q, s, b)
+    assert_bit_exact(y, orc.q6k_project(x, b6, k, n), "Q6KDotKernel.Project")
+    rows = 4
+    xb = normal(rng, (rows, k))
+    yb = np.zeros(rows * n, np.float32)
+    ov.Q6KDotKernel.ProjectBatched(xb, rows, w6, bias, yb, np.zeros(rows * k, np.int8), np.zeros(rows * 2, np.float32),
+                                   np.zeros(rows * 32, np.int16))
+    assert_bit_exact(yb, orc.q6k_project_batched(xb, rows, b6, k, n, bias), "Q6KDotKernel.ProjectBatched")
+    wq, ws = orc.q8_quantize_rows(normal(rng, (n, 128), 0.05))
+    w8 = ov.Q8Weight(wq, ws, 128, n)
+    x8 = normal(rng, 128)
+    y8 = np.zeros(n, np.float32)
+    ov.Q8DotKernel.Project(x8, w8, bias, y8, np.zeros(128, np.int8), np.zeros(4, np.float32))
+    assert_bit_exact(y8, orc.q8_project(x8, wq, ws, 128, n, bias), "Q8DotKernel.Project")
+    dw = ov.DecodeWeight(w)
+    assert dw.IsQ4K and not dw.IsQ6K and not dw.IsQuantized
+    yb4 = np.zeros(rows * n, np.float32)
+    ov.BatchedQuantProjection.Dispatch(xb, rows, dw, bias, yb4, k, n)
+    assert_bit_exact(yb4, orc.q4k_project_batched(xb, rows, blocks, k, n, bias), "BatchedQuantProjection")
+
+
+@pytest.mark.parametrize("fmt", ["q4k", "q6k", "q8"])
+def test_decode_row_bit_exact(orc, fmt):
+    case("DecodeRow", fmt)
+    rng = np.random.default_rng(4)
+    k, n = 1024, 9
+    if fmt == "q8":
+        wq, ws = orc.q8_quantize_rows(normal(rng, (n, k), 0.05))
+        w = ov.Q8Weight(wq, ws, k, n)
+        ref = lambda r: np.repeat(ws[r], 32) * wq[r].astype(np.float32)  # noqa: E731  RT/Q8Weight.cs:81-106
+    else:
+        blocks = _kq_blocks(rng, fmt, n, k)
+        w = (ov.Q4KWeight if fmt == "q4k" else ov.Q6KWeight)(blocks, k, n)
+        dec = orc.q4k_decode_row if fmt == "q4k" else orc.q6k_decode_row
+        ref = lambda r: dec(blocks, k, n, r)  # noqa: E731
+    for r in (0, 4, n - 1):
+        dst = np.zeros(k, np.float32)
+        w.DecodeRow(r, dst)
+        assert_bit_exact(dst, ref(r), f"{fmt} row {r}")
+    with pytest.raises(ov.OverfitArgumentOutOfRangeError):
+        w.DecodeRow(n, np.zeros(k, np.float32))
+
+
+# ------------------------------------------------------------------------------------------------ full sizes
+
+def test_llama3_8b_layer_decode_projections_bit_exact(orc, ctx):
+    """BASELINE config 2 at full size: q 4096x4096, k/v 1024x4096, o 4096x4096, gate/up 14336x4096 (Q4_K),
+    down 4096x14336 (Q6_K); weights N(0, 0.02) quantized on the device, activations N(0, 1)."""
+    case("config2 full-size layer")
+    gen = torch.Generator(device=DEV).manual_seed(20260519)
+    shapes = {"q": (4096, 4096), "k": (1024, 4096), "v": (1024, 4096), "o": (4096, 4096),
+              "gate": (14336, 4096), "up": (14336, 4096), "down": (4096, 14336)}
+    rng = np.random.default_rng(8)
+    for name, (n, k) in shapes.items():
+        case("config2", name, n, k)
+        wf = torch.randn(n, k, generator=gen, device=DEV) * 0.02
+        fmt = ov.TYPE_Q6_K if name == "down" else ov.TYPE_Q4_K
+        blocks = ov.quantize_weight(wf, fmt)
+        del wf
+        w = (ov.Q6KWeight if name == "down" else ov.Q4KWeight)(blocks, k, n)
+        x = normal(rng, k)
+        y = ov.project(w, t(x))
+        torch.cuda.synchronize()
+        hb = blocks.cpu().numpy().reshape(n, -1)
+        ref = (orc.q6k_project if name == "down" else orc.q4k_project)(x, hb, k, n)
+        assert_bit_exact(y.cpu().numpy(), ref, f"config2 {name}")
+        rel, cos = north_star(y.cpu().numpy(), ref)
+        assert rel <= 1e-3 and cos >= 0.99999
+
+
+def test_q6k_lm_head_full_size_bit_exact(orc):
+    """The Llama-3-8B Q6_K output head (128256 x 4096) of BASELINE config 4."""
+    case("LM head 128256x4096 Q6_K")
+    gen = torch.Generator(device=DEV).manual_seed(7)
+    n, k = 128256, 4096
+    wf = torch.randn(n, k, generator=gen, device=DEV) * 0.02
+    blocks = ov.quantize_weight(wf, ov.TYPE_Q6_K)
+    del wf
+    w = ov.Q6KWeight(blocks, k, n)
+    x = normal(np.random.default_rng(1), k)
+    y = ov.project(w, t(x))
+    torch.cuda.synchronize()
+    ref = orc.q6k_project(x, blocks.cpu().numpy().reshape(n, -1), k, n)
+    assert_bit_exact(y.cpu().numpy(), ref, "LM head")
