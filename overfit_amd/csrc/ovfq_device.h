@@ -47,6 +47,10 @@ __device__ __forceinline__ uint32_t ld1(__amdgpu_buffer_rsrc_t r, uint32_t off) 
     return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
 }
 
+// Reinterpret a 32-bit word as fp32. Always pass a scalar: __builtin_bit_cast applied directly to an
+// ext_vector element (v.y) reads element 0 with this compiler, so vector lanes are copied out first.
+__device__ __forceinline__ float as_float(uint32_t u) { return __builtin_bit_cast(float, u); }
+
 // Exact fp16 -> fp32 widening (v_cvt_f32_f16; fp16 denormals are preserved in the default MODE).
 __device__ __forceinline__ float half_lo(uint32_t w) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));

@@ -133,8 +133,8 @@ struct Q6K {
         const u32x3 sv = ld3(r, so & ~3u);
         w.s0 = __builtin_amdgcn_alignbyte(sv.y, sv.x, sh);
         w.s1 = __builtin_amdgcn_alignbyte(sv.z, sv.y, sh);
-        const uint32_t dw = ld1(r, (off + 208) & ~3u);
-        w.d = (off & 2u) ? (dw >> 16) : (dw & 0xffffu);
+        // d (bytes 208-209) with a 16-bit load: a dword read would run past the last block of the matrix.
+        w.d = __builtin_amdgcn_raw_buffer_load_b16(r, (int)(off + 208), 0, 0);
         return w;
     }
     __device__ __forceinline__ static A load_a(__amdgpu_buffer_rsrc_t qr, __amdgpu_buffer_rsrc_t sr,

@@ -17,13 +17,14 @@ namespace ovfq {
 __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float* __restrict__ x, int64_t n_blocks,
                                                             int8_t* __restrict__ q, float* __restrict__ s,
                                                             int16_t* __restrict__ bs) {
-    const int64_t blk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    // wave_id() is a readfirstlane value, so the buffer resource below is provably wave-uniform (SGPRs).
+    const int64_t blk = (int64_t)blockIdx.x * 4 + wave_id();
     if (blk >= n_blocks) return;
     const int lane = threadIdx.x & 63;
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(x + blk * kQK, kQK * 4);
     const u32x4 raw = ld4(xr, lane * 16);
-    const float v0 = __builtin_bit_cast(float, raw.x), v1 = __builtin_bit_cast(float, raw.y);
-    const float v2 = __builtin_bit_cast(float, raw.z), v3 = __builtin_bit_cast(float, raw.w);
+    const float v0 = as_float(raw.x), v1 = as_float(raw.y);
+    const float v2 = as_float(raw.z), v3 = as_float(raw.w);
     float am = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) am = fmaxf(am, __shfl_xor(am, off, 64));
@@ -45,13 +46,16 @@ __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float* __restri
 // Q8DotKernel.Quantize (RT/Q8DotKernel.cs:42-91): 32-element blocks, eight lanes per block.
 __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float* __restrict__ x, int64_t n_blocks,
                                                              int8_t* __restrict__ q, float* __restrict__ s) {
-    const int64_t blk = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 3;
-    if (blk >= n_blocks) return;
-    const int sub = threadIdx.x & 7;
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(x + blk * 32, 32 * 4);
-    const u32x4 raw = ld4(xr, sub * 16);
-    const float v0 = __builtin_bit_cast(float, raw.x), v1 = __builtin_bit_cast(float, raw.y);
-    const float v2 = __builtin_bit_cast(float, raw.z), v3 = __builtin_bit_cast(float, raw.w);
+    // One wave covers 8 consecutive blocks; the resource starts at the wave's first block (wave-uniform).
+    const int64_t wblk = ((int64_t)blockIdx.x * 4 + wave_id()) * 8;
+    const int lane = threadIdx.x & 63;
+    const int64_t blk = wblk + (lane >> 3);
+    if (wblk >= n_blocks) return;
+    const int sub = lane & 7;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(x + wblk * 32, rsrc_bytes((uint64_t)n_blocks * 128, (uint64_t)wblk * 128));
+    const u32x4 raw = ld4(xr, lane * 16);
+    const float v0 = as_float(raw.x), v1 = as_float(raw.y);
+    const float v2 = as_float(raw.z), v3 = as_float(raw.w);
     float am = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
     am = fmaxf(am, __shfl_xor(am, 1, 64));
     am = fmaxf(am, __shfl_xor(am, 2, 64));
@@ -64,8 +68,10 @@ __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float* __restr
     const int q3 = (int)fminf(fmaxf(rintf(v3 * inv), -127.0f), 127.0f);
     const uint32_t packed = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) |
                             ((uint32_t)(q3 & 0xff) << 24);
-    reinterpret_cast<uint32_t*>(q + blk * 32)[sub] = packed;
-    if (sub == 0) s[blk] = scale;
+    if (blk < n_blocks) {
+        reinterpret_cast<uint32_t*>(q + blk * 32)[sub] = packed;
+        if (sub == 0) s[blk] = scale;
+    }
 }
 
 // ------------------------------------------------------------------------------------------ Q4_K encoder

@@ -68,3 +68,16 @@ def test_product_package_does_not_import_the_oracle():
             if f.endswith((".py", ".cpp", ".hip", ".h")):
                 text = open(os.path.join(dirpath, f)).read()
                 assert not re.search(r"\boracle\b|ovfq_oracle|cpu_baseline", text), f
+
+
+def test_kernels_never_bit_cast_a_vector_element():
+    # __builtin_bit_cast(T, v.y) on an ext_vector element reads element 0 with this hipcc (it narrowed the Q8_K
+    # quantiser's 16-byte load to one dword); kernels copy lanes to scalars first (as_float).
+    import os
+    import re
+
+    csrc = os.path.join(os.path.dirname(overfit_amd.__file__), "csrc")
+    pat = re.compile(r"__builtin_bit_cast\s*\([^,]+,\s*[\w\.\[\]]+\.[xyzw]\s*\)")
+    for f in os.listdir(csrc):
+        text = open(os.path.join(csrc, f)).read()
+        assert not pat.search(text), f
