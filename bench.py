@@ -5,9 +5,9 @@ at M = 1 with the Q4_K_M mix — q 4096x4096, k/v 1024x4096, o 4096x4096, gate/u
 4096x14336 in Q6_K. Weights N(0, 0.02) from a seed, quantised on the device with the reference quantizer
 (GgmlQuant.QuantizeQ4_K) and the library's Q6_K encoder; activations N(0, 1) fp32, resident in HBM.
 
-One step = the layer's four distinct activations quantised to Q8_K and its seven projections:
-  quantize(x_attn) + fused q/k/v GEMV, quantize(x_o) + o GEMV, quantize(x_ffn) + fused gate/up GEMV,
-  quantize(x_down) + down GEMV.
+One step = the layer's four distinct activations quantised to Q8_K and its seven projections, in four launches
+(each launch quantises its fp32 activation in-kernel, then runs its projections): fused q/k/v, o, fused
+gate/up, down.
 To measure HBM rather than the 256 MB Infinity Cache, steps rotate over several independent layer copies
 (> 2x the cache). value = algorithmic bytes per step / time per step (weights + fp32 activations read once
 + fp32 outputs), in GB/s; decode_proj_tok_s = steps per second.
@@ -143,19 +143,16 @@ def main():
     x_in = {name: torch.randn(k, generator=gen, device=dev) for name, k in
             (("attn", 4096), ("o", 4096), ("ffn", 4096), ("down", 14336))}
     ys = {name: torch.empty(n, device=dev) for name, n, _, _ in LAYER}
-    qa = {name: (torch.empty(k, dtype=torch.int8, device=dev), torch.empty(k // 256, device=dev),
-                 torch.empty(k // 16, dtype=torch.int16, device=dev)) for name, k in
-          (("attn", 4096), ("o", 4096), ("ffn", 4096), ("down", 14336))}
 
     def step(ws):
-        for act, k in (("attn", 4096), ("o", 4096), ("ffn", 4096), ("down", 14336)):
-            q, s, b = qa[act]
-            ctx.quantize_q8k_dev(x_in[act], 1, k, q, s, b)
-        ctx.project_multi_prequantized_dev([ws["q"], ws["k"], ws["v"]], *qa["attn"], [ys["q"], ys["k"], ys["v"]])
-        ctx.project_multi_prequantized_dev([ws["o"]], *qa["o"], [ys["o"]])
-        ctx.project_multi_prequantized_dev([ws["gate"], ws["up"]], *qa["ffn"], [ys["gate"], ys["up"]])
-        ctx.project_multi_prequantized_dev([ws["down"]], *qa["down"], [ys["down"]])
+        # four launches: each quantises its fp32 activation to Q8_K in-kernel, then runs its projection(s)
+        ctx.project_multi_dev([ws["q"], ws["k"], ws["v"]], x_in["attn"], [ys["q"], ys["k"], ys["v"]])
+        ctx.project_multi_dev([ws["o"]], x_in["o"], [ys["o"]])
+        ctx.project_multi_dev([ws["gate"], ws["up"]], x_in["ffn"], [ys["gate"], ys["up"]])
+        ctx.project_multi_dev([ws["down"]], x_in["down"], [ys["down"]])
 
+    # Warm up eagerly (allocates any scratch), time K eager steps, then also capture one rotation over the layer
+    # copies into a HIP graph on a side stream and time its replays (GPU time without Python launch overhead).
     for i in range(args.warmup):
         step(copies[i % len(copies)])
     torch.cuda.synchronize()
@@ -166,25 +163,52 @@ def main():
         step(copies[i % len(copies)])
     t1.record()
     torch.cuda.synchronize()
-    ms = t0.elapsed_time(t1) / args.steps
+    eager_ms = t0.elapsed_time(t1) / args.steps
+
+    side = torch.cuda.Stream()
+
+    def capture(calls):
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            ctx.set_stream(side.cuda_stream)
+            for fn in calls:  # warm-up on the capture stream
+                fn()
+            side.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=side):
+                for fn in calls:
+                    fn()
+        ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        return g
+
+    def replay_us(g, n_calls, reps):
+        g.replay()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / (reps * n_calls)
+
+    g_step = capture([(lambda ws=ws: step(ws)) for ws in copies])
+    graph_reps = max(1, args.steps // len(copies))
+    graph_ms = replay_us(g_step, len(copies), graph_reps) / 1e3
+    ms = eager_ms  # headline: the plain eager loop, exactly K timed steps
     w_bytes, alg_bytes = layer_algorithmic_bytes()
     gbs = alg_bytes / (ms * 1e-3) / 1e9
     if args.profile_only:
-        print(json.dumps({"ms_per_step": ms, "GB/s": gbs}), flush=True)
+        print(json.dumps({"ms_per_step": ms, "graph_ms_per_step": graph_ms, "GB/s": gbs}), flush=True)
         return
 
-    # Dominant kernel: the fused gate/up Q4_K GEMV (66 MB per launch). Per-launch events on the same stream.
-    reps = 64
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-    q, s, b = qa["ffn"]
-    for i in range(reps):
-        ws = copies[i % len(copies)]
-        ev[i][0].record()
-        ctx.project_multi_prequantized_dev([ws["gate"], ws["up"]], q, s, b, [ys["gate"], ys["up"]])
-        ev[i][1].record()
-    torch.cuda.synchronize()
-    gu_us = sorted(a.elapsed_time(c) * 1e3 for a, c in ev)
-    gu_avg = sum(gu_us) / len(gu_us)
+    # Dominant kernel: the gate/up launch (Q8_K quantise + both 14336x4096 Q4_K GEMVs, 66 MB), replayed from a
+    # graph over the layer copies; per-launch time = graph time / launches.
+    g_gu = capture([(lambda ws=ws: ctx.project_multi_dev([ws["gate"], ws["up"]], x_in["ffn"], [ys["gate"], ys["up"]]))
+                    for ws in copies] * 4)
+    gu_avg = replay_us(g_gu, 4 * len(copies), 16)
     gu_bytes = 2 * weight_bytes(14336, 4096, "q4k") + 4 * 4096 + 4 * 2 * 14336
     achieved = gu_bytes / (gu_avg * 1e-6) / 1e9
     traffic = None
@@ -193,35 +217,33 @@ def main():
         traffic = json.load(open(tfile)).get("bytes_per_launch")
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                "kernel": "kquant_project_kernel<Q4K> (fused gate+up, 2x14336x4096)",
-                "avg_us": round(gu_avg, 3), "median_us": round(gu_us[len(gu_us) // 2], 3),
-                "algorithmic_bytes": gu_bytes}
+                "kernel": "kquant_gemv_kernel<Q4K,2> (Q8_K quantise + fused gate+up GEMV, 2x14336x4096)",
+                "avg_us": round(gu_avg, 3), "algorithmic_bytes": gu_bytes,
+                "timing": "HIP graph replay of 4x%d launches over %d weight copies, /launch" % (len(copies), len(copies))}
 
-    # Q4_K 4096x4096 GEMV, 64 weight copies (604 MB) rotated.
-    gen1 = torch.Generator(device="cuda:0").manual_seed(77)
-    c1 = []
-    for i in range(64):
-        wf = torch.randn(4096, 4096, generator=gen1, device=dev) * 0.02
-        c1.append(ov.Q4KWeight(ov.quantize_weight(wf, ov.TYPE_Q4_K), 4096, 4096))
-        del wf
-    q1, s1, b1 = qa["attn"]
-    y1 = torch.empty(4096, device=dev)
-    for i in range(8):
-        ctx.project_multi_prequantized_dev([c1[i]], q1, s1, b1, [y1])
-    ev1 = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(128)]
-    for i in range(128):
-        ev1[i][0].record()
-        ctx.project_multi_prequantized_dev([c1[i % 64]], q1, s1, b1, [y1])
-        ev1[i][1].record()
-    torch.cuda.synchronize()
-    c1_us = sorted(a.elapsed_time(c) * 1e3 for a, c in ev1)
-    c1_avg = sum(c1_us) / len(c1_us)
-    c1_bytes = weight_bytes(4096, 4096, "q4k") + 4 * 4096 + 4 * 4096
-    config1 = {"avg_us": round(c1_avg, 3), "median_us": round(c1_us[len(c1_us) // 2], 3),
-               "GB_s": round(c1_bytes / (c1_avg * 1e-6) / 1e9, 1),
-               "pct_peak": round(100 * c1_bytes / (c1_avg * 1e-6) / 1e9 / HBM_PEAK_GBS, 2),
-               "algorithmic_bytes": c1_bytes, "copies": 64}
-    del c1
+    def gemv_line(n, k, fmt, n_copies, label):
+        gen1 = torch.Generator(device="cuda:0").manual_seed(77 + n)
+        ws = []
+        for _ in range(n_copies):
+            wf = torch.randn(n, k, generator=gen1, device=dev) * 0.02
+            blocks = ov.quantize_weight(wf, ov.TYPE_Q6_K if fmt == "q6k" else ov.TYPE_Q4_K)
+            del wf
+            ws.append((ov.Q6KWeight if fmt == "q6k" else ov.Q4KWeight)(blocks, k, n))
+            del blocks
+        xk = torch.randn(k, generator=gen1, device=dev)
+        yk = torch.empty(n, device=dev)
+        g = capture([(lambda w=w: ctx.project_multi_dev([w], xk, [yk])) for w in ws])
+        us = replay_us(g, n_copies, max(2, 128 // n_copies))
+        nbytes = weight_bytes(n, k, fmt) + 4 * k + 4 * n
+        del g, ws
+        torch.cuda.empty_cache()
+        return {"shape": f"{n}x{k} {fmt}", "avg_us": round(us, 3), "GB_s": round(nbytes / (us * 1e-6) / 1e9, 1),
+                "pct_peak": round(100 * nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 2), "algorithmic_bytes": nbytes,
+                "copies": n_copies, "what": label}
+
+    config1 = gemv_line(4096, 4096, "q4k", 64, "BASELINE config 1: Q4_K 4096x4096 GEMV (quantise in-launch)")
+    large_q4k = gemv_line(128256, 4096, "q4k", 2, "Q4_K GEMV at LM-head size (asymptotic efficiency)")
+    lm_head = gemv_line(128256, 4096, "q6k", 2, "Llama-3-8B Q6_K LM head 128256x4096 (config 4)")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -247,9 +269,13 @@ def main():
                    "layer_copies_rotated": args.copies},
         "pct_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "decode_proj_tok_s": round(1e3 / ms, 1),
-        "decode_proj_tok_s_32_layers_plus_lm_head_est": None,
+        "graph_ms_per_step": round(graph_ms, 5),
+        "timing": "eager loop of K steps between two events (HIP-graph replay of the same steps: graph_ms_per_step)",
+        "decode_proj_tok_s_32_layers_plus_lm_head_est": round(1e3 / (32 * ms + lm_head["avg_us"] * 1e-3), 2),
         "roofline": roofline,
         "config1_q4k_gemv_4096x4096": config1,
+        "q4k_gemv_128256x4096": large_q4k,
+        "q6k_lm_head_128256x4096": lm_head,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -7,6 +7,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -174,8 +175,19 @@ int quantize_into_scratch(ovfq_ctx* c, int type, const float* x_dev, int rows, i
     return OVFQ_OK;
 }
 
+// Decode-kernel selection knob for experiments: OVFQ_GEMV_DISABLE=1 routes M = 1 through the general kernel.
+bool gemv_enabled() {
+    static const bool on = [] {
+        const char* v = getenv("OVFQ_GEMV_DISABLE");
+        return !(v && *v == '1');
+    }();
+    return on;
+}
+
+// One launch for `count` weights sharing an activation: either the fp32 activation x (quantised inside the
+// decode kernel) or an already-quantised `act`.
 int launch_projection(ovfq_ctx* c, const ovfq_weight* const* ws, int count, const float* const* biases,
-                      float* const* ys, int rows, ovfq::ActQ act) {
+                      float* const* ys, int rows, ovfq::ActQ act, const float* x = nullptr) {
     ovfq::ProjJob jobs[ovfq::kMaxJobs];
     for (int i = 0; i < count; i++) {
         jobs[i].w = static_cast<const uint8_t*>(ws[i]->blocks);
@@ -188,6 +200,8 @@ int launch_projection(ovfq_ctx* c, const ovfq_weight* const* ws, int count, cons
     const int in = ws[0]->in;
     if (type == OVFQ_TYPE_Q8_0) {
         HIP_TRY(ovfq::launch_project_q8_0(jobs, count, in, rows, act, c->stream));
+    } else if (rows == 1 && gemv_enabled() && ovfq::gemv_supported(in)) {
+        HIP_TRY(ovfq::launch_gemv_kquant(type, jobs, count, in, x, act, c->stream));
     } else {
         HIP_TRY(ovfq::launch_project_kquant(type, jobs, count, in, rows, act, c->stream));
     }
@@ -460,9 +474,16 @@ static int project_impl(ovfq_ctx* ctx, int count, const ovfq_weight* const* ws, 
             bd[i] = biases ? biases[i] : nullptr;
         }
     }
-    ovfq::ActQ act;
-    if ((rc = quantize_into_scratch(ctx, ws[0]->type, xd, rows, in, &act))) return rc;
-    if ((rc = launch_projection(ctx, ws, count, bd, yd, rows, act))) return rc;
+    if (rows == 1 && ws[0]->type != OVFQ_TYPE_Q8_0 && gemv_enabled() && ovfq::gemv_supported(in) &&
+        ovfq::gemv_quantize_inside(in)) {
+        // Decode: the Q8_K quantisation happens inside the projection launch.
+        if ((rc = launch_projection(ctx, ws, count, bd, yd, rows, ovfq::ActQ{nullptr, nullptr, nullptr}, xd)))
+            return rc;
+    } else {
+        ovfq::ActQ act;
+        if ((rc = quantize_into_scratch(ctx, ws[0]->type, xd, rows, in, &act))) return rc;
+        if ((rc = launch_projection(ctx, ws, count, bd, yd, rows, act))) return rc;
+    }
     if (host) {
         for (int i = 0; i < count; i++) {
             HIP_TRY(hipMemcpyAsync(ys[i], yd[i], (size_t)rows * ws[i]->out * 4, hipMemcpyDeviceToHost, ctx->stream));

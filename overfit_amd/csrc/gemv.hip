@@ -1,0 +1,297 @@
+// gemv.hip — decode (M = 1) Q4_K / Q6_K projection, one launch per (fused) projection.
+//
+// The launch covers everything the reference does for one ProjectParallel / ProjectGateUpParallel call
+// (RT/Q4KDotKernel.cs:485-645): each workgroup first quantises the fp32 activation to Q8_K into LDS (or copies
+// an already-quantised one, the ProjectPreQuantized case), then its waves stream weight rows. The quantiser is
+// the same device function as the standalone Q8_K kernel, so the activation is bit-identical to the
+// reference's QuantizeActivationQ8K.
+//
+// Grid: persistent — about `wg_per_cu` workgroups per CU, each wave walking row groups (R consecutive output
+// rows) with a stride of the total wave count, so the activation prologue is paid once per workgroup. The
+// weight stream is double-buffered in registers: the next (row group, 16-block chunk) item's loads are issued
+// before the current item is computed.
+//
+// Per item, a quad owns one super-block column; its fp32 block value is computed exactly as the reference's
+// Dot, and the row's sum over blocks is accumulated in ascending block order by one lane per row, so every
+// output is bit-identical to the reference's sequential loop.
+#include <cstdlib>
+
+#include "kquant_blocks.h"
+#include "ovfq_device.h"
+#include "ovfq_launch.h"
+
+namespace ovfq {
+
+struct GJob {
+    const uint8_t* w;
+    const float* bias;
+    float* y;
+    int n_rows;
+    int g_begin;  // first row group of this job
+};
+
+struct GArgs {
+    GJob job[kMaxJobs];
+    int njobs;
+    int total_groups;
+    int spr;
+    const float* x;  // fp32 activation, quantised in the kernel; NULL -> use q/s/b
+    const int8_t* q;
+    const float* s;
+    const int16_t* b;
+};
+
+constexpr int kGemvMaxSpr = 64;  // K <= 16384: the whole Q8_K activation fits in LDS (<= 23 KB)
+
+// Activation prologue: each wave takes four super-blocks at a time, one per 16-lane DPP row; lane l of a row
+// owns elements [16l, 16l+16) of its block, i.e. bsum group l, and writes one 16-byte LDS chunk.
+// `prefetch` issues the first weight item's loads; it runs after the activation loads so that waiting for the
+// activation does not also wait for the weights.
+template <class F, class Prefetch>
+__device__ __forceinline__ void stage_activation(const GArgs& a, uint8_t* lq, int16_t* lb, float* ls, int wave,
+                                                 int lane, Prefetch prefetch) {
+    constexpr int kPasses = kGemvMaxSpr / 16;
+    const int spr = a.spr;
+    const int l16 = lane & 15, row = lane >> 4;
+    const int pos = F::lds_pos(16 * l16);
+    if (a.x) {
+        const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)spr * kQK * 4);
+        u32x4 xv[kPasses][4];
+#pragma unroll
+        for (int p = 0; p < kPasses; p++) {
+            const int sb = p * 16 + wave * 4 + row;
+            if (p * 16 < spr) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) xv[p][i] = ld4(xr, (uint32_t)sb * 1024 + l16 * 64 + i * 16);
+            }
+        }
+        prefetch();
+#pragma unroll
+        for (int p = 0; p < kPasses; p++) {
+            if (p * 16 >= spr) break;
+            const int sb = p * 16 + wave * 4 + row;
+            float v[16];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                v[4 * i + 0] = as_float(xv[p][i].x);
+                v[4 * i + 1] = as_float(xv[p][i].y);
+                v[4 * i + 2] = as_float(xv[p][i].z);
+                v[4 * i + 3] = as_float(xv[p][i].w);
+            }
+            const Q8KRow r = q8k_quantize_row16(v);
+            if (sb < spr) {
+                *reinterpret_cast<u32x4*>(lq + sb * kLdsSlot + pos) = r.packed;
+                lb[sb * 16 + l16] = (int16_t)r.group_sum;
+                if (l16 == 0) ls[sb] = r.scale;
+            }
+        }
+    } else {
+        const __amdgpu_buffer_rsrc_t qr = make_rsrc(a.q, (uint32_t)spr * kQK);
+        const __amdgpu_buffer_rsrc_t br = make_rsrc(a.b, (uint32_t)spr * 32);
+        const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.s, (uint32_t)spr * 4);
+        u32x4 qv[kPasses];
+        uint32_t bv[kPasses], sv[kPasses];
+#pragma unroll
+        for (int p = 0; p < kPasses; p++) {
+            const int sb = p * 16 + wave * 4 + row;
+            if (p * 16 < spr) {
+                qv[p] = ld4(qr, (uint32_t)sb * kQK + l16 * 16);
+                bv[p] = __builtin_amdgcn_raw_buffer_load_b16(br, (int)((uint32_t)sb * 32 + l16 * 2), 0, 0);
+                sv[p] = ld1(sr, (uint32_t)sb * 4);
+            }
+        }
+        prefetch();
+#pragma unroll
+        for (int p = 0; p < kPasses; p++) {
+            if (p * 16 >= spr) break;
+            const int sb = p * 16 + wave * 4 + row;
+            if (sb < spr) {
+                *reinterpret_cast<u32x4*>(lq + sb * kLdsSlot + pos) = qv[p];
+                lb[sb * 16 + l16] = (int16_t)bv[p];
+                if (l16 == 0) ls[sb] = as_float(sv[p]);
+            }
+        }
+    }
+}
+
+template <class F, int R>
+__global__ __launch_bounds__(256) void kquant_gemv_kernel(const GArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int spr = a.spr;
+    uint8_t* lq = smem;
+    int16_t* lb = reinterpret_cast<int16_t*>(smem + spr * kLdsSlot);
+    float* ls = reinterpret_cast<float*>(smem + spr * (kLdsSlot + 32));
+    float* red = reinterpret_cast<float*>(smem + ((spr * (kLdsSlot + 36) + 15) & ~15));
+    const int wave = wave_id();
+    const int lane = threadIdx.x & 63;
+    const int q = lane >> 2, t = lane & 3;
+    const int nchunks = (spr + 15) >> 4;
+    const int stride = gridDim.x * 4;
+    const int total = a.total_groups;
+    const uint32_t row_bytes = (uint32_t)spr * F::kBytes;
+    float* rw = red + wave * R * 17;
+
+    // One work item = (row group g, 16-block chunk c): the weights of R rows plus, on a row group's last chunk,
+    // the bias of those rows.
+    struct Item {
+        typename F::W w[R];
+        uint32_t bias;
+    };
+
+    // Job and first row of row group g (wave-uniform).
+    auto locate = [&](int g, int& j, int& row0) {
+        j = 0;
+#pragma unroll
+        for (int i = 1; i < kMaxJobs; i++) j = (i < a.njobs && g >= a.job[i].g_begin) ? i : j;
+        row0 = (g - a.job[j].g_begin) * R;
+    };
+    // Issues the loads of item (g, c). The instruction stream is the same whether or not the item exists (past
+    // the end the resources have zero length, so the loads return 0 without touching memory): the compiler's
+    // wait counts then see a fixed number of younger loads and the prefetch overlaps the current item's math.
+    auto load_item = [&](int g, int c, bool valid, Item& it) {
+        int j, row0;
+        locate(valid ? g : 0, j, row0);
+        const uint64_t base_off = (uint64_t)row0 * row_bytes;
+        const uint64_t al = base_off & ~3ull;
+        const uint32_t extra = (uint32_t)(base_off & 3ull);
+        const __amdgpu_buffer_rsrc_t wr =
+            make_rsrc(a.job[j].w + al, valid ? rsrc_bytes((uint64_t)a.job[j].n_rows * row_bytes, al) : 0u);
+        const uint32_t sb = (uint32_t)(c * 16 + q);
+#pragma unroll
+        for (int r = 0; r < R; r++) it.w[r] = F::load_w(wr, extra + r * row_bytes + sb * F::kBytes, t);
+        const float* bias = a.job[j].bias;
+        const bool want_bias = valid && bias != nullptr && c == nchunks - 1;
+        const __amdgpu_buffer_rsrc_t bsr = make_rsrc(bias, want_bias ? (uint32_t)a.job[j].n_rows * 4 : 0u);
+        it.bias = ld1(bsr, (uint32_t)(row0 + (lane < R ? lane : 0)) * 4);
+    };
+
+    int g = blockIdx.x * 4 + wave;
+    int c = 0;
+    Item ia, ib;
+    stage_activation<F>(a, lq, lb, ls, wave, lane, [&] { load_item(g, 0, g < total, ia); });
+    __syncthreads();
+    if (g >= total) return;
+
+    float acc = 0.0f;
+    int a_chunk = -1;
+    typename F::A av;
+    // Computes item (g, c) from `cur` after issuing the loads of the next item into `nxt`.
+    auto step = [&](Item& cur, Item& nxt) -> bool {
+        int ng = g, nc = c + 1;
+        if (nc == nchunks) {
+            nc = 0;
+            ng += stride;
+        }
+        const bool more = ng < total;
+        load_item(ng, nc, more, nxt);
+        const int sb = c * 16 + q;
+        const bool live = sb < spr;
+        if (c != a_chunk) {
+            av = F::load_a_lds(lq, lb, ls, live ? sb : 0, t);
+            a_chunk = c;
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const float v = F::dot(cur.w[r], av, t);
+            if (t == 0 && live) rw[r * 17 + q] = v;
+        }
+        wave_sync();
+        if (lane < R) {
+            const int nq = min(16, spr - c * 16);
+            for (int qq = 0; qq < nq; qq++) acc += rw[lane * 17 + qq];
+        }
+        wave_sync();
+        if (c == nchunks - 1) {
+            int j, row0;
+            locate(g, j, row0);
+            if (lane < R && row0 + lane < a.job[j].n_rows) {
+                // bias[o] + sum (RT/Q4KDotKernel.cs:473); no add at all without a bias
+                a.job[j].y[row0 + lane] = a.job[j].bias ? as_float(cur.bias) + acc : acc;
+            }
+            acc = 0.0f;
+        }
+        g = ng;
+        c = nc;
+        return more;
+    };
+    while (step(ia, ib) && step(ib, ia)) {
+    }
+}
+
+namespace {
+
+int env_int(const char* name, int dflt) {
+    const char* v = getenv(name);
+    return v && *v ? atoi(v) : dflt;
+}
+
+int cu_count() {
+    static int cus[16] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return 256;
+    if (!cus[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
+template <class F, int R>
+hipError_t launch_gemv(GArgs& ga, const ProjJob* jobs, int njobs, hipStream_t st) {
+    int groups = 0;
+    for (int i = 0; i < njobs; i++) {
+        ga.job[i].g_begin = groups;
+        groups += (jobs[i].n_rows + R - 1) / R;
+    }
+    ga.total_groups = groups;
+    // Workgroups per CU (measured on MI355X): 2 for rows of up to 16 blocks, 3 for longer rows.
+    static const int forced_wg = env_int("OVFQ_GEMV_WG_PER_CU", 0);
+    const int wg_per_cu = forced_wg > 0 ? forced_wg : (ga.spr <= 16 ? 2 : 3);
+    int wgs = (groups + 3) / 4;
+    const int cap = cu_count() * wg_per_cu;
+    if (wgs > cap) wgs = cap;
+    const size_t lds = (size_t)((ga.spr * (kLdsSlot + 36) + 15) & ~15) + 4 * R * 17 * sizeof(float);
+    hipLaunchKernelGGL((kquant_gemv_kernel<F, R>), dim3(wgs), dim3(256), lds, st, ga);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool gemv_supported(int in) { return in % kQK == 0 && in / kQK <= kGemvMaxSpr; }
+
+// Every workgroup of the decode kernel quantises the whole activation; past 32 super-blocks (K > 8192) that
+// prologue costs more than one standalone quantise launch, so long rows are quantised once beforehand.
+bool gemv_quantize_inside(int in) { return in / kQK <= 32; }
+
+hipError_t launch_gemv_kquant(int type, const ProjJob* jobs, int njobs, int in, const float* x, ActQ act,
+                              hipStream_t st) {
+    GArgs ga{};
+    for (int i = 0; i < kMaxJobs; i++) {
+        if (i < njobs) {
+            ga.job[i] = GJob{jobs[i].w, jobs[i].bias, jobs[i].y, jobs[i].n_rows, 0};
+        } else {
+            ga.job[i] = GJob{nullptr, nullptr, nullptr, 0, 0x7fffffff};
+        }
+    }
+    ga.njobs = njobs;
+    ga.spr = in / kQK;
+    ga.x = x;
+    ga.q = act.q;
+    ga.s = act.s;
+    ga.b = act.b;
+    static const int forced_r = env_int("OVFQ_GEMV_ROWS_PER_WAVE", 0);
+    int R = forced_r;
+    // Rows per wave (measured on MI355X): 2 for rows of up to 16 blocks (K <= 4096), 1 for longer rows.
+    if (R != 1 && R != 2 && R != 4) R = ga.spr <= 16 ? 2 : 1;
+    if (type == 12) {
+        if (R == 4) return launch_gemv<Q4K, 4>(ga, jobs, njobs, st);
+        if (R == 2) return launch_gemv<Q4K, 2>(ga, jobs, njobs, st);
+        return launch_gemv<Q4K, 1>(ga, jobs, njobs, st);
+    }
+    if (R == 4) return launch_gemv<Q6K, 4>(ga, jobs, njobs, st);
+    if (R == 2) return launch_gemv<Q6K, 2>(ga, jobs, njobs, st);
+    return launch_gemv<Q6K, 1>(ga, jobs, njobs, st);
+}
+
+}  // namespace ovfq

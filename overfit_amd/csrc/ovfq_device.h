@@ -112,4 +112,74 @@ __device__ __forceinline__ uint16_t float_to_half_rne(float f) {
 
 __device__ __forceinline__ float half_bits_to_float(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 
+// Q4KDotKernel.QuantizeActivationQ8K (RT/Q4KDotKernel.cs:71-136) for one 256-element super-block held by a
+// whole wave, four consecutive elements per lane: absMax is a max (exact in any order); scale = absMax / 127f;
+// inverse = scale > 0 ? 1f / scale : 0f; q = clamp(rint(x * inverse), -127, 127). Returns the four quants
+// packed in a dword (element 4*lane in the low byte), the sum of the 16-element group (every lane of the quad
+// holds it) and the block scale.
+struct Q8KLane {
+    uint32_t packed;
+    int group_sum;
+    float scale;
+};
+
+__device__ __forceinline__ Q8KLane q8k_quantize_wave(float v0, float v1, float v2, float v3) {
+    float am = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) am = fmaxf(am, __shfl_xor(am, off, 64));
+    const float scale = am / 127.0f;
+    const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+    const int q0 = (int)fminf(fmaxf(rintf(v0 * inv), -127.0f), 127.0f);
+    const int q1 = (int)fminf(fmaxf(rintf(v1 * inv), -127.0f), 127.0f);
+    const int q2 = (int)fminf(fmaxf(rintf(v2 * inv), -127.0f), 127.0f);
+    const int q3 = (int)fminf(fmaxf(rintf(v3 * inv), -127.0f), 127.0f);
+    Q8KLane r;
+    r.packed = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) |
+               ((uint32_t)(q3 & 0xff) << 24);
+    r.group_sum = quad_sum(q0 + q1 + q2 + q3);
+    r.scale = scale;
+    return r;
+}
+
+// Max over the 16 lanes of a DPP row; every lane of the row receives it. Used on the bit patterns of
+// non-negative floats, whose unsigned integer order is their numeric order.
+__device__ __forceinline__ uint32_t row16_max_u32(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xb1, 0xf, 0xf, false));   // quad_perm [1,0,3,2]
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4e, 0xf, 0xf, false));   // quad_perm [2,3,0,1]
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xf, 0xf, false));  // row_half_mirror
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xf, 0xf, false));  // row_mirror
+    return v;
+}
+
+// The same Q8_K quantisation with one super-block spread over a 16-lane row, sixteen consecutive elements per
+// lane (the lane's elements are exactly one bsum group). x holds the lane's 16 values; returns the 16 quants
+// in four dwords, the group sum and the block scale.
+struct Q8KRow {
+    u32x4 packed;
+    int group_sum;
+    float scale;
+};
+
+__device__ __forceinline__ Q8KRow q8k_quantize_row16(const float (&x)[16]) {
+    uint32_t am = 0;
+#pragma unroll
+    for (int i = 0; i < 16; i++) am = max(am, __builtin_bit_cast(uint32_t, fabsf(x[i])));
+    const float absmax = __builtin_bit_cast(float, row16_max_u32(am));
+    const float scale = absmax / 127.0f;
+    const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+    Q8KRow r;
+    int sum = 0;
+    uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int qv = (int)fminf(fmaxf(rintf(x[i] * inv), -127.0f), 127.0f);
+        sum += qv;
+        w[i >> 2] |= (uint32_t)(qv & 0xff) << (8 * (i & 3));
+    }
+    r.packed = u32x4{w[0], w[1], w[2], w[3]};
+    r.group_sum = sum;
+    r.scale = scale;
+    return r;
+}
+
 }  // namespace ovfq

@@ -30,6 +30,12 @@ hipError_t launch_quantize_q8_0(const float* x, int64_t n_blocks, int8_t* q, flo
 // type: 12 (Q4_K) or 14 (Q6_K). `in` % 256 == 0. rows = activation rows (M).
 hipError_t launch_project_kquant(int type, const ProjJob* jobs, int njobs, int in, int rows, ActQ act,
                                  hipStream_t st);
+// Decode (M = 1) K-quant projection with the activation staged in LDS: x != NULL quantises the fp32 activation
+// inside the launch; x == NULL copies the prequantised `act`. Requires gemv_supported(in).
+bool gemv_supported(int in);
+bool gemv_quantize_inside(int in);
+hipError_t launch_gemv_kquant(int type, const ProjJob* jobs, int njobs, int in, const float* x, ActQ act,
+                              hipStream_t st);
 hipError_t launch_project_q8_0(const ProjJob* jobs, int njobs, int in, int rows, ActQ act, hipStream_t st);
 
 hipError_t launch_encode_q4k(const float* w, int64_t n_blocks, uint8_t* dst, hipStream_t st);

@@ -23,23 +23,10 @@ __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float* __restri
     const int lane = threadIdx.x & 63;
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(x + blk * kQK, kQK * 4);
     const u32x4 raw = ld4(xr, lane * 16);
-    const float v0 = as_float(raw.x), v1 = as_float(raw.y);
-    const float v2 = as_float(raw.z), v3 = as_float(raw.w);
-    float am = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) am = fmaxf(am, __shfl_xor(am, off, 64));
-    const float scale = am / 127.0f;
-    const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
-    const int q0 = (int)fminf(fmaxf(rintf(v0 * inv), -127.0f), 127.0f);
-    const int q1 = (int)fminf(fmaxf(rintf(v1 * inv), -127.0f), 127.0f);
-    const int q2 = (int)fminf(fmaxf(rintf(v2 * inv), -127.0f), 127.0f);
-    const int q3 = (int)fminf(fmaxf(rintf(v3 * inv), -127.0f), 127.0f);
-    const uint32_t packed = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) |
-                            ((uint32_t)(q3 & 0xff) << 24);
-    reinterpret_cast<uint32_t*>(q + blk * kQK)[lane] = packed;
-    const int gsum = quad_sum(q0 + q1 + q2 + q3);
-    if ((lane & 3) == 0) bs[blk * 16 + (lane >> 2)] = (int16_t)gsum;
-    if (lane == 0) s[blk] = scale;
+    const Q8KLane r = q8k_quantize_wave(as_float(raw.x), as_float(raw.y), as_float(raw.z), as_float(raw.w));
+    reinterpret_cast<uint32_t*>(q + blk * kQK)[lane] = r.packed;
+    if ((lane & 3) == 0) bs[blk * 16 + (lane >> 2)] = (int16_t)r.group_sum;
+    if (lane == 0) s[blk] = r.scale;
 }
 
 // ------------------------------------------------------------------------------------------ Q8_0 activation

@@ -341,3 +341,43 @@ def test_q6k_lm_head_full_size_bit_exact(orc):
     torch.cuda.synchronize()
     ref = orc.q6k_project(x, blocks.cpu().numpy().reshape(n, -1), k, n)
     assert_bit_exact(y.cpu().numpy(), ref, "LM head")
+
+
+def test_graph_replay_matches_eager(orc, ctx):
+    """The bench replays captured decode steps; every replay must reproduce the eager outputs bit-for-bit
+    (replays interleaved with eager work and synchronisations)."""
+    case("graph replay")
+    rng = np.random.default_rng(12)
+    k, n, k2 = 4096, 512, 14336
+    wq = ov.Q4KWeight(_kq_blocks(rng, "q4k", n, k), k, n)
+    wu = ov.Q4KWeight(_kq_blocks(rng, "q4k", n, k), k, n)
+    wd = ov.Q6KWeight(_kq_blocks(rng, "q6k", 256, k2), k2, 256)
+    x, xd = t(normal(rng, k)), t(normal(rng, k2))
+    ys = [torch.empty(n, device=DEV), torch.empty(n, device=DEV), torch.empty(256, device=DEV)]
+
+    def step():
+        ctx.project_multi_dev([wq, wu], x, ys[:2])
+        ctx.project_multi_dev([wd], xd, ys[2:])
+
+    step()
+    torch.cuda.synchronize()
+    eager = [y.cpu().numpy().copy() for y in ys]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        ctx.set_stream(side.cuda_stream)
+        step()
+        side.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=side):
+            step()
+    ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+    for rep in range(4):
+        for y in ys:
+            y.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        for y, e in zip(ys, eager):
+            assert np.array_equal(y.cpu().numpy().view(np.uint32), e.view(np.uint32)), f"replay {rep}"
+        step()  # eager work between replays
+        torch.cuda.synchronize()
