@@ -121,6 +121,9 @@ def main():
     ap.add_argument("--copies", type=int, default=4, help="layer copies rotated to defeat the 256 MB cache")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-only", action="store_true", help="only the timed layer loop (for rocprof runs)")
+    ap.add_argument("--pmc", action="store_true",
+                    help="for rocprofv3 --pmc runs: 16 gate/up launches, then 16 plain 64 MiB device copies "
+                         "(the counter calibration reference)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -153,6 +156,19 @@ def main():
 
     # Warm up eagerly (allocates any scratch), time K eager steps, then also capture one rotation over the layer
     # copies into a HIP graph on a side stream and time its replays (GPU time without Python launch overhead).
+    if args.pmc:
+        for i in range(16):
+            ws = copies[i % len(copies)]
+            ctx.project_multi_dev([ws["gate"], ws["up"]], x_in["ffn"], [ys["gate"], ys["up"]])
+        torch.cuda.synchronize()
+        src = torch.ones(16 * 1024 * 1024, device=dev)  # 64 MiB
+        dst = torch.empty_like(src)
+        for _ in range(16):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"pmc_run": "gate/up x16 then copy 64MiB x16"}), flush=True)
+        return
+
     for i in range(args.warmup):
         step(copies[i % len(copies)])
     torch.cuda.synchronize()
