@@ -202,6 +202,8 @@ int launch_projection(ovfq_ctx* c, const ovfq_weight* const* ws, int count, cons
         HIP_TRY(ovfq::launch_project_q8_0(jobs, count, in, rows, act, c->stream));
     } else if (rows == 1 && gemv_enabled() && ovfq::gemv_supported(in)) {
         HIP_TRY(ovfq::launch_gemv_kquant(type, jobs, count, in, x, act, c->stream));
+    } else if (ovfq::mfma_supported(type, rows)) {
+        HIP_TRY(ovfq::launch_project_mfma(type, jobs, count, in, rows, act, c->stream));
     } else {
         HIP_TRY(ovfq::launch_project_kquant(type, jobs, count, in, rows, act, c->stream));
     }

@@ -36,6 +36,10 @@ bool gemv_supported(int in);
 bool gemv_quantize_inside(int in);
 hipError_t launch_gemv_kquant(int type, const ProjJob* jobs, int njobs, int in, const float* x, ActQ act,
                               hipStream_t st);
+// Batched (M >= mfma_min_rows) K-quant projection on int8 MFMA; bit-identical to launch_project_kquant.
+bool mfma_supported(int type, int rows);
+hipError_t launch_project_mfma(int type, const ProjJob* jobs, int njobs, int in, int rows, ActQ act,
+                               hipStream_t st);
 hipError_t launch_project_q8_0(const ProjJob* jobs, int njobs, int in, int rows, ActQ act, hipStream_t st);
 
 hipError_t launch_encode_q4k(const float* w, int64_t n_blocks, uint8_t* dst, hipStream_t st);

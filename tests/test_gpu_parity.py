@@ -172,6 +172,92 @@ def test_kquant_batched_bit_exact(orc, fmt, rows):
     assert_bit_exact(y, ref, f"{fmt} batched rows={rows}")
 
 
+# ------------------------------------------------------------------------------------------------ prefill (MFMA)
+
+# rows >= 32 run on the int8-MFMA kernel: partial activation tiles (33, 70, 200), partial 64-row weight tiles
+# (n = 130, 200, 1000), an odd super-block count (k = 2304: Q6_K rows only 2-byte aligned), one super-block.
+PREFILL_SHAPES = [(32, 256, 64), (33, 768, 1000), (64, 1024, 96), (70, 512, 200), (128, 4096, 130),
+                  (200, 2304, 64)]
+
+
+@pytest.mark.parametrize("fmt", ["q4k", "q6k"])
+@pytest.mark.parametrize("rows,k,n", PREFILL_SHAPES)
+def test_kquant_prefill_bit_exact(orc, ctx, fmt, rows, k, n):
+    case("prefill", fmt, rows, k, n)
+    rng = np.random.default_rng(rows * 7 + k + n)
+    blocks = _kq_blocks(rng, fmt, n, k)
+    x = normal(rng, (rows, k))
+    bias = normal(rng, n)
+    w = (ov.Q4KWeight if fmt == "q4k" else ov.Q6KWeight)(blocks, k, n)
+    batched = orc.q4k_project_batched if fmt == "q4k" else orc.q6k_project_batched
+    ref = batched(x, rows, blocks, k, n, bias)
+    yd = ov.project(w, t(x), t(bias), rows=rows)
+    torch.cuda.synchronize()
+    assert_bit_exact(yd.cpu().numpy().reshape(rows, n), ref, f"{fmt} prefill {rows}x{k}x{n} device")
+    ref0 = batched(x, rows, blocks, k, n, None)
+    assert_bit_exact(ov.project(w, x, None, rows=rows).reshape(rows, n), ref0, f"{fmt} prefill host, no bias")
+
+
+def _extreme_blocks(fmt, n, k):
+    """Blocks at the ends of the integer ranges the MFMA operand split must hold: Q4_K sc = m = 63 with nibble 15
+    (sc*nib = 945) and nibble 0; Q6_K scale -128 with q = 0 (sc*(q-32) = +4096), scale 127 with q = 63 and q = 0
+    (3937, -4064), scale -128 with q = 63 (-3968)."""
+    spr = k // 256
+    if fmt == "q4k":
+        b = np.zeros((n * spr, 144), np.uint8)
+        b[:, 0:2] = np.frombuffer(np.float16(0.25).tobytes(), np.uint8)
+        b[:, 2:4] = np.frombuffer(np.float16(0.125).tobytes(), np.uint8)
+        b[:, 4:16] = 0xFF
+        b[:, 16:] = np.where((np.arange(n * spr) % 2 == 0)[:, None], 0xFF, 0x00)
+        return b.reshape(n, -1)
+    b = np.zeros((n * spr, 210), np.uint8)
+    kind = np.arange(n * spr) % 4
+    b[:, 192:208] = np.where((kind % 2 == 0)[:, None], 0x80, 0x7F)
+    q63 = (kind == 1) | (kind == 3)
+    b[q63, :192] = 0xFF
+    b[:, 208:210] = np.frombuffer(np.float16(0.01).tobytes(), np.uint8)
+    return b.reshape(n, -1)
+
+
+@pytest.mark.parametrize("fmt", ["q4k", "q6k"])
+def test_kquant_prefill_range_extremes(orc, fmt):
+    case("prefill extremes", fmt)
+    rows, k, n = 48, 1024, 64
+    blocks = _extreme_blocks(fmt, n, k)
+    rng = np.random.default_rng(5)
+    x = np.sign(normal(rng, (rows, k))).astype(np.float32)  # every quant +-127
+    x[1::2] = normal(rng, (rows // 2, k))
+    w = (ov.Q4KWeight if fmt == "q4k" else ov.Q6KWeight)(blocks, k, n)
+    ref = (orc.q4k_project_batched if fmt == "q4k" else orc.q6k_project_batched)(x, rows, blocks, k, n)
+    assert_bit_exact(ov.project(w, x, None, rows=rows).reshape(rows, n), ref, f"{fmt} extremes")
+
+
+def test_llama3_8b_layer_prefill_sampled_rows(orc):
+    """BASELINE config 3 shapes at M = 512 (q 4096x4096, gate 14336x4096 Q4_K; down 4096x14336 Q6_K) at full size
+    on the device; 40 sampled weight rows (all 512 activation rows each) are checked against the oracle: output
+    rows of a projection are independent, so the sample is exact evidence for the rows it covers."""
+    m = 512
+    gen = torch.Generator(device=DEV).manual_seed(3)
+    rng = np.random.default_rng(33)
+    for name, (n, k, fmt) in {"q": (4096, 4096, "q4k"), "gate": (14336, 4096, "q4k"),
+                              "down": (4096, 14336, "q6k")}.items():
+        case("config3", name, m, n, k)
+        wf = torch.randn(n, k, generator=gen, device=DEV) * 0.02
+        blocks = ov.quantize_weight(wf, ov.TYPE_Q6_K if fmt == "q6k" else ov.TYPE_Q4_K)
+        del wf
+        w = (ov.Q6KWeight if fmt == "q6k" else ov.Q4KWeight)(blocks, k, n)
+        x = normal(rng, (m, k))
+        y = ov.project(w, t(x), rows=m)
+        torch.cuda.synchronize()
+        sel = np.sort(rng.choice(n, 40, replace=False))
+        hb = blocks.cpu().numpy().reshape(n, -1)[sel]
+        ref = (orc.q6k_project_batched if fmt == "q6k" else orc.q4k_project_batched)(x, m, hb, k, len(sel))
+        got = y.cpu().numpy().reshape(m, n)[:, sel]
+        assert_bit_exact(got, ref, f"config3 {name}")
+        rel, cos = north_star(got, ref)
+        assert rel <= 1e-3 and cos >= 0.99999
+
+
 @pytest.mark.parametrize("k,n", [(32, 5), (128, 4096), (4096, 300), (14336, 40)])
 @pytest.mark.parametrize("rows", [1, 3])
 def test_q8_0_project_bit_exact(orc, k, n, rows):
