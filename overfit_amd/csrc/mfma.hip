@@ -32,6 +32,7 @@ namespace ovfq {
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
 struct MJob {
     const uint8_t* w;
@@ -52,61 +53,76 @@ struct MArgs {
     const float* s;
 };
 
-constexpr int kActStride = 272;  // LDS bytes per staged activation row: 256 quants + 16 bytes padding
 
 __device__ __forceinline__ i32x4 mfma16(i32x4 a, i32x4 b, i32x4 c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
 
-// Four 16-bit values, two per dword (pe: bytes 0 and 2 of the result, po: bytes 1 and 3), each in [0, 2^15):
-// lo = v & 127 and h = (v >> 7) & 255 as packed bytes in the original byte order.
-__device__ __forceinline__ void split_lo_hi(uint32_t pe, uint32_t po, uint32_t& lo, uint32_t& h) {
-    lo = (pe & 0x007f007fu) | ((po & 0x007f007fu) << 8);
-    h = ((pe >> 7) & 0x00ff00ffu) | (((po >> 7) & 0x00ff00ffu) << 8);
+// Two dwords of 16-bit lanes (pe: K bytes 0 and 2, po: K bytes 1 and 3), each value v in [-2^15, 2^15) as two's
+// complement: lo = v & 127 and hi = floor(v / 128) (the low byte of v >> 7, an int8 for |v| <= 2^14) as packed
+// bytes in K order. v_perm_b32 gathers bytes 0 and 2 of each source: selector 0x06020400 = [pe.b0, po.b0, pe.b2,
+// po.b2].
+__device__ __forceinline__ void split_lo_hi(uint32_t pe, uint32_t po, uint32_t& lo, uint32_t& hi) {
+    lo = __builtin_amdgcn_perm(po, pe, 0x06020400u) & 0x7f7f7f7fu;
+    hi = __builtin_amdgcn_perm(po >> 7, pe >> 7, 0x06020400u);
 }
+
+// K permutation. The four MFMAs t = 0..3 of a super-block each cover 64 of its 256 elements; lane-group g of
+// MFMA t holds 16 consecutive elements starting at base(t, g), in both operands. The activation row is staged in
+// LDS as 16-byte pieces in (t, g) order (logical slot 4t + g), so a lane reads its A operand with one
+// ds_read_b128. The bases are chosen so that every nibble/bit-field shift on the weight side is a compile-time
+// constant. Rows are 256 bytes with the slot XOR-swizzled by (row % 16): the 16 lanes of an A read (16 rows, one
+// logical slot) then hit 16 distinct 16-byte bank groups.
 
 // ------------------------------------------------------------------------------------------ Q4_K weight operands
 struct Q4KMfma {
     static constexpr int kBytes = kQ4KBytes;
     static constexpr int kNumMfma = 3;  // lo, hi, min
+    // MFMA t: nibble (t >> 1) of qs[64(t & 1) + 16g + j]  ->  element 128(t&1) + 64(g>>1) + 32(t>>1) + 16(g&1) + j
+    // (qs byte b holds elements 64(b/32) + b%32 in its low nibble and +32 in its high nibble).
+    // LDS slot 4t + g holds source piece (element / 16) s with bits [t&1, g>>1, t>>1, g&1].
+    __device__ __forceinline__ static uint32_t src_piece(uint32_t slot) {
+        const uint32_t t = slot >> 2, g = slot & 3u;
+        return 8u * (t & 1u) + 4u * (g >> 1) + 2u * (t >> 1) + (g & 1u);
+    }
     struct W {
         u32x4 h;      // d, dmin, 12 packed scale/min bytes
-        u32x4 qs[4];  // chunk c: qs[32c + 16*(g & 1) .. +16]
+        u32x4 q[2];   // qs[16g .. +16], qs[64 + 16g .. +16]
     };
     __device__ __forceinline__ static W load(__amdgpu_buffer_rsrc_t r, uint32_t off, int g) {
         W w;
         w.h = ld4(r, off);
-#pragma unroll
-        for (int c = 0; c < 4; c++) w.qs[c] = ld4(r, off + 16 + 32 * c + 16 * (g & 1));
+        w.q[0] = ld4(r, off + 16 + 16 * g);
+        w.q[1] = ld4(r, off + 16 + 64 + 16 * g);
         return w;
     }
-    // Chunk c = elements 64c..64c+63; lane-group g holds 64c + 16g + j: the low (g < 2) or high nibble of
-    // qs[32c + 16(g&1) + j], sub-block 2c + (g >> 1) (LD/GgmlDequant.cs:64-79 for the scale/min unpacking).
-    __device__ __forceinline__ static void operands(const W& w, int c, int g, i32x4 (&op)[kNumMfma]) {
-        const int js = 2 * c + (g >> 1);
-        const uint32_t jj = (uint32_t)(js & 3) * 8;
-        const uint32_t A = (w.h.y >> jj) & 0xffu, B = (w.h.z >> jj) & 0xffu, C = (w.h.w >> jj) & 0xffu;
+    // Sub-block of MFMA t, lane-group g: js = 4(t&1) + 2(g>>1) + (t>>1) (LD/GgmlDequant.cs:64-79 unpacking).
+    template <int T>
+    __device__ __forceinline__ static void operands(const W& w, int g, i32x4 (&op)[kNumMfma]) {
+        const uint32_t jj = (uint32_t)(2 * (g >> 1) + (T >> 1)) * 8;  // byte index js & 3
         uint32_t sc, m;
-        if (c < 2) {
-            sc = A & 63u;
-            m = B & 63u;
+        if ((T & 1) == 0) {  // js < 4
+            sc = (w.h.y >> jj) & 63u;
+            m = (w.h.z >> jj) & 63u;
         } else {
-            sc = (C & 0x0fu) | ((A >> 6) << 4);
-            m = (C >> 4) | ((B >> 6) << 4);
+            const uint32_t A = w.h.y >> jj, B = w.h.z >> jj, C = (w.h.w >> jj) & 0xffu;
+            sc = (C & 0x0fu) | ((A >> 2) & 0x30u);
+            m = (C >> 4) | ((B >> 2) & 0x30u);
         }
-        const uint32_t shift = (uint32_t)(g >> 1) * 4;
-        const uint32_t qv[4] = {w.qs[c].x, w.qs[c].y, w.qs[c].z, w.qs[c].w};
+        const u32x4 src = w.q[T & 1];
+        const uint32_t qv[4] = {src.x, src.y, src.z, src.w};
+        constexpr uint32_t kShift = (T >> 1) * 4;
         uint32_t lo[4], hi[4];
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            const uint32_t nib = (qv[k] >> shift) & 0x0f0f0f0fu;
-            const uint32_t pe = __umul24(nib & 0x00ff00ffu, sc);  // two 16-bit products per dword
-            const uint32_t po = __umul24((nib >> 8) & 0x00ff00ffu, sc);
+            const uint32_t v = qv[k] >> kShift;
+            const uint32_t pe = __umul24(v & 0x000f000fu, sc);          // sc * nibble of K bytes 0, 2 (<= 945)
+            const uint32_t po = __umul24((v >> 8) & 0x000f000fu, sc);   // K bytes 1, 3
             split_lo_hi(pe, po, lo[k], hi[k]);
         }
         op[0] = i32x4{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3]};
         op[1] = i32x4{(int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-        const int mm = (int)(m * 0x01010101u);
+        const int mm = (int)__builtin_amdgcn_perm(0u, m, 0u);  // m in all four bytes
         op[2] = i32x4{mm, mm, mm, mm};
     }
     __device__ __forceinline__ static float d_of(const W& w) { return half_lo(w.h.x); }
@@ -123,62 +139,50 @@ struct Q4KMfma {
 struct Q6KMfma {
     static constexpr int kBytes = kQ6KBytes;
     static constexpr int kNumMfma = 2;  // lo, hi
+    // MFMA t = qh bit pair p: element 128h + 32p + l with h = g >> 1, l = 16(g&1) + j: nibble (p >> 1) of
+    // ql[64h + 32(p&1) + l], bits 2p of qh[32h + l], scale sc[8h + 2p + (g&1)] (RT/Q6KDotKernel.cs:189-213).
+    // LDS slot 4p + g holds source piece s with bits [g>>1, p, p, g&1].
+    __device__ __forceinline__ static uint32_t src_piece(uint32_t slot) {
+        const uint32_t p = slot >> 2, g = slot & 3u;
+        return 8u * (g >> 1) + 2u * p + (g & 1u);
+    }
     struct W {
-        uint32_t ql[2][4];  // half h: ql[64h + 16g .. +16]
-        uint32_t qh[2][4];  // half h: qh[32h + 16(g & 1) .. +16]
-        uint32_t sc;        // byte c = scales[4c + g]
+        uint32_t ql[2][4];  // ql[64h + 16(g&1) .. +16], ql[64h + 32 + 16(g&1) .. +16]
+        uint32_t qh[4];     // qh[32h + 16(g&1) .. +16]
+        uint32_t sc;        // byte p = sc[8h + 2p + (g&1)]
         uint32_t d;
     };
-    // 16 bytes at any byte offset (Q6_K rows are only 2-byte aligned).
-    __device__ __forceinline__ static void run16(__amdgpu_buffer_rsrc_t r, uint32_t o, uint32_t (&out)[4]) {
-        const uint32_t o4 = o & ~3u, sh = o & 3u;
-        const u32x4 v = ld4(r, o4);
-        const uint32_t v4 = ld1(r, o4 + 16);
-        const uint32_t x0 = v.x, x1 = v.y, x2 = v.z, x3 = v.w;
-        out[0] = __builtin_amdgcn_alignbyte(x1, x0, sh);
-        out[1] = __builtin_amdgcn_alignbyte(x2, x1, sh);
-        out[2] = __builtin_amdgcn_alignbyte(x3, x2, sh);
-        out[3] = __builtin_amdgcn_alignbyte(v4, x3, sh);
-    }
     __device__ __forceinline__ static W load(__amdgpu_buffer_rsrc_t r, uint32_t off, int g) {
         W w;
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-            run16(r, off + 64 * h + 16 * g, w.ql[h]);
-            run16(r, off + 128 + 32 * h + 16 * (g & 1), w.qh[h]);
-        }
-        uint32_t sc = 0;
-#pragma unroll
-        for (int c = 0; c < 4; c++)
-            sc |= (__builtin_amdgcn_raw_buffer_load_b8(r, (int)(off + 192 + 4 * c + g), 0, 0) & 0xffu) << (8 * c);
-        w.sc = sc;
+        const uint32_t h = (uint32_t)g >> 1, l0 = 16u * (uint32_t)(g & 1);
+        Q6K::run16(r, off + 64 * h + l0, w.ql[0]);
+        Q6K::run16(r, off + 64 * h + 32 + l0, w.ql[1]);
+        Q6K::run16(r, off + 128 + 32 * h + l0, w.qh);
+        const uint32_t so = off + 192 + 8 * h, sh = so & 3u;
+        const u32x3 sv = ld3(r, so & ~3u);
+        const uint32_t s0 = __builtin_amdgcn_alignbyte(sv.y, sv.x, sh), s1 = __builtin_amdgcn_alignbyte(sv.z, sv.y, sh);
+        w.sc = __builtin_amdgcn_perm(s1, s0, (g & 1) ? 0x07050301u : 0x06040200u);
         w.d = __builtin_amdgcn_raw_buffer_load_b16(r, (int)(off + 208), 0, 0);
         return w;
     }
-    // Chunk c = elements 64c..64c+63 = half h = c/2, quant group grp = 2(c&1) + (g>>1), l = 16(g&1) + j:
-    // ql[64h + 16g + j] (low nibble for grp < 2), qh[32h + l] bits 2*grp, scale scales[4c + g]
-    // (RT/Q6KDotKernel.cs:189-213).
-    __device__ __forceinline__ static void operands(const W& w, int c, int g, i32x4 (&op)[kNumMfma]) {
-        const int h = c >> 1;
-        const uint32_t nsh = (uint32_t)(c & 1) * 4;
-        const uint32_t hsh = (uint32_t)(c & 1) * 4 + (uint32_t)(g >> 1) * 2;
-        const int sc = (int)(int8_t)((w.sc >> (8 * c)) & 0xffu);
-        const bool neg = sc < 0;
-        const uint32_t asc = (uint32_t)(neg ? -sc : sc);
-        // Wb = W + 4096 in [0, 8192] per 16-bit half, built without carry or borrow between the halves:
-        //   sc >= 0: (4096 - 32*sc) + q*sc        sc < 0: (4096 + 32*|sc|) - q*|sc|
-        const uint32_t k16 = neg ? 4096u + 32u * asc : 4096u - 32u * asc;
-        const uint32_t kk = k16 | (k16 << 16);
+    template <int P>
+    __device__ __forceinline__ static void operands(const W& w, int, i32x4 (&op)[kNumMfma]) {
+        // W = sc * (q - 32) in [-4064, 4096], computed per 16-bit lane modulo 2^16 (two's complement).
+        const uint32_t scp = (uint32_t)(int)(int8_t)((w.sc >> (8 * P)) & 0xffu);
+        const uint32_t sc16 = scp & 0xffffu, bias16 = (0u - 32u * scp) & 0xffffu;
+        const u16x2 sc2 = {(unsigned short)sc16, (unsigned short)sc16};
+        const u16x2 bias2 = {(unsigned short)bias16, (unsigned short)bias16};
+        constexpr uint32_t kNib = (P >> 1) * 4, kBits = 2 * P;
         uint32_t lo[4], hi[4];
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            const uint32_t q = ((w.ql[h][k] >> nsh) & 0x0f0f0f0fu) | (((w.qh[h][k] >> hsh) & 0x03030303u) << 4);
-            const uint32_t pe = __umul24(q & 0x00ff00ffu, asc);
-            const uint32_t po = __umul24((q >> 8) & 0x00ff00ffu, asc);
-            uint32_t l, hb;
-            split_lo_hi(neg ? kk - pe : kk + pe, neg ? kk - po : kk + po, l, hb);
-            lo[k] = l;                                                  // W & 127 (Wb and W agree mod 128)
-            hi[k] = ((hb | 0x80808080u) - 0x20202020u) ^ 0x80808080u;  // per byte hb - 32 (hb <= 64: no borrow)
+            const uint32_t qhb = kBits <= 4 ? (w.qh[k] << (4 - kBits)) : (w.qh[k] >> (kBits - 4));
+            const uint32_t q = ((w.ql[P & 1][k] >> kNib) & 0x0f0f0f0fu) | (qhb & 0x30303030u);
+            const uint32_t qe = __builtin_amdgcn_perm(0u, q, 0x0c020c00u);  // K bytes 0, 2 as 16-bit lanes
+            const uint32_t qo = __builtin_amdgcn_perm(0u, q, 0x0c030c01u);  // K bytes 1, 3
+            const u16x2 we = __builtin_bit_cast(u16x2, qe) * sc2 + bias2;
+            const u16x2 wo = __builtin_bit_cast(u16x2, qo) * sc2 + bias2;
+            split_lo_hi(__builtin_bit_cast(uint32_t, we), __builtin_bit_cast(uint32_t, wo), lo[k], hi[k]);
         }
         op[0] = i32x4{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3]};
         op[1] = i32x4{(int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
@@ -194,10 +198,10 @@ struct Q6KMfma {
 
 // ------------------------------------------------------------------------------------------ kernel
 template <class F, int NT>
-__global__ __launch_bounds__(256) void kquant_mfma_kernel(const MArgs a) {
+__global__ __launch_bounds__(256, 2) void kquant_mfma_kernel(const MArgs a) {
     constexpr int kSub = NT / 16;
-    constexpr int kStage = NT / 16;  // 16-byte activation pieces per thread per super-block
-    __shared__ __align__(16) uint8_t act[2][NT * kActStride];
+    constexpr int kDma = NT / 16;  // 1 KiB (4-row) activation DMA chunks per wave per super-block
+    __shared__ __align__(16) uint8_t act[2][NT * 256];
     __shared__ __align__(16) float act_s[2][NT];
 
     const int wave = wave_id();
@@ -229,25 +233,30 @@ __global__ __launch_bounds__(256) void kquant_mfma_kernel(const MArgs a) {
     const __amdgpu_buffer_rsrc_t sr = make_rsrc(
         a.s + (uint64_t)n0 * spr, rsrc_bytes((uint64_t)a.m_rows * spr * 4, (uint64_t)n0 * spr * 4));
 
-    u32x4 stg[kStage];
-    uint32_t stg_s = 0;
-    // Reads past the last super-block of a row land in the next row or past the resource: harmless (not stored).
-    auto stage_load = [&](int sb) {
+    // DMA chunk c = wave * kDma + i covers LDS bytes [1024c, 1024c + 1024): lane L writes physical slot L % 16 of
+    // row 4c + L / 16, which holds logical slot (L % 16) ^ (row % 16).
+    uint32_t dma_src[kDma];
 #pragma unroll
-        for (int i = 0; i < kStage; i++) {
-            const uint32_t idx = (uint32_t)(i * 256) + threadIdx.x;
-            stg[i] = ld4(qr, (idx >> 4) * K + (uint32_t)sb * kQK + (idx & 15) * 16);
-        }
-        if (threadIdx.x < NT) stg_s = ld1(sr, threadIdx.x * (uint32_t)spr * 4 + (uint32_t)sb * 4);
-    };
-    auto stage_store = [&](int buf) {
+    for (int i = 0; i < kDma; i++) {
+        const uint32_t row = 4u * (uint32_t)(wave * kDma + i) + ((uint32_t)lane >> 4);
+        dma_src[i] = row * K + 16u * F::src_piece(((uint32_t)lane & 15u) ^ (row & 15u));
+    }
+    // Reads past the last super-block of a row land in the next row or past the resource: harmless (not used).
+    auto stage = [&](int sb, int buf) {
 #pragma unroll
-        for (int i = 0; i < kStage; i++) {
-            const uint32_t idx = (uint32_t)(i * 256) + threadIdx.x;
-            *reinterpret_cast<u32x4*>(&act[buf][(idx >> 4) * kActStride + (idx & 15) * 16]) = stg[i];
-        }
-        if (threadIdx.x < NT) act_s[buf][threadIdx.x] = as_float(stg_s);
+        for (int i = 0; i < kDma; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                qr, (__attribute__((address_space(3))) void*)&act[buf][1024 * (wave * kDma + i)], 16,
+                (int)(dma_src[i] + (uint32_t)sb * kQK), 0, 0, 0);
+        if (wave * 64 < NT)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                sr, (__attribute__((address_space(3))) void*)&act_s[buf][wave * 64], 4,
+                (int)(((uint32_t)threadIdx.x * (uint32_t)spr + (uint32_t)sb) * 4u), 0, 0, 0);
     };
+    // A-operand byte offset of logical slot 4t + g in row r16 of a sub-tile: ((4t + g) ^ r16) = 4t ^ (g ^ r16).
+    uint32_t a_off[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) a_off[t] = (uint32_t)r16 * 256u + (((uint32_t)(g ^ r16)) ^ (4u * t)) * 16u;
 
     float out[kSub][4];
 #pragma unroll
@@ -257,21 +266,23 @@ __global__ __launch_bounds__(256) void kquant_mfma_kernel(const MArgs a) {
 
     auto compute = [&](int buf, const typename F::W& w) {
         i32x4 op[4][F::kNumMfma];
-#pragma unroll
-        for (int c = 0; c < 4; c++) F::operands(w, c, g, op[c]);
+        F::template operands<0>(w, g, op[0]);
+        F::template operands<1>(w, g, op[1]);
+        F::template operands<2>(w, g, op[2]);
+        F::template operands<3>(w, g, op[3]);
         const float d = F::d_of(w), dmin = F::dmin_of(w);
+        const uint8_t* tile = act[buf];
 #pragma unroll
         for (int s = 0; s < kSub; s++) {
             i32x4 acc[F::kNumMfma];
 #pragma unroll
             for (int k = 0; k < F::kNumMfma; k++) acc[k] = i32x4{0, 0, 0, 0};
-            const uint8_t* arow = &act[buf][(s * 16 + r16) * kActStride + 16 * g];
 #pragma unroll
-            for (int c = 0; c < 4; c++) {
-                const u32x4 av = *reinterpret_cast<const u32x4*>(arow + 64 * c);
+            for (int t = 0; t < 4; t++) {
+                const u32x4 av = *reinterpret_cast<const u32x4*>(tile + s * 4096 + a_off[t]);
                 const i32x4 aop = i32x4{(int)av.x, (int)av.y, (int)av.z, (int)av.w};
 #pragma unroll
-                for (int k = 0; k < F::kNumMfma; k++) acc[k] = mfma16(aop, op[c][k], acc[k]);
+                for (int k = 0; k < F::kNumMfma; k++) acc[k] = mfma16(aop, op[t][k], acc[k]);
             }
             const f32x4 q8s = *reinterpret_cast<const f32x4*>(&act_s[buf][s * 16 + 4 * g]);
 #pragma unroll
@@ -279,23 +290,19 @@ __global__ __launch_bounds__(256) void kquant_mfma_kernel(const MArgs a) {
         }
     };
 
-    typename F::W wa = F::load(wr, woff, g), wb;
-    stage_load(0);
-    stage_store(0);
+    typename F::W wcur = F::load(wr, woff, g);
+    stage(0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    auto step = [&](int sb, const typename F::W& cur, typename F::W& nxt) {
-        stage_load(sb + 1);
-        nxt = F::load(wr, woff + (uint32_t)(sb + 1) * F::kBytes, g);
-        compute(sb & 1, cur);
-        if (sb + 1 < spr) stage_store((sb + 1) & 1);
+    for (int sb = 0; sb < spr; sb++) {
+        // next super-block's weights (registers) and activation (LDS DMA) in flight during this one's compute
+        const typename F::W wnxt = F::load(wr, woff + (uint32_t)(sb + 1) * F::kBytes, g);  // past the row: unused
+        if (sb + 1 < spr) stage(sb + 1, (sb + 1) & 1);
+        compute(sb & 1, wcur);
+        wcur = wnxt;
+        __builtin_amdgcn_s_waitcnt(0);  // the DMA writes to LDS are complete before the barrier publishes them
         __syncthreads();
-    };
-    int sb = 0;
-    for (; sb + 1 < spr; sb += 2) {
-        step(sb, wa, wb);
-        step(sb + 1, wb, wa);
     }
-    if (sb < spr) step(sb, wa, wb);
 
     // y[n][o] = biasO + sum   (RT/Q4KDotKernel.cs:951, RT/Q6KDotKernel.cs:507)
     const int o = o0 + r16;
@@ -328,6 +335,18 @@ int mfma_min_rows() {
     return v;
 }
 
+// 128 activation rows per workgroup halve the operand-build cost per output but allow only two workgroups per CU;
+// 64 rows fit four, which hides more latency. Measured on MI355X (Llama-3-8B layer shapes): 64 is faster up to
+// M = 512, 128 from M = 2048.
+static int mfma_tile_rows(int rows) {
+    static const int forced = [] {
+        const char* e = getenv("OVFQ_MFMA_TILE_ROWS");
+        return e && *e ? atoi(e) : 0;
+    }();
+    if (forced == 64 || forced == 128) return forced;
+    return rows >= 1024 ? 128 : 64;
+}
+
 bool mfma_supported(int type, int rows) { return (type == 12 || type == 14) && rows >= mfma_min_rows(); }
 
 hipError_t launch_project_mfma(int type, const ProjJob* jobs, int njobs, int in, int rows, ActQ act,
@@ -344,8 +363,9 @@ hipError_t launch_project_mfma(int type, const ProjJob* jobs, int njobs, int in,
     ma.spr = in / kQK;
     ma.q = act.q;
     ma.s = act.s;
-    if (type == 12) return launch_mfma<Q4KMfma, 64>(ma, st);
-    return launch_mfma<Q6KMfma, 64>(ma, st);
+    const int nt = mfma_tile_rows(rows);
+    if (type == 12) return nt == 128 ? launch_mfma<Q4KMfma, 128>(ma, st) : launch_mfma<Q4KMfma, 64>(ma, st);
+    return nt == 128 ? launch_mfma<Q6KMfma, 128>(ma, st) : launch_mfma<Q6KMfma, 64>(ma, st);
 }
 
 }  // namespace ovfq
