@@ -13,8 +13,10 @@ To measure HBM rather than the 256 MB Infinity Cache, steps rotate over several 
 + fp32 outputs), in GB/s; decode_proj_tok_s = steps per second.
 
 Also reported: the dominant kernel's roofline (the fused gate/up Q4_K GEMV, per-launch HIP-event timing on
-the stream it runs on), BASELINE config 1 (a single Q4_K 4096x4096 GEMV rotated over 64 copies), and the
-CPU baseline (the AVX2 C restatement of the reference's CPU path, on a bounded sample, rank 0 only).
+the stream it runs on), BASELINE config 1 (a single Q4_K 4096x4096 GEMV rotated over 64 copies), config 3
+(the layer at M = 512 on int8 MFMA, with its MFMA roofline), config 4 (32 distinct layers + the Q6_K LM head,
+one token's projections), and the CPU baseline (the AVX2 C restatement of the reference's CPU path, on a
+bounded sample, rank 0 only).
 """
 import argparse
 import json
@@ -27,6 +29,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "Q4_K GEMV HBM GB/s (% peak) + decode proj tok/s, Llama-3-8B shape"
 HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
 LAYER = [  # name, out, in, format
     ("q", 4096, 4096, "q4k"), ("k", 1024, 4096, "q4k"), ("v", 1024, 4096, "q4k"), ("o", 4096, 4096, "q4k"),
     ("gate", 14336, 4096, "q4k"), ("up", 14336, 4096, "q4k"), ("down", 4096, 14336, "q6k"),
@@ -257,9 +260,78 @@ def main():
                 "pct_peak": round(100 * nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 2), "algorithmic_bytes": nbytes,
                 "copies": n_copies, "what": label}
 
+    def prefill_line(m=512, n_layers=2):
+        """the layer's seven projections at M = m rows on the int8-MFMA kernel, in four launches
+        (fused q/k/v, o, fused gate/up, down; each quantises its fp32 input to Q8_K first), graph-replayed over
+        n_layers weight copies."""
+        gen2 = torch.Generator(device="cuda:0").manual_seed(9)
+        xp = {name: torch.randn(m * k, generator=gen2, device=dev) for name, k in
+              (("attn", 4096), ("o", 4096), ("ffn", 4096), ("down", 14336))}
+        yp = {name: torch.empty(m * n, device=dev) for name, n, _, _ in LAYER}
+
+        def pstep(ws):
+            ctx.project_multi_dev([ws["q"], ws["k"], ws["v"]], xp["attn"], [yp["q"], yp["k"], yp["v"]], rows=m)
+            ctx.project_multi_dev([ws["o"]], xp["o"], [yp["o"]], rows=m)
+            ctx.project_multi_dev([ws["gate"], ws["up"]], xp["ffn"], [yp["gate"], yp["up"]], rows=m)
+            ctx.project_multi_dev([ws["down"]], xp["down"], [yp["down"]], rows=m)
+
+        g = capture([(lambda ws=ws: pstep(ws)) for ws in copies[:n_layers]])
+        us = replay_us(g, n_layers, 8)
+        ops = 2 * m * sum(n * k for _, n, k, _ in LAYER)
+        tops = ops / (us * 1e-6) / 1e12
+        del g, xp, yp
+        torch.cuda.empty_cache()
+        return {"what": "BASELINE config 3: Llama-3-8B layer projections at M=%d (prefill) on int8 MFMA" % m,
+                "us_per_layer": round(us, 2), "tokens_per_s": round(m / (us * 1e-6), 1),
+                "useful_TOPS": round(tops, 1),
+                "roofline": {"bound": "mfma", "achieved": round(tops, 1), "peak": INT8_PEAK_TOPS, "unit": "TOPS",
+                             "frac": round(tops / INT8_PEAK_TOPS, 4),
+                             "note": "useful int8 ops 2*M*N*K; the exact kernel issues 3 (Q4_K) / 2 (Q6_K) MFMAs "
+                                     "per 64-wide K chunk (lo/hi operand split + min term)"},
+                "timing": "HIP graph replay of the 4 launches x %d layer copies, per layer" % n_layers}
+
+    def model_line(n_layers=32):
+        """one decode token's projections through n_layers distinct Q4_K_M layers plus the
+        Q6_K 128256x4096 LM head (RMSNorm / RoPE / attention stay on the host path and are not timed)."""
+        layers = copies + [make_layer(ov, torch, 2000 + i) for i in range(n_layers - len(copies))]
+        gen3 = torch.Generator(device="cuda:0").manual_seed(4)
+        wf = torch.randn(128256, 4096, generator=gen3, device=dev) * 0.02
+        head = ov.Q6KWeight(ov.quantize_weight(wf, ov.TYPE_Q6_K), 4096, 128256)
+        del wf
+        logits = torch.empty(128256, device=dev)
+
+        def token():
+            for ws in layers:
+                step(ws)
+            ctx.project_multi_dev([head], x_in["ffn"], [logits])
+
+        token()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        reps = 5
+        e0.record()
+        for _ in range(reps):
+            token()
+        e1.record()
+        torch.cuda.synchronize()
+        eager_us = e0.elapsed_time(e1) * 1e3 / reps
+        g = capture([token])
+        graph_us = replay_us(g, 1, 10)
+        w = n_layers * layer_algorithmic_bytes()[0] + weight_bytes(128256, 4096, "q6k")
+        del g, layers[len(copies):], head
+        torch.cuda.empty_cache()
+        return {"what": "BASELINE config 4: %d Llama-3-8B Q4_K_M layers + Q6_K LM head, one decode token, "
+                        "projections only (%d launches)" % (n_layers, 4 * n_layers + 1),
+                "weight_bytes": w, "eager_us": round(eager_us, 1), "graph_us": round(graph_us, 1),
+                "proj_tok_s_eager": round(1e6 / eager_us, 1), "proj_tok_s_graph": round(1e6 / graph_us, 1),
+                "GB_s_graph": round(w / (graph_us * 1e-6) / 1e9, 1)}
+
     config1 = gemv_line(4096, 4096, "q4k", 64, "BASELINE config 1: Q4_K 4096x4096 GEMV (quantise in-launch)")
     large_q4k = gemv_line(128256, 4096, "q4k", 2, "Q4_K GEMV at LM-head size (asymptotic efficiency)")
     lm_head = gemv_line(128256, 4096, "q6k", 2, "Llama-3-8B Q6_K LM head 128256x4096 (config 4)")
+    config3 = prefill_line()
+    config4 = model_line()
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -287,9 +359,10 @@ def main():
         "decode_proj_tok_s": round(1e3 / ms, 1),
         "graph_ms_per_step": round(graph_ms, 5),
         "timing": "eager loop of K steps between two events (HIP-graph replay of the same steps: graph_ms_per_step)",
-        "decode_proj_tok_s_32_layers_plus_lm_head_est": round(1e3 / (32 * ms + lm_head["avg_us"] * 1e-3), 2),
         "roofline": roofline,
         "config1_q4k_gemv_4096x4096": config1,
+        "config3_prefill_m512": config3,
+        "config4_32_layers_lm_head": config4,
         "q4k_gemv_128256x4096": large_q4k,
         "q6k_lm_head_128256x4096": lm_head,
         "cpu_baseline": cpu,

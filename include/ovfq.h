@@ -146,18 +146,18 @@ OVFQ_API int ovfq_project_gate_up_dev(ovfq_ctx* ctx, const ovfq_weight* gate, co
 
 /* Several projections of the SAME activation in one launch (the generalisation of gate/up that the
  * attention block's shared quantised hidden row needs, RT/CachedMultiHeadAttention.cs:196-207): weights[i]
- * share input_size and type; ys[i] receives rows x output_size_i; biases may be NULL or hold NULL entries.
- * At most 4 weights. rows == 1 only. */
+ * share input_size and type; x is rows x input_size; ys[i] receives rows x output_size_i; biases may be NULL or
+ * hold NULL entries. At most 4 weights. Prefill (rows >= 2) uses it for the fused q/k/v and gate/up GEMMs. */
 OVFQ_API int ovfq_project_multi_dev(ovfq_ctx* ctx, int count, const ovfq_weight* const* weights,
-                                    const float* x, const float* const* biases, float* const* ys);
+                                    const float* x, int rows, const float* const* biases, float* const* ys);
 
-/* ovfq_project_multi_dev from an already-quantised Q8_K activation (one row): the attention block quantises
+/* ovfq_project_multi_dev from an already-quantised Q8_K activation (rows rows): the attention block quantises
  * its hidden row once and runs every head's projection against it with ProjectPreQuantized
  * (RT/CachedMultiHeadAttention.cs:196-207, RT/Q4KDotKernel.cs:445-476); here all of them run in one launch.
  * K-quant weights only; at most 4. */
 OVFQ_API int ovfq_project_multi_prequantized_dev(ovfq_ctx* ctx, int count, const ovfq_weight* const* weights,
                                                  const int8_t* quants, const float* scales, const int16_t* bsums,
-                                                 const float* const* biases, float* const* ys);
+                                                 int rows, const float* const* biases, float* const* ys);
 
 /* ---------------------------------------------------------------------------------- weight quantisation */
 

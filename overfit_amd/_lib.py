@@ -51,8 +51,8 @@ SIGNATURES = {
     "ovfq_project_prequantized_dev": (ci, [vp, vp, vp, vp, vp, ci, vp, vp]),
     "ovfq_project_gate_up": (ci, [vp, vp, vp, vp, vp, vp]),
     "ovfq_project_gate_up_dev": (ci, [vp, vp, vp, vp, vp, vp]),
-    "ovfq_project_multi_dev": (ci, [vp, ci, PP, vp, PP, PP]),
-    "ovfq_project_multi_prequantized_dev": (ci, [vp, ci, PP, vp, vp, vp, PP, PP]),
+    "ovfq_project_multi_dev": (ci, [vp, ci, PP, vp, ci, PP, PP]),
+    "ovfq_project_multi_prequantized_dev": (ci, [vp, ci, PP, vp, vp, vp, ci, PP, PP]),
     "ovfq_quantize_weight_q4k_dev": (ci, [vp, vp, ci, ci, vp]),
     "ovfq_quantize_weight_q6k_dev": (ci, [vp, vp, ci, ci, vp]),
     "ovfq_quantize_weight_q8_0_dev": (ci, [vp, vp, ci, ci, vp, vp]),

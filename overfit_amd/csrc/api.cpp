@@ -526,9 +526,9 @@ int ovfq_project_gate_up_dev(ovfq_ctx* ctx, const ovfq_weight* gate, const ovfq_
     return project_impl(ctx, 2, ws, x, 1, nullptr, ys, false);
 }
 
-int ovfq_project_multi_dev(ovfq_ctx* ctx, int count, const ovfq_weight* const* weights, const float* x,
+int ovfq_project_multi_dev(ovfq_ctx* ctx, int count, const ovfq_weight* const* weights, const float* x, int rows,
                            const float* const* biases, float* const* ys) {
-    return project_impl(ctx, count, weights, x, 1, biases, ys, false);
+    return project_impl(ctx, count, weights, x, rows, biases, ys, false);
 }
 
 static int prequant_impl(ovfq_ctx* ctx, const ovfq_weight* w, const int8_t* q, const float* s, const int16_t* b,
@@ -590,7 +590,7 @@ int ovfq_project_prequantized_dev(ovfq_ctx* ctx, const ovfq_weight* w, const int
 }
 
 int ovfq_project_multi_prequantized_dev(ovfq_ctx* ctx, int count, const ovfq_weight* const* ws, const int8_t* q,
-                                        const float* s, const int16_t* b, const float* const* biases,
+                                        const float* s, const int16_t* b, int rows, const float* const* biases,
                                         float* const* ys) {
     if (!ctx) return fail(OVFQ_ERR_NULL, "ctx is NULL");
     if (count < 1 || count > ovfq::kMaxJobs) return fail(OVFQ_ERR_RANGE, "count (%d) must be in [1, 4]", count);
@@ -605,11 +605,12 @@ int ovfq_project_multi_prequantized_dev(ovfq_ctx* ctx, int count, const ovfq_wei
         if (ws[i]->in != ws[0]->in) return fail(OVFQ_ERR_SIZE, "fused weights must share inputSize");
         if ((rc = check_dev_align(ys[i], "output"))) return rc;
     }
+    if ((rc = check_rows(rows))) return rc;
     if ((rc = check_dev_align(q, "quants")) || (rc = check_dev_align(s, "scales")) || (rc = check_dev_align(b, "bsums")))
         return rc;
     std::lock_guard<std::mutex> lk(ctx->mu);
     HIP_TRY(hipSetDevice(ctx->device));
-    if ((rc = launch_projection(ctx, ws, count, biases, ys, 1, ovfq::ActQ{q, s, b}))) return rc;
+    if ((rc = launch_projection(ctx, ws, count, biases, ys, rows, ovfq::ActQ{q, s, b}))) return rc;
     return ok();
 }
 

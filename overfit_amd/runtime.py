@@ -115,16 +115,16 @@ class Context:
         self.check(self.lib.ovfq_project_dev(self.handle, weight.handle, x.data_ptr(), rows,
                                              None if bias is None else bias.data_ptr(), y.data_ptr()))
 
-    def project_multi_dev(self, weights, x, ys, biases=None):
+    def project_multi_dev(self, weights, x, ys, biases=None, rows=1):
         n = len(weights)
         W = (ctypes.c_void_p * n)(*[w.handle.value for w in weights])
         Y = (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys])
         B = None
         if biases is not None:
             B = (ctypes.c_void_p * n)(*[None if b is None else b.data_ptr() for b in biases])
-        self.check(self.lib.ovfq_project_multi_dev(self.handle, n, W, x.data_ptr(), B, Y))
+        self.check(self.lib.ovfq_project_multi_dev(self.handle, n, W, x.data_ptr(), rows, B, Y))
 
-    def project_multi_prequantized_dev(self, weights, q, s, b, ys, biases=None):
+    def project_multi_prequantized_dev(self, weights, q, s, b, ys, biases=None, rows=1):
         n = len(weights)
         W = (ctypes.c_void_p * n)(*[w.handle.value for w in weights])
         Y = (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys])
@@ -132,7 +132,7 @@ class Context:
         if biases is not None:
             B = (ctypes.c_void_p * n)(*[None if x is None else x.data_ptr() for x in biases])
         self.check(self.lib.ovfq_project_multi_prequantized_dev(self.handle, n, W, q.data_ptr(), s.data_ptr(),
-                                                                b.data_ptr(), B, Y))
+                                                                b.data_ptr(), rows, B, Y))
 
     def project_prequantized_dev(self, weight, q, s, b, y, rows=1, bias=None):
         self.check(self.lib.ovfq_project_prequantized_dev(

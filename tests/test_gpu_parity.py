@@ -198,6 +198,35 @@ def test_kquant_prefill_bit_exact(orc, ctx, fmt, rows, k, n):
     assert_bit_exact(ov.project(w, x, None, rows=rows).reshape(rows, n), ref0, f"{fmt} prefill host, no bias")
 
 
+@pytest.mark.parametrize("rows", [5, 40])
+def test_multi_projection_rows_bit_exact(orc, ctx, rows):
+    """Fused q/k/v-style launch over `rows` activation rows (rows = 40 takes the MFMA kernel's multi-job grid,
+    rows = 5 the small-M kernel), from the fp32 input and from a shared prequantised activation."""
+    case("multi rows", rows)
+    rng = np.random.default_rng(400 + rows)
+    k, shapes = 1024, [192, 64, 80]
+    blocks = [_kq_blocks(rng, "q4k", n, k) for n in shapes]
+    ws = [ov.Q4KWeight(b, k, n) for b, n in zip(blocks, shapes)]
+    x = normal(rng, (rows, k))
+    bias = normal(rng, shapes[2])
+    refs = [orc.q4k_project_batched(x, rows, b, k, n, bias if i == 2 else None)
+            for i, (b, n) in enumerate(zip(blocks, shapes))]
+    ys = [torch.empty(rows * n, device=DEV) for n in shapes]
+    ctx.project_multi_dev(ws, t(x), ys, [None, None, t(bias)], rows=rows)
+    torch.cuda.synchronize()
+    for i, (y, ref) in enumerate(zip(ys, refs)):
+        assert_bit_exact(y.cpu().numpy().reshape(rows, -1), ref, f"multi rows={rows} job {i}")
+    q = torch.empty(rows * k, dtype=torch.int8, device=DEV)
+    s = torch.empty(rows * k // 256, dtype=torch.float32, device=DEV)
+    b = torch.empty(rows * k // 16, dtype=torch.int16, device=DEV)
+    ctx.quantize_q8k_dev(t(x), rows, k, q, s, b)
+    ys2 = [torch.empty(rows * n, device=DEV) for n in shapes]
+    ctx.project_multi_prequantized_dev(ws, q, s, b, ys2, [None, None, t(bias)], rows=rows)
+    torch.cuda.synchronize()
+    for i, (y, ref) in enumerate(zip(ys2, refs)):
+        assert_bit_exact(y.cpu().numpy().reshape(rows, -1), ref, f"multi prequantized rows={rows} job {i}")
+
+
 def _extreme_blocks(fmt, n, k):
     """Blocks at the ends of the integer ranges the MFMA operand split must hold: Q4_K sc = m = 63 with nibble 15
     (sc*nib = 945) and nibble 0; Q6_K scale -128 with q = 0 (sc*(q-32) = +4096), scale 127 with q = 63 and q = 0
