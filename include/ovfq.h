@@ -159,6 +159,37 @@ OVFQ_API int ovfq_project_multi_prequantized_dev(ovfq_ctx* ctx, int count, const
                                                  const int8_t* quants, const float* scales, const int16_t* bsums,
                                                  int rows, const float* const* biases, float* const* ys);
 
+/* ---------------------------------------------------------------------------------- routed MoE */
+
+#define OVFQ_MAX_EXPERTS 64
+
+/* MoeRouter.SelectTopK (RT/MoeRouter.cs:40-128) for each of `rows` tokens: logits [rows][n_experts] ->
+ * expert_indices / expert_weights [rows][top_k], indices descending by logit (ties keep the lower index),
+ * weights the softmax over the kept logits (normalize != 0) or the full softmax at them (normalize == 0).
+ * When top_k > n_experts only the first n_experts slots of each row are written (the reference returns
+ * min(topK, n)). n_experts <= OVFQ_MAX_EXPERTS. The weights go through expf, so they match the reference to
+ * within a few ULP; the indices are exact. */
+OVFQ_API int ovfq_moe_select_topk(ovfq_ctx* ctx, const float* logits, int rows, int n_experts, int top_k,
+                                  int normalize, int* expert_indices, float* expert_weights);
+OVFQ_API int ovfq_moe_select_topk_dev(ovfq_ctx* ctx, const float* logits, int rows, int n_experts, int top_k,
+                                      int normalize, int* expert_indices, float* expert_weights);
+
+/* MoeFeedForwardBlock.DecodeBatched (RT/MoeFeedForwardBlock.cs:140-241) after routing: for `rows` tokens x
+ * [rows][d_model] with their top_k experts (indices/weights [rows][top_k], e.g. from ovfq_moe_select_topk),
+ * groups the tokens by expert, runs each used expert's SwiGLU FFN (gate/up [d_ff][d_model], down
+ * [d_model][d_ff], K-quant weights; gate and up of one type) on its tokens with the batched projections, and
+ * writes y[rows][d_model] = sum over slots j in order of weight[j] * expert output. Every projection is
+ * bit-identical to the reference's; SiLU uses expf (the reference's TensorPrimitives.Sigmoid is itself only
+ * specified to a few ULP), so y matches to the projection tolerance. An index outside [0, n_experts), or a
+ * repeated index in a token's slots, contributes nothing. n_experts <= OVFQ_MAX_EXPERTS. */
+OVFQ_API int ovfq_moe_ffn(ovfq_ctx* ctx, int n_experts, const ovfq_weight* const* gate,
+                          const ovfq_weight* const* up, const ovfq_weight* const* down, const float* x, int rows,
+                          int top_k, const int* expert_indices, const float* expert_weights, float* y);
+OVFQ_API int ovfq_moe_ffn_dev(ovfq_ctx* ctx, int n_experts, const ovfq_weight* const* gate,
+                              const ovfq_weight* const* up, const ovfq_weight* const* down, const float* x,
+                              int rows, int top_k, const int* expert_indices, const float* expert_weights,
+                              float* y);
+
 /* ---------------------------------------------------------------------------------- weight quantisation */
 
 /* GgmlQuant.QuantizeQ4_K (LD/GgmlQuant.cs:132-161): output-major f32 [out][in] (in % 256 == 0) -> Q4_K

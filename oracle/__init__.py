@@ -68,6 +68,9 @@ _SIGS = {
     "orc_quantize_q6k": (c_int, [c_f32p, c_int, c_int, c_u8p]),
     "orc_q8_quantize_rows": (c_int, [c_f32p, c_int, c_int, c_i8p, c_f32p]),
     "orc_moe_select_topk": (c_int, [c_f32p, c_int, c_int, c_i32p, c_f32p, c_int]),
+    "orc_swiglu_batched": (c_int, [c_f32p, c_int, c_u8p, c_u8p, c_u8p, c_int, c_int, c_int, c_int, c_f32p]),
+    "orc_moe_ffn_batched": (c_int, [c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, c_int, c_int, c_f32p,
+                                    c_int, c_int, c_int, c_int, c_i32p, c_f32p, c_f32p]),
     # CPU baseline (cpu_baseline.c)
     "cpub_set_workers": (c_int, [c_int]),
     "cpub_has_avx2": (c_int, []),
@@ -318,6 +321,31 @@ def q6k_decode_row(blocks, k, n, row):
     dst = np.zeros(k, np.float32)
     _check(lib().orc_q6k_decode_row(P(np.ascontiguousarray(blocks, np.uint8)), k, n, row, P(dst)))
     return dst
+
+
+def swiglu_batched(x, rows, gate, up, down, gate_type, down_type, d_model, d_ff):
+    """CachedFeedForwardBlock.DecodeSwiGluBatchedDispatched (oracle): y[rows][d_model]."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(rows, d_model)
+    y = np.zeros((rows, d_model), np.float32)
+    g, u, d = (np.ascontiguousarray(a, np.uint8) for a in (gate, up, down))
+    _check(lib().orc_swiglu_batched(P(x), rows, P(g), P(u), P(d), gate_type, down_type, d_model, d_ff, P(y)))
+    return y
+
+
+def moe_ffn_batched(gates, ups, downs, gate_type, down_type, x, rows, d_model, d_ff, top_k, idx, w):
+    """MoeFeedForwardBlock.DecodeBatched after routing (oracle): idx/w [rows][top_k] -> y[rows][d_model]."""
+    E = len(gates)
+    keep = [np.ascontiguousarray(a, np.uint8) for a in list(gates) + list(ups) + list(downs)]
+    ptrs = [ctypes.c_void_p(a.ctypes.data) for a in keep]
+    arr = lambda ps: (ctypes.c_void_p * E)(*[p.value for p in ps])
+    G, U, D = arr(ptrs[:E]), arr(ptrs[E:2 * E]), arr(ptrs[2 * E:])
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(rows, d_model)
+    idx = np.ascontiguousarray(idx, dtype=np.int32).reshape(rows, top_k)
+    w = np.ascontiguousarray(w, dtype=np.float32).reshape(rows, top_k)
+    y = np.zeros((rows, d_model), np.float32)
+    _check(lib().orc_moe_ffn_batched(E, G, U, D, gate_type, down_type, P(x), rows, d_model, d_ff, top_k, P(idx),
+                                     P(w), P(y)))
+    return y
 
 
 def moe_select_topk(logits, top_k, normalize=True):

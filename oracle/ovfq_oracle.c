@@ -6,6 +6,7 @@
 #include "ovfq_oracle.h"
 
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 /* ---------------------------------------------------------------- fp16 */
@@ -818,4 +819,103 @@ int orc_moe_select_topk(const float* logits, int n, int top_k, int* idx, float* 
         for (int i = 0; i < k; i++) w[i] = expf(w[i] - max) * inv;
     }
     return k;
+}
+
+/* ------------------------------------------------------------------------------------------ routed MoE FFN */
+
+static int batched_kq(int type, const float* x, int rows, const uint8_t* blocks, int in, int out, float* y,
+                      int8_t* q, float* s, int16_t* b) {
+    if (type == 12) return orc_q4k_project_batched(x, rows, blocks, in, out, NULL, y, q, s, b);
+    if (type == 14) return orc_q6k_project_batched(x, rows, blocks, in, out, NULL, y, q, s, b);
+    return ORC_ERR_RANGE;
+}
+
+int orc_swiglu_batched(const float* x, int rows, const uint8_t* gate, const uint8_t* up, const uint8_t* down,
+                       int gate_type, int down_type, int d_model, int d_ff, float* y) {
+    /* RT/CachedFeedForwardBlock.cs:328-344 (DecodeSwiGluBatchedDispatched): gate = ProjectBatched(x); gate *=
+     * sigmoid(gate) (ApplySiLU, :464-472); up = ProjectBatched(x); up = gate * up; y = ProjectBatched(up). */
+    if (!x || !gate || !up || !down || !y) return ORC_ERR_NULL;
+    if (rows <= 0 || d_model % 256 || d_ff % 256) return ORC_ERR_SIZE;
+    const int kmax = d_model > d_ff ? d_model : d_ff;
+    float* g = (float*)malloc(sizeof(float) * (size_t)rows * d_ff);
+    float* u = (float*)malloc(sizeof(float) * (size_t)rows * d_ff);
+    int8_t* q = (int8_t*)malloc((size_t)rows * kmax);
+    float* s = (float*)malloc(sizeof(float) * (size_t)rows * (kmax / 256));
+    int16_t* b = (int16_t*)malloc(sizeof(int16_t) * (size_t)rows * (kmax / 16));
+    int rc = (g && u && q && s && b) ? ORC_OK : ORC_ERR_SIZE;
+    if (!rc) rc = batched_kq(gate_type, x, rows, gate, d_model, d_ff, g, q, s, b);
+    if (!rc) {
+        for (size_t i = 0; i < (size_t)rows * d_ff; i++) {
+            const float sig = 1.0f / (1.0f + expf(-g[i]));
+            g[i] = g[i] * sig;
+        }
+        rc = batched_kq(gate_type, x, rows, up, d_model, d_ff, u, q, s, b);
+    }
+    if (!rc) {
+        for (size_t i = 0; i < (size_t)rows * d_ff; i++) u[i] = g[i] * u[i];
+        rc = batched_kq(down_type, u, rows, down, d_ff, d_model, y, q, s, b);
+    }
+    free(g);
+    free(u);
+    free(q);
+    free(s);
+    free(b);
+    return rc;
+}
+
+int orc_moe_ffn_batched(int n_experts, const uint8_t* const* gate, const uint8_t* const* up,
+                        const uint8_t* const* down, int gate_type, int down_type, const float* x, int rows,
+                        int d_model, int d_ff, int top_k, const int* idx, const float* w, float* y) {
+    /* RT/MoeFeedForwardBlock.cs:140-241 (DecodeBatched) after routing. */
+    if (!gate || !up || !down || !x || !idx || !w || !y) return ORC_ERR_NULL;
+    if (n_experts <= 0 || rows <= 0 || top_k <= 0) return ORC_ERR_RANGE;
+    const size_t P = (size_t)rows * top_k;
+    int* row_buf = (int*)malloc(sizeof(int) * (size_t)rows);
+    int* slot_buf = (int*)malloc(sizeof(int) * (size_t)rows);
+    int* have = (int*)calloc(P, sizeof(int));
+    float* gathered = (float*)malloc(sizeof(float) * (size_t)rows * d_model);
+    float* expert_out = (float*)malloc(sizeof(float) * (size_t)rows * d_model);
+    float* slot_out = (float*)malloc(sizeof(float) * P * d_model);
+    int rc = (row_buf && slot_buf && have && gathered && expert_out && slot_out) ? ORC_OK : ORC_ERR_SIZE;
+    /* 2. group rows by expert (first matching slot), gather, batched SwiGLU, stash at (row, slot) */
+    for (int e = 0; e < n_experts && !rc; e++) {
+        int count = 0;
+        for (int n = 0; n < rows; n++)
+            for (int j = 0; j < top_k; j++)
+                if (idx[n * top_k + j] == e) {
+                    row_buf[count] = n;
+                    slot_buf[count] = j;
+                    count++;
+                    break;
+                }
+        if (count == 0) continue;
+        for (int c = 0; c < count; c++)
+            memcpy(gathered + (size_t)c * d_model, x + (size_t)row_buf[c] * d_model, sizeof(float) * d_model);
+        rc = orc_swiglu_batched(gathered, count, gate[e], up[e], down[e], gate_type, down_type, d_model, d_ff,
+                                expert_out);
+        for (int c = 0; c < count && !rc; c++) {
+            const size_t slot = (size_t)row_buf[c] * top_k + slot_buf[c];
+            memcpy(slot_out + slot * d_model, expert_out + (size_t)c * d_model, sizeof(float) * d_model);
+            have[slot] = 1;
+        }
+    }
+    /* 3. per-row weighted sum in slot order (a slot no expert claimed contributes nothing) */
+    for (int n = 0; n < rows && !rc; n++) {
+        float* dst = y + (size_t)n * d_model;
+        for (int d = 0; d < d_model; d++) dst[d] = 0.0f;
+        for (int j = 0; j < top_k; j++) {
+            const size_t slot = (size_t)n * top_k + j;
+            if (!have[slot]) continue;
+            const float wj = w[slot];
+            const float* src = slot_out + slot * d_model;
+            for (int d = 0; d < d_model; d++) dst[d] += wj * src[d];
+        }
+    }
+    free(row_buf);
+    free(slot_buf);
+    free(have);
+    free(gathered);
+    free(expert_out);
+    free(slot_out);
+    return rc;
 }

@@ -131,6 +131,15 @@ int orc_q8_quantize_rows(const float* row_major, int row_count, int row_length, 
 int orc_moe_select_topk(const float* logits, int n, int top_k, int* expert_indices, float* expert_weights,
                         int normalize);
 
+/* RT/CachedFeedForwardBlock.cs:328-344 (DecodeSwiGluBatchedDispatched): batched SwiGLU FFN of `rows` rows,
+ * gate/up [d_ff][d_model], down [d_model][d_ff]; types 12 (Q4_K) or 14 (Q6_K). SiLU via expf. */
+int orc_swiglu_batched(const float* x, int rows, const uint8_t* gate, const uint8_t* up, const uint8_t* down,
+                       int gate_type, int down_type, int d_model, int d_ff, float* y);
+/* RT/MoeFeedForwardBlock.cs:140-241 (DecodeBatched) after routing: idx/w [rows][top_k]. */
+int orc_moe_ffn_batched(int n_experts, const uint8_t* const* gate, const uint8_t* const* up,
+                        const uint8_t* const* down, int gate_type, int down_type, const float* x, int rows,
+                        int d_model, int d_ff, int top_k, const int* idx, const float* w, float* y);
+
 /* Status codes shared with the product's C ABI. */
 #define ORC_OK 0
 #define ORC_ERR_NULL (-1)

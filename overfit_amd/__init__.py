@@ -6,8 +6,8 @@ Q4_K / Q6_K / Q8_0 block-dequantize-and-dot projections as hand-written HIP kern
 from . import _lib
 from .errors import (OverfitArgumentError, OverfitArgumentNullError, OverfitArgumentOutOfRangeError,
                      OverfitHipError, OverfitUnsupportedTypeError)
-from .kernels import (BatchedQuantProjection, Q4KDotKernel, Q6KDotKernel, Q8DotKernel, project,
-                      project_gate_up, quantize_weight)
+from .kernels import (BatchedQuantProjection, MoeRouter, Q4KDotKernel, Q6KDotKernel, Q8DotKernel, moe_ffn,
+                      project, project_gate_up, quantize_weight)
 from .runtime import Context, default_context
 from .weights import DecodeWeight, Q4KWeight, Q6KWeight, Q8Weight
 
@@ -16,7 +16,7 @@ TYPE_Q4_K = _lib.TYPE_Q4_K
 TYPE_Q6_K = _lib.TYPE_Q6_K
 
 __all__ = [
-    "BatchedQuantProjection", "Context", "DecodeWeight", "OverfitArgumentError", "OverfitArgumentNullError",
+    "BatchedQuantProjection", "Context", "DecodeWeight", "MoeRouter", "moe_ffn", "OverfitArgumentError", "OverfitArgumentNullError",
     "OverfitArgumentOutOfRangeError", "OverfitHipError", "OverfitUnsupportedTypeError", "Q4KDotKernel",
     "Q4KWeight", "Q6KDotKernel", "Q6KWeight", "Q8DotKernel", "Q8Weight", "TYPE_Q4_K", "TYPE_Q6_K", "TYPE_Q8_0",
     "default_context", "project", "project_gate_up", "quantize_weight",

@@ -50,6 +50,10 @@ SIGNATURES = {
     "ovfq_project_prequantized": (ci, [vp, vp, vp, vp, vp, ci, vp, vp]),
     "ovfq_project_prequantized_dev": (ci, [vp, vp, vp, vp, vp, ci, vp, vp]),
     "ovfq_project_gate_up": (ci, [vp, vp, vp, vp, vp, vp]),
+    "ovfq_moe_select_topk": (ci, [vp, vp, ci, ci, ci, ci, vp, vp]),
+    "ovfq_moe_select_topk_dev": (ci, [vp, vp, ci, ci, ci, ci, vp, vp]),
+    "ovfq_moe_ffn": (ci, [vp, ci, PP, PP, PP, vp, ci, ci, vp, vp, vp]),
+    "ovfq_moe_ffn_dev": (ci, [vp, ci, PP, PP, PP, vp, ci, ci, vp, vp, vp]),
     "ovfq_project_gate_up_dev": (ci, [vp, vp, vp, vp, vp, vp]),
     "ovfq_project_multi_dev": (ci, [vp, ci, PP, vp, ci, PP, PP]),
     "ovfq_project_multi_prequantized_dev": (ci, [vp, ci, PP, vp, vp, vp, ci, PP, PP]),

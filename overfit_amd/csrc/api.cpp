@@ -55,6 +55,8 @@ struct ovfq_ctx {
     std::mutex mu;
     // Activation quantisation scratch (Q8_K / Q8_0) and host-call staging.
     DevBuf act_q, act_s, act_b, x_stage, y_stage, y2_stage, bias_stage;
+    // Routed-MoE scratch (plan, gate/up/intermediate/expert outputs, host staging), carved from one buffer.
+    DevBuf moe;
 };
 
 struct ovfq_weight {
@@ -184,6 +186,15 @@ bool gemv_enabled() {
     return on;
 }
 
+// Kernel-selection knob for experiments: OVFQ_ROWS_DISABLE=1 routes 2 <= M < 32 through the general kernel.
+bool rows_enabled() {
+    static const bool on = [] {
+        const char* v = getenv("OVFQ_ROWS_DISABLE");
+        return !(v && *v == '1');
+    }();
+    return on;
+}
+
 // One launch for `count` weights sharing an activation: either the fp32 activation x (quantised inside the
 // decode kernel) or an already-quantised `act`.
 int launch_projection(ovfq_ctx* c, const ovfq_weight* const* ws, int count, const float* const* biases,
@@ -204,6 +215,26 @@ int launch_projection(ovfq_ctx* c, const ovfq_weight* const* ws, int count, cons
         HIP_TRY(ovfq::launch_gemv_kquant(type, jobs, count, in, x, act, c->stream));
     } else if (ovfq::mfma_supported(type, rows)) {
         HIP_TRY(ovfq::launch_project_mfma(type, jobs, count, in, rows, act, c->stream));
+    } else if (rows >= 2 && rows_enabled() && ovfq::rows_supported(type, in)) {
+        // Few rows: weight streaming with the rows staged in LDS; a gate/up-shaped pair shares one launch.
+        const bool pair = count == 2 && jobs[0].n_rows == jobs[1].n_rows;
+        for (int i = 0; i < count; i += pair ? 2 : 1) {
+            const uint8_t* w0 = jobs[i].w;
+            const uint8_t* w1 = pair ? jobs[i + 1].w : nullptr;
+            ovfq::RowsLaunch L{};
+            L.w0 = &w0;
+            L.w1 = pair ? &w1 : nullptr;
+            L.bias0 = jobs[i].bias;
+            L.bias1 = pair ? jobs[i + 1].bias : nullptr;
+            L.y0 = jobs[i].y;
+            L.y1 = pair ? jobs[i + 1].y : nullptr;
+            L.n_rows = jobs[i].n_rows;
+            L.in = in;
+            L.experts = 1;
+            L.rows = rows;
+            L.act = act;
+            HIP_TRY(ovfq::launch_rows_kquant(type, L, c->stream));
+        }
     } else {
         HIP_TRY(ovfq::launch_project_kquant(type, jobs, count, in, rows, act, c->stream));
     }
@@ -223,6 +254,20 @@ int check_rows(int rows) {
 }
 
 // Device pointers handed to the _dev entry points must keep the kernels' 4-byte (quants/bsums) alignment.
+// Carves 256-byte-aligned pieces off a base pointer.
+struct Carver {
+    char* p;
+    size_t used = 0;
+    template <class T>
+    T* take(size_t bytes) {
+        T* r = reinterpret_cast<T*>(p ? p + used : nullptr);
+        used += (bytes + 255) & ~size_t(255);
+        return r;
+    }
+};
+
+bool rc_align(const void* p) { return p && !aligned(p, 4); }
+
 int check_dev_align(const void* p, const char* name) {
     if (p && !aligned(p, 4)) return fail(OVFQ_ERR_SIZE, "%s must be 4-byte aligned", name);
     return OVFQ_OK;
@@ -260,7 +305,8 @@ int ovfq_ctx_destroy(ovfq_ctx* c) {
         std::lock_guard<std::mutex> lk(c->mu);
         (void)hipSetDevice(c->device);
         (void)hipStreamSynchronize(c->stream);
-        DevBuf* bufs[] = {&c->act_q, &c->act_s, &c->act_b, &c->x_stage, &c->y_stage, &c->y2_stage, &c->bias_stage};
+        DevBuf* bufs[] = {&c->act_q,   &c->act_s,   &c->act_b,      &c->x_stage,
+                          &c->y_stage, &c->y2_stage, &c->bias_stage, &c->moe};
         for (DevBuf* b : bufs)
             if (b->p) (void)hipFree(b->p);
         if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
@@ -612,6 +658,184 @@ int ovfq_project_multi_prequantized_dev(ovfq_ctx* ctx, int count, const ovfq_wei
     HIP_TRY(hipSetDevice(ctx->device));
     if ((rc = launch_projection(ctx, ws, count, biases, ys, rows, ovfq::ActQ{q, s, b}))) return rc;
     return ok();
+}
+
+// ---------------------------------------------------------------------------------------- routed MoE
+
+static int topk_impl(ovfq_ctx* ctx, const float* logits, int rows, int n_experts, int top_k, int normalize, int* idx,
+                     float* w, bool host) {
+    if (!ctx) return fail(OVFQ_ERR_NULL, "ctx is NULL");
+    if (!logits || !idx || !w) return fail(OVFQ_ERR_NULL, "logits / expert_indices / expert_weights is NULL");
+    if (n_experts < 1) return fail(OVFQ_ERR_SIZE, "Router logits cannot be empty (n_experts = %d)", n_experts);
+    if (n_experts > OVFQ_MAX_EXPERTS)
+        return fail(OVFQ_ERR_SIZE, "n_experts (%d) above %d", n_experts, OVFQ_MAX_EXPERTS);
+    if (top_k < 1) return fail(OVFQ_ERR_RANGE, "top_k (%d) must be positive", top_k);
+    if (rows < 1) return fail(OVFQ_ERR_RANGE, "rows (%d) must be positive", rows);
+    if (!host && (rc_align(logits) || rc_align(idx) || rc_align(w)))
+        return fail(OVFQ_ERR_SIZE, "device pointers must be 4-byte aligned");
+    const int k = top_k < n_experts ? top_k : n_experts;
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    HIP_TRY(hipSetDevice(ctx->device));
+    if (!host) {
+        HIP_TRY(ovfq::launch_moe_topk(logits, rows, n_experts, k, top_k, normalize, idx, w, ctx->stream));
+        return ok();
+    }
+    const size_t lb = (size_t)rows * n_experts * 4, ob = (size_t)rows * top_k * 4;
+    int rc;
+    if ((rc = ensure(ctx, ctx->moe, ((lb + 255) & ~size_t(255)) + 2 * ((ob + 255) & ~size_t(255))))) return rc;
+    char* base = static_cast<char*>(ctx->moe.p);
+    float* dl = reinterpret_cast<float*>(base);
+    int* di = reinterpret_cast<int*>(base + ((lb + 255) & ~size_t(255)));
+    float* dw = reinterpret_cast<float*>(base + ((lb + 255) & ~size_t(255)) + ((ob + 255) & ~size_t(255)));
+    HIP_TRY(hipMemcpyAsync(dl, logits, lb, hipMemcpyHostToDevice, ctx->stream));
+    // slots past min(top_k, n_experts) keep the caller's values
+    HIP_TRY(hipMemcpyAsync(di, idx, ob, hipMemcpyHostToDevice, ctx->stream));
+    HIP_TRY(hipMemcpyAsync(dw, w, ob, hipMemcpyHostToDevice, ctx->stream));
+    HIP_TRY(ovfq::launch_moe_topk(dl, rows, n_experts, k, top_k, normalize, di, dw, ctx->stream));
+    HIP_TRY(hipMemcpyAsync(idx, di, ob, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(hipMemcpyAsync(w, dw, ob, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return ok();
+}
+
+int ovfq_moe_select_topk(ovfq_ctx* ctx, const float* logits, int rows, int n_experts, int top_k, int normalize,
+                         int* expert_indices, float* expert_weights) {
+    return topk_impl(ctx, logits, rows, n_experts, top_k, normalize, expert_indices, expert_weights, true);
+}
+
+int ovfq_moe_select_topk_dev(ovfq_ctx* ctx, const float* logits, int rows, int n_experts, int top_k, int normalize,
+                             int* expert_indices, float* expert_weights) {
+    return topk_impl(ctx, logits, rows, n_experts, top_k, normalize, expert_indices, expert_weights, false);
+}
+
+static int moe_impl(ovfq_ctx* ctx, int E, const ovfq_weight* const* gate, const ovfq_weight* const* up,
+                    const ovfq_weight* const* down, const float* x, int rows, int k, const int* idx, const float* w,
+                    float* y, bool host) {
+    if (!ctx) return fail(OVFQ_ERR_NULL, "ctx is NULL");
+    if (!gate || !up || !down) return fail(OVFQ_ERR_NULL, "expert weight arrays are NULL");
+    if (!x || !idx || !w || !y) return fail(OVFQ_ERR_NULL, "x / expert_indices / expert_weights / y is NULL");
+    if (E < 1 || E > OVFQ_MAX_EXPERTS) return fail(OVFQ_ERR_RANGE, "n_experts (%d) must be in [1, %d]", E, OVFQ_MAX_EXPERTS);
+    if (rows < 1) return fail(OVFQ_ERR_RANGE, "rows (%d) must be positive", rows);
+    if (k < 1 || k > E) return fail(OVFQ_ERR_RANGE, "top_k (%d) must be in [1, n_experts]", k);
+    int rc;
+    for (int e = 0; e < E; e++) {
+        if (!gate[e] || !up[e] || !down[e]) return fail(OVFQ_ERR_NULL, "expert %d has a NULL weight", e);
+        if ((rc = check_weight(ctx, gate[e])) || (rc = check_weight(ctx, up[e])) || (rc = check_weight(ctx, down[e])))
+            return rc;
+    }
+    const int gt = gate[0]->type, dt = down[0]->type;
+    const int dmodel = gate[0]->in, dff = gate[0]->out;
+    for (int e = 0; e < E; e++) {
+        if (gate[e]->type == OVFQ_TYPE_Q8_0 || down[e]->type == OVFQ_TYPE_Q8_0)
+            return fail(OVFQ_ERR_TYPE, "expert weights must be Q4_K or Q6_K");
+        if (gate[e]->type != gt || up[e]->type != gt || down[e]->type != dt)
+            return fail(OVFQ_ERR_TYPE, "gate/up experts must share one type and down experts another");
+        if (gate[e]->in != dmodel || up[e]->in != dmodel || gate[e]->out != dff || up[e]->out != dff ||
+            down[e]->in != dff || down[e]->out != dmodel)
+            return fail(OVFQ_ERR_SIZE, "expert %d shapes differ (gate/up [d_ff][d_model], down [d_model][d_ff])", e);
+    }
+    if (!ovfq::rows_supported(gt, dmodel) || !ovfq::rows_supported(dt, dff))
+        return fail(OVFQ_ERR_SIZE, "d_model / d_ff above 16384");
+    if (!host && (rc_align(x) || rc_align(idx) || rc_align(w) || rc_align(y)))
+        return fail(OVFQ_ERR_SIZE, "device pointers must be 4-byte aligned");
+    const size_t P = (size_t)rows * k;
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    HIP_TRY(hipSetDevice(ctx->device));
+    // scratch layout (sizes first, then the pointers into one buffer)
+    auto carve = [&](Carver& c, int** off, int** prow, int** pof, float** g, float** u, int8_t** iq, float** is,
+                     int16_t** ib, float** out, float** hx, int** hidx, float** hw, float** hy) {
+        *off = c.take<int>((size_t)(E + 1) * 4);
+        *prow = c.take<int>(P * 4);
+        *pof = c.take<int>(P * 4);
+        *g = c.take<float>(P * dff * 4);
+        *u = c.take<float>(P * dff * 4);
+        *iq = c.take<int8_t>(P * dff);
+        *is = c.take<float>(P * (dff / OVFQ_QK) * 4);
+        *ib = c.take<int16_t>(P * (dff / 16) * 2);
+        *out = c.take<float>(P * dmodel * 4);
+        if (host) {
+            *hx = c.take<float>((size_t)rows * dmodel * 4);
+            *hidx = c.take<int>(P * 4);
+            *hw = c.take<float>(P * 4);
+            *hy = c.take<float>((size_t)rows * dmodel * 4);
+        }
+    };
+    int *off, *prow, *pof, *hidx = nullptr;
+    float *g, *u, *is, *out, *hx = nullptr, *hw = nullptr, *hy = nullptr;
+    int8_t* iq;
+    int16_t* ib;
+    Carver sizing{nullptr};
+    carve(sizing, &off, &prow, &pof, &g, &u, &iq, &is, &ib, &out, &hx, &hidx, &hw, &hy);
+    if ((rc = ensure(ctx, ctx->moe, sizing.used))) return rc;
+    Carver c{static_cast<char*>(ctx->moe.p)};
+    carve(c, &off, &prow, &pof, &g, &u, &iq, &is, &ib, &out, &hx, &hidx, &hw, &hy);
+    const float* xd = x;
+    const int* idxd = idx;
+    const float* wd = w;
+    float* yd = y;
+    if (host) {
+        HIP_TRY(hipMemcpyAsync(hx, x, (size_t)rows * dmodel * 4, hipMemcpyHostToDevice, ctx->stream));
+        HIP_TRY(hipMemcpyAsync(hidx, idx, P * 4, hipMemcpyHostToDevice, ctx->stream));
+        HIP_TRY(hipMemcpyAsync(hw, w, P * 4, hipMemcpyHostToDevice, ctx->stream));
+        xd = hx;
+        idxd = hidx;
+        wd = hw;
+        yd = hy;
+    }
+    ovfq::ActQ act;
+    if ((rc = quantize_into_scratch(ctx, gt, xd, rows, dmodel, &act))) return rc;
+    HIP_TRY(ovfq::launch_moe_plan(idxd, rows, k, E, off, prow, pof, ctx->stream));
+    const uint8_t* gw[OVFQ_MAX_EXPERTS];
+    const uint8_t* uw[OVFQ_MAX_EXPERTS];
+    const uint8_t* dw[OVFQ_MAX_EXPERTS];
+    for (int e = 0; e < E; e++) {
+        gw[e] = static_cast<const uint8_t*>(gate[e]->blocks);
+        uw[e] = static_cast<const uint8_t*>(up[e]->blocks);
+        dw[e] = static_cast<const uint8_t*>(down[e]->blocks);
+    }
+    ovfq::RowsLaunch L{};
+    L.w0 = gw;
+    L.w1 = uw;
+    L.y0 = g;
+    L.y1 = u;
+    L.n_rows = dff;
+    L.in = dmodel;
+    L.experts = E;
+    L.rows = rows;
+    L.expert_off = off;
+    L.pair_row = prow;
+    L.act = act;
+    HIP_TRY(ovfq::launch_rows_kquant(gt, L, ctx->stream));
+    HIP_TRY(ovfq::launch_swiglu_q8k(g, u, off, E, (int)P, dff, iq, is, ib, ctx->stream));
+    ovfq::RowsLaunch D{};
+    D.w0 = dw;
+    D.y0 = out;
+    D.n_rows = dmodel;
+    D.in = dff;
+    D.experts = E;
+    D.rows = (int)P;
+    D.expert_off = off;
+    D.pair_row = nullptr;  // the intermediate is already pair-major
+    D.act = ovfq::ActQ{iq, is, ib};
+    HIP_TRY(ovfq::launch_rows_kquant(dt, D, ctx->stream));
+    HIP_TRY(ovfq::launch_moe_combine(out, pof, wd, rows, k, dmodel, yd, ctx->stream));
+    if (host) {
+        HIP_TRY(hipMemcpyAsync(y, yd, (size_t)rows * dmodel * 4, hipMemcpyDeviceToHost, ctx->stream));
+        HIP_TRY(hipStreamSynchronize(ctx->stream));
+    }
+    return ok();
+}
+
+int ovfq_moe_ffn(ovfq_ctx* ctx, int n_experts, const ovfq_weight* const* gate, const ovfq_weight* const* up,
+                 const ovfq_weight* const* down, const float* x, int rows, int top_k, const int* expert_indices,
+                 const float* expert_weights, float* y) {
+    return moe_impl(ctx, n_experts, gate, up, down, x, rows, top_k, expert_indices, expert_weights, y, true);
+}
+
+int ovfq_moe_ffn_dev(ovfq_ctx* ctx, int n_experts, const ovfq_weight* const* gate, const ovfq_weight* const* up,
+                     const ovfq_weight* const* down, const float* x, int rows, int top_k, const int* expert_indices,
+                     const float* expert_weights, float* y) {
+    return moe_impl(ctx, n_experts, gate, up, down, x, rows, top_k, expert_indices, expert_weights, y, false);
 }
 
 // ---------------------------------------------------------------------------------------- weight encoders

@@ -1,0 +1,203 @@
+// moe.hip — the routed-MoE pieces around the grouped expert projections (rows.hip).
+//
+// MoeFeedForwardBlock.DecodeBatched (RT/MoeFeedForwardBlock.cs:140-241) without its router projection:
+//   1. MoeRouter.SelectTopK per token (RT/MoeRouter.cs:40-128)                       -> moe_topk_kernel
+//   2. group the (token, top-k slot) pairs by expert, tokens ascending               -> moe_plan_kernel
+//   3. per expert: gate/up = batched projections of its tokens                        (rows.hip, grid.y = expert)
+//   4. SiLU(gate) * up, quantised to Q8_K for the down projection                    -> swiglu_q8k_kernel
+//   5. per expert: down projection of its pairs                                       (rows.hip)
+//   6. y[token] = sum over top-k slots, in slot order, of weight * expert output     -> moe_combine_kernel
+// Pairs are numbered expert-major (expert 0's tokens first, ascending), which is the order the reference
+// gathers rows in; pair_of[token * k + slot] maps a slot back to its pair.
+#include <cmath>
+
+#include "ovfq_device.h"
+#include "ovfq_launch.h"
+
+namespace ovfq {
+
+// ------------------------------------------------------------------------------------------ router
+// One thread per token: insertion of each logit into a descending top-k list (ties keep the lower index), then
+// softmax over the k kept logits (normalize) or the full softmax evaluated at them.
+__global__ void moe_topk_kernel(const float* __restrict__ logits, int rows, int n_experts, int k, int stride,
+                                int normalize, int* __restrict__ idx_out, float* __restrict__ w_out) {
+    const int n = blockIdx.x * blockDim.x + threadIdx.x;
+    if (n >= rows) return;
+    const float* l = logits + (size_t)n * n_experts;
+    int idx[kMaxExperts];
+    float wv[kMaxExperts];
+    for (int i = 0; i < k; i++) {
+        idx[i] = -1;
+        wv[i] = -INFINITY;
+    }
+    int filled = 0;
+    for (int e = 0; e < n_experts; e++) {
+        const float v = l[e];
+        if (filled == k && v <= wv[k - 1]) continue;
+        int pos = filled < k ? filled : k - 1;
+        while (pos > 0 && wv[pos - 1] < v) {
+            wv[pos] = wv[pos - 1];
+            idx[pos] = idx[pos - 1];
+            pos--;
+        }
+        wv[pos] = v;
+        idx[pos] = e;
+        if (filled < k) filled++;
+    }
+    const float mx = wv[0];
+    if (normalize) {
+        float sum = 0.0f;
+        for (int i = 0; i < k; i++) {
+            const float w = expf(wv[i] - mx);
+            wv[i] = w;
+            sum += w;
+        }
+        const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+        for (int i = 0; i < k; i++) wv[i] *= inv;
+    } else {
+        float total = 0.0f;
+        for (int e = 0; e < n_experts; e++) total += expf(l[e] - mx);
+        const float inv = total > 0.0f ? 1.0f / total : 0.0f;
+        for (int i = 0; i < k; i++) wv[i] = expf(wv[i] - mx) * inv;
+    }
+    for (int i = 0; i < k; i++) {
+        idx_out[(size_t)n * stride + i] = idx[i];
+        w_out[(size_t)n * stride + i] = wv[i];
+    }
+}
+
+// ------------------------------------------------------------------------------------------ grouping
+// One workgroup. Expert e's pairs are the tokens n (ascending) with a slot j such that idx[n][j] == e (the first
+// such slot: RT/MoeFeedForwardBlock.cs:191-204). A slot whose expert is out of range, or repeats an earlier slot's
+// expert, belongs to no pair (pair_of = -1) and contributes nothing to the combine.
+__global__ __launch_bounds__(256) void moe_plan_kernel(const int* __restrict__ idx, int rows, int k, int n_experts,
+                                                       int* __restrict__ expert_off, int* __restrict__ pair_row,
+                                                       int* __restrict__ pair_of) {
+    __shared__ int cnt[kMaxExperts];
+    __shared__ int off[kMaxExperts + 1];
+    const int tid = threadIdx.x;
+    for (int i = tid; i < rows * k; i += blockDim.x) pair_of[i] = -1;
+    if (tid < n_experts) {
+        int c = 0;
+        for (int n = 0; n < rows; n++)
+            for (int j = 0; j < k; j++)
+                if (idx[n * k + j] == tid) {
+                    c++;
+                    break;
+                }
+        cnt[tid] = c;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int acc = 0;
+        for (int e = 0; e < n_experts; e++) {
+            off[e] = acc;
+            expert_off[e] = acc;
+            acc += cnt[e];
+        }
+        off[n_experts] = acc;
+        expert_off[n_experts] = acc;
+    }
+    __syncthreads();
+    if (tid < n_experts) {
+        int p = off[tid];
+        for (int n = 0; n < rows; n++)
+            for (int j = 0; j < k; j++)
+                if (idx[n * k + j] == tid) {
+                    pair_row[p] = n;
+                    pair_of[n * k + j] = p;
+                    p++;
+                    break;
+                }
+    }
+}
+
+// ------------------------------------------------------------------------------------------ SwiGLU
+// One wave per (pair, 256-element block) of the intermediate: gate <- gate * sigmoid(gate), up <- gate * up
+// (ApplySiLU + TensorPrimitives.Multiply, RT/CachedFeedForwardBlock.cs:339-343, :464-472), then the Q8_K
+// quantisation the down projection's BatchedQuantProjection.Dispatch applies to its input
+// (RT/Q4KDotKernel.cs:71-136). Pairs at or past expert_off[n_experts] are skipped.
+__global__ __launch_bounds__(256) void swiglu_q8k_kernel(const float* __restrict__ gate, const float* __restrict__ up,
+                                                         const int* __restrict__ expert_off, int n_experts,
+                                                         int max_pairs, int spr, int8_t* __restrict__ q,
+                                                         float* __restrict__ s, int16_t* __restrict__ bs) {
+    const int64_t blk = (int64_t)blockIdx.x * 4 + wave_id();
+    if (blk >= (int64_t)max_pairs * spr) return;
+    const int pairs = expert_off ? expert_off[n_experts] : max_pairs;
+    if (blk / spr >= pairs) return;
+    const int lane = threadIdx.x & 63;
+    const __amdgpu_buffer_rsrc_t gr = make_rsrc(gate + blk * kQK, kQK * 4);
+    const __amdgpu_buffer_rsrc_t ur = make_rsrc(up + blk * kQK, kQK * 4);
+    const u32x4 gv = ld4(gr, lane * 16), uv = ld4(ur, lane * 16);
+    const float g[4] = {as_float(gv.x), as_float(gv.y), as_float(gv.z), as_float(gv.w)};
+    const float u[4] = {as_float(uv.x), as_float(uv.y), as_float(uv.z), as_float(uv.w)};
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float sig = 1.0f / (1.0f + expf(-g[i]));
+        const float act = g[i] * sig;
+        v[i] = act * u[i];
+    }
+    const Q8KLane r = q8k_quantize_wave(v[0], v[1], v[2], v[3]);
+    reinterpret_cast<uint32_t*>(q + blk * kQK)[lane] = r.packed;
+    if ((lane & 3) == 0) bs[blk * 16 + (lane >> 2)] = (int16_t)r.group_sum;
+    if (lane == 0) s[blk] = r.scale;
+}
+
+// ------------------------------------------------------------------------------------------ combine
+// y[n][d] = 0; for each slot j in order: y[n][d] += w[n][j] * out[pair_of[n][j]][d] (RT/MoeFeedForwardBlock.cs:
+// 225-239). Each thread owns four consecutive d of one token.
+__global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ out, const int* __restrict__ pair_of,
+                                                          const float* __restrict__ w, int rows, int k, int dmodel,
+                                                          float* __restrict__ y) {
+    const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+    if (i >= (int64_t)rows * dmodel) return;
+    const int n = (int)(i / dmodel), d = (int)(i % dmodel);
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < k; j++) {
+        const int p = pair_of[n * k + j];
+        if (p < 0) continue;
+        const float wj = w[n * k + j];
+        const float* src = out + (size_t)p * dmodel + d;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const float prod = wj * src[c];
+            acc[c] = acc[c] + prod;
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; c++) y[i + c] = acc[c];
+}
+
+hipError_t launch_moe_topk(const float* logits, int rows, int n_experts, int k, int stride, int normalize, int* idx,
+                           float* w, hipStream_t st) {
+    hipLaunchKernelGGL(moe_topk_kernel, dim3((rows + 63) / 64), dim3(64), 0, st, logits, rows, n_experts, k, stride,
+                       normalize, idx, w);
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_plan(const int* idx, int rows, int k, int n_experts, int* expert_off, int* pair_row,
+                           int* pair_of, hipStream_t st) {
+    hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(256), 0, st, idx, rows, k, n_experts, expert_off, pair_row,
+                       pair_of);
+    return hipGetLastError();
+}
+
+hipError_t launch_swiglu_q8k(const float* gate, const float* up, const int* expert_off, int n_experts, int max_pairs,
+                             int dff, int8_t* q, float* s, int16_t* b, hipStream_t st) {
+    const int spr = dff / kQK;
+    const int64_t waves = (int64_t)max_pairs * spr;
+    hipLaunchKernelGGL(swiglu_q8k_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, gate, up, expert_off,
+                       n_experts, max_pairs, spr, q, s, b);
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_combine(const float* out, const int* pair_of, const float* w, int rows, int k, int dmodel,
+                              float* y, hipStream_t st) {
+    const int64_t threads = (int64_t)rows * dmodel / 4;
+    hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, out, pair_of, w,
+                       rows, k, dmodel, y);
+    return hipGetLastError();
+}
+
+}  // namespace ovfq

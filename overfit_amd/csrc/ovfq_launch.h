@@ -7,6 +7,7 @@
 namespace ovfq {
 
 constexpr int kMaxJobs = 4;
+constexpr int kMaxExperts = 64;
 
 // One output matrix of a (possibly fused) projection launch. Every job of a launch shares the activation.
 struct ProjJob {
@@ -40,6 +41,38 @@ hipError_t launch_gemv_kquant(int type, const ProjJob* jobs, int njobs, int in, 
 bool mfma_supported(int type, int rows);
 hipError_t launch_project_mfma(int type, const ProjJob* jobs, int njobs, int in, int rows, ActQ act,
                                hipStream_t st);
+// Small-batch / grouped-expert K-quant projection (rows.hip). One or two matrices per expert (gate, up) of
+// equal shape; expert_off/pair_row (device arrays) select each expert's activation rows, or NULL for a single
+// expert over activation rows 0..rows-1 (outputs row-major [pairs][n_rows]).
+struct RowsLaunch {
+    const uint8_t* const* w0;  // [experts]
+    const uint8_t* const* w1;  // [experts] or NULL
+    const float* bias0;        // single expert only
+    const float* bias1;
+    float* y0;
+    float* y1;
+    int n_rows;
+    int in;
+    int experts;
+    int rows;
+    const int* expert_off;
+    const int* pair_row;
+    ActQ act;
+    int pass_rows;  // activation rows per pass (4 or 8); 0 = default
+};
+bool rows_supported(int type, int in);
+hipError_t launch_rows_kquant(int type, const RowsLaunch& launch, hipStream_t st);
+
+// Routed MoE (moe.hip).
+hipError_t launch_moe_topk(const float* logits, int rows, int n_experts, int k, int stride, int normalize, int* idx,
+                           float* w, hipStream_t st);
+hipError_t launch_moe_plan(const int* idx, int rows, int k, int n_experts, int* expert_off, int* pair_row,
+                           int* pair_of, hipStream_t st);
+hipError_t launch_swiglu_q8k(const float* gate, const float* up, const int* expert_off, int n_experts, int max_pairs,
+                             int dff, int8_t* q, float* s, int16_t* b, hipStream_t st);
+hipError_t launch_moe_combine(const float* out, const int* pair_of, const float* w, int rows, int k, int dmodel,
+                              float* y, hipStream_t st);
+
 hipError_t launch_project_q8_0(const ProjJob* jobs, int njobs, int in, int rows, ActQ act, hipStream_t st);
 
 hipError_t launch_encode_q4k(const float* w, int64_t n_blocks, uint8_t* dst, hipStream_t st);

@@ -7,6 +7,8 @@ Same class and method names, argument meaning and argument checks as the referen
   Q6KDotKernel  RT/Q6KDotKernel.cs   (the same minus gate/up and weight-stationary)
   Q8DotKernel   RT/Q8DotKernel.cs    (Quantize, Dot, Project, ProjectParallel, ProjectBatched)
   BatchedQuantProjection.Dispatch    RT/BatchedQuantProjection.cs:26-87
+  MoeRouter.SelectTopK               RT/MoeRouter.cs:40-128 (plus moe_ffn: MoeFeedForwardBlock.DecodeBatched
+                                     after routing, RT/MoeFeedForwardBlock.cs:140-241)
 
 Spans become numpy arrays (host memory, synchronous) or torch GPU tensors (device memory, asynchronous on
 the context stream). An empty or None bias means "no bias". Outputs and the caller-owned activation scratch
@@ -345,6 +347,60 @@ class BatchedQuantProjection:
         ctx = w.context
         fn = ctx.lib.ovfq_project_dev if inp.device else ctx.lib.ovfq_project
         raise_for_status(fn(ctx.handle, w.handle, inp.ptr, rows, None if is_empty(bb) else bb.ptr, out.ptr), ctx.lib)
+
+
+class MoeRouter:
+    """RT/MoeRouter.cs:40-128 on the device: per-token top-k expert selection and combine weights."""
+
+    @staticmethod
+    def SelectTopK(logits, topK, expertIndices, expertWeights, normalize=True, rows=1) -> int:
+        """Writes the top-`topK` expert indices (descending by logit, ties to the lower index) and their
+        softmax weights for `rows` tokens of logits [rows][nExperts]; returns min(topK, nExperts)."""
+        lg = as_buf(logits, np.float32, "logits")
+        ix = as_buf(expertIndices, np.int32, "expertIndices")
+        wt = as_buf(expertWeights, np.float32, "expertWeights")
+        same_side(lg, ix, wt)
+        if rows <= 0:
+            raise OverfitArgumentOutOfRangeError(f"rows ({rows}) must be positive")
+        n = lg.size // rows
+        if n == 0:
+            raise OverfitArgumentError("Router logits cannot be empty.")
+        if topK <= 0:
+            raise OverfitArgumentOutOfRangeError(f"topK ({topK}) must be positive")
+        k = min(topK, n)
+        if ix.size < rows * topK or wt.size < rows * topK:
+            raise OverfitArgumentError("expertIndices / expertWeights smaller than rows * topK")
+        ctx = default_context()
+        fn = ctx.lib.ovfq_moe_select_topk_dev if lg.device else ctx.lib.ovfq_moe_select_topk
+        raise_for_status(fn(ctx.handle, lg.ptr, rows, n, topK, int(bool(normalize)), ix.ptr, wt.ptr), ctx.lib)
+        return k
+
+
+def moe_ffn(gate_experts, up_experts, down_experts, x, rows, top_k, expert_indices, expert_weights, out=None):
+    """MoeFeedForwardBlock.DecodeBatched after routing (RT/MoeFeedForwardBlock.cs:140-241): tokens grouped by
+    expert, each used expert's SwiGLU FFN on its tokens, weighted sum over the top-k slots in order."""
+    E = len(gate_experts)
+    if not (len(up_experts) == len(down_experts) == E):
+        raise OverfitArgumentError("gate/up/down expert lists differ in length")
+    inp = as_buf(x, np.float32, "x")
+    d_model = gate_experts[0].InputSize
+    if out is None:
+        if inp.device:
+            import torch
+
+            out = torch.empty(rows * d_model, dtype=torch.float32, device=inp.obj.device)
+        else:
+            out = np.zeros(rows * d_model, np.float32)
+    o = as_buf(out, np.float32, "out")
+    ix = as_buf(expert_indices, np.int32, "expert_indices")
+    wt = as_buf(expert_weights, np.float32, "expert_weights")
+    same_side(inp, o, ix, wt)
+    ctx = gate_experts[0].context
+    arr = lambda ws: (ctypes.c_void_p * E)(*[w.handle.value for w in ws])
+    fn = ctx.lib.ovfq_moe_ffn_dev if inp.device else ctx.lib.ovfq_moe_ffn
+    raise_for_status(fn(ctx.handle, E, arr(gate_experts), arr(up_experts), arr(down_experts), inp.ptr, rows, top_k,
+                        ix.ptr, wt.ptr, o.ptr), ctx.lib)
+    return out
 
 
 def project(weight, x, bias=None, rows=1, out=None):

@@ -227,6 +227,132 @@ def test_multi_projection_rows_bit_exact(orc, ctx, rows):
         assert_bit_exact(y.cpu().numpy().reshape(rows, -1), ref, f"multi prequantized rows={rows} job {i}")
 
 
+# ------------------------------------------------------------------------------------------------ small batch
+
+# 2 <= rows < 32 stream the weights with the rows staged in LDS (passes of 4): long rows (R = 1 path), the
+# largest K (64 super-blocks), an odd super-block count with 2-byte-aligned Q6_K rows, partial passes.
+SMALL_SHAPES = [("q4k", 4, 14336, 300), ("q6k", 7, 2304, 130), ("q4k", 31, 4096, 64), ("q6k", 9, 16384, 70),
+                ("q4k", 2, 256, 3)]
+
+
+@pytest.mark.parametrize("fmt,rows,k,n", SMALL_SHAPES)
+def test_small_batch_bit_exact(orc, fmt, rows, k, n):
+    case("small batch", fmt, rows, k, n)
+    rng = np.random.default_rng(rows * 31 + n)
+    blocks = _kq_blocks(rng, fmt, n, k)
+    x = normal(rng, (rows, k))
+    bias = normal(rng, n)
+    w = (ov.Q4KWeight if fmt == "q4k" else ov.Q6KWeight)(blocks, k, n)
+    ref = (orc.q4k_project_batched if fmt == "q4k" else orc.q6k_project_batched)(x, rows, blocks, k, n, bias)
+    y = ov.project(w, t(x), t(bias), rows=rows)
+    torch.cuda.synchronize()
+    assert_bit_exact(y.cpu().numpy().reshape(rows, n), ref, f"{fmt} small batch {rows}x{k}x{n}")
+
+
+# ------------------------------------------------------------------------------------------------ routed MoE
+
+@pytest.mark.parametrize("normalize", [True, False])
+def test_moe_select_topk_matches_oracle(orc, normalize):
+    case("moe topk", normalize)
+    rng = np.random.default_rng(8 + normalize)
+    rows, E, k = 37, 8, 2
+    logits = rng.random((rows, E)).astype(np.float32)
+    logits[3, 5] = logits[3, 2]  # a tie: the lower index wins
+    idx = torch.zeros(rows * k, dtype=torch.int32, device=DEV)
+    w = torch.zeros(rows * k, dtype=torch.float32, device=DEV)
+    assert ov.MoeRouter.SelectTopK(t(logits), k, idx, w, normalize, rows=rows) == k
+    torch.cuda.synchronize()
+    hi, hw = np.zeros(rows * k, np.int32), np.zeros(rows * k, np.float32)
+    ov.MoeRouter.SelectTopK(logits, k, hi, hw, normalize, rows=rows)
+    for n in range(rows):
+        ri, rw = orc.moe_select_topk(logits[n], k, normalize)
+        for gi, gw in ((idx.cpu().numpy(), w.cpu().numpy()), (hi, hw)):
+            assert np.array_equal(gi[n * k:(n + 1) * k], ri), n
+            np.testing.assert_allclose(gw[n * k:(n + 1) * k], rw, rtol=4e-7, atol=0)
+    # top_k above the expert count: min(top_k, n) slots written, the rest untouched
+    li, lw = np.full(2 * 5, 99, np.int32), np.full(2 * 5, 7.0, np.float32)
+    assert ov.MoeRouter.SelectTopK(logits[:2, :3].copy(), 5, li, lw, True, rows=2) == 3
+    for n in range(2):
+        ri, _ = orc.moe_select_topk(logits[n, :3], 5)
+        assert np.array_equal(li[n * 5:n * 5 + 3], ri) and np.all(li[n * 5 + 3:(n + 1) * 5] == 99)
+
+
+def _moe_check(y, ref, what):
+    y = np.asarray(y, np.float32).reshape(ref.shape)
+    rel, cos = north_star(y, ref)
+    scale = float(np.max(np.abs(ref)))
+    err = float(np.max(np.abs(y.astype(np.float64) - ref)))
+    exact = float(np.mean(y.view(np.uint32) == ref.astype(np.float32).view(np.uint32)))
+    print(f"[moe] {what}: max abs err / max|ref| = {err / scale:.2e}, cos = {cos:.9f}, bit-exact {exact:.3f}",
+          file=sys.stderr)
+    # SiLU goes through expf on both sides (a few ULP apart); one ULP can move a Q8_K quant of the down
+    # projection's input by one step, so the FFN output is held to the north-star tolerance, not bit-exactness.
+    assert cos >= 0.99999 and err <= 1e-3 * scale, what
+
+
+@pytest.mark.parametrize("gfmt,dfmt", [("q4k", "q6k"), ("q4k", "q4k"), ("q6k", "q6k")])
+def test_moe_ffn_matches_oracle(orc, gfmt, dfmt):
+    case("moe ffn", gfmt, dfmt)
+    rng = np.random.default_rng(21)
+    E, dm, dff, rows, k = 8, 512, 1024, 16, 2
+    T = {"q4k": ov.TYPE_Q4_K, "q6k": ov.TYPE_Q6_K}
+    W = {"q4k": ov.Q4KWeight, "q6k": ov.Q6KWeight}
+    enc = {"q4k": orc.quantize_q4k, "q6k": orc.quantize_q6k}
+    gb = [enc[gfmt](normal(rng, (dff, dm), 0.05)) for _ in range(E)]
+    ub = [enc[gfmt](normal(rng, (dff, dm), 0.05)) for _ in range(E)]
+    db = [enc[dfmt](normal(rng, (dm, dff), 0.05)) for _ in range(E)]
+    gw = [W[gfmt](b, dm, dff) for b in gb]
+    uw = [W[gfmt](b, dm, dff) for b in ub]
+    dw = [W[dfmt](b, dff, dm) for b in db]
+    x = normal(rng, (rows, dm))
+    idx = np.stack([rng.choice(E, k, replace=False) for _ in range(rows)]).astype(np.int32)
+    idx[:5, 0] = 3  # one expert with many tokens (more than one pass of rows)
+    idx[:5, 1] = np.where(idx[:5, 1] == 3, 4, idx[:5, 1])
+    w = rng.random((rows, k)).astype(np.float32)
+    ref = orc.moe_ffn_batched(gb, ub, db, T[gfmt], T[dfmt], x, rows, dm, dff, k, idx, w)
+    y = ov.moe_ffn(gw, uw, dw, t(x), rows, k, t(idx), t(w))
+    torch.cuda.synchronize()
+    _moe_check(y.cpu().numpy(), ref, f"{gfmt}/{dfmt} device")
+    _moe_check(ov.moe_ffn(gw, uw, dw, x, rows, k, idx, w), ref, f"{gfmt}/{dfmt} host")
+    # an expert with no tokens, and an unclaimed slot
+    idx2 = idx.copy()
+    idx2[idx2 == 6] = 7
+    idx2[2, 1] = E + 1
+    ref2 = orc.moe_ffn_batched(gb, ub, db, T[gfmt], T[dfmt], x, rows, dm, dff, k, idx2, w)
+    _moe_check(ov.moe_ffn(gw, uw, dw, x, rows, k, idx2, w), ref2, f"{gfmt}/{dfmt} sparse routing")
+
+
+def test_moe_config5_full_size(orc):
+    """8 Mixtral-shaped experts (gate/up 14336x4096, down 4096x14336, Q4_K), 16 tokens, top-2 of
+    seeded uniform router logits, routed on the device; checked against the oracle's DecodeBatched restatement."""
+    case("config5 full size")
+    gen = torch.Generator(device=DEV).manual_seed(55)
+    E, dm, dff, rows, k = 8, 4096, 14336, 16, 2
+    mats = {"gate": [], "up": [], "down": []}
+    host = {"gate": [], "up": [], "down": []}
+    for name in ("gate", "up", "down"):
+        n, kk = (dm, dff) if name == "down" else (dff, dm)
+        for _ in range(E):
+            wf = torch.randn(n, kk, generator=gen, device=DEV) * 0.02
+            b = ov.quantize_weight(wf, ov.TYPE_Q4_K)
+            del wf
+            mats[name].append(ov.Q4KWeight(b, kk, n))
+            host[name].append(b.cpu().numpy().reshape(n, -1))
+    rng = np.random.default_rng(56)
+    x = normal(rng, (rows, dm))
+    logits = rng.random((rows, E)).astype(np.float32)
+    idx = torch.empty(rows * k, dtype=torch.int32, device=DEV)
+    w = torch.empty(rows * k, dtype=torch.float32, device=DEV)
+    ov.MoeRouter.SelectTopK(t(logits), k, idx, w, rows=rows)
+    y = ov.moe_ffn(mats["gate"], mats["up"], mats["down"], t(x), rows, k, idx, w)
+    torch.cuda.synchronize()
+    hi, hw = idx.cpu().numpy().reshape(rows, k), w.cpu().numpy().reshape(rows, k)
+    for n in range(rows):
+        assert np.array_equal(hi[n], orc.moe_select_topk(logits[n], k)[0])
+    ref = orc.moe_ffn_batched(host["gate"], host["up"], host["down"], 12, 12, x, rows, dm, dff, k, hi, hw)
+    _moe_check(y.cpu().numpy(), ref, "config5")
+
+
 def _extreme_blocks(fmt, n, k):
     """Blocks at the ends of the integer ranges the MFMA operand split must hold: Q4_K sc = m = 63 with nibble 15
     (sc*nib = 945) and nibble 0; Q6_K scale -128 with q = 0 (sc*(q-32) = +4096), scale 127 with q = 63 and q = 0

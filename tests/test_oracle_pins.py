@@ -488,6 +488,79 @@ def test_moe_router_kats(orc):
     assert list(idx) == [0]  # ties keep the lower index
 
 
+# ------------------------------------------------------------------------------------------------ MoE FFN
+
+def _small_experts(orc, rng, E, dm, dff, gate_fmt="q4k", down_fmt="q6k"):
+    """E experts of N(0, 0.05) weights quantised by the oracle's own (pinned) encoders."""
+    enc = {"q4k": orc.quantize_q4k, "q6k": orc.quantize_q6k}
+    mk = lambda fmt, n, k: enc[fmt](normal(rng, (n, k), 0.05))
+    return ([mk(gate_fmt, dff, dm) for _ in range(E)], [mk(gate_fmt, dff, dm) for _ in range(E)],
+            [mk(down_fmt, dm, dff) for _ in range(E)])
+
+
+def test_swiglu_batched_matches_f64_dequantised_ffn(orc):
+    """orc_swiglu_batched against W_down (silu(W_gate x) * (W_up x)) in float64 on the dequantised weights: only
+    the Q8_K activation quantisation separates them (~1%); swapping gate and up, dropping SiLU or feeding the
+    down projection the wrong operand fails by far more."""
+    rng = np.random.default_rng(77)
+    dm, dff, rows = 512, 768, 3
+    (g,), (u,), (d,) = _small_experts(orc, rng, 1, dm, dff)
+    x = normal(rng, (rows, dm))
+    y = orc.swiglu_batched(x, rows, g, u, d, 12, 14, dm, dff)
+    dq = lambda blocks, k, n, fn: np.stack([fn(blocks, k, n, r) for r in range(n)]).astype(np.float64)
+    Wg, Wu = dq(g, dm, dff, orc.q4k_decode_row), dq(u, dm, dff, orc.q4k_decode_row)
+    Wd = dq(d, dff, dm, orc.q6k_decode_row)
+    a = x.astype(np.float64) @ Wg.T
+    ref = ((a / (1 + np.exp(-a))) * (x.astype(np.float64) @ Wu.T)) @ Wd.T
+    err = np.linalg.norm(y - ref) / np.linalg.norm(ref)
+    assert err < 0.02, err
+    bad = ((a * (x.astype(np.float64) @ Wu.T)) / (1 + np.exp(-(x.astype(np.float64) @ Wu.T)))) @ Wd.T  # gate<->up
+    assert np.linalg.norm(y - bad) / np.linalg.norm(ref) > 5 * err
+
+
+def test_moe_ffn_single_expert_is_the_swiglu_ffn(orc):
+    rng = np.random.default_rng(5)
+    dm, dff, rows = 256, 512, 4
+    g, u, d = _small_experts(orc, rng, 1, dm, dff)
+    x = normal(rng, (rows, dm))
+    y = orc.moe_ffn_batched(g, u, d, 12, 14, x, rows, dm, dff, 1, np.zeros((rows, 1)), np.ones((rows, 1)))
+    assert np.array_equal(y, orc.swiglu_batched(x, rows, g[0], u[0], d[0], 12, 14, dm, dff))
+
+
+def test_moe_ffn_grouping_and_combine_invariants(orc):
+    """Relabelling experts and permuting tokens change nothing but the labels (each token's FFN is row-local);
+    two identical experts combine to (0 + w0*o) + w1*o in float32, slot order; an unclaimed slot (index out of
+    range, or a repeat of an earlier slot's expert) contributes nothing."""
+    rng = np.random.default_rng(6)
+    E, dm, dff, rows, k = 4, 256, 512, 7, 2
+    g, u, d = _small_experts(orc, rng, E, dm, dff)
+    x = normal(rng, (rows, dm))
+    idx = np.stack([rng.choice(E, k, replace=False) for _ in range(rows)]).astype(np.int32)
+    w = rng.random((rows, k)).astype(np.float32)
+    y = orc.moe_ffn_batched(g, u, d, 12, 14, x, rows, dm, dff, k, idx, w)
+    perm = rng.permutation(E)  # new label of expert e is perm[e]
+    inv = np.argsort(perm)
+    y2 = orc.moe_ffn_batched([g[i] for i in inv], [u[i] for i in inv], [d[i] for i in inv], 12, 14, x, rows, dm,
+                             dff, k, perm[idx], w)
+    assert np.array_equal(y, y2)
+    tp = rng.permutation(rows)
+    y3 = orc.moe_ffn_batched(g, u, d, 12, 14, x[tp], rows, dm, dff, k, idx[tp], w[tp])
+    assert np.array_equal(y3, y[tp])
+    # two identical experts
+    o = orc.swiglu_batched(x, rows, g[0], u[0], d[0], 12, 14, dm, dff)
+    twin = orc.moe_ffn_batched([g[0], g[0]], [u[0], u[0]], [d[0], d[0]], 12, 14, x, rows, dm, dff, 2,
+                               np.tile([0, 1], (rows, 1)), w)
+    ref = (np.float32(0) + w[:, :1] * o) + w[:, 1:] * o
+    assert np.array_equal(twin, ref.astype(np.float32))
+    # unclaimed slots
+    idx_bad = idx.copy()
+    idx_bad[:, 1] = E + 3
+    idx_bad[0, 1] = idx_bad[0, 0]
+    y4 = orc.moe_ffn_batched(g, u, d, 12, 14, x, rows, dm, dff, k, idx_bad, w)
+    only0 = orc.moe_ffn_batched(g, u, d, 12, 14, x, rows, dm, dff, 1, idx[:, :1], w[:, :1])
+    assert np.array_equal(y4, only0)
+
+
 # ------------------------------------------------------------------------------------------------ CPU baseline
 
 def test_cpu_baseline_is_bit_identical_to_oracle(orc):
