@@ -186,13 +186,14 @@ bool gemv_enabled() {
     return on;
 }
 
-// Kernel-selection knob for experiments: OVFQ_ROWS_DISABLE=1 routes 2 <= M < 32 through the general kernel.
-bool rows_enabled() {
-    static const bool on = [] {
-        const char* v = getenv("OVFQ_ROWS_DISABLE");
-        return !(v && *v == '1');
+// Kernel for 3 <= M < 32: the super-block-parallel MFMA kernel, unless OVFQ_SMALL_KERNEL=general (for
+// measurements). At M = 2 the general kernel is faster on MI355X for every Llama-3-8B shape.
+bool small_mfma_enabled(int rows) {
+    static const bool general = [] {
+        const char* v = getenv("OVFQ_SMALL_KERNEL");
+        return v && !strcmp(v, "general");
     }();
-    return on;
+    return rows >= 3 && !general;
 }
 
 // One launch for `count` weights sharing an activation: either the fp32 activation x (quantised inside the
@@ -215,13 +216,13 @@ int launch_projection(ovfq_ctx* c, const ovfq_weight* const* ws, int count, cons
         HIP_TRY(ovfq::launch_gemv_kquant(type, jobs, count, in, x, act, c->stream));
     } else if (ovfq::mfma_supported(type, rows)) {
         HIP_TRY(ovfq::launch_project_mfma(type, jobs, count, in, rows, act, c->stream));
-    } else if (rows >= 2 && rows_enabled() && ovfq::rows_supported(type, in)) {
-        // Few rows: weight streaming with the rows staged in LDS; a gate/up-shaped pair shares one launch.
+    } else if (small_mfma_enabled(rows) && ovfq::mfma_small_supported(type, in)) {
+        // Few rows: 16-row MFMA tiles with super-block-parallel waves; a gate/up-shaped pair shares one launch.
         const bool pair = count == 2 && jobs[0].n_rows == jobs[1].n_rows;
         for (int i = 0; i < count; i += pair ? 2 : 1) {
             const uint8_t* w0 = jobs[i].w;
             const uint8_t* w1 = pair ? jobs[i + 1].w : nullptr;
-            ovfq::RowsLaunch L{};
+            ovfq::GroupLaunch L{};
             L.w0 = &w0;
             L.w1 = pair ? &w1 : nullptr;
             L.bias0 = jobs[i].bias;
@@ -233,7 +234,7 @@ int launch_projection(ovfq_ctx* c, const ovfq_weight* const* ws, int count, cons
             L.experts = 1;
             L.rows = rows;
             L.act = act;
-            HIP_TRY(ovfq::launch_rows_kquant(type, L, c->stream));
+            HIP_TRY(ovfq::launch_mfma_small(type, L, c->stream));
         }
     } else {
         HIP_TRY(ovfq::launch_project_kquant(type, jobs, count, in, rows, act, c->stream));
@@ -734,7 +735,7 @@ static int moe_impl(ovfq_ctx* ctx, int E, const ovfq_weight* const* gate, const 
             down[e]->in != dff || down[e]->out != dmodel)
             return fail(OVFQ_ERR_SIZE, "expert %d shapes differ (gate/up [d_ff][d_model], down [d_model][d_ff])", e);
     }
-    if (!ovfq::rows_supported(gt, dmodel) || !ovfq::rows_supported(dt, dff))
+    if (!ovfq::mfma_small_supported(gt, dmodel) || !ovfq::mfma_small_supported(dt, dff))
         return fail(OVFQ_ERR_SIZE, "d_model / d_ff above 16384");
     if (!host && (rc_align(x) || rc_align(idx) || rc_align(w) || rc_align(y)))
         return fail(OVFQ_ERR_SIZE, "device pointers must be 4-byte aligned");
@@ -793,7 +794,7 @@ static int moe_impl(ovfq_ctx* ctx, int E, const ovfq_weight* const* gate, const 
         uw[e] = static_cast<const uint8_t*>(up[e]->blocks);
         dw[e] = static_cast<const uint8_t*>(down[e]->blocks);
     }
-    ovfq::RowsLaunch L{};
+    ovfq::GroupLaunch L{};
     L.w0 = gw;
     L.w1 = uw;
     L.y0 = g;
@@ -805,9 +806,9 @@ static int moe_impl(ovfq_ctx* ctx, int E, const ovfq_weight* const* gate, const 
     L.expert_off = off;
     L.pair_row = prow;
     L.act = act;
-    HIP_TRY(ovfq::launch_rows_kquant(gt, L, ctx->stream));
+    HIP_TRY(ovfq::launch_mfma_small(gt, L, ctx->stream));
     HIP_TRY(ovfq::launch_swiglu_q8k(g, u, off, E, (int)P, dff, iq, is, ib, ctx->stream));
-    ovfq::RowsLaunch D{};
+    ovfq::GroupLaunch D{};
     D.w0 = dw;
     D.y0 = out;
     D.n_rows = dmodel;
@@ -817,7 +818,7 @@ static int moe_impl(ovfq_ctx* ctx, int E, const ovfq_weight* const* gate, const 
     D.expert_off = off;
     D.pair_row = nullptr;  // the intermediate is already pair-major
     D.act = ovfq::ActQ{iq, is, ib};
-    HIP_TRY(ovfq::launch_rows_kquant(dt, D, ctx->stream));
+    HIP_TRY(ovfq::launch_mfma_small(dt, D, ctx->stream));
     HIP_TRY(ovfq::launch_moe_combine(out, pof, wd, rows, k, dmodel, yd, ctx->stream));
     if (host) {
         HIP_TRY(hipMemcpyAsync(y, yd, (size_t)rows * dmodel * 4, hipMemcpyDeviceToHost, ctx->stream));

@@ -368,4 +368,168 @@ hipError_t launch_project_mfma(int type, const ProjJob* jobs, int njobs, int in,
     return nt == 128 ? launch_mfma<Q6KMfma, 128>(ma, st) : launch_mfma<Q6KMfma, 64>(ma, st);
 }
 
+// ------------------------------------------------------------------------------------------ small M
+// Few activation rows (M <= 16 per tile; MoE experts' token groups): one workgroup owns 16 weight rows and its
+// four waves split the row's super-blocks (wave w takes w, w+4, ...), so a 4096-row matrix already gives 1024
+// waves. Each wave loads the weights of kBatch super-blocks at once, reads its A operands straight from the
+// (L2-resident) Q8_K activation in the same K order the big kernel stages in LDS, runs the super-block's MFMAs and
+// fp32 tail, and stores the 16 x 16 block values in LDS; then one lane per (output, row) adds the values in
+// ascending super-block order (the reference's sequential sum) and writes biasO + sum.
+// grid.x = 16-row tiles over one or two matrices (gate/up), grid.y = expert: expert e owns pairs
+// [expert_off[e], expert_off[e+1]) of a pair list; pair p reads activation row pair_row[p] and writes output row p
+// (without a pair list: one expert over activation rows 0..rows-1).
+struct SArgs {
+    const uint8_t* w0[kMaxExperts];
+    const uint8_t* w1[kMaxExperts];
+    const float* bias0;
+    const float* bias1;
+    float* y0;
+    float* y1;
+    int n_rows;
+    int spr;
+    int tiles;  // 16-row tiles of one matrix
+    int rows;      // pairs of the single expert when expert_off == NULL
+    int act_rows;  // rows of the Q8_K activation (< 2^31 bytes in total)
+    const int* expert_off;
+    const int* pair_row;
+    const int8_t* q;
+    const float* s;
+};
+
+template <class F, int kBatch>
+__global__ __launch_bounds__(256) void kquant_mfma_small_kernel(const SArgs a) {
+    extern __shared__ __align__(16) float vals[];  // [spr][16 rows n][16 outputs o]
+    const int wave = wave_id();
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4, r16 = lane & 15;
+    const int e = blockIdx.y;
+    const int pbeg = a.expert_off ? a.expert_off[e] : 0;
+    const int cnt = a.expert_off ? a.expert_off[e + 1] - pbeg : a.rows;
+    if (cnt <= 0) return;  // uniform over the workgroup
+    const int mat = (int)blockIdx.x >= a.tiles ? 1 : 0;
+    const int o0 = ((int)blockIdx.x - mat * a.tiles) * 16;
+    const uint8_t* wptr = mat ? a.w1[e] : a.w0[e];
+    const int spr = a.spr;
+    const uint32_t K = (uint32_t)spr * kQK;
+    const uint32_t row_bytes = (uint32_t)spr * F::kBytes;
+    const uint64_t wbase = (uint64_t)o0 * row_bytes;
+    const uint64_t wbase4 = wbase & ~3ull;
+    const __amdgpu_buffer_rsrc_t wr =
+        make_rsrc(wptr + wbase4, rsrc_bytes((uint64_t)a.n_rows * row_bytes, wbase4));
+    const uint32_t woff = (uint32_t)(wbase - wbase4) + (uint32_t)r16 * row_bytes;
+    uint32_t a_off[4];  // byte offset inside a super-block of this lane's 16 A-operand bytes for MFMA t
+#pragma unroll
+    for (int t = 0; t < 4; t++) a_off[t] = 16u * F::src_piece(4u * t + (uint32_t)g);
+
+    // One wave-uniform resource over all activation rows (a per-lane resource would be re-made uniform by a
+    // readfirstlane loop around every load); the lane's row goes into the 32-bit offset.
+    const __amdgpu_buffer_rsrc_t qr = make_rsrc(a.q, (uint32_t)a.act_rows * K);
+    const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.s, (uint32_t)a.act_rows * (uint32_t)spr * 4u);
+    for (int n0 = 0; n0 < cnt; n0 += 16) {
+        // A operand row r16 of this tile: pair pbeg + n0 + r16; an absent row reads past the resource (zeros)
+        const bool have = n0 + r16 < cnt;
+        const int p = pbeg + n0 + r16;
+        const int arow = have ? (a.pair_row ? a.pair_row[p] : p) : 0;
+        const uint32_t qbase = have ? (uint32_t)arow * K : 0x80000000u;
+        const uint32_t sbase = have ? (uint32_t)arow * (uint32_t)spr * 4u : 0x80000000u;
+        for (int sb0 = wave; sb0 < spr; sb0 += 4 * kBatch) {
+            typename F::W w[kBatch];
+            u32x4 av[kBatch][4];
+            uint32_t sv[kBatch];
+#pragma unroll
+            for (int i = 0; i < kBatch; i++) {
+                const int sb = sb0 + 4 * i;  // past the row: reads are harmless and the values are not stored
+                w[i] = F::load(wr, woff + (uint32_t)sb * F::kBytes, g);
+#pragma unroll
+                for (int t = 0; t < 4; t++) av[i][t] = ld4(qr, qbase + (uint32_t)sb * kQK + a_off[t]);
+                sv[i] = ld1(sr, sbase + (uint32_t)sb * 4);
+            }
+#pragma unroll
+            for (int i = 0; i < kBatch; i++) {
+                // Every slot of the batch is computed (so the batch's loads stay ahead of all of its math); a
+                // slot past the row only skips its store.
+                const int sb = sb0 + 4 * i;
+                i32x4 op[4][F::kNumMfma];
+                F::template operands<0>(w[i], g, op[0]);
+                F::template operands<1>(w[i], g, op[1]);
+                F::template operands<2>(w[i], g, op[2]);
+                F::template operands<3>(w[i], g, op[3]);
+                i32x4 acc[F::kNumMfma];
+#pragma unroll
+                for (int k = 0; k < F::kNumMfma; k++) acc[k] = i32x4{0, 0, 0, 0};
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    const i32x4 aop = i32x4{(int)av[i][t].x, (int)av[i][t].y, (int)av[i][t].z, (int)av[i][t].w};
+#pragma unroll
+                    for (int k = 0; k < F::kNumMfma; k++) acc[k] = mfma16(aop, op[t][k], acc[k]);
+                }
+                const float d = F::d_of(w[i]), dmin = F::dmin_of(w[i]);
+                const float sc = as_float(sv[i]);  // q8 scale of row r16; rows 4g+i are needed below
+                float v[4];
+#pragma unroll
+                for (int j = 0; j < 4; j++) v[j] = F::tail(acc, j, d, dmin, __shfl(sc, 4 * g + j, 64));
+                if (sb < spr) {
+                    float* vrow = vals + sb * 256;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) vrow[(4 * g + j) * 16 + r16] = v[j];
+                }
+            }
+        }
+        __syncthreads();
+        // one lane per (row n, output o): ascending super-block sum, then biasO + sum
+        {
+            const int n = threadIdx.x >> 4, o = threadIdx.x & 15;
+            float sum = 0.0f;
+            for (int sb = 0; sb < spr; sb++) sum += vals[sb * 256 + threadIdx.x];
+            if (n0 + n < cnt && o0 + o < a.n_rows) {
+                const float* bias = mat ? a.bias1 : a.bias0;
+                float* y = mat ? a.y1 : a.y0;
+                y[(size_t)(pbeg + n0 + n) * a.n_rows + o0 + o] = bias ? bias[o0 + o] + sum : sum;
+            }
+        }
+        __syncthreads();  // the next row tile overwrites vals
+    }
+}
+
+template <class F, int kBatch>
+static hipError_t launch_small(SArgs& sa, int nmat, int experts, hipStream_t st) {
+    sa.tiles = (sa.n_rows + 15) / 16;
+    const size_t lds = (size_t)sa.spr * 256 * sizeof(float);
+    hipLaunchKernelGGL((kquant_mfma_small_kernel<F, kBatch>), dim3(sa.tiles * nmat, experts), dim3(256), lds, st, sa);
+    return hipGetLastError();
+}
+
+bool mfma_small_supported(int type, int in) { return (type == 12 || type == 14) && in % kQK == 0 && in / kQK <= 64; }
+
+hipError_t launch_mfma_small(int type, const GroupLaunch& L, hipStream_t st) {
+    SArgs sa{};
+    for (int i = 0; i < L.experts; i++) {
+        sa.w0[i] = L.w0[i];
+        sa.w1[i] = L.w1 ? L.w1[i] : nullptr;
+    }
+    sa.bias0 = L.bias0;
+    sa.bias1 = L.bias1;
+    sa.y0 = L.y0;
+    sa.y1 = L.y1;
+    sa.n_rows = L.n_rows;
+    sa.spr = L.in / kQK;
+    sa.rows = L.rows;
+    sa.act_rows = L.rows;
+    sa.expert_off = L.expert_off;
+    sa.pair_row = L.pair_row;
+    sa.q = L.act.q;
+    sa.s = L.act.s;
+    const int nmat = L.w1 ? 2 : 1;
+    // super-blocks per wave batch (measured on MI355X: 2 beats 4 for every Llama/Mixtral shape)
+    static const int forced = [] {
+        const char* v = getenv("OVFQ_SMALL_BATCH");
+        return v && *v ? atoi(v) : 0;
+    }();
+    const int batch = forced == 4 ? 4 : 2;
+    if (type == 12) return batch == 2 ? launch_small<Q4KMfma, 2>(sa, nmat, L.experts, st)
+                                      : launch_small<Q4KMfma, 4>(sa, nmat, L.experts, st);
+    return batch == 2 ? launch_small<Q6KMfma, 2>(sa, nmat, L.experts, st)
+                      : launch_small<Q6KMfma, 4>(sa, nmat, L.experts, st);
+}
+
 }  // namespace ovfq

@@ -1,11 +1,11 @@
-// moe.hip — the routed-MoE pieces around the grouped expert projections (rows.hip).
+// moe.hip — the routed-MoE pieces around the grouped expert projections (mfma.hip, small-M kernel).
 //
 // MoeFeedForwardBlock.DecodeBatched (RT/MoeFeedForwardBlock.cs:140-241) without its router projection:
 //   1. MoeRouter.SelectTopK per token (RT/MoeRouter.cs:40-128)                       -> moe_topk_kernel
 //   2. group the (token, top-k slot) pairs by expert, tokens ascending               -> moe_plan_kernel
-//   3. per expert: gate/up = batched projections of its tokens                        (rows.hip, grid.y = expert)
+//   3. per expert: gate/up = batched projections of its tokens                   (mfma.hip, grid.y = expert)
 //   4. SiLU(gate) * up, quantised to Q8_K for the down projection                    -> swiglu_q8k_kernel
-//   5. per expert: down projection of its pairs                                       (rows.hip)
+//   5. per expert: down projection of its pairs                                  (mfma.hip)
 //   6. y[token] = sum over top-k slots, in slot order, of weight * expert output     -> moe_combine_kernel
 // Pairs are numbered expert-major (expert 0's tokens first, ascending), which is the order the reference
 // gathers rows in; pair_of[token * k + slot] maps a slot back to its pair.

@@ -41,10 +41,10 @@ hipError_t launch_gemv_kquant(int type, const ProjJob* jobs, int njobs, int in, 
 bool mfma_supported(int type, int rows);
 hipError_t launch_project_mfma(int type, const ProjJob* jobs, int njobs, int in, int rows, ActQ act,
                                hipStream_t st);
-// Small-batch / grouped-expert K-quant projection (rows.hip). One or two matrices per expert (gate, up) of
-// equal shape; expert_off/pair_row (device arrays) select each expert's activation rows, or NULL for a single
-// expert over activation rows 0..rows-1 (outputs row-major [pairs][n_rows]).
-struct RowsLaunch {
+// Small-batch / grouped-expert K-quant projection. One or two matrices per expert (gate, up) of equal shape;
+// expert_off/pair_row (device arrays) select each expert's activation rows, or NULL for a single expert over
+// activation rows 0..rows-1 (outputs row-major [pairs][n_rows]).
+struct GroupLaunch {
     const uint8_t* const* w0;  // [experts]
     const uint8_t* const* w1;  // [experts] or NULL
     const float* bias0;        // single expert only
@@ -58,10 +58,10 @@ struct RowsLaunch {
     const int* expert_off;
     const int* pair_row;
     ActQ act;
-    int pass_rows;  // activation rows per pass (4 or 8); 0 = default
 };
-bool rows_supported(int type, int in);
-hipError_t launch_rows_kquant(int type, const RowsLaunch& launch, hipStream_t st);
+// On MFMA with super-block-parallel waves (mfma.hip), 16 activation rows per tile.
+bool mfma_small_supported(int type, int in);
+hipError_t launch_mfma_small(int type, const GroupLaunch& launch, hipStream_t st);
 
 // Routed MoE (moe.hip).
 hipError_t launch_moe_topk(const float* logits, int rows, int n_experts, int k, int stride, int normalize, int* idx,
