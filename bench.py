@@ -15,7 +15,7 @@ To measure HBM rather than the 256 MB Infinity Cache, steps rotate over several 
 Also reported: the dominant kernel's roofline (the fused gate/up Q4_K GEMV, per-launch HIP-event timing on
 the stream it runs on), BASELINE config 1 (a single Q4_K 4096x4096 GEMV rotated over 64 copies), config 3
 (the layer at M = 512 on int8 MFMA, with its MFMA roofline), config 4 (32 distinct layers + the Q6_K LM head,
-one token's projections), and the CPU baseline (the AVX2 C restatement of the reference's CPU path, on a
+one token's projections), config 5 (a Mixtral-shaped routed MoE step of 16 tokens), and the CPU baseline (the AVX2 C restatement of the reference's CPU path, on a
 bounded sample, rank 0 only).
 """
 import argparse
@@ -123,7 +123,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--copies", type=int, default=4, help="layer copies rotated to defeat the 256 MB cache")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--profile-only", action="store_true", help="only the timed layer loop (for rocprof runs)")
+    ap.add_argument("--profile", choices=["layer", "prefill", "moe"], default=None,
+                    help="for rocprof runs: only the timed decode-layer loop, the config-3 prefill line, or the "
+                         "config-5 MoE line")
     ap.add_argument("--pmc", action="store_true",
                     help="for rocprofv3 --pmc runs: 16 gate/up launches, then 16 plain 64 MiB device copies "
                          "(the counter calibration reference)")
@@ -172,18 +174,6 @@ def main():
         print(json.dumps({"pmc_run": "gate/up x16 then copy 64MiB x16"}), flush=True)
         return
 
-    for i in range(args.warmup):
-        step(copies[i % len(copies)])
-    torch.cuda.synchronize()
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    t0.record()
-    for i in range(args.steps):
-        step(copies[i % len(copies)])
-    t1.record()
-    torch.cuda.synchronize()
-    eager_ms = t0.elapsed_time(t1) / args.steps
-
     side = torch.cuda.Stream()
 
     def capture(calls):
@@ -212,33 +202,6 @@ def main():
         e1.record()
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) * 1e3 / (reps * n_calls)
-
-    g_step = capture([(lambda ws=ws: step(ws)) for ws in copies])
-    graph_reps = max(1, args.steps // len(copies))
-    graph_ms = replay_us(g_step, len(copies), graph_reps) / 1e3
-    ms = eager_ms  # headline: the plain eager loop, exactly K timed steps
-    w_bytes, alg_bytes = layer_algorithmic_bytes()
-    gbs = alg_bytes / (ms * 1e-3) / 1e9
-    if args.profile_only:
-        print(json.dumps({"ms_per_step": ms, "graph_ms_per_step": graph_ms, "GB/s": gbs}), flush=True)
-        return
-
-    # Dominant kernel: the gate/up launch (Q8_K quantise + both 14336x4096 Q4_K GEMVs, 66 MB), replayed from a
-    # graph over the layer copies; per-launch time = graph time / launches.
-    g_gu = capture([(lambda ws=ws: ctx.project_multi_dev([ws["gate"], ws["up"]], x_in["ffn"], [ys["gate"], ys["up"]]))
-                    for ws in copies] * 4)
-    gu_avg = replay_us(g_gu, 4 * len(copies), 16)
-    gu_bytes = 2 * weight_bytes(14336, 4096, "q4k") + 4 * 4096 + 4 * 2 * 14336
-    achieved = gu_bytes / (gu_avg * 1e-6) / 1e9
-    traffic = None
-    tfile = os.path.join(ROOT, "profiles", "traffic_q4k_gate_up_gemv.json")
-    if os.path.exists(tfile):
-        traffic = json.load(open(tfile)).get("bytes_per_launch")
-    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                "kernel": "kquant_gemv_kernel<Q4K,2> (Q8_K quantise + fused gate+up GEMV, 2x14336x4096)",
-                "avg_us": round(gu_avg, 3), "algorithmic_bytes": gu_bytes,
-                "timing": "HIP graph replay of 4x%d launches over %d weight copies, /launch" % (len(copies), len(copies))}
 
     def gemv_line(n, k, fmt, n_copies, label):
         gen1 = torch.Generator(device="cuda:0").manual_seed(77 + n)
@@ -327,11 +290,92 @@ def main():
                 "proj_tok_s_eager": round(1e6 / eager_us, 1), "proj_tok_s_graph": round(1e6 / graph_us, 1),
                 "GB_s_graph": round(w / (graph_us * 1e-6) / 1e9, 1)}
 
+    def moe_line(n_sets=2, tokens=16, top_k=2, n_experts=8):
+        """Mixtral-8x7B-shaped experts (gate/up 14336x4096, down 4096x14336, Q4_K), 16 tokens
+        routed top-2 on the device from seeded U[0,1) logits, grouped per-expert SwiGLU; graph-replayed over
+        n_sets independent expert sets (> 1.5 GB, past the 256 MB cache)."""
+        gen4 = torch.Generator(device="cuda:0").manual_seed(15)
+        sets = []
+        for _ in range(n_sets):
+            mats = {"gate": [], "up": [], "down": []}
+            for name in ("gate", "up", "down"):
+                n, kk = (4096, 14336) if name == "down" else (14336, 4096)
+                for _ in range(n_experts):
+                    wf = torch.randn(n, kk, generator=gen4, device=dev) * 0.02
+                    mats[name].append(ov.Q4KWeight(ov.quantize_weight(wf, ov.TYPE_Q4_K), kk, n))
+                    del wf
+            sets.append(mats)
+        xm = torch.randn(tokens * 4096, generator=gen4, device=dev)
+        logits = torch.rand(tokens * n_experts, generator=gen4, device=dev)
+        idx = torch.empty(tokens * top_k, dtype=torch.int32, device=dev)
+        wts = torch.empty(tokens * top_k, dtype=torch.float32, device=dev)
+        ym = torch.empty(tokens * 4096, device=dev)
+
+        def moe_step(m):
+            ov.MoeRouter.SelectTopK(logits, top_k, idx, wts, rows=tokens)
+            ov.moe_ffn(m["gate"], m["up"], m["down"], xm, tokens, top_k, idx, wts, out=ym)
+
+        g = capture([(lambda m=m: moe_step(m)) for m in sets])
+        us = replay_us(g, n_sets, 10)
+        used = len(set(idx.cpu().numpy().tolist()))
+        wb = used * (2 * weight_bytes(14336, 4096, "q4k") + weight_bytes(4096, 14336, "q4k"))
+        del g, sets
+        torch.cuda.empty_cache()
+        return {"what": "BASELINE config 5: Mixtral-8x7B experts (Q4_K gate/up/down), 16 tokens, top-2, one MoE "
+                        "step (route + group + 2 grouped projections + SwiGLU + combine, 7 launches)",
+                "us": round(us, 1), "experts_used": used, "weight_bytes": wb,
+                "GB_s": round(wb / (us * 1e-6) / 1e9, 1), "pct_peak": round(100 * wb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 2),
+                "timing": "HIP graph replay over %d expert sets, per step" % n_sets}
+
+    if args.profile in ("prefill", "moe"):
+        print(json.dumps(prefill_line() if args.profile == "prefill" else moe_line()), flush=True)
+        return
+
+    for i in range(args.warmup):
+        step(copies[i % len(copies)])
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for i in range(args.steps):
+        step(copies[i % len(copies)])
+    t1.record()
+    torch.cuda.synchronize()
+    eager_ms = t0.elapsed_time(t1) / args.steps
+
+    g_step = capture([(lambda ws=ws: step(ws)) for ws in copies])
+    graph_reps = max(1, args.steps // len(copies))
+    graph_ms = replay_us(g_step, len(copies), graph_reps) / 1e3
+    ms = eager_ms  # headline: the plain eager loop, exactly K timed steps
+    w_bytes, alg_bytes = layer_algorithmic_bytes()
+    gbs = alg_bytes / (ms * 1e-3) / 1e9
+    if args.profile == "layer":
+        print(json.dumps({"ms_per_step": ms, "graph_ms_per_step": graph_ms, "GB/s": gbs}), flush=True)
+        return
+
+    # Dominant kernel: the gate/up launch (Q8_K quantise + both 14336x4096 Q4_K GEMVs, 66 MB), replayed from a
+    # graph over the layer copies; per-launch time = graph time / launches.
+    g_gu = capture([(lambda ws=ws: ctx.project_multi_dev([ws["gate"], ws["up"]], x_in["ffn"], [ys["gate"], ys["up"]]))
+                    for ws in copies] * 4)
+    gu_avg = replay_us(g_gu, 4 * len(copies), 16)
+    gu_bytes = 2 * weight_bytes(14336, 4096, "q4k") + 4 * 4096 + 4 * 2 * 14336
+    achieved = gu_bytes / (gu_avg * 1e-6) / 1e9
+    traffic = None
+    tfile = os.path.join(ROOT, "profiles", "traffic_q4k_gate_up_gemv.json")
+    if os.path.exists(tfile):
+        traffic = json.load(open(tfile)).get("bytes_per_launch")
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                "kernel": "kquant_gemv_kernel<Q4K,2> (Q8_K quantise + fused gate+up GEMV, 2x14336x4096)",
+                "avg_us": round(gu_avg, 3), "algorithmic_bytes": gu_bytes,
+                "timing": "HIP graph replay of 4x%d launches over %d weight copies, /launch" % (len(copies), len(copies))}
+
     config1 = gemv_line(4096, 4096, "q4k", 64, "BASELINE config 1: Q4_K 4096x4096 GEMV (quantise in-launch)")
     large_q4k = gemv_line(128256, 4096, "q4k", 2, "Q4_K GEMV at LM-head size (asymptotic efficiency)")
     lm_head = gemv_line(128256, 4096, "q6k", 2, "Llama-3-8B Q6_K LM head 128256x4096 (config 4)")
     config3 = prefill_line()
     config4 = model_line()
+    config5 = moe_line()
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -363,6 +407,7 @@ def main():
         "config1_q4k_gemv_4096x4096": config1,
         "config3_prefill_m512": config3,
         "config4_32_layers_lm_head": config4,
+        "config5_moe_mixtral_16tok_top2": config5,
         "q4k_gemv_128256x4096": large_q4k,
         "q6k_lm_head_128256x4096": lm_head,
         "cpu_baseline": cpu,

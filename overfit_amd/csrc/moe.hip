@@ -18,12 +18,19 @@ namespace ovfq {
 
 // ------------------------------------------------------------------------------------------ router
 // One thread per token: insertion of each logit into a descending top-k list (ties keep the lower index), then
-// softmax over the k kept logits (normalize) or the full softmax evaluated at them.
-__global__ void moe_topk_kernel(const float* __restrict__ logits, int rows, int n_experts, int k, int stride,
-                                int normalize, int* __restrict__ idx_out, float* __restrict__ w_out) {
-    const int n = blockIdx.x * blockDim.x + threadIdx.x;
+// softmax over the k kept logits (normalize) or the full softmax evaluated at them. The workgroup's 64 logit rows
+// are first copied to LDS with coalesced loads, so the sequential scan reads LDS, not memory.
+__global__ __launch_bounds__(64) void moe_topk_kernel(const float* __restrict__ logits, int rows, int n_experts,
+                                                      int k, int stride, int normalize, int* __restrict__ idx_out,
+                                                      float* __restrict__ w_out) {
+    __shared__ float sl[64 * kMaxExperts];
+    const int row0 = blockIdx.x * 64;
+    const int nrow = min(64, rows - row0);
+    for (int i = threadIdx.x; i < nrow * n_experts; i += 64) sl[i] = logits[(size_t)row0 * n_experts + i];
+    __syncthreads();
+    const int n = row0 + threadIdx.x;
     if (n >= rows) return;
-    const float* l = logits + (size_t)n * n_experts;
+    const float* l = sl + threadIdx.x * n_experts;
     int idx[kMaxExperts];
     float wv[kMaxExperts];
     for (int i = 0; i < k; i++) {
@@ -70,13 +77,21 @@ __global__ void moe_topk_kernel(const float* __restrict__ logits, int rows, int 
 // One workgroup. Expert e's pairs are the tokens n (ascending) with a slot j such that idx[n][j] == e (the first
 // such slot: RT/MoeFeedForwardBlock.cs:191-204). A slot whose expert is out of range, or repeats an earlier slot's
 // expert, belongs to no pair (pair_of = -1) and contributes nothing to the combine.
-__global__ __launch_bounds__(256) void moe_plan_kernel(const int* __restrict__ idx, int rows, int k, int n_experts,
+// The routing table is copied to LDS first (dynamic LDS of rows * k ints when it fits), so the per-expert scans
+// read LDS instead of issuing one dependent memory load per entry.
+__global__ __launch_bounds__(256) void moe_plan_kernel(const int* __restrict__ idx_g, int rows, int k, int n_experts,
                                                        int* __restrict__ expert_off, int* __restrict__ pair_row,
-                                                       int* __restrict__ pair_of) {
+                                                       int* __restrict__ pair_of, int staged) {
+    extern __shared__ int sidx[];
     __shared__ int cnt[kMaxExperts];
     __shared__ int off[kMaxExperts + 1];
     const int tid = threadIdx.x;
-    for (int i = tid; i < rows * k; i += blockDim.x) pair_of[i] = -1;
+    for (int i = tid; i < rows * k; i += blockDim.x) {
+        pair_of[i] = -1;
+        if (staged) sidx[i] = idx_g[i];
+    }
+    __syncthreads();
+    const int* idx = staged ? sidx : idx_g;
     if (tid < n_experts) {
         int c = 0;
         for (int n = 0; n < rows; n++)
@@ -178,8 +193,10 @@ hipError_t launch_moe_topk(const float* logits, int rows, int n_experts, int k, 
 
 hipError_t launch_moe_plan(const int* idx, int rows, int k, int n_experts, int* expert_off, int* pair_row,
                            int* pair_of, hipStream_t st) {
-    hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(256), 0, st, idx, rows, k, n_experts, expert_off, pair_row,
-                       pair_of);
+    const size_t bytes = (size_t)rows * k * sizeof(int);
+    const int staged = bytes <= 48 * 1024;
+    hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(256), staged ? bytes : 0, st, idx, rows, k, n_experts, expert_off,
+                       pair_row, pair_of, staged);
     return hipGetLastError();
 }
 
