@@ -86,6 +86,15 @@ OVFQ_API int ovfq_weight_create(ovfq_ctx* ctx, int type, const void* blocks, siz
 OVFQ_API int ovfq_weight_create_from_device(ovfq_ctx* ctx, int type, const void* blocks, size_t nbytes,
                                             const float* q8_scales, int input_size, int output_size,
                                             ovfq_weight** out);
+/* A tensor exactly as stored in a GGUF file (a slice of the memory-mapped file): Q4_K / Q6_K super-blocks are
+ * uploaded verbatim (GgufReader.LoadTensorQ4_KRaw / Q6_KRaw, LD/GgufReader.cs:276-344); Q8_0's 34-byte blocks (fp16 d +
+ * 32 int8, GgufReader.LoadTensorQ8_0Raw, LD/GgufReader.cs:198-266) are de-interleaved on the device into the
+ * resident int8 quant plane and f32 scale plane (d widened exactly). `nbytes` must cover output_size rows. */
+OVFQ_API int ovfq_weight_create_gguf(ovfq_ctx* ctx, int type, const void* gguf_bytes, size_t nbytes, int input_size,
+                                     int output_size, ovfq_weight** out);
+/* As ovfq_weight_create_gguf, from device memory. */
+OVFQ_API int ovfq_weight_create_gguf_dev(ovfq_ctx* ctx, int type, const void* gguf_bytes, size_t nbytes,
+                                         int input_size, int output_size, ovfq_weight** out);
 OVFQ_API int ovfq_weight_destroy(ovfq_weight* w);
 /* Shape/format query (InputSize / OutputSize / ByteCount of the weight classes). Any out pointer may be NULL.
  * `device_blocks` receives the HBM address of the resident blocks (the quant plane for Q8_0). */

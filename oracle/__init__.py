@@ -68,6 +68,7 @@ _SIGS = {
     "orc_quantize_q6k": (c_int, [c_f32p, c_int, c_int, c_u8p]),
     "orc_q8_quantize_rows": (c_int, [c_f32p, c_int, c_int, c_i8p, c_f32p]),
     "orc_moe_select_topk": (c_int, [c_f32p, c_int, c_int, c_i32p, c_f32p, c_int]),
+    "orc_q8_0_deinterleave": (c_int, [c_u8p, ctypes.c_long, c_i8p, c_f32p]),
     "orc_swiglu_batched": (c_int, [c_f32p, c_int, c_u8p, c_u8p, c_u8p, c_int, c_int, c_int, c_int, c_f32p]),
     "orc_moe_ffn_batched": (c_int, [c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, c_int, c_int, c_f32p,
                                     c_int, c_int, c_int, c_int, c_i32p, c_f32p, c_f32p]),
@@ -321,6 +322,16 @@ def q6k_decode_row(blocks, k, n, row):
     dst = np.zeros(k, np.float32)
     _check(lib().orc_q6k_decode_row(P(np.ascontiguousarray(blocks, np.uint8)), k, n, row, P(dst)))
     return dst
+
+
+def q8_0_deinterleave(gguf):
+    """GgufReader.LoadTensorQ8_0Raw (oracle): 34-byte blocks -> (int8 quants, f32 scales)."""
+    g = np.ascontiguousarray(gguf, np.uint8).ravel()
+    nb = g.size // 34
+    q = np.zeros(nb * 32, np.int8)
+    s = np.zeros(nb, np.float32)
+    _check(lib().orc_q8_0_deinterleave(P(g), nb, P(q), P(s)))
+    return q, s
 
 
 def swiglu_batched(x, rows, gate, up, down, gate_type, down_type, d_model, d_ff):

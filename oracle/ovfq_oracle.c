@@ -778,6 +778,17 @@ int orc_q8_quantize_rows(const float* rm, int rows, int len, int8_t* quants, flo
 
 /* ---------------------------------------------------------------- MoE router */
 
+int orc_q8_0_deinterleave(const uint8_t* gguf, long n_blocks, int8_t* quants, float* scales) {
+    /* LD/GgufReader.cs:250-260: scale = (float)Half(bits), quants copied */
+    if (!gguf || !quants || !scales) return ORC_ERR_NULL;
+    for (long b = 0; b < n_blocks; b++) {
+        const uint8_t* p = gguf + b * 34;
+        scales[b] = orc_half_to_float((uint16_t)(p[0] | (p[1] << 8)));
+        memcpy(quants + b * 32, p + 2, 32);
+    }
+    return ORC_OK;
+}
+
 int orc_moe_select_topk(const float* logits, int n, int top_k, int* idx, float* w, int normalize) {
     /* RT/MoeRouter.cs:40-128 */
     if (!logits || !idx || !w) return ORC_ERR_NULL;

@@ -127,6 +127,9 @@ int orc_quantize_q6k(const float* f32, int input_size, int output_size, uint8_t*
 /* a11 applied row by row: RT/Q8Weight.cs:115-175 (QuantizeRows). */
 int orc_q8_quantize_rows(const float* row_major, int row_count, int row_length, int8_t* quants, float* scales);
 
+/* LD/GgufReader.cs:198-266 (LoadTensorQ8_0Raw): 34-byte blocks -> int8 quants + f32 scales. */
+int orc_q8_0_deinterleave(const uint8_t* gguf, long n_blocks, int8_t* quants, float* scales);
+
 /* RT/MoeRouter.cs:40-128 (SelectTopK). Returns k, or a negative status. */
 int orc_moe_select_topk(const float* logits, int n, int top_k, int* expert_indices, float* expert_weights,
                         int normalize);

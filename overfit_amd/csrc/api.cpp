@@ -354,6 +354,62 @@ int ovfq_weight_create_from_device(ovfq_ctx* ctx, int type, const void* blocks, 
                          hipMemcpyDeviceToDevice);
 }
 
+static int weight_create_gguf(ovfq_ctx* ctx, int type, const void* src, size_t nbytes, int in, int out,
+                              ovfq_weight** res, bool host) {
+    if (type != OVFQ_TYPE_Q8_0)
+        return weight_create(ctx, type, src, nbytes, nullptr, in, out, res,
+                             host ? hipMemcpyHostToDevice : hipMemcpyDeviceToDevice);
+    if (!ctx) return fail(OVFQ_ERR_NULL, "ctx is NULL");
+    if (!src) return fail(OVFQ_ERR_NULL, "gguf_bytes is NULL");
+    if (!res) return fail(OVFQ_ERR_NULL, "out is NULL");
+    int rc = check_weight_shape(type, in, out);
+    if (rc) return rc;
+    const int64_t n_blocks = (int64_t)out * (in / OVFQ_Q8_BLOCK);
+    const size_t gguf_len = (size_t)n_blocks * 34;
+    if (nbytes < gguf_len)
+        return fail(OVFQ_ERR_SIZE, "Q8_0 region (%zu B) is smaller than the expected %zu B", nbytes, gguf_len);
+    if (!host && !aligned(src, 2)) return fail(OVFQ_ERR_SIZE, "device gguf_bytes must be 2-byte aligned");
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    HIP_TRY(hipSetDevice(ctx->device));
+    ovfq_weight* w = new ovfq_weight();
+    w->ctx = ctx;
+    w->type = type;
+    w->in = in;
+    w->out = out;
+    void* staged = nullptr;
+    hipError_t e = hipMalloc(&w->blocks, (size_t)n_blocks * OVFQ_Q8_BLOCK);
+    if (e == hipSuccess) e = hipMalloc(&w->scales, (size_t)n_blocks * sizeof(float));
+    const void* dsrc = src;
+    if (e == hipSuccess && host) {
+        e = hipMalloc(&staged, gguf_len);
+        if (e == hipSuccess) e = hipMemcpyAsync(staged, src, gguf_len, hipMemcpyHostToDevice, ctx->stream);
+        dsrc = staged;
+    }
+    if (e == hipSuccess)
+        e = ovfq::launch_q8_0_deinterleave(dsrc, n_blocks, static_cast<int8_t*>(w->blocks), w->scales, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (staged) (void)hipFree(staged);
+    if (e != hipSuccess) {
+        if (w->blocks) (void)hipFree(w->blocks);
+        if (w->scales) (void)hipFree(w->scales);
+        delete w;
+        return fail(OVFQ_ERR_HIP, "Q8_0 GGUF upload failed: %s", hipGetErrorString(e));
+    }
+    w->nbytes = (size_t)n_blocks * (OVFQ_Q8_BLOCK + sizeof(float));
+    *res = w;
+    return ok();
+}
+
+int ovfq_weight_create_gguf(ovfq_ctx* ctx, int type, const void* gguf_bytes, size_t nbytes, int input_size,
+                            int output_size, ovfq_weight** out) {
+    return weight_create_gguf(ctx, type, gguf_bytes, nbytes, input_size, output_size, out, true);
+}
+
+int ovfq_weight_create_gguf_dev(ovfq_ctx* ctx, int type, const void* gguf_bytes, size_t nbytes, int input_size,
+                                int output_size, ovfq_weight** out) {
+    return weight_create_gguf(ctx, type, gguf_bytes, nbytes, input_size, output_size, out, false);
+}
+
 int ovfq_weight_destroy(ovfq_weight* w) {
     if (!w) return fail(OVFQ_ERR_NULL, "weight is NULL");
     {

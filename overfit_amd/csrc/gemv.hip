@@ -262,7 +262,10 @@ bool gemv_supported(int in) { return in % kQK == 0 && in / kQK <= kGemvMaxSpr; }
 
 // Every workgroup of the decode kernel quantises the whole activation; past 32 super-blocks (K > 8192) that
 // prologue costs more than one standalone quantise launch, so long rows are quantised once beforehand.
-bool gemv_quantize_inside(int in) { return in / kQK <= 32; }
+bool gemv_quantize_inside(int in) {
+    static const int limit = env_int("OVFQ_GEMV_QUANT_INSIDE_MAX_SPR", 32);
+    return in / kQK <= limit;
+}
 
 hipError_t launch_gemv_kquant(int type, const ProjJob* jobs, int njobs, int in, const float* x, ActQ act,
                               hipStream_t st) {

@@ -75,6 +75,8 @@ hipError_t launch_moe_combine(const float* out, const int* pair_of, const float*
 
 hipError_t launch_project_q8_0(const ProjJob* jobs, int njobs, int in, int rows, ActQ act, hipStream_t st);
 
+// GGUF Q8_0 (34-byte blocks) -> int8 quant plane + f32 scale plane.
+hipError_t launch_q8_0_deinterleave(const void* gguf, int64_t n_blocks, int8_t* q, float* s, hipStream_t st);
 hipError_t launch_encode_q4k(const float* w, int64_t n_blocks, uint8_t* dst, hipStream_t st);
 hipError_t launch_encode_q6k(const float* w, int64_t n_blocks, uint8_t* dst, hipStream_t st);
 

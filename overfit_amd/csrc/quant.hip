@@ -250,6 +250,20 @@ __global__ __launch_bounds__(256) void decode_row_q8_0_kernel(const int8_t* __re
 
 // ------------------------------------------------------------------------------------------ launchers
 
+// ------------------------------------------------------------------------------------------ GGUF Q8_0 upload
+// GgufReader.LoadTensorQ8_0Raw (LD/GgufReader.cs:198-266): the file's 34-byte blocks (fp16 d, 32 int8) become the
+// resident planes — quants copied, d widened exactly to f32. One thread per block; blocks are 2-byte aligned, so
+// the block is read as 17 halfwords.
+__global__ __launch_bounds__(256) void q8_0_deinterleave_kernel(const uint16_t* __restrict__ src, int64_t n_blocks,
+                                                                uint32_t* __restrict__ q, float* __restrict__ s) {
+    const int64_t blk = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (blk >= n_blocks) return;
+    const uint16_t* b = src + blk * 17;
+    s[blk] = half_bits_to_float(b[0]);
+#pragma unroll
+    for (int i = 0; i < 8; i++) q[blk * 8 + i] = (uint32_t)b[1 + 2 * i] | ((uint32_t)b[2 + 2 * i] << 16);
+}
+
 hipError_t launch_quantize_q8k(const float* x, int64_t n_blocks, int8_t* q, float* s, int16_t* b, hipStream_t st) {
     if (n_blocks <= 0) return hipSuccess;
     const int64_t grid = (n_blocks + 3) / 4;
@@ -261,6 +275,13 @@ hipError_t launch_quantize_q8_0(const float* x, int64_t n_blocks, int8_t* q, flo
     if (n_blocks <= 0) return hipSuccess;
     const int64_t grid = (n_blocks * 8 + 255) / 256;
     hipLaunchKernelGGL(quantize_q8_0_kernel, dim3((unsigned)grid), dim3(256), 0, st, x, n_blocks, q, s);
+    return hipGetLastError();
+}
+
+hipError_t launch_q8_0_deinterleave(const void* gguf, int64_t n_blocks, int8_t* q, float* s, hipStream_t st) {
+    if (n_blocks <= 0) return hipSuccess;
+    hipLaunchKernelGGL(q8_0_deinterleave_kernel, dim3((unsigned)((n_blocks + 255) / 256)), dim3(256), 0, st,
+                       static_cast<const uint16_t*>(gguf), n_blocks, reinterpret_cast<uint32_t*>(q), s);
     return hipGetLastError();
 }
 

@@ -10,7 +10,7 @@ import numpy as np
 
 from . import _lib
 from .errors import (OverfitArgumentError, OverfitArgumentNullError, OverfitArgumentOutOfRangeError,
-                     raise_for_status)
+                     OverfitUnsupportedTypeError, raise_for_status)
 from .runtime import as_buf, default_context
 
 
@@ -131,6 +131,26 @@ class Q8Weight(_ResidentWeight):
         if s.size < output_size * (input_size // self.BlockSize):
             raise OverfitArgumentError("Scales array is smaller than outputSize * blocksPerRow.")
         self._upload(q, q.size, s, input_size, output_size, ctx)
+
+
+def load_gguf_tensor(type_id, data, input_size: int, output_size: int, ctx=None):
+    """A quantized tensor exactly as a GGUF file stores it -> the matching resident weight (GgufReader's
+    LoadTensorQ4_KRaw / LoadTensorQ6_KRaw / LoadTensorQ8_0Raw, LD/GgufReader.cs:198-344): Q4_K/Q6_K bytes verbatim,
+    Q8_0's 34-byte blocks de-interleaved on the device into the int8 + f32 planes."""
+    cls = {_lib.TYPE_Q4_K: Q4KWeight, _lib.TYPE_Q6_K: Q6KWeight, _lib.TYPE_Q8_0: Q8Weight}.get(type_id)
+    if cls is None:
+        raise OverfitUnsupportedTypeError(f"type {type_id}")
+    buf = as_buf(data, np.uint8, "data")
+    w = cls.__new__(cls)
+    w._ctx = ctx or default_context()
+    lib = w._ctx.lib
+    h = ctypes.c_void_p()
+    fn = lib.ovfq_weight_create_gguf_dev if buf.device else lib.ovfq_weight_create_gguf
+    raise_for_status(fn(w._ctx.handle, type_id, buf.ptr, buf.size, input_size, output_size, ctypes.byref(h)), lib)
+    w.handle = h
+    w._input_size = input_size
+    w._output_size = output_size
+    return w
 
 
 class DecodeWeight:

@@ -227,6 +227,36 @@ def test_multi_projection_rows_bit_exact(orc, ctx, rows):
         assert_bit_exact(y.cpu().numpy().reshape(rows, -1), ref, f"multi prequantized rows={rows} job {i}")
 
 
+# ------------------------------------------------------------------------------------------------ GGUF upload
+
+@pytest.mark.parametrize("on_device", [False, True])
+def test_gguf_upload_q8_0_q4k_q6k(orc, on_device):
+    """Tensors in their GGUF bytes: Q8_0's 34-byte blocks de-interleaved on the device must project exactly like the
+    oracle's LoadTensorQ8_0Raw planes; Q4_K / Q6_K bytes go up verbatim."""
+    case("gguf upload", on_device)
+    rng = np.random.default_rng(31 + on_device)
+    k, n = 1024, 96
+    wq, ws = orc.q8_quantize_rows(normal(rng, (n, k), 0.05))
+    blocks = np.zeros((n * k // 32, 34), np.uint8)
+    half = ws.astype(np.float16)  # a GGUF file stores fp16 scales
+    blocks[:, 0:2] = half.view(np.uint8).reshape(-1, 2)
+    blocks[:, 2:] = wq.reshape(-1, 32).view(np.uint8)
+    rq, rs = orc.q8_0_deinterleave(blocks)
+    src = t(blocks.ravel()) if on_device else blocks.ravel()
+    w8 = ov.load_gguf_tensor(ov.TYPE_Q8_0, src, k, n)
+    x = normal(rng, k)
+    assert_bit_exact(ov.project(w8, x), orc.q8_project_batched(x, 1, rq, rs, k, n).ravel(), "gguf Q8_0")
+    dec = np.zeros(k, np.float32)
+    w8.DecodeRow(5, dec)
+    assert np.array_equal(dec, rq.reshape(n, k)[5].astype(np.float32) * np.repeat(rs.reshape(n, -1)[5], 32))
+    for fmt in ("q4k", "q6k"):
+        b = _kq_blocks(rng, fmt, n, k)
+        w = ov.load_gguf_tensor(ov.TYPE_Q4_K if fmt == "q4k" else ov.TYPE_Q6_K, t(b.ravel()) if on_device else b.ravel(),
+                                k, n)
+        ref = (orc.q4k_project if fmt == "q4k" else orc.q6k_project)(x, b, k, n)
+        assert_bit_exact(ov.project(w, x), ref, f"gguf {fmt}")
+
+
 # ------------------------------------------------------------------------------------------------ small batch
 
 # 2 <= rows < 32 stream the weights with the rows staged in LDS (passes of 4): long rows (R = 1 path), the

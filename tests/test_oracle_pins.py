@@ -488,6 +488,27 @@ def test_moe_router_kats(orc):
     assert list(idx) == [0]  # ties keep the lower index
 
 
+# ------------------------------------------------------------------------------------------------ GGUF Q8_0
+
+def test_q8_0_deinterleave_round_trip(orc):
+    """LoadTensorQ8_0Raw: interleaving (quants, fp16 scale bits) into 34-byte blocks and back returns the quants and
+    the scale widened exactly (numpy float16 -> float32), for every fp16 pattern class (subnormal, inf, -0)."""
+    rng = np.random.default_rng(9)
+    nb = 4096
+    q = rng.integers(-128, 128, size=(nb, 32), dtype=np.int8)
+    bits = rng.integers(0, 65536, size=nb, dtype=np.uint32).astype(np.uint16)
+    bits[:4] = [0x0001, 0x8000, 0x7C00, 0x3C00]
+    blocks = np.zeros((nb, 34), np.uint8)
+    blocks[:, 0] = bits & 0xFF
+    blocks[:, 1] = bits >> 8
+    blocks[:, 2:] = q.view(np.uint8)
+    gq, gs = orc.q8_0_deinterleave(blocks)
+    assert np.array_equal(gq, q.ravel())
+    ref = bits.view(np.float16).astype(np.float32)
+    finite = ~np.isnan(ref)
+    assert np.array_equal(gs[finite].view(np.uint32), ref[finite].view(np.uint32))
+
+
 # ------------------------------------------------------------------------------------------------ MoE FFN
 
 def _small_experts(orc, rng, E, dm, dff, gate_fmt="q4k", down_fmt="q6k"):
