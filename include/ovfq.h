@@ -168,6 +168,19 @@ OVFQ_API int ovfq_project_multi_prequantized_dev(ovfq_ctx* ctx, int count, const
                                                  const int8_t* quants, const float* scales, const int16_t* bsums,
                                                  int rows, const float* const* biases, float* const* ys);
 
+/* ---------------------------------------------------------------------------------- SwiGLU FFN */
+
+/* CachedFeedForwardBlock.DecodeSwiGluDispatched / DecodeSwiGluBatchedDispatched (RT/CachedFeedForwardBlock.cs:
+ * 261-344) on the device: y[rows][d_model] = down(SiLU(gate(x)) * up(x)) for x[rows][d_model], gate/up
+ * [d_ff][d_model] of one K-quant type, down [d_model][d_ff] K-quant. Three launches (gate/up, SiLU*up with the
+ * Q8_K quantisation of the down input, down) and no host round trip. The projections are bit-identical to the
+ * reference's; SiLU uses expf (the reference's TensorPrimitives.Sigmoid is itself few-ULP), so y matches to the
+ * projection tolerance. No counterpart entry point in the reference (it runs the steps on the host). */
+OVFQ_API int ovfq_ffn_swiglu(ovfq_ctx* ctx, const ovfq_weight* gate, const ovfq_weight* up, const ovfq_weight* down,
+                             const float* x, int rows, float* y);
+OVFQ_API int ovfq_ffn_swiglu_dev(ovfq_ctx* ctx, const ovfq_weight* gate, const ovfq_weight* up,
+                                 const ovfq_weight* down, const float* x, int rows, float* y);
+
 /* ---------------------------------------------------------------------------------- routed MoE */
 
 #define OVFQ_MAX_EXPERTS 64

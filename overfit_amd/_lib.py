@@ -52,6 +52,8 @@ SIGNATURES = {
     "ovfq_project_gate_up": (ci, [vp, vp, vp, vp, vp, vp]),
     "ovfq_weight_create_gguf": (ci, [vp, ci, vp, ctypes.c_size_t, ci, ci, ctypes.POINTER(vp)]),
     "ovfq_weight_create_gguf_dev": (ci, [vp, ci, vp, ctypes.c_size_t, ci, ci, ctypes.POINTER(vp)]),
+    "ovfq_ffn_swiglu": (ci, [vp, vp, vp, vp, vp, ci, vp]),
+    "ovfq_ffn_swiglu_dev": (ci, [vp, vp, vp, vp, vp, ci, vp]),
     "ovfq_moe_select_topk": (ci, [vp, vp, ci, ci, ci, ci, vp, vp]),
     "ovfq_moe_select_topk_dev": (ci, [vp, vp, ci, ci, ci, ci, vp, vp]),
     "ovfq_moe_ffn": (ci, [vp, ci, PP, PP, PP, vp, ci, ci, vp, vp, vp]),

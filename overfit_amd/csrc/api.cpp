@@ -883,6 +883,85 @@ static int moe_impl(ovfq_ctx* ctx, int E, const ovfq_weight* const* gate, const 
     return ok();
 }
 
+// ---------------------------------------------------------------------------------------- SwiGLU FFN
+
+static int ffn_impl(ovfq_ctx* ctx, const ovfq_weight* gate, const ovfq_weight* up, const ovfq_weight* down,
+                    const float* x, int rows, float* y, bool host) {
+    if (!ctx) return fail(OVFQ_ERR_NULL, "ctx is NULL");
+    if (!gate || !up || !down) return fail(OVFQ_ERR_NULL, "gate / up / down is NULL");
+    if (!x || !y) return fail(OVFQ_ERR_NULL, "x / y is NULL");
+    int rc;
+    if ((rc = check_weight(ctx, gate)) || (rc = check_weight(ctx, up)) || (rc = check_weight(ctx, down))) return rc;
+    if ((rc = check_rows(rows))) return rc;
+    if (gate->type == OVFQ_TYPE_Q8_0 || down->type == OVFQ_TYPE_Q8_0)
+        return fail(OVFQ_ERR_TYPE, "the fused FFN takes Q4_K / Q6_K weights");
+    if (up->type != gate->type) return fail(OVFQ_ERR_TYPE, "gate and up must share a type");
+    const int dmodel = gate->in, dff = gate->out;
+    if (up->in != dmodel || up->out != dff || down->in != dff || down->out != dmodel)
+        return fail(OVFQ_ERR_SIZE, "shapes must be gate/up [d_ff][d_model] and down [d_model][d_ff]");
+    if (!host && (rc_align(x) || rc_align(y))) return fail(OVFQ_ERR_SIZE, "device pointers must be 4-byte aligned");
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    HIP_TRY(hipSetDevice(ctx->device));
+    const size_t R = (size_t)rows;
+    auto carve = [&](Carver& c, float** g, float** u, int8_t** iq, float** is, int16_t** ib, float** hx, float** hy) {
+        *g = c.take<float>(R * dff * 4);
+        *u = c.take<float>(R * dff * 4);
+        *iq = c.take<int8_t>(R * dff);
+        *is = c.take<float>(R * (dff / OVFQ_QK) * 4);
+        *ib = c.take<int16_t>(R * (dff / 16) * 2);
+        if (host) {
+            *hx = c.take<float>(R * dmodel * 4);
+            *hy = c.take<float>(R * dmodel * 4);
+        }
+    };
+    float *g, *u, *is, *hx = nullptr, *hy = nullptr;
+    int8_t* iq;
+    int16_t* ib;
+    Carver sizing{nullptr};
+    carve(sizing, &g, &u, &iq, &is, &ib, &hx, &hy);
+    if ((rc = ensure(ctx, ctx->moe, sizing.used))) return rc;
+    Carver c{static_cast<char*>(ctx->moe.p)};
+    carve(c, &g, &u, &iq, &is, &ib, &hx, &hy);
+    const float* xd = x;
+    float* yd = y;
+    if (host) {
+        HIP_TRY(hipMemcpyAsync(hx, x, R * dmodel * 4, hipMemcpyHostToDevice, ctx->stream));
+        xd = hx;
+        yd = hy;
+    }
+    // gate/up (one launch; for one row the Q8_K quantisation runs inside it)
+    const ovfq_weight* gu[2] = {gate, up};
+    float* gu_out[2] = {g, u};
+    if (rows == 1 && gemv_enabled() && ovfq::gemv_supported(dmodel) && ovfq::gemv_quantize_inside(dmodel)) {
+        if ((rc = launch_projection(ctx, gu, 2, nullptr, gu_out, rows, ovfq::ActQ{nullptr, nullptr, nullptr}, xd)))
+            return rc;
+    } else {
+        ovfq::ActQ act;
+        if ((rc = quantize_into_scratch(ctx, gate->type, xd, rows, dmodel, &act))) return rc;
+        if ((rc = launch_projection(ctx, gu, 2, nullptr, gu_out, rows, act))) return rc;
+    }
+    // SiLU(gate) * up, quantised to Q8_K for the down projection
+    HIP_TRY(ovfq::launch_swiglu_q8k(g, u, nullptr, 0, rows, dff, iq, is, ib, ctx->stream));
+    const ovfq_weight* dw[1] = {down};
+    float* dy[1] = {yd};
+    if ((rc = launch_projection(ctx, dw, 1, nullptr, dy, rows, ovfq::ActQ{iq, is, ib}))) return rc;
+    if (host) {
+        HIP_TRY(hipMemcpyAsync(y, yd, R * dmodel * 4, hipMemcpyDeviceToHost, ctx->stream));
+        HIP_TRY(hipStreamSynchronize(ctx->stream));
+    }
+    return ok();
+}
+
+int ovfq_ffn_swiglu(ovfq_ctx* ctx, const ovfq_weight* gate, const ovfq_weight* up, const ovfq_weight* down,
+                    const float* x, int rows, float* y) {
+    return ffn_impl(ctx, gate, up, down, x, rows, y, true);
+}
+
+int ovfq_ffn_swiglu_dev(ovfq_ctx* ctx, const ovfq_weight* gate, const ovfq_weight* up, const ovfq_weight* down,
+                        const float* x, int rows, float* y) {
+    return ffn_impl(ctx, gate, up, down, x, rows, y, false);
+}
+
 int ovfq_moe_ffn(ovfq_ctx* ctx, int n_experts, const ovfq_weight* const* gate, const ovfq_weight* const* up,
                  const ovfq_weight* const* down, const float* x, int rows, int top_k, const int* expert_indices,
                  const float* expert_weights, float* y) {

@@ -376,6 +376,26 @@ class MoeRouter:
         return k
 
 
+def ffn_swiglu(gate, up, down, x, rows=1, out=None):
+    """CachedFeedForwardBlock.DecodeSwiGluDispatched / DecodeSwiGluBatchedDispatched (RT/CachedFeedForwardBlock.cs:
+    261-344) on the device: down(SiLU(gate(x)) * up(x)) in three launches, no host round trip."""
+    inp = as_buf(x, np.float32, "x")
+    d_model = gate.InputSize
+    if out is None:
+        if inp.device:
+            import torch
+
+            out = torch.empty(rows * d_model, dtype=torch.float32, device=inp.obj.device)
+        else:
+            out = np.zeros(rows * d_model, np.float32)
+    o = as_buf(out, np.float32, "out")
+    same_side(inp, o)
+    ctx = gate.context
+    fn = ctx.lib.ovfq_ffn_swiglu_dev if inp.device else ctx.lib.ovfq_ffn_swiglu
+    raise_for_status(fn(ctx.handle, gate.handle, up.handle, down.handle, inp.ptr, rows, o.ptr), ctx.lib)
+    return out
+
+
 def moe_ffn(gate_experts, up_experts, down_experts, x, rows, top_k, expert_indices, expert_weights, out=None):
     """MoeFeedForwardBlock.DecodeBatched after routing (RT/MoeFeedForwardBlock.cs:140-241): tokens grouped by
     expert, each used expert's SwiGLU FFN on its tokens, weighted sum over the top-k slots in order."""

@@ -320,6 +320,42 @@ def _moe_check(y, ref, what):
     assert cos >= 0.99999 and err <= 1e-3 * scale, what
 
 
+@pytest.mark.parametrize("rows", [1, 5, 40])
+def test_ffn_swiglu_matches_oracle(orc, rows):
+    """The fused decode/prefill FFN (gate/up -> SiLU*up + Q8_K -> down) against the oracle's
+    DecodeSwiGluBatchedDispatched restatement: rows 1 (GEMV), 5 (small-M MFMA), 40 (prefill MFMA)."""
+    case("ffn swiglu", rows)
+    rng = np.random.default_rng(70 + rows)
+    dm, dff = 1024, 2048
+    gb, ub = orc.quantize_q4k(normal(rng, (dff, dm), 0.05)), orc.quantize_q4k(normal(rng, (dff, dm), 0.05))
+    db = orc.quantize_q6k(normal(rng, (dm, dff), 0.05))
+    g, u, d = ov.Q4KWeight(gb, dm, dff), ov.Q4KWeight(ub, dm, dff), ov.Q6KWeight(db, dff, dm)
+    x = normal(rng, (rows, dm))
+    ref = orc.swiglu_batched(x, rows, gb, ub, db, 12, 14, dm, dff)
+    y = ov.ffn_swiglu(g, u, d, t(x), rows)
+    torch.cuda.synchronize()
+    _moe_check(y.cpu().numpy(), ref, f"ffn rows={rows} device")
+    _moe_check(ov.ffn_swiglu(g, u, d, x, rows), ref, f"ffn rows={rows} host")
+
+
+def test_ffn_swiglu_llama3_full_size(orc):
+    """The Llama-3-8B FFN (gate/up 14336x4096 Q4_K, down 4096x14336 Q6_K) for one decode token."""
+    case("ffn llama3 full size")
+    gen = torch.Generator(device=DEV).manual_seed(90)
+    mats = {}
+    for name, (n, k, typ) in {"gate": (14336, 4096, ov.TYPE_Q4_K), "up": (14336, 4096, ov.TYPE_Q4_K),
+                              "down": (4096, 14336, ov.TYPE_Q6_K)}.items():
+        wf = torch.randn(n, k, generator=gen, device=DEV) * 0.02
+        b = ov.quantize_weight(wf, typ)
+        del wf
+        mats[name] = ((ov.Q6KWeight if typ == ov.TYPE_Q6_K else ov.Q4KWeight)(b, k, n), b.cpu().numpy())
+    x = normal(np.random.default_rng(91), (1, 4096))
+    y = ov.ffn_swiglu(mats["gate"][0], mats["up"][0], mats["down"][0], t(x), 1)
+    torch.cuda.synchronize()
+    ref = orc.swiglu_batched(x, 1, mats["gate"][1], mats["up"][1], mats["down"][1], 12, 14, 4096, 14336)
+    _moe_check(y.cpu().numpy(), ref, "ffn llama3")
+
+
 @pytest.mark.parametrize("gfmt,dfmt", [("q4k", "q6k"), ("q4k", "q4k"), ("q6k", "q6k")])
 def test_moe_ffn_matches_oracle(orc, gfmt, dfmt):
     case("moe ffn", gfmt, dfmt)
