@@ -327,6 +327,19 @@ def main():
                 "GB_s": round(wb / (us * 1e-6) / 1e9, 1), "pct_peak": round(100 * wb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 2),
                 "timing": "HIP graph replay over %d expert sets, per step" % n_sets}
 
+    def ffn_line():
+        """The fused decode FFN: gate/up -> SiLU*up + Q8_K -> down for one token, 3 launches, over the
+        layer copies (the down input is the SwiGLU output, unlike the config-2 step's independent input)."""
+        yf = torch.empty(4096, device=dev)
+        g = capture([(lambda ws=ws: ov.ffn_swiglu(ws["gate"], ws["up"], ws["down"], x_in["ffn"], 1, out=yf))
+                     for ws in copies] * 4)
+        us = replay_us(g, 4 * len(copies), 16)
+        wb = 2 * weight_bytes(14336, 4096, "q4k") + weight_bytes(4096, 14336, "q6k")
+        del g
+        return {"what": "fused SwiGLU decode FFN (Llama-3-8B: gate/up Q4_K, down Q6_K), one token, 3 launches",
+                "us": round(us, 2), "weight_bytes": wb, "GB_s": round(wb / (us * 1e-6) / 1e9, 1),
+                "timing": "HIP graph replay over %d layer copies x 4" % len(copies)}
+
     if args.profile in ("prefill", "moe"):
         print(json.dumps(prefill_line() if args.profile == "prefill" else moe_line()), flush=True)
         return
@@ -376,6 +389,7 @@ def main():
     config3 = prefill_line()
     config4 = model_line()
     config5 = moe_line()
+    ffn = ffn_line()
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -408,6 +422,7 @@ def main():
         "config3_prefill_m512": config3,
         "config4_32_layers_lm_head": config4,
         "config5_moe_mixtral_16tok_top2": config5,
+        "ffn_swiglu_decode": ffn,
         "q4k_gemv_128256x4096": large_q4k,
         "q6k_lm_head_128256x4096": lm_head,
         "cpu_baseline": cpu,

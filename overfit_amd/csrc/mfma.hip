@@ -368,6 +368,36 @@ hipError_t launch_project_mfma(int type, const ProjJob* jobs, int njobs, int in,
     return nt == 128 ? launch_mfma<Q6KMfma, 128>(ma, st) : launch_mfma<Q6KMfma, 64>(ma, st);
 }
 
+// The 16 x 16 fp32 values of one super-block for the small-M kernel: MFMAs over the four 64-element chunks (A
+// operands av[t] already in the weight operands' K order), then the reference's fp32 tail per (row 4g+j, output
+// r16); `q8s` is the q8 scale of activation row lane % 16.
+template <class F>
+__device__ __forceinline__ void lohi_block_values(const typename F::W& w, const u32x4 (&av)[4], int g, float q8s,
+                                                  float (&v)[4]) {
+    i32x4 op[4][F::kNumMfma];
+    F::template operands<0>(w, g, op[0]);
+    F::template operands<1>(w, g, op[1]);
+    F::template operands<2>(w, g, op[2]);
+    F::template operands<3>(w, g, op[3]);
+    i32x4 acc[F::kNumMfma];
+#pragma unroll
+    for (int k = 0; k < F::kNumMfma; k++) acc[k] = i32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const i32x4 aop = i32x4{(int)av[t].x, (int)av[t].y, (int)av[t].z, (int)av[t].w};
+#pragma unroll
+        for (int k = 0; k < F::kNumMfma; k++) acc[k] = mfma16(aop, op[t][k], acc[k]);
+    }
+    const float d = F::d_of(w), dmin = F::dmin_of(w);
+#pragma unroll
+    for (int j = 0; j < 4; j++) v[j] = F::tail(acc, j, d, dmin, __shfl(q8s, 4 * g + j, 64));
+}
+
+// Q4_K for the small-M kernel, where the operand build is paid once per 16 activation rows: the weight operand is
+// the raw nibble (<= 15, an int8) masked to one lane half, so each chunk's two MFMAs give one sub-block's
+// sum nib * q8 each; mainAcc = sum_s sc[s] * that is then formed with lane-local integer multiply-adds (the lane's
+// outputs all belong to its own weight row, whose scales it holds). The min term is the broadcast-min MFMA of
+// Q4KMfma. Same integers, same fp32 tail, so the values are identical to the lo/hi form.
 // ------------------------------------------------------------------------------------------ small M
 // Few activation rows (M <= 16 per tile; MoE experts' token groups): one workgroup owns 16 weight rows and its
 // four waves split the row's super-blocks (wave w takes w, w+4, ...), so a 4096-row matrix already gives 1024
@@ -449,25 +479,8 @@ __global__ __launch_bounds__(256) void kquant_mfma_small_kernel(const SArgs a) {
                 // Every slot of the batch is computed (so the batch's loads stay ahead of all of its math); a
                 // slot past the row only skips its store.
                 const int sb = sb0 + 4 * i;
-                i32x4 op[4][F::kNumMfma];
-                F::template operands<0>(w[i], g, op[0]);
-                F::template operands<1>(w[i], g, op[1]);
-                F::template operands<2>(w[i], g, op[2]);
-                F::template operands<3>(w[i], g, op[3]);
-                i32x4 acc[F::kNumMfma];
-#pragma unroll
-                for (int k = 0; k < F::kNumMfma; k++) acc[k] = i32x4{0, 0, 0, 0};
-#pragma unroll
-                for (int t = 0; t < 4; t++) {
-                    const i32x4 aop = i32x4{(int)av[i][t].x, (int)av[i][t].y, (int)av[i][t].z, (int)av[i][t].w};
-#pragma unroll
-                    for (int k = 0; k < F::kNumMfma; k++) acc[k] = mfma16(aop, op[t][k], acc[k]);
-                }
-                const float d = F::d_of(w[i]), dmin = F::dmin_of(w[i]);
-                const float sc = as_float(sv[i]);  // q8 scale of row r16; rows 4g+i are needed below
                 float v[4];
-#pragma unroll
-                for (int j = 0; j < 4; j++) v[j] = F::tail(acc, j, d, dmin, __shfl(sc, 4 * g + j, 64));
+                lohi_block_values<F>(w[i], av[i], g, as_float(sv[i]), v);  // sv: q8 scale of activation row r16
                 if (sb < spr) {
                     float* vrow = vals + sb * 256;
 #pragma unroll
