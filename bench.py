@@ -1,6 +1,6 @@
 """Benchmark of the GGUF quantized-linear decode path on one MI355X.
 
-Workload ("the metric's configuration"): one Llama-3-8B-shaped layer's decode projections
+Workload (benchmark config 2, "the metric's configuration"): one Llama-3-8B-shaped layer's decode projections
 at M = 1 with the Q4_K_M mix — q 4096x4096, k/v 1024x4096, o 4096x4096, gate/up 14336x4096 in Q4_K, down
 4096x14336 in Q6_K. Weights N(0, 0.02) from a seed, quantised on the device with the reference quantizer
 (GgmlQuant.QuantizeQ4_K) and the library's Q6_K encoder; activations N(0, 1) fp32, resident in HBM.
@@ -13,7 +13,7 @@ To measure HBM rather than the 256 MB Infinity Cache, steps rotate over several 
 + fp32 outputs), in GB/s; decode_proj_tok_s = steps per second.
 
 Also reported: the dominant kernel's roofline (the fused gate/up Q4_K GEMV, per-launch HIP-event timing on
-the stream it runs on), BASELINE config 1 (a single Q4_K 4096x4096 GEMV rotated over 64 copies), config 3
+the stream it runs on), benchmark config 1 (a single Q4_K 4096x4096 GEMV rotated over 64 copies), config 3
 (the layer at M = 512 on int8 MFMA, with its MFMA roofline), config 4 (32 distinct layers + the Q6_K LM head,
 one token's projections), config 5 (a Mixtral-shaped routed MoE step of 16 tokens), and the CPU baseline (the AVX2 C restatement of the reference's CPU path, on a
 bounded sample, rank 0 only).
@@ -132,8 +132,8 @@ def main():
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py: this build measures one GPU only (the path shards by output rows across GPUs, see "
-              "DESIGN.md); run with --gpus 1", file=sys.stderr)
+        print("bench.py: this build measures one GPU only (the path would shard by output rows across GPUs); "
+              "run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
@@ -224,7 +224,7 @@ def main():
                 "copies": n_copies, "what": label}
 
     def prefill_line(m=512, n_layers=2):
-        """the layer's seven projections at M = m rows on the int8-MFMA kernel, in four launches
+        """benchmark config 3: the layer's seven projections at M = m rows on the int8-MFMA kernel, in four launches
         (fused q/k/v, o, fused gate/up, down; each quantises its fp32 input to Q8_K first), graph-replayed over
         n_layers weight copies."""
         gen2 = torch.Generator(device="cuda:0").manual_seed(9)
@@ -244,7 +244,7 @@ def main():
         tops = ops / (us * 1e-6) / 1e12
         del g, xp, yp
         torch.cuda.empty_cache()
-        return {"what": "BASELINE config 3: Llama-3-8B layer projections at M=%d (prefill) on int8 MFMA" % m,
+        return {"what": "benchmark config 3: Llama-3-8B layer projections at M=%d (prefill) on int8 MFMA" % m,
                 "us_per_layer": round(us, 2), "tokens_per_s": round(m / (us * 1e-6), 1),
                 "useful_TOPS": round(tops, 1),
                 "roofline": {"bound": "mfma", "achieved": round(tops, 1), "peak": INT8_PEAK_TOPS, "unit": "TOPS",
@@ -254,7 +254,7 @@ def main():
                 "timing": "HIP graph replay of the 4 launches x %d layer copies, per layer" % n_layers}
 
     def model_line(n_layers=32):
-        """one decode token's projections through n_layers distinct Q4_K_M layers plus the
+        """benchmark config 4: one decode token's projections through n_layers distinct Q4_K_M layers plus the
         Q6_K 128256x4096 LM head (RMSNorm / RoPE / attention stay on the host path and are not timed)."""
         layers = copies + [make_layer(ov, torch, 2000 + i) for i in range(n_layers - len(copies))]
         gen3 = torch.Generator(device="cuda:0").manual_seed(4)
@@ -284,14 +284,14 @@ def main():
         w = n_layers * layer_algorithmic_bytes()[0] + weight_bytes(128256, 4096, "q6k")
         del g, layers[len(copies):], head
         torch.cuda.empty_cache()
-        return {"what": "BASELINE config 4: %d Llama-3-8B Q4_K_M layers + Q6_K LM head, one decode token, "
+        return {"what": "benchmark config 4: %d Llama-3-8B Q4_K_M layers + Q6_K LM head, one decode token, "
                         "projections only (%d launches)" % (n_layers, 4 * n_layers + 1),
                 "weight_bytes": w, "eager_us": round(eager_us, 1), "graph_us": round(graph_us, 1),
                 "proj_tok_s_eager": round(1e6 / eager_us, 1), "proj_tok_s_graph": round(1e6 / graph_us, 1),
                 "GB_s_graph": round(w / (graph_us * 1e-6) / 1e9, 1)}
 
     def moe_line(n_sets=2, tokens=16, top_k=2, n_experts=8):
-        """Mixtral-8x7B-shaped experts (gate/up 14336x4096, down 4096x14336, Q4_K), 16 tokens
+        """benchmark config 5: Mixtral-8x7B-shaped experts (gate/up 14336x4096, down 4096x14336, Q4_K), 16 tokens
         routed top-2 on the device from seeded U[0,1) logits, grouped per-expert SwiGLU; graph-replayed over
         n_sets independent expert sets (> 1.5 GB, past the 256 MB cache)."""
         gen4 = torch.Generator(device="cuda:0").manual_seed(15)
@@ -321,14 +321,14 @@ def main():
         wb = used * (2 * weight_bytes(14336, 4096, "q4k") + weight_bytes(4096, 14336, "q4k"))
         del g, sets
         torch.cuda.empty_cache()
-        return {"what": "BASELINE config 5: Mixtral-8x7B experts (Q4_K gate/up/down), 16 tokens, top-2, one MoE "
+        return {"what": "benchmark config 5: Mixtral-8x7B experts (Q4_K gate/up/down), 16 tokens, top-2, one MoE "
                         "step (route + group + 2 grouped projections + SwiGLU + combine, 7 launches)",
                 "us": round(us, 1), "experts_used": used, "weight_bytes": wb,
                 "GB_s": round(wb / (us * 1e-6) / 1e9, 1), "pct_peak": round(100 * wb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 2),
                 "timing": "HIP graph replay over %d expert sets, per step" % n_sets}
 
     def ffn_line():
-        """The fused decode FFN (SURVEY 8f): gate/up -> SiLU*up + Q8_K -> down for one token, 3 launches, over the
+        """The fused decode FFN: gate/up -> SiLU*up + Q8_K -> down for one token, 3 launches, over the
         layer copies (the down input is the SwiGLU output, unlike the config-2 step's independent input)."""
         yf = torch.empty(4096, device=dev)
         g = capture([(lambda ws=ws: ov.ffn_swiglu(ws["gate"], ws["up"], ws["down"], x_in["ffn"], 1, out=yf))
@@ -383,7 +383,7 @@ def main():
                 "avg_us": round(gu_avg, 3), "algorithmic_bytes": gu_bytes,
                 "timing": "HIP graph replay of 4x%d launches over %d weight copies, /launch" % (len(copies), len(copies))}
 
-    config1 = gemv_line(4096, 4096, "q4k", 64, "BASELINE config 1: Q4_K 4096x4096 GEMV (quantise in-launch)")
+    config1 = gemv_line(4096, 4096, "q4k", 64, "benchmark config 1: Q4_K 4096x4096 GEMV (quantise in-launch)")
     large_q4k = gemv_line(128256, 4096, "q4k", 2, "Q4_K GEMV at LM-head size (asymptotic efficiency)")
     lm_head = gemv_line(128256, 4096, "q6k", 2, "Llama-3-8B Q6_K LM head 128256x4096 (config 4)")
     config3 = prefill_line()
@@ -409,7 +409,7 @@ def main():
         "vs_baseline": None,
         "dtype": "int8",
         "data": "synthetic (seeded N(0,0.02) weights quantised on device; N(0,1) fp32 activations)",
-        "config": {"workload": "llama3-8b layer decode projections, M=1, Q4_K_M mix (BASELINE config 2)",
+        "config": {"workload": "llama3-8b layer decode projections, M=1, Q4_K_M mix (benchmark config 2)",
                    "hidden": 4096, "ffn": 14336, "kv_rows": 1024, "formats": "Q4_K q,k,v,o,gate,up + Q6_K down",
                    "weight_bytes_per_step": w_bytes, "algorithmic_bytes_per_step": alg_bytes,
                    "layer_copies_rotated": args.copies},
