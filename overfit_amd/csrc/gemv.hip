@@ -154,8 +154,10 @@ __global__ __launch_bounds__(256) void kquant_gemv_kernel(const GArgs a) {
         const uint64_t base_off = (uint64_t)row0 * row_bytes;
         const uint64_t al = base_off & ~3ull;
         const uint32_t extra = (uint32_t)(base_off & 3ull);
-        const __amdgpu_buffer_rsrc_t wr =
-            make_rsrc(a.job[j].w + al, valid ? rsrc_bytes((uint64_t)a.job[j].n_rows * row_bytes, al) : 0u);
+        // The resource ends with the row group's last block: quads past the last super-block of a short final
+        // chunk then read nothing (instead of the next row's blocks). No block read uses bytes past its block.
+        const uint64_t end = (uint64_t)min(row0 + R, a.job[j].n_rows) * row_bytes;
+        const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.job[j].w + al, valid ? rsrc_bytes(end, al) : 0u);
         const uint32_t sb = (uint32_t)(c * 16 + q);
 #pragma unroll
         for (int r = 0; r < R; r++) it.w[r] = F::load_w(wr, extra + r * row_bytes + sb * F::kBytes, t);

@@ -4,8 +4,9 @@
 // y[n][o] = biasO + sum over super-blocks (ascending) of the block's fp32 value, for every activation row n.
 //
 // Exactness. Everything before the per-super-block fp32 tail is integer arithmetic, so it can be regrouped:
-//  Q4_K  mainAcc = sum_e (sc*nib)_e * q8_e. sc*nib <= 945 does not fit int8, so it is split as 128*hi + lo
-//        (lo in [0,127], hi in [0,7]); two MFMAs give sum lo*q8 and sum hi*q8, mainAcc = acc_lo + (acc_hi << 7).
+//  Q4_K  mainAcc = sum_e (sc*nib)_e * q8_e. sc*nib <= 945 does not fit int8, so the scale is split as
+//        sc = 8*sc_hi + sc_lo (both in [0,7]); the operands sc_lo*nib and sc_hi*nib are <= 105, two MFMAs give
+//        sum lo*q8 and sum hi*q8, mainAcc = acc_lo + (acc_hi << 3).
 //        minAcc = sum_s m_s * (bsums[2s] + bsums[2s+1]) = sum_e m_{s(e)} * q8_e: a third MFMA whose weight operand
 //        is the sub-block min broadcast over its 32 elements.
 //  Q6_K  unsignedTerm - 32*bsumTerm = sum_e sc_{s(e)} * (q_e - 32) * q8_e. W = sc*(q-32) lies in [-4064, 4096]
@@ -112,13 +113,16 @@ struct Q4KMfma {
         const u32x4 src = w.q[T & 1];
         const uint32_t qv[4] = {src.x, src.y, src.z, src.w};
         constexpr uint32_t kShift = (T >> 1) * 4;
+        // sc = 8*sc_hi + sc_lo with both parts in [0, 7]: sc_lo*nib and sc_hi*nib are <= 105, so one packed 16-bit
+        // multiply of the four nibble bytes gives the four byte products with no carry between bytes.
+        const unsigned short sl = (unsigned short)(sc & 7u), sh = (unsigned short)(sc >> 3);
+        const u16x2 sl2 = {sl, sl}, sh2 = {sh, sh};
         uint32_t lo[4], hi[4];
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            const uint32_t v = qv[k] >> kShift;
-            const uint32_t pe = __umul24(v & 0x000f000fu, sc);          // sc * nibble of K bytes 0, 2 (<= 945)
-            const uint32_t po = __umul24((v >> 8) & 0x000f000fu, sc);   // K bytes 1, 3
-            split_lo_hi(pe, po, lo[k], hi[k]);
+            const u16x2 nib = __builtin_bit_cast(u16x2, (qv[k] >> kShift) & 0x0f0f0f0fu);
+            lo[k] = __builtin_bit_cast(uint32_t, nib * sl2);
+            hi[k] = __builtin_bit_cast(uint32_t, nib * sh2);
         }
         op[0] = i32x4{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3]};
         op[1] = i32x4{(int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
@@ -130,7 +134,7 @@ struct Q4KMfma {
     // q8Scale * (d * mainAcc - dmin * minAcc)   (RT/Q4KDotKernel.cs:944)
     __device__ __forceinline__ static float tail(const i32x4 (&acc)[kNumMfma], int i, float d, float dmin,
                                                  float q8s) {
-        const int main_acc = acc[0][i] + (acc[1][i] << 7);
+        const int main_acc = acc[0][i] + (acc[1][i] << 3);
         return q8s * (d * (float)main_acc - dmin * (float)acc[2][i]);
     }
 };
@@ -393,11 +397,6 @@ __device__ __forceinline__ void lohi_block_values(const typename F::W& w, const 
     for (int j = 0; j < 4; j++) v[j] = F::tail(acc, j, d, dmin, __shfl(q8s, 4 * g + j, 64));
 }
 
-// Q4_K for the small-M kernel, where the operand build is paid once per 16 activation rows: the weight operand is
-// the raw nibble (<= 15, an int8) masked to one lane half, so each chunk's two MFMAs give one sub-block's
-// sum nib * q8 each; mainAcc = sum_s sc[s] * that is then formed with lane-local integer multiply-adds (the lane's
-// outputs all belong to its own weight row, whose scales it holds). The min term is the broadcast-min MFMA of
-// Q4KMfma. Same integers, same fp32 tail, so the values are identical to the lo/hi form.
 // ------------------------------------------------------------------------------------------ small M
 // Few activation rows (M <= 16 per tile; MoE experts' token groups): one workgroup owns 16 weight rows and its
 // four waves split the row's super-blocks (wave w takes w, w+4, ...), so a 4096-row matrix already gives 1024
