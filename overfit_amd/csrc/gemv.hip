@@ -138,32 +138,49 @@ __global__ __launch_bounds__(256) void kquant_gemv_kernel(const GArgs a) {
         uint32_t bias;
     };
 
-    // Job and first row of row group g (wave-uniform).
-    auto locate = [&](int g, int& j, int& row0) {
-        j = 0;
+    // Job fields and first row of row group g (wave-uniform). Every job field is read with a compile-time index
+    // and chosen by select, so the table stays in scalar registers: indexing it with a run-time job number would
+    // re-read the kernel arguments through scalar memory (a dependent wait) for every item.
+    struct Cur {
+        const uint8_t* w;
+        const float* bias;
+        float* y;
+        int n_rows;
+        int row0;
+    };
+    auto locate = [&](int g) -> Cur {
+        Cur c{a.job[0].w, a.job[0].bias, a.job[0].y, a.job[0].n_rows, a.job[0].g_begin};
 #pragma unroll
-        for (int i = 1; i < kMaxJobs; i++) j = (i < a.njobs && g >= a.job[i].g_begin) ? i : j;
-        row0 = (g - a.job[j].g_begin) * R;
+        for (int i = 1; i < kMaxJobs; i++) {
+            const bool take = i < a.njobs && g >= a.job[i].g_begin;
+            c.w = take ? a.job[i].w : c.w;
+            c.bias = take ? a.job[i].bias : c.bias;
+            c.y = take ? a.job[i].y : c.y;
+            c.n_rows = take ? a.job[i].n_rows : c.n_rows;
+            c.row0 = take ? a.job[i].g_begin : c.row0;
+        }
+        c.row0 = (g - c.row0) * R;
+        return c;
     };
     // Issues the loads of item (g, c). The instruction stream is the same whether or not the item exists (past
     // the end the resources have zero length, so the loads return 0 without touching memory): the compiler's
     // wait counts then see a fixed number of younger loads and the prefetch overlaps the current item's math.
     auto load_item = [&](int g, int c, bool valid, Item& it) {
-        int j, row0;
-        locate(valid ? g : 0, j, row0);
+        const Cur jb = locate(valid ? g : 0);
+        const int row0 = jb.row0;
         const uint64_t base_off = (uint64_t)row0 * row_bytes;
         const uint64_t al = base_off & ~3ull;
         const uint32_t extra = (uint32_t)(base_off & 3ull);
         // The resource ends with the row group's last block: quads past the last super-block of a short final
         // chunk then read nothing (instead of the next row's blocks). No block read uses bytes past its block.
-        const uint64_t end = (uint64_t)min(row0 + R, a.job[j].n_rows) * row_bytes;
-        const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.job[j].w + al, valid ? rsrc_bytes(end, al) : 0u);
+        const uint64_t end = (uint64_t)min(row0 + R, jb.n_rows) * row_bytes;
+        const __amdgpu_buffer_rsrc_t wr = make_rsrc(jb.w + al, valid ? rsrc_bytes(end, al) : 0u);
         const uint32_t sb = (uint32_t)(c * 16 + q);
 #pragma unroll
         for (int r = 0; r < R; r++) it.w[r] = F::load_w(wr, extra + r * row_bytes + sb * F::kBytes, t);
-        const float* bias = a.job[j].bias;
+        const float* bias = jb.bias;
         const bool want_bias = valid && bias != nullptr && c == nchunks - 1;
-        const __amdgpu_buffer_rsrc_t bsr = make_rsrc(bias, want_bias ? (uint32_t)a.job[j].n_rows * 4 : 0u);
+        const __amdgpu_buffer_rsrc_t bsr = make_rsrc(bias, want_bias ? (uint32_t)jb.n_rows * 4 : 0u);
         it.bias = ld1(bsr, (uint32_t)(row0 + (lane < R ? lane : 0)) * 4);
     };
 
@@ -204,11 +221,10 @@ __global__ __launch_bounds__(256) void kquant_gemv_kernel(const GArgs a) {
         }
         wave_sync();
         if (c == nchunks - 1) {
-            int j, row0;
-            locate(g, j, row0);
-            if (lane < R && row0 + lane < a.job[j].n_rows) {
+            const Cur jb = locate(g);
+            if (lane < R && jb.row0 + lane < jb.n_rows) {
                 // bias[o] + sum (RT/Q4KDotKernel.cs:473); no add at all without a bias
-                a.job[j].y[row0 + lane] = a.job[j].bias ? as_float(cur.bias) + acc : acc;
+                jb.y[jb.row0 + lane] = jb.bias ? as_float(cur.bias) + acc : acc;
             }
             acc = 0.0f;
         }
