@@ -124,6 +124,13 @@ class Context:
             B = (ctypes.c_void_p * n)(*[None if b is None else b.data_ptr() for b in biases])
         self.check(self.lib.ovfq_project_multi_dev(self.handle, n, W, x.data_ptr(), rows, B, Y))
 
+    def bind_multi_dev(self, weights, x, ys, biases=None, rows=1):
+        """`project_multi_dev` with its arguments converted once: returns a callable that issues exactly
+        ovfq_project_multi_dev(ctx, n, weights, x, rows, biases, ys) on every call. For hot decode loops, where
+        rebuilding the pointer arrays each call costs more host time than the launch itself; the tensors are
+        held until the callable is dropped."""
+        return BoundMulti(self, weights, x, ys, biases, rows)
+
     def project_multi_prequantized_dev(self, weights, q, s, b, ys, biases=None, rows=1):
         n = len(weights)
         W = (ctypes.c_void_p * n)(*[w.handle.value for w in weights])
@@ -138,6 +145,31 @@ class Context:
         self.check(self.lib.ovfq_project_prequantized_dev(
             self.handle, weight.handle, q.data_ptr(), s.data_ptr(), None if b is None else b.data_ptr(), rows,
             None if bias is None else bias.data_ptr(), y.data_ptr()))
+
+
+class BoundMulti:
+    """A prepared ovfq_project_multi_dev call (see Context.bind_multi_dev)."""
+
+    __slots__ = ("_fn", "_args", "_ctx", "_keep")
+
+    def __init__(self, ctx, weights, x, ys, biases, rows):
+        n = len(weights)
+        if len(ys) != n or (biases is not None and len(biases) != n):
+            raise ValueError("weights, ys and biases must have the same length")
+        W = (ctypes.c_void_p * n)(*[w.handle.value for w in weights])
+        Y = (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys])
+        B = None
+        if biases is not None:
+            B = (ctypes.c_void_p * n)(*[None if b is None else b.data_ptr() for b in biases])
+        self._ctx = ctx
+        self._fn = ctx.lib.ovfq_project_multi_dev
+        self._args = (ctx.handle, n, W, ctypes.c_void_p(x.data_ptr()), rows, B, Y)
+        self._keep = (list(weights), x, list(ys), None if biases is None else list(biases))
+
+    def __call__(self):
+        rc = self._fn(*self._args)
+        if rc:
+            self._ctx.check(rc)
 
 
 _default = {}

@@ -227,6 +227,29 @@ def test_multi_projection_rows_bit_exact(orc, ctx, rows):
         assert_bit_exact(y.cpu().numpy().reshape(rows, -1), ref, f"multi prequantized rows={rows} job {i}")
 
 
+def test_bound_multi_call_matches_oracle(orc, ctx):
+    """A prepared multi-projection call (pointer arrays built once) replayed over new inputs: every call reads the
+    bound tensors' current contents and is bit-exact, with and without a bias, M = 1 (decode GEMV) and M = 3."""
+    case("bound multi", 0)
+    rng = np.random.default_rng(77)
+    k, shapes = 4096, [256, 64]
+    blocks = [_kq_blocks(rng, "q4k", n, k) for n in shapes]
+    ws = [ov.Q4KWeight(b, k, n) for b, n in zip(blocks, shapes)]
+    bias = normal(rng, shapes[1])
+    for rows in (1, 3):
+        xd = torch.empty(rows * k, device=DEV)
+        ys = [torch.empty(rows * n, device=DEV) for n in shapes]
+        call = ctx.bind_multi_dev(ws, xd, ys, [None, t(bias)], rows=rows)
+        for rep in range(3):
+            x = normal(rng, (rows, k))
+            xd.copy_(t(x).reshape(-1))
+            call()
+            torch.cuda.synchronize()
+            for i, (y, b, n) in enumerate(zip(ys, blocks, shapes)):
+                ref = orc.q4k_project_batched(x, rows, b, k, n, bias if i == 1 else None)
+                assert_bit_exact(y.cpu().numpy().reshape(rows, n), ref, f"bound rows={rows} rep={rep} job {i}")
+
+
 # ------------------------------------------------------------------------------------------------ GGUF upload
 
 @pytest.mark.parametrize("on_device", [False, True])
