@@ -160,12 +160,12 @@ def main():
                 ctx.bind_multi_dev([ws["gate"], ws["up"]], x_in["ffn"], [ys["gate"], ys["up"]]),
                 ctx.bind_multi_dev([ws["down"]], x_in["down"], [ys["down"]]))
 
-    for ws in copies:
-        ws["_step"] = bind_step(ws)
-
     def step(ws):
         # four launches: each quantises its fp32 activation to Q8_K in-kernel, then runs its projection(s)
-        for call in ws["_step"]:
+        calls = ws.get("_step")
+        if calls is None:
+            calls = ws["_step"] = bind_step(ws)
+        for call in calls:
             call()
 
     # Warm up eagerly (allocates any scratch), time K eager steps, then also capture one rotation over the layer
