@@ -44,3 +44,21 @@ def set_subnormal_scales(blocks, every=7, q6=False):
 
 def normal(rng, shape, sigma=1.0):
     return (rng.standard_normal(shape) * sigma).astype(np.float32)
+
+
+def q8_0_gguf_blocks(scales, quants):
+    """GGUF Q8_0 blocks as a file stores them: fp16 scale, then 32 int8 quants."""
+    nb = len(scales)
+    blocks = np.zeros((nb, 34), np.uint8)
+    blocks[:, 0:2] = np.asarray(scales, np.float16).view(np.uint8).reshape(nb, 2)
+    blocks[:, 2:] = np.asarray(quants, np.int8).reshape(nb, 32).view(np.uint8)
+    return blocks
+
+
+# GgmlDequantTests.Q8_0_DequantizesSingleBlock_RoundTrip (TL/Loading/GgmlDequantTests.cs:20-46): scale 2.0, quants
+# -128, -1, 0, 1, 127, then i - 16; Q8_0_DequantizesMultipleBlocks_DifferentScales (:48-78): scales 0.5, 1, 0.125,
+# quant b * 10 + i - 5 for element i of block b.
+Q8_0_KATS = [
+    ([2.0], np.array([-128, -1, 0, 1, 127] + [i - 16 for i in range(5, 32)], np.int8)),
+    ([0.5, 1.0, 0.125], np.array([b * 10 + i - 5 for b in range(3) for i in range(32)], np.int8)),
+]

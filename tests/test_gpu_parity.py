@@ -10,7 +10,7 @@ import sys
 import numpy as np
 import pytest
 
-from qdata import normal, random_q4k_blocks, random_q6k_blocks, set_subnormal_scales
+from qdata import Q8_0_KATS, normal, q8_0_gguf_blocks, random_q4k_blocks, random_q6k_blocks, set_subnormal_scales
 
 pytestmark = pytest.mark.gpu
 
@@ -251,6 +251,24 @@ def test_bound_multi_call_matches_oracle(orc, ctx):
 
 
 # ------------------------------------------------------------------------------------------------ GGUF upload
+
+@pytest.mark.parametrize("on_device", [False, True])
+def test_gguf_q8_0_known_answer_blocks(orc, on_device):
+    """The reference's Q8_0 dequant KATs (TL/Loading/GgmlDequantTests.cs:20-94) through the GGUF upload and
+    DecodeRow: scale * quant for a block with -128 and 127 at scale 2 and for three blocks with their own scales;
+    an input size that is not a multiple of 32 is rejected before any device work."""
+    case("gguf q8_0 kats", on_device)
+    for scales, quants in Q8_0_KATS:
+        k = 32 * len(scales)
+        blocks = q8_0_gguf_blocks(scales, quants)
+        w = ov.load_gguf_tensor(ov.TYPE_Q8_0, t(blocks) if on_device else blocks, k, 1)
+        dst = np.zeros(k, np.float32)
+        w.DecodeRow(0, dst)
+        expected = np.repeat(np.asarray(scales, np.float32), 32) * quants.astype(np.float32)
+        assert_bit_exact(dst, expected, f"q8_0 kat k={k}")
+    with pytest.raises(ov.OverfitArgumentError, match="32"):
+        ov.load_gguf_tensor(ov.TYPE_Q8_0, np.zeros(34, np.uint8), 31, 1)
+
 
 @pytest.mark.parametrize("on_device", [False, True])
 def test_gguf_upload_q8_0_q4k_q6k(orc, on_device):
@@ -503,7 +521,7 @@ def test_llama3_8b_layer_prefill_sampled_rows(orc):
 
 
 @pytest.mark.parametrize("k,n", [(32, 5), (128, 4096), (4096, 300), (14336, 40)])
-@pytest.mark.parametrize("rows", [1, 3])
+@pytest.mark.parametrize("rows", [1, 2, 3, 7, 16])
 def test_q8_0_project_bit_exact(orc, k, n, rows):
     case("q8_0 project", k, n, rows)
     rng = np.random.default_rng(k + n + rows)

@@ -8,7 +8,7 @@ fp16 conversions), by brute force on small inputs, and by identities chosen so t
 import numpy as np
 import pytest
 
-from qdata import half_bits, normal, random_q4k_blocks, random_q6k_blocks
+from qdata import Q8_0_KATS, half_bits, normal, q8_0_gguf_blocks, random_q4k_blocks, random_q6k_blocks
 
 
 # ------------------------------------------------------------------------------------------------ fp16
@@ -507,6 +507,21 @@ def test_q8_0_deinterleave_round_trip(orc):
     ref = bits.view(np.float16).astype(np.float32)
     finite = ~np.isnan(ref)
     assert np.array_equal(gs[finite].view(np.uint32), ref[finite].view(np.uint32))
+
+
+def test_q8_0_gguf_dequant_kats(orc):
+    """LoadTensorQ8_0Raw on the reference's two Q8_0 known-answer blocks: the planes hold the quants and the exactly
+    widened scales, so dequantised values are scale * quant: -256 and 254 for -128 and 127 at scale 2."""
+    for scales, quants in Q8_0_KATS:
+        q, s = orc.q8_0_deinterleave(q8_0_gguf_blocks(scales, quants))
+        assert np.array_equal(q, quants)
+        assert s.tolist() == scales
+        deq = np.repeat(s, 32) * q.astype(np.float32)
+        for b, sc in enumerate(scales):
+            for i in (0, 1, 4, 31):
+                assert deq[32 * b + i] == sc * int(quants[32 * b + i])
+    q, s = orc.q8_0_deinterleave(q8_0_gguf_blocks(*Q8_0_KATS[0]))
+    assert (np.repeat(s, 32) * q.astype(np.float32))[[0, 1, 2, 3, 4]].tolist() == [-256.0, -2.0, 0.0, 2.0, 254.0]
 
 
 # ------------------------------------------------------------------------------------------------ MoE FFN
