@@ -482,6 +482,24 @@ def _extreme_blocks(fmt, n, k):
 
 
 @pytest.mark.parametrize("fmt", ["q4k", "q6k"])
+@pytest.mark.parametrize("rows", [1, 3, 40])
+def test_kquant_long_rows_bit_exact(orc, fmt, rows):
+    """K = 28672 (a Llama-3-70B down projection row: 112 super-blocks, past the decode GEMV's LDS-staged activation
+    and the small-M kernel's limit): every row count takes its path and stays bit-exact, with a bias."""
+    case("long rows", fmt, rows)
+    rng = np.random.default_rng(rows + (7 if fmt == "q6k" else 0))
+    k, n = 28672, 40
+    blocks = _kq_blocks(rng, fmt, n, k)
+    w = (ov.Q4KWeight if fmt == "q4k" else ov.Q6KWeight)(blocks, k, n)
+    x = normal(rng, (rows, k))
+    bias = normal(rng, n)
+    batched = orc.q4k_project_batched if fmt == "q4k" else orc.q6k_project_batched
+    ref = batched(x, rows, blocks, k, n, bias)
+    y = ov.project(w, x, bias, rows=rows).reshape(rows, n)
+    assert_bit_exact(y, ref, f"{fmt} K={k} rows={rows}")
+
+
+@pytest.mark.parametrize("fmt", ["q4k", "q6k"])
 def test_kquant_prefill_range_extremes(orc, fmt):
     case("prefill extremes", fmt)
     rows, k, n = 48, 1024, 64
