@@ -77,53 +77,76 @@ __global__ __launch_bounds__(64) void moe_topk_kernel(const float* __restrict__ 
 // One workgroup. Expert e's pairs are the tokens n (ascending) with a slot j such that idx[n][j] == e (the first
 // such slot: RT/MoeFeedForwardBlock.cs:191-204). A slot whose expert is out of range, or repeats an earlier slot's
 // expert, belongs to no pair (pair_of = -1) and contributes nothing to the combine.
-// The routing table is copied to LDS first (dynamic LDS of rows * k ints when it fits), so the per-expert scans
-// read LDS instead of issuing one dependent memory load per entry.
+// Tokens are taken 256 at a time, one per thread. For each expert a wave ballot of the tokens that claim it gives
+// the per-wave count and each token's rank among the wave's claimers (popcount of the lower lanes), so a pair's
+// position is expert_off[e] + (claimers of e in earlier chunks) + (in earlier waves of this chunk) + rank. The
+// routing table is staged in LDS when it fits (rows * k ints <= 48 KB).
 __global__ __launch_bounds__(256) void moe_plan_kernel(const int* __restrict__ idx_g, int rows, int k, int n_experts,
                                                        int* __restrict__ expert_off, int* __restrict__ pair_row,
                                                        int* __restrict__ pair_of, int staged) {
     extern __shared__ int sidx[];
-    __shared__ int cnt[kMaxExperts];
-    __shared__ int off[kMaxExperts + 1];
-    const int tid = threadIdx.x;
+    __shared__ int run[kMaxExperts];        // first position of the current chunk's claimers, per expert
+    __shared__ int wcnt[4][kMaxExperts];    // claimers per wave of the current chunk, per expert
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const uint64_t below = (1ull << lane) - 1ull;
     for (int i = tid; i < rows * k; i += blockDim.x) {
         pair_of[i] = -1;
         if (staged) sidx[i] = idx_g[i];
     }
+    if (tid < n_experts) run[tid] = 0;
     __syncthreads();
     const int* idx = staged ? sidx : idx_g;
-    if (tid < n_experts) {
-        int c = 0;
-        for (int n = 0; n < rows; n++)
-            for (int j = 0; j < k; j++)
-                if (idx[n * k + j] == tid) {
-                    c++;
-                    break;
-                }
-        cnt[tid] = c;
+    // first slot of token n holding expert e, or -1
+    auto claim_slot = [&](int n, int e) -> int {
+        if (n >= rows) return -1;
+        for (int j = 0; j < k; j++)
+            if (idx[n * k + j] == e) return j;
+        return -1;
+    };
+    // pass 1: claimers per expert
+    for (int c0 = 0; c0 < rows; c0 += 256) {
+        for (int e = 0; e < n_experts; e++) {
+            const uint64_t m = __ballot(claim_slot(c0 + tid, e) >= 0);
+            if (lane == 0) wcnt[wave][e] = __popcll(m);
+        }
+        __syncthreads();
+        if (tid < n_experts) run[tid] += wcnt[0][tid] + wcnt[1][tid] + wcnt[2][tid] + wcnt[3][tid];
+        __syncthreads();
     }
-    __syncthreads();
     if (tid == 0) {
         int acc = 0;
         for (int e = 0; e < n_experts; e++) {
-            off[e] = acc;
+            const int c = run[e];
+            run[e] = acc;
             expert_off[e] = acc;
-            acc += cnt[e];
+            acc += c;
         }
-        off[n_experts] = acc;
         expert_off[n_experts] = acc;
     }
     __syncthreads();
-    if (tid < n_experts) {
-        int p = off[tid];
-        for (int n = 0; n < rows; n++)
-            for (int j = 0; j < k; j++)
-                if (idx[n * k + j] == tid) {
-                    pair_row[p] = n;
-                    pair_of[n * k + j] = p;
-                    p++;
-                    break;
-                }
+    // pass 2: positions, tokens ascending within each expert
+    for (int c0 = 0; c0 < rows; c0 += 256) {
+        const int n = c0 + tid;
+        for (int e = 0; e < n_experts; e++) {
+            const int j = claim_slot(n, e);
+            const uint64_t m = __ballot(j >= 0);
+            if (lane == 0) wcnt[wave][e] = __popcll(m);
+            if (j >= 0) pair_of[n * k + j] = __popcll(m & below);  // rank within the wave, completed below
+        }
+        __syncthreads();
+        if (n < rows) {
+            for (int j = 0; j < k; j++) {
+                const int e = idx[n * k + j];
+                if (e < 0 || e >= n_experts || claim_slot(n, e) != j) continue;
+                int p = run[e] + pair_of[n * k + j];
+                for (int w = 0; w < wave; w++) p += wcnt[w][e];
+                pair_of[n * k + j] = p;
+                pair_row[p] = n;
+            }
+        }
+        __syncthreads();
+        if (tid < n_experts) run[tid] += wcnt[0][tid] + wcnt[1][tid] + wcnt[2][tid] + wcnt[3][tid];
+        __syncthreads();
     }
 }
 

@@ -429,6 +429,29 @@ def test_moe_ffn_matches_oracle(orc, gfmt, dfmt):
     _moe_check(ov.moe_ffn(gw, uw, dw, x, rows, k, idx2, w), ref2, f"{gfmt}/{dfmt} sparse routing")
 
 
+def test_moe_ffn_many_tokens(orc):
+    """A prefill-sized MoE batch: 300 tokens (more than one 256-token grouping chunk), top-3 of 8 experts, with a
+    repeated expert in one token's slots, an out-of-range expert id and an expert no token chose."""
+    case("moe ffn many tokens", 300)
+    rng = np.random.default_rng(300)
+    E, dm, dff, rows, k = 8, 256, 512, 300, 3
+    gb = [orc.quantize_q4k(normal(rng, (dff, dm), 0.05)) for _ in range(E)]
+    ub = [orc.quantize_q4k(normal(rng, (dff, dm), 0.05)) for _ in range(E)]
+    db = [orc.quantize_q6k(normal(rng, (dm, dff), 0.05)) for _ in range(E)]
+    gw = [ov.Q4KWeight(b, dm, dff) for b in gb]
+    uw = [ov.Q4KWeight(b, dm, dff) for b in ub]
+    dw = [ov.Q6KWeight(b, dff, dm) for b in db]
+    x = normal(rng, (rows, dm))
+    idx = np.stack([rng.choice(E - 1, k, replace=False) for _ in range(rows)]).astype(np.int32)  # expert 7 unused
+    idx[10, 2] = idx[10, 0]  # a repeated expert: only the first slot is a pair
+    idx[299, 1] = -1         # an out-of-range id: no pair
+    w = rng.random((rows, k)).astype(np.float32)
+    ref = orc.moe_ffn_batched(gb, ub, db, ov.TYPE_Q4_K, ov.TYPE_Q6_K, x, rows, dm, dff, k, idx, w)
+    y = ov.moe_ffn(gw, uw, dw, t(x), rows, k, t(idx), t(w))
+    torch.cuda.synchronize()
+    _moe_check(y.cpu().numpy(), ref, "300 tokens top-3")
+
+
 def test_moe_config5_full_size(orc):
     """8 Mixtral-shaped experts (gate/up 14336x4096, down 4096x14336, Q4_K), 16 tokens, top-2 of
     seeded uniform router logits, routed on the device; checked against the oracle's DecodeBatched restatement."""
