@@ -96,6 +96,15 @@ OVFQ_API int ovfq_weight_create_gguf(ovfq_ctx* ctx, int type, const void* gguf_b
 OVFQ_API int ovfq_weight_create_gguf_dev(ovfq_ctx* ctx, int type, const void* gguf_bytes, size_t nbytes,
                                          int input_size, int output_size, ovfq_weight** out);
 OVFQ_API int ovfq_weight_destroy(ovfq_weight* w);
+/* Opt-in MFMA-ready copy of a Q6_K weight, written on the device: for every 16 output rows and super-block, the
+ * int8 weight operands the batched (M >= 32) int8-MFMA kernel otherwise rebuilds from the GGUF bytes for every
+ * activation tile, plus the block scale. Batched projections whose weights all have it skip that build; outputs
+ * are bit-identical with or without it. Costs 8704 bytes per 16 rows and super-block (~2.5x the Q6_K bytes), freed
+ * with the weight; the GGUF blocks stay resident for decode. Idempotent. For a Q4_K weight the call succeeds and
+ * changes nothing (its operands are cheaper to build than to stream); other types: OVFQ_ERR_TYPE. The reference's
+ * counterpart is its opt-in repacked CPU layout (RT/Q4KRepack.cs, RT/Q6KRepack.cs): a load-time layout change
+ * trading memory for throughput. */
+OVFQ_API int ovfq_weight_prepare_mfma(ovfq_ctx* ctx, ovfq_weight* w);
 /* Shape/format query (InputSize / OutputSize / ByteCount of the weight classes). Any out pointer may be NULL.
  * `device_blocks` receives the HBM address of the resident blocks (the quant plane for Q8_0). */
 OVFQ_API int ovfq_weight_info(const ovfq_weight* w, int* type, int* input_size, int* output_size,

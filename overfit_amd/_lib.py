@@ -37,6 +37,7 @@ SIGNATURES = {
     "ovfq_weight_create": (ci, [vp, ci, vp, sz, vp, ci, ci, PP]),
     "ovfq_weight_create_from_device": (ci, [vp, ci, vp, sz, vp, ci, ci, PP]),
     "ovfq_weight_destroy": (ci, [vp]),
+    "ovfq_weight_prepare_mfma": (ci, [vp, vp]),
     "ovfq_weight_info": (ci, [vp, ctypes.POINTER(ci), ctypes.POINTER(ci), ctypes.POINTER(ci),
                               ctypes.POINTER(sz), PP]),
     "ovfq_weight_decode_row": (ci, [vp, vp, ci, vp]),

@@ -67,6 +67,7 @@ struct ovfq_weight {
     void* blocks = nullptr;  // Q4_K/Q6_K blocks or Q8_0 quant plane
     float* scales = nullptr; // Q8_0 scale plane
     size_t nbytes = 0;       // resident bytes (blocks + scales)
+    void* mfma = nullptr;    // MFMA-ready copy (ovfq_weight_prepare_mfma), or NULL
 };
 
 namespace {
@@ -207,6 +208,7 @@ int launch_projection(ovfq_ctx* c, const ovfq_weight* const* ws, int count, cons
         jobs[i].bias = biases ? biases[i] : nullptr;
         jobs[i].y = ys[i];
         jobs[i].n_rows = ws[i]->out;
+        jobs[i].pre = static_cast<const uint8_t*>(ws[i]->mfma);
     }
     const int type = ws[0]->type;
     const int in = ws[0]->in;
@@ -418,8 +420,35 @@ int ovfq_weight_destroy(ovfq_weight* w) {
         (void)hipStreamSynchronize(w->ctx->stream);
         if (w->blocks) (void)hipFree(w->blocks);
         if (w->scales) (void)hipFree(w->scales);
+        if (w->mfma) (void)hipFree(w->mfma);
     }
     delete w;
+    return ok();
+}
+
+int ovfq_weight_prepare_mfma(ovfq_ctx* ctx, ovfq_weight* w) {
+    if (!ctx) return fail(OVFQ_ERR_NULL, "ctx is NULL");
+    int rc = check_weight(ctx, w);
+    if (rc) return rc;
+    if (w->type != OVFQ_TYPE_Q4_K && w->type != OVFQ_TYPE_Q6_K)
+        return fail(OVFQ_ERR_TYPE, "an MFMA-ready copy exists for K-quant weights only");
+    // Q4_K operands cost a few packed multiplies per dword to build in registers; streaming them prepared
+    // (3.7x the bytes) measured slower, so Q4_K weights keep the GGUF-operand path.
+    if (w->type == OVFQ_TYPE_Q4_K) return ok();
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    if (w->mfma) return ok();
+    HIP_TRY(hipSetDevice(ctx->device));
+    void* pre = nullptr;
+    hipError_t e = hipMalloc(&pre, ovfq::mfma_prepared_bytes(w->in, w->out));
+    if (e == hipSuccess)
+        e = ovfq::launch_mfma_prepare(w->type, static_cast<const uint8_t*>(w->blocks), w->in, w->out,
+                                      static_cast<uint8_t*>(pre), ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        if (pre) (void)hipFree(pre);
+        return fail(OVFQ_ERR_HIP, "MFMA-ready copy failed: %s", hipGetErrorString(e));
+    }
+    w->mfma = pre;
     return ok();
 }
 

@@ -37,6 +37,7 @@ typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
 struct MJob {
     const uint8_t* w;
+    const uint8_t* pre;  // MFMA-ready copy (used when the launch is the prepared variant)
     const float* bias;
     float* y;
     int n_out;  // output size of this weight
@@ -131,6 +132,7 @@ struct Q4KMfma {
     }
     __device__ __forceinline__ static float d_of(const W& w) { return half_lo(w.h.x); }
     __device__ __forceinline__ static float dmin_of(const W& w) { return half_hi(w.h.x); }
+    __device__ __forceinline__ static uint32_t raw_scales(const W& w) { return w.h.x; }  // fp16 d | fp16 dmin << 16
     // q8Scale * (d * mainAcc - dmin * minAcc)   (RT/Q4KDotKernel.cs:944)
     __device__ __forceinline__ static float tail(const i32x4 (&acc)[kNumMfma], int i, float d, float dmin,
                                                  float q8s) {
@@ -193,6 +195,7 @@ struct Q6KMfma {
     }
     __device__ __forceinline__ static float d_of(const W& w) { return half_lo(w.d); }
     __device__ __forceinline__ static float dmin_of(const W&) { return 0.0f; }
+    __device__ __forceinline__ static uint32_t raw_scales(const W& w) { return w.d; }  // fp16 d
     // d * q8Scale * mainAcc   (RT/Q6KDotKernel.cs:114-115)
     __device__ __forceinline__ static float tail(const i32x4 (&acc)[kNumMfma], int i, float d, float, float q8s) {
         const int main_acc = acc[0][i] + (acc[1][i] << 7);
@@ -200,8 +203,68 @@ struct Q6KMfma {
     }
 };
 
+// ------------------------------------------------------------------------------------------ MFMA-ready weights
+// An optional second resident copy of a Q6_K weight holding, for every 16-row tile and super-block, exactly the B
+// operands the kernels below build from the GGUF bytes: the lo and hi operand of each of the four 64-element
+// chunks (1 KiB each, lane-major, so a wave loads one with a single coalesced dwordx4 per lane), then 8 bytes per
+// lane: a word left for per-chunk bytes (the Q4_K mins, were a Q4_K copy kept) and the block's raw fp16 d (| dmin
+// << 16 for Q4_K). The copy is written by the same operand functions, so a prepared weight's MFMA inputs - and
+// outputs - are bit-identical; the batched kernel then skips the per-block operand build (for Q6_K, 12 VALU per
+// 4 weights). Q4_K keeps building its operands: after the split-scale form they cost less than streaming 3.7x the
+// bytes (measured: the Q4_K gate/up launch at M = 512 was 10 % slower prepared, the Q6_K down 23 % faster).
+constexpr int kPreOps = 8 * 1024;
+constexpr int kPreHdr = 64 * 8;
+constexpr int kPreBlock = kPreOps + kPreHdr;
+
+size_t mfma_prepared_bytes(int in, int out) { return (size_t)((out + 63) / 64) * 4 * (size_t)(in / kQK) * kPreBlock; }
+
+// One wave per (16-row tile, super-block); rows past the matrix read zero bytes (their outputs are never stored).
+template <class F>
+__global__ __launch_bounds__(256) void mfma_prepare_kernel(const uint8_t* __restrict__ w, int n_rows, int spr,
+                                                           int tiles16, uint8_t* __restrict__ pre) {
+    const int item = (int)blockIdx.x * 4 + wave_id();
+    if (item >= tiles16 * spr) return;
+    const int tile = item / spr, sb = item % spr;
+    const int lane = threadIdx.x & 63, g = lane >> 4, r16 = lane & 15;
+    const uint32_t row_bytes = (uint32_t)spr * F::kBytes;
+    const uint64_t wbase = (uint64_t)tile * 16 * row_bytes;
+    const uint64_t wbase4 = wbase & ~3ull;
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(w + wbase4, rsrc_bytes((uint64_t)n_rows * row_bytes, wbase4));
+    const typename F::W wv =
+        F::load(wr, (uint32_t)(wbase - wbase4) + (uint32_t)r16 * row_bytes + (uint32_t)sb * F::kBytes, g);
+    i32x4 op[4][F::kNumMfma];
+    F::template operands<0>(wv, g, op[0]);
+    F::template operands<1>(wv, g, op[1]);
+    F::template operands<2>(wv, g, op[2]);
+    F::template operands<3>(wv, g, op[3]);
+    uint8_t* dst = pre + ((size_t)tile * spr + sb) * kPreBlock;
+    uint32_t mins = 0;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        *reinterpret_cast<i32x4*>(dst + (2 * t) * 1024 + lane * 16) = op[t][0];
+        *reinterpret_cast<i32x4*>(dst + (2 * t + 1) * 1024 + lane * 16) = op[t][1];
+        if constexpr (F::kNumMfma == 3) mins |= ((uint32_t)op[t][2][0] & 0xffu) << (8 * t);
+    }
+    *reinterpret_cast<u32x2*>(dst + kPreOps + lane * 8) = u32x2{mins, F::raw_scales(wv)};
+}
+
+hipError_t launch_mfma_prepare(int type, const uint8_t* w, int in, int out, uint8_t* pre, hipStream_t st) {
+    const int spr = in / kQK, tiles16 = (out + 63) / 64 * 4;
+    const int64_t waves = (int64_t)tiles16 * spr;
+    const dim3 grid((unsigned)((waves + 3) / 4));
+    if (type != 14) return hipErrorInvalidValue;  // Q6_K only (the batched kernel reads no Q4_K copy)
+    hipLaunchKernelGGL(mfma_prepare_kernel<Q6KMfma>, grid, dim3(256), 0, st, w, out, spr, tiles16, pre);
+    return hipGetLastError();
+}
+
+// A prepared super-block of one lane: the eight chunk operands and the header.
+struct PreW {
+    u32x4 op[8];
+    u32x2 hdr;
+};
+
 // ------------------------------------------------------------------------------------------ kernel
-template <class F, int NT>
+template <class F, int NT, bool PRE>
 __global__ __launch_bounds__(256, 2) void kquant_mfma_kernel(const MArgs a) {
     constexpr int kSub = NT / 16;
     constexpr int kDma = NT / 16;  // 1 KiB (4-row) activation DMA chunks per wave per super-block
@@ -232,6 +295,11 @@ __global__ __launch_bounds__(256, 2) void kquant_mfma_kernel(const MArgs a) {
     const uint64_t wbase4 = wbase & ~3ull;
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(wptr + wbase4, rsrc_bytes((uint64_t)n_out * row_bytes, wbase4));
     const uint32_t woff = (uint32_t)(wbase - wbase4) + (uint32_t)r16 * row_bytes;
+    // prepared copy: this wave's 16-row tile, spr blocks of kPreBlock bytes
+    const uint64_t pbase = (uint64_t)(o0 / 16) * (uint64_t)spr * kPreBlock;
+    const __amdgpu_buffer_rsrc_t pr =
+        make_rsrc(a.job[j].pre + (PRE ? pbase : 0),
+                  PRE ? rsrc_bytes((uint64_t)((n_out + 63) / 64) * 4 * spr * kPreBlock, pbase) : 0u);
     const __amdgpu_buffer_rsrc_t qr =
         make_rsrc(a.q + (uint64_t)n0 * K, rsrc_bytes((uint64_t)a.m_rows * K, (uint64_t)n0 * K));
     const __amdgpu_buffer_rsrc_t sr = make_rsrc(
@@ -268,13 +336,8 @@ __global__ __launch_bounds__(256, 2) void kquant_mfma_kernel(const MArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; i++) out[s][i] = 0.0f;
 
-    auto compute = [&](int buf, const typename F::W& w) {
-        i32x4 op[4][F::kNumMfma];
-        F::template operands<0>(w, g, op[0]);
-        F::template operands<1>(w, g, op[1]);
-        F::template operands<2>(w, g, op[2]);
-        F::template operands<3>(w, g, op[3]);
-        const float d = F::d_of(w), dmin = F::dmin_of(w);
+    // MFMAs and fp32 tail of one super-block from the weight operands `op` and the block's d / dmin
+    auto mma_tail = [&](int buf, const i32x4 (&op)[4][F::kNumMfma], float d, float dmin) {
         const uint8_t* tile = act[buf];
 #pragma unroll
         for (int s = 0; s < kSub; s++) {
@@ -294,18 +357,62 @@ __global__ __launch_bounds__(256, 2) void kquant_mfma_kernel(const MArgs a) {
         }
     };
 
-    typename F::W wcur = F::load(wr, woff, g);
-    stage(0, 0);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    for (int sb = 0; sb < spr; sb++) {
-        // next super-block's weights (registers) and activation (LDS DMA) in flight during this one's compute
-        const typename F::W wnxt = F::load(wr, woff + (uint32_t)(sb + 1) * F::kBytes, g);  // past the row: unused
-        if (sb + 1 < spr) stage(sb + 1, (sb + 1) & 1);
-        compute(sb & 1, wcur);
-        wcur = wnxt;
-        __builtin_amdgcn_s_waitcnt(0);  // the DMA writes to LDS are complete before the barrier publishes them
+    if constexpr (!PRE) {
+        auto compute = [&](int buf, const typename F::W& w) {
+            i32x4 op[4][F::kNumMfma];
+            F::template operands<0>(w, g, op[0]);
+            F::template operands<1>(w, g, op[1]);
+            F::template operands<2>(w, g, op[2]);
+            F::template operands<3>(w, g, op[3]);
+            mma_tail(buf, op, F::d_of(w), F::dmin_of(w));
+        };
+        typename F::W wcur = F::load(wr, woff, g);
+        stage(0, 0);
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
+        for (int sb = 0; sb < spr; sb++) {
+            // next super-block's weights (registers) and activation (LDS DMA) in flight during this one's compute
+            const typename F::W wnxt = F::load(wr, woff + (uint32_t)(sb + 1) * F::kBytes, g);  // past the row: unused
+            if (sb + 1 < spr) stage(sb + 1, (sb + 1) & 1);
+            compute(sb & 1, wcur);
+            wcur = wnxt;
+            __builtin_amdgcn_s_waitcnt(0);  // the DMA writes to LDS are complete before the barrier publishes them
+            __syncthreads();
+        }
+    } else {
+        auto load_pre = [&](int sb) {
+            PreW p;
+            const uint32_t base = (uint32_t)sb * kPreBlock + (uint32_t)lane * 16u;
+#pragma unroll
+            for (int q = 0; q < 8; q++) p.op[q] = ld4(pr, base + (uint32_t)q * 1024u);
+            p.hdr = ld2(pr, (uint32_t)sb * kPreBlock + kPreOps + (uint32_t)lane * 8u);
+            return p;
+        };
+        auto compute = [&](int buf, const PreW& p) {
+            i32x4 op[4][F::kNumMfma];
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                op[t][0] = __builtin_bit_cast(i32x4, p.op[2 * t]);
+                op[t][1] = __builtin_bit_cast(i32x4, p.op[2 * t + 1]);
+                if constexpr (F::kNumMfma == 3) {
+                    const int mm = (int)__builtin_amdgcn_perm(0u, p.hdr.x, 0x01010101u * (uint32_t)t);
+                    op[t][2] = i32x4{mm, mm, mm, mm};
+                }
+            }
+            mma_tail(buf, op, half_lo(p.hdr.y), F::kNumMfma == 3 ? half_hi(p.hdr.y) : 0.0f);
+        };
+        PreW pcur = load_pre(0);
+        stage(0, 0);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        for (int sb = 0; sb < spr; sb++) {
+            const PreW pnxt = load_pre(sb + 1);  // past the tile's blocks: resource-clamped or unused
+            if (sb + 1 < spr) stage(sb + 1, (sb + 1) & 1);
+            compute(sb & 1, pcur);
+            pcur = pnxt;
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+        }
     }
 
     // y[n][o] = biasO + sum   (RT/Q4KDotKernel.cs:951, RT/Q6KDotKernel.cs:507)
@@ -324,10 +431,16 @@ __global__ __launch_bounds__(256, 2) void kquant_mfma_kernel(const MArgs a) {
 }
 
 template <class F, int NT>
-static hipError_t launch_mfma(MArgs& ma, hipStream_t st) {
+static hipError_t launch_mfma(MArgs& ma, bool pre, hipStream_t st) {
     ma.n_tiles = (ma.m_rows + NT - 1) / NT;
     const int grid = (ma.o_tiles + 7) / 8 * 8 * ma.n_tiles;
-    hipLaunchKernelGGL((kquant_mfma_kernel<F, NT>), dim3(grid), dim3(256), 0, st, ma);
+    if constexpr (F::kNumMfma == 2) {  // only Q6_K weights carry the MFMA-ready copy
+        if (pre) {
+            hipLaunchKernelGGL((kquant_mfma_kernel<F, NT, true>), dim3(grid), dim3(256), 0, st, ma);
+            return hipGetLastError();
+        }
+    }
+    hipLaunchKernelGGL((kquant_mfma_kernel<F, NT, false>), dim3(grid), dim3(256), 0, st, ma);
     return hipGetLastError();
 }
 
@@ -357,9 +470,11 @@ hipError_t launch_project_mfma(int type, const ProjJob* jobs, int njobs, int in,
                                hipStream_t st) {
     MArgs ma{};
     int tiles = 0;
+    bool pre = true;  // the prepared variant when every weight of the launch has its MFMA-ready copy
     for (int i = 0; i < njobs; i++) {
-        ma.job[i] = MJob{jobs[i].w, jobs[i].bias, jobs[i].y, jobs[i].n_rows, tiles};
+        ma.job[i] = MJob{jobs[i].w, jobs[i].pre, jobs[i].bias, jobs[i].y, jobs[i].n_rows, tiles};
         tiles += (jobs[i].n_rows + 63) / 64;
+        pre = pre && jobs[i].pre != nullptr;
     }
     ma.njobs = njobs;
     ma.o_tiles = tiles;
@@ -368,8 +483,9 @@ hipError_t launch_project_mfma(int type, const ProjJob* jobs, int njobs, int in,
     ma.q = act.q;
     ma.s = act.s;
     const int nt = mfma_tile_rows(rows);
-    if (type == 12) return nt == 128 ? launch_mfma<Q4KMfma, 128>(ma, st) : launch_mfma<Q4KMfma, 64>(ma, st);
-    return nt == 128 ? launch_mfma<Q6KMfma, 128>(ma, st) : launch_mfma<Q6KMfma, 64>(ma, st);
+    if (type == 12)
+        return nt == 128 ? launch_mfma<Q4KMfma, 128>(ma, pre, st) : launch_mfma<Q4KMfma, 64>(ma, pre, st);
+    return nt == 128 ? launch_mfma<Q6KMfma, 128>(ma, pre, st) : launch_mfma<Q6KMfma, 64>(ma, pre, st);
 }
 
 // The 16 x 16 fp32 values of one super-block for the small-M kernel: MFMAs over the four 64-element chunks (A

@@ -16,6 +16,7 @@ struct ProjJob {
     const float* bias;  // may be NULL
     float* y;           // [rows][n_rows]
     int n_rows;         // output size of this matrix
+    const uint8_t* pre = nullptr;  // MFMA-ready copy of a K-quant weight (batched kernel), or NULL
 };
 
 // Q8_K activation (RT/Q4KDotKernel.cs:64-136 layout) or Q8_0 activation (bsums == NULL).
@@ -62,6 +63,9 @@ struct GroupLaunch {
 // On MFMA with super-block-parallel waves (mfma.hip), 16 activation rows per tile.
 bool mfma_small_supported(int type, int in);
 hipError_t launch_mfma_small(int type, const GroupLaunch& launch, hipStream_t st);
+// MFMA-ready copy of a Q4_K / Q6_K weight: its size, and the kernel that writes it from the GGUF blocks.
+size_t mfma_prepared_bytes(int in, int out);
+hipError_t launch_mfma_prepare(int type, const uint8_t* w, int in, int out, uint8_t* pre, hipStream_t st);
 
 // Routed MoE (moe.hip).
 hipError_t launch_moe_topk(const float* logits, int rows, int n_experts, int k, int stride, int normalize, int* idx,

@@ -61,6 +61,13 @@ class _ResidentWeight:
                          self._ctx.lib)
         return n.value
 
+    def prepare_mfma(self):
+        """Adds the opt-in MFMA-ready copy of a Q6_K weight (ovfq_weight_prepare_mfma): batched projections
+        (M >= 32) then skip the per-block operand build, bit-identically, for ~2.5x the weight's bytes. A no-op for
+        Q4_K weights. Returns self."""
+        raise_for_status(self._ctx.lib.ovfq_weight_prepare_mfma(self._ctx.handle, self.handle), self._ctx.lib)
+        return self
+
     def DecodeRow(self, row: int, dst) -> None:
         """Dequantises output row `row` into dst[InputSize] (numpy host array or torch GPU tensor)."""
         if row < 0 or row >= self.OutputSize:

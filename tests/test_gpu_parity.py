@@ -198,6 +198,52 @@ def test_kquant_prefill_bit_exact(orc, ctx, fmt, rows, k, n):
     assert_bit_exact(ov.project(w, x, None, rows=rows).reshape(rows, n), ref0, f"{fmt} prefill host, no bias")
 
 
+@pytest.mark.parametrize("fmt", ["q4k", "q6k"])
+@pytest.mark.parametrize("rows,k,n", [(32, 256, 64), (70, 512, 200), (128, 4096, 130), (200, 2304, 64)])
+def test_prepared_mfma_prefill_bit_exact(orc, ctx, fmt, rows, k, n):
+    """The opt-in MFMA-ready copy (ovfq_weight_prepare_mfma; Q6_K, a no-op for Q4_K): batched projections read the
+    prepared operands and stay bit-exact (n not a multiple of 64: the last tile's absent rows), before and after
+    preparing, repeatedly."""
+    case("prepared prefill", fmt, rows, k, n)
+    rng = np.random.default_rng(rows * 11 + k + n)
+    blocks = _kq_blocks(rng, fmt, n, k)
+    x = normal(rng, (rows, k))
+    bias = normal(rng, n)
+    w = (ov.Q4KWeight if fmt == "q4k" else ov.Q6KWeight)(blocks, k, n)
+    batched = orc.q4k_project_batched if fmt == "q4k" else orc.q6k_project_batched
+    ref = batched(x, rows, blocks, k, n, bias)
+    assert_bit_exact(ov.project(w, x, bias, rows=rows).reshape(rows, n), ref, f"{fmt} {rows}x{k}x{n} unprepared")
+    assert w.prepare_mfma() is w
+    w.prepare_mfma()  # idempotent
+    for rep in range(2):
+        yd = ov.project(w, t(x), t(bias), rows=rows)
+        torch.cuda.synchronize()
+        assert_bit_exact(yd.cpu().numpy().reshape(rows, n), ref, f"{fmt} {rows}x{k}x{n} prepared rep {rep}")
+
+
+def test_prepared_mfma_multi_job_and_mixed(orc, ctx):
+    """A fused q/k/v-style launch of Q6_K weights over M = 48 rows with every weight prepared (the prepared kernel
+    variant), with one weight unprepared (the GGUF-operand variant for the whole launch), and Q8_0 rejected."""
+    case("prepared multi", 48)
+    rng = np.random.default_rng(48)
+    rows, k, shapes = 48, 1024, [192, 64, 80]
+    blocks = [_kq_blocks(rng, "q6k", n, k) for n in shapes]
+    x = normal(rng, (rows, k))
+    refs = [orc.q6k_project_batched(x, rows, b, k, n, None) for b, n in zip(blocks, shapes)]
+    for prepared in ([0, 1, 2], [0, 2]):
+        ws = [ov.Q6KWeight(b, k, n) for b, n in zip(blocks, shapes)]
+        for i in prepared:
+            ws[i].prepare_mfma()
+        ys = [torch.empty(rows * n, device=DEV) for n in shapes]
+        ctx.project_multi_dev(ws, t(x), ys, rows=rows)
+        torch.cuda.synchronize()
+        for i, (y, ref) in enumerate(zip(ys, refs)):
+            assert_bit_exact(y.cpu().numpy().reshape(rows, -1), ref, f"prepared {prepared} job {i}")
+    wq, wsc = orc.q8_quantize_rows(normal(rng, (8, 64), 0.05))
+    with pytest.raises(ov.OverfitArgumentError):
+        ov.Q8Weight(wq, wsc, 64, 8).prepare_mfma()
+
+
 @pytest.mark.parametrize("rows", [5, 40])
 def test_multi_projection_rows_bit_exact(orc, ctx, rows):
     """Fused q/k/v-style launch over `rows` activation rows (rows = 40 takes the MFMA kernel's multi-job grid,
@@ -453,7 +499,7 @@ def test_moe_ffn_many_tokens(orc):
 
 
 def test_moe_config5_full_size(orc):
-    """8 Mixtral-shaped experts (gate/up 14336x4096, down 4096x14336, Q4_K), 16 tokens, top-2 of
+    """benchmark config 5: 8 Mixtral-shaped experts (gate/up 14336x4096, down 4096x14336, Q4_K), 16 tokens, top-2 of
     seeded uniform router logits, routed on the device; checked against the oracle's DecodeBatched restatement."""
     case("config5 full size")
     gen = torch.Generator(device=DEV).manual_seed(55)
@@ -536,7 +582,7 @@ def test_kquant_prefill_range_extremes(orc, fmt):
 
 
 def test_llama3_8b_layer_prefill_sampled_rows(orc):
-    """BASELINE config 3 shapes at M = 512 (q 4096x4096, gate 14336x4096 Q4_K; down 4096x14336 Q6_K) at full size
+    """benchmark config 3 shapes at M = 512 (q 4096x4096, gate 14336x4096 Q4_K; down 4096x14336 Q6_K) at full size
     on the device; 40 sampled weight rows (all 512 activation rows each) are checked against the oracle: output
     rows of a projection are independent, so the sample is exact evidence for the rows it covers."""
     m = 512
@@ -692,7 +738,7 @@ def test_decode_row_bit_exact(orc, fmt):
 # ------------------------------------------------------------------------------------------------ full sizes
 
 def test_llama3_8b_layer_decode_projections_bit_exact(orc, ctx):
-    """BASELINE config 2 at full size: q 4096x4096, k/v 1024x4096, o 4096x4096, gate/up 14336x4096 (Q4_K),
+    """benchmark config 2 at full size: q 4096x4096, k/v 1024x4096, o 4096x4096, gate/up 14336x4096 (Q4_K),
     down 4096x14336 (Q6_K); weights N(0, 0.02) quantized on the device, activations N(0, 1)."""
     case("config2 full-size layer")
     gen = torch.Generator(device=DEV).manual_seed(20260519)
@@ -717,7 +763,7 @@ def test_llama3_8b_layer_decode_projections_bit_exact(orc, ctx):
 
 
 def test_q6k_lm_head_full_size_bit_exact(orc):
-    """The Llama-3-8B Q6_K output head (128256 x 4096) of BASELINE config 4."""
+    """The Llama-3-8B Q6_K output head (128256 x 4096) of benchmark config 4."""
     case("LM head 128256x4096 Q6_K")
     gen = torch.Generator(device=DEV).manual_seed(7)
     n, k = 128256, 4096
