@@ -778,6 +778,53 @@ def test_q6k_lm_head_full_size_bit_exact(orc):
     assert_bit_exact(y.cpu().numpy(), ref, "LM head")
 
 
+def test_graph_replay_moe_and_ffn(orc, ctx):
+    """Captured MoE steps (router, grouping, grouped experts, SwiGLU, combine) and fused FFNs, as the bench replays
+    them: every replay reproduces the eager outputs bit-for-bit, with eager work and synchronisations between the
+    replays (the grouping kernel clears its own tables: nothing in the graph is a memset node)."""
+    case("graph replay moe/ffn")
+    rng = np.random.default_rng(44)
+    E, dm, dff, rows, k = 8, 256, 512, 16, 2
+    gw = [ov.Q4KWeight(orc.quantize_q4k(normal(rng, (dff, dm), 0.05)), dm, dff) for _ in range(E)]
+    uw = [ov.Q4KWeight(orc.quantize_q4k(normal(rng, (dff, dm), 0.05)), dm, dff) for _ in range(E)]
+    dw = [ov.Q4KWeight(orc.quantize_q4k(normal(rng, (dm, dff), 0.05)), dff, dm) for _ in range(E)]
+    fd = ov.Q6KWeight(orc.quantize_q6k(normal(rng, (dm, dff), 0.05)), dff, dm)
+    logits = t(rng.random((rows, E)).astype(np.float32))
+    x = t(normal(rng, (rows, dm)))
+    idx = torch.empty(rows * k, dtype=torch.int32, device=DEV)
+    wt = torch.empty(rows * k, dtype=torch.float32, device=DEV)
+    ys = [torch.empty(rows * dm, device=DEV), torch.empty(dm, device=DEV)]
+
+    def step():
+        ov.MoeRouter.SelectTopK(logits, k, idx, wt, True, rows=rows)
+        ov.moe_ffn(gw, uw, dw, x, rows, k, idx, wt, out=ys[0])
+        ov.ffn_swiglu(gw[0], uw[0], fd, x[:1].reshape(-1), 1, out=ys[1])
+
+    step()
+    torch.cuda.synchronize()
+    eager = [y.cpu().numpy().copy() for y in ys]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        ctx.set_stream(side.cuda_stream)
+        step()
+        side.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=side):
+            step()
+    ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+    for rep in range(4):
+        for y in ys:
+            y.fill_(float("nan"))
+        idx.fill_(-7)
+        g.replay()
+        torch.cuda.synchronize()
+        for y, e in zip(ys, eager):
+            assert np.array_equal(y.cpu().numpy().view(np.uint32), e.view(np.uint32)), f"replay {rep}"
+        step()  # eager work between replays
+        torch.cuda.synchronize()
+
+
 def test_graph_replay_matches_eager(orc, ctx):
     """The bench replays captured decode steps; every replay must reproduce the eager outputs bit-for-bit
     (replays interleaved with eager work and synchronisations)."""
