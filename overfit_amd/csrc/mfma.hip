@@ -541,7 +541,7 @@ struct SArgs {
     const float* s;
 };
 
-template <class F, int kBatch>
+template <class F, int kBatch, bool kPipe>
 __global__ __launch_bounds__(256) void kquant_mfma_small_kernel(const SArgs a) {
     extern __shared__ __align__(16) float vals[];  // [spr][16 rows n][16 outputs o]
     const int wave = wave_id();
@@ -577,30 +577,58 @@ __global__ __launch_bounds__(256) void kquant_mfma_small_kernel(const SArgs a) {
         const int arow = have ? (a.pair_row ? a.pair_row[p] : p) : 0;
         const uint32_t qbase = have ? (uint32_t)arow * K : 0x80000000u;
         const uint32_t sbase = have ? (uint32_t)arow * (uint32_t)spr * 4u : 0x80000000u;
-        for (int sb0 = wave; sb0 < spr; sb0 += 4 * kBatch) {
+        // Batches of kBatch super-blocks (wave w: w, w + 4, ...). With kPipe (long rows) the batches are
+        // double-buffered: the next batch's weights and A operands are issued before the current batch is computed
+        // (twice the registers, so fewer waves: it pays from about four batches per wave). Loads past the row are
+        // harmless (resource-clamped or unused) and keep the instruction stream fixed; a slot past the row only
+        // skips its store.
+        struct Batch {
             typename F::W w[kBatch];
             u32x4 av[kBatch][4];
             uint32_t sv[kBatch];
+        };
+        auto load_batch = [&](int sb0, Batch& bt) {
 #pragma unroll
             for (int i = 0; i < kBatch; i++) {
-                const int sb = sb0 + 4 * i;  // past the row: reads are harmless and the values are not stored
-                w[i] = F::load(wr, woff + (uint32_t)sb * F::kBytes, g);
+                const int sb = sb0 + 4 * i;
+                bt.w[i] = F::load(wr, woff + (uint32_t)sb * F::kBytes, g);
 #pragma unroll
-                for (int t = 0; t < 4; t++) av[i][t] = ld4(qr, qbase + (uint32_t)sb * kQK + a_off[t]);
-                sv[i] = ld1(sr, sbase + (uint32_t)sb * 4);
+                for (int t = 0; t < 4; t++) bt.av[i][t] = ld4(qr, qbase + (uint32_t)sb * kQK + a_off[t]);
+                bt.sv[i] = ld1(sr, sbase + (uint32_t)sb * 4);
             }
+        };
+        auto compute_batch = [&](int sb0, const Batch& cur) {
 #pragma unroll
             for (int i = 0; i < kBatch; i++) {
-                // Every slot of the batch is computed (so the batch's loads stay ahead of all of its math); a
-                // slot past the row only skips its store.
                 const int sb = sb0 + 4 * i;
                 float v[4];
-                lohi_block_values<F>(w[i], av[i], g, as_float(sv[i]), v);  // sv: q8 scale of activation row r16
+                lohi_block_values<F>(cur.w[i], cur.av[i], g, as_float(cur.sv[i]), v);  // sv: q8 scale of row r16
                 if (sb < spr) {
                     float* vrow = vals + sb * 256;
 #pragma unroll
                     for (int j = 0; j < 4; j++) vrow[(4 * g + j) * 16 + r16] = v[j];
                 }
+            }
+        };
+        if constexpr (kPipe) {
+            int sb0 = wave;
+            auto step = [&](const Batch& cur, Batch& nxt) -> bool {
+                load_batch(sb0 + 4 * kBatch, nxt);
+                compute_batch(sb0, cur);
+                sb0 += 4 * kBatch;
+                return sb0 < spr;
+            };
+            Batch ba, bb;
+            load_batch(sb0, ba);
+            if (sb0 < spr) {
+                while (step(ba, bb) && step(bb, ba)) {
+                }
+            }
+        } else {
+            for (int sb0 = wave; sb0 < spr; sb0 += 4 * kBatch) {
+                Batch bt;
+                load_batch(sb0, bt);
+                compute_batch(sb0, bt);
             }
         }
         __syncthreads();
@@ -623,7 +651,17 @@ template <class F, int kBatch>
 static hipError_t launch_small(SArgs& sa, int nmat, int experts, hipStream_t st) {
     sa.tiles = (sa.n_rows + 15) / 16;
     const size_t lds = (size_t)sa.spr * 256 * sizeof(float);
-    hipLaunchKernelGGL((kquant_mfma_small_kernel<F, kBatch>), dim3(sa.tiles * nmat, experts), dim3(256), lds, st, sa);
+    const dim3 grid(sa.tiles * nmat, experts);
+    // measured on MI355X: double-buffered batches win for Q6_K from K = 8192 (4 batches per wave: 4096x14336 at
+    // M = 4..16 is 10-20 % faster); they lose below, and for Q4_K, whose cheaper batches do not repay the halved
+    // occupancy (config-5 MoE step 263 -> 268 us)
+    if constexpr (kBatch == 2 && F::kNumMfma == 2) {
+        if (sa.spr >= 32) {
+            hipLaunchKernelGGL((kquant_mfma_small_kernel<F, kBatch, true>), grid, dim3(256), lds, st, sa);
+            return hipGetLastError();
+        }
+    }
+    hipLaunchKernelGGL((kquant_mfma_small_kernel<F, kBatch, false>), grid, dim3(256), lds, st, sa);
     return hipGetLastError();
 }
 
