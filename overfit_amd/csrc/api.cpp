@@ -828,9 +828,14 @@ static int moe_impl(ovfq_ctx* ctx, int E, const ovfq_weight* const* gate, const 
     std::lock_guard<std::mutex> lk(ctx->mu);
     HIP_TRY(hipSetDevice(ctx->device));
     // scratch layout (sizes first, then the pointers into one buffer)
+    // Many pairs per expert: the batched int8-MFMA kernel over expert groups (64-row tiles, operand build amortised
+    // over the tile); few: the small-M kernel (16-row tiles, super-block-parallel waves). Measured crossover about
+    // 32 pairs per expert on average.
+    const bool grouped_big = P >= (size_t)32 * E;
+    const int max_tiles = (int)((P + ovfq::kGroupedTileRows - 1) / ovfq::kGroupedTileRows) + E;
     auto carve = [&](Carver& c, int** off, int** prow, int** pof, float** g, float** u, int8_t** iq, float** is,
                      int16_t** ib, float** out, float** hx, int** hidx, float** hw, float** hy) {
-        *off = c.take<int>((size_t)(E + 1) * 4);
+        *off = c.take<int>((size_t)(E + 2 + max_tiles) * 4);  // expert_off[E + 1], tile count, tile list
         *prow = c.take<int>(P * 4);
         *pof = c.take<int>(P * 4);
         *g = c.take<float>(P * dff * 4);
@@ -870,7 +875,10 @@ static int moe_impl(ovfq_ctx* ctx, int E, const ovfq_weight* const* gate, const 
     }
     ovfq::ActQ act;
     if ((rc = quantize_into_scratch(ctx, gt, xd, rows, dmodel, &act))) return rc;
-    HIP_TRY(ovfq::launch_moe_plan(idxd, rows, k, E, off, prow, pof, ctx->stream));
+    int* tile_count = off + E + 1;
+    int* tiles = off + E + 2;
+    HIP_TRY(ovfq::launch_moe_plan(idxd, rows, k, E, off, prow, pof, ovfq::kGroupedTileRows,
+                                  grouped_big ? tiles : nullptr, tile_count, ctx->stream));
     const uint8_t* gw[OVFQ_MAX_EXPERTS];
     const uint8_t* uw[OVFQ_MAX_EXPERTS];
     const uint8_t* dw[OVFQ_MAX_EXPERTS];
@@ -891,7 +899,10 @@ static int moe_impl(ovfq_ctx* ctx, int E, const ovfq_weight* const* gate, const 
     L.expert_off = off;
     L.pair_row = prow;
     L.act = act;
-    HIP_TRY(ovfq::launch_mfma_small(gt, L, ctx->stream));
+    if (grouped_big)
+        HIP_TRY(ovfq::launch_mfma_grouped(gt, L, tiles, tile_count, max_tiles, ctx->stream));
+    else
+        HIP_TRY(ovfq::launch_mfma_small(gt, L, ctx->stream));
     HIP_TRY(ovfq::launch_swiglu_q8k(g, u, off, E, (int)P, dff, iq, is, ib, ctx->stream));
     ovfq::GroupLaunch D{};
     D.w0 = dw;
@@ -903,7 +914,10 @@ static int moe_impl(ovfq_ctx* ctx, int E, const ovfq_weight* const* gate, const 
     D.expert_off = off;
     D.pair_row = nullptr;  // the intermediate is already pair-major
     D.act = ovfq::ActQ{iq, is, ib};
-    HIP_TRY(ovfq::launch_mfma_small(dt, D, ctx->stream));
+    if (grouped_big)
+        HIP_TRY(ovfq::launch_mfma_grouped(dt, D, tiles, tile_count, max_tiles, ctx->stream));
+    else
+        HIP_TRY(ovfq::launch_mfma_small(dt, D, ctx->stream));
     HIP_TRY(ovfq::launch_moe_combine(out, pof, wd, rows, k, dmodel, yd, ctx->stream));
     if (host) {
         HIP_TRY(hipMemcpyAsync(y, yd, (size_t)rows * dmodel * 4, hipMemcpyDeviceToHost, ctx->stream));

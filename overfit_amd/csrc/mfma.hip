@@ -44,15 +44,31 @@ struct MJob {
     int tile0;  // first 64-row tile index of this job in the launch
 };
 
+// Grouped (MoE) launch: tile list entry t = expert e | (tile i << 8) covers pairs expert_off[e] + [64 i, 64 i + 64);
+// gate/up pairs (w1 set) share the launch, the first o_tiles1 weight tiles being gate's.
+struct MGroup {
+    const uint8_t* w0[kMaxExperts];
+    const uint8_t* w1[kMaxExperts];
+    const int* expert_off;
+    const int* pair_row;  // activation row of each pair (NULL: pair p reads row p)
+    const int* tiles;
+    const int* tile_count;
+    float* y0;
+    float* y1;
+    int n_rows;    // outputs per matrix
+    int o_tiles1;  // 64-row weight tiles of one matrix
+};
+
 struct MArgs {
     MJob job[kMaxJobs];
     int njobs;
     int o_tiles;  // 64-row weight tiles over all jobs
-    int n_tiles;  // ceil(M / NT)
-    int m_rows;   // M
+    int n_tiles;  // ceil(M / NT); grouped: the tile list's bound
+    int m_rows;   // M; grouped: activation rows
     int spr;      // K / 256
     const int8_t* q;
     const float* s;
+    MGroup grp;
 };
 
 
@@ -264,8 +280,9 @@ struct PreW {
 };
 
 // ------------------------------------------------------------------------------------------ kernel
-template <class F, int NT, bool PRE>
+template <class F, int NT, bool PRE, bool GRP>
 __global__ __launch_bounds__(256, 2) void kquant_mfma_kernel(const MArgs a) {
+    static_assert(!(PRE && GRP), "grouped launches read the GGUF operands");
     constexpr int kSub = NT / 16;
     constexpr int kDma = NT / 16;  // 1 KiB (4-row) activation DMA chunks per wave per super-block
     __shared__ __align__(16) uint8_t act[2][NT * 256];
@@ -279,14 +296,39 @@ __global__ __launch_bounds__(256, 2) void kquant_mfma_kernel(const MArgs a) {
     const int o_tile = (b & 7) + 8 * (local / a.n_tiles);
     const int n_tile = local % a.n_tiles;
     if (o_tile >= a.o_tiles) return;  // uniform over the workgroup
-    int j = 0;
+    // weight rows, output and activation rows of this tile (all wave-uniform)
+    const uint8_t* wptr;
+    const uint8_t* preptr = nullptr;
+    const float* bias = nullptr;
+    float* y;
+    int n_out, o0, n0, m_valid;
+    int pbeg = 0;  // grouped: the expert's first pair (output row of tile row 0 is pbeg + n0)
+    if constexpr (GRP) {
+        if (n_tile >= a.grp.tile_count[0]) return;
+        const int te = a.grp.tiles[n_tile];
+        const int e = te & 0xff;
+        const int mat = o_tile >= a.grp.o_tiles1 ? 1 : 0;
+        wptr = mat ? a.grp.w1[e] : a.grp.w0[e];
+        y = mat ? a.grp.y1 : a.grp.y0;
+        n_out = a.grp.n_rows;
+        o0 = (o_tile - mat * a.grp.o_tiles1) * 64 + wave * 16;
+        pbeg = a.grp.expert_off[e];
+        n0 = (te >> 8) * NT;
+        m_valid = min(NT, a.grp.expert_off[e + 1] - pbeg - n0);
+    } else {
+        int j = 0;
 #pragma unroll
-    for (int t = 1; t < kMaxJobs; t++)
-        if (t < a.njobs && o_tile >= a.job[t].tile0) j = t;
-    const uint8_t* wptr = a.job[j].w;
-    const int n_out = a.job[j].n_out;
-    const int o0 = (o_tile - a.job[j].tile0) * 64 + wave * 16;  // this wave's first weight row
-    const int n0 = n_tile * NT;
+        for (int t = 1; t < kMaxJobs; t++)
+            if (t < a.njobs && o_tile >= a.job[t].tile0) j = t;
+        wptr = a.job[j].w;
+        preptr = a.job[j].pre;
+        bias = a.job[j].bias;
+        y = a.job[j].y;
+        n_out = a.job[j].n_out;
+        o0 = (o_tile - a.job[j].tile0) * 64 + wave * 16;  // this wave's first weight row
+        n0 = n_tile * NT;
+        m_valid = min(NT, a.m_rows - n0);
+    }
     const int spr = a.spr;
     const uint32_t K = (uint32_t)spr * kQK;
     const uint32_t row_bytes = (uint32_t)spr * F::kBytes;
@@ -298,12 +340,24 @@ __global__ __launch_bounds__(256, 2) void kquant_mfma_kernel(const MArgs a) {
     // prepared copy: this wave's 16-row tile, spr blocks of kPreBlock bytes
     const uint64_t pbase = (uint64_t)(o0 / 16) * (uint64_t)spr * kPreBlock;
     const __amdgpu_buffer_rsrc_t pr =
-        make_rsrc(a.job[j].pre + (PRE ? pbase : 0),
+        make_rsrc(preptr + (PRE ? pbase : 0),
                   PRE ? rsrc_bytes((uint64_t)((n_out + 63) / 64) * 4 * spr * kPreBlock, pbase) : 0u);
+    // Activation: the tile's rows from row n0 on; grouped, the whole activation with each row gathered (tile row r
+    // is pair pbeg + n0 + r, activation row pair_row[that]); rows past the tile's pairs point past the resource.
+    const uint64_t a0 = GRP ? 0 : (uint64_t)n0;
     const __amdgpu_buffer_rsrc_t qr =
-        make_rsrc(a.q + (uint64_t)n0 * K, rsrc_bytes((uint64_t)a.m_rows * K, (uint64_t)n0 * K));
-    const __amdgpu_buffer_rsrc_t sr = make_rsrc(
-        a.s + (uint64_t)n0 * spr, rsrc_bytes((uint64_t)a.m_rows * spr * 4, (uint64_t)n0 * spr * 4));
+        make_rsrc(a.q + a0 * K, rsrc_bytes((uint64_t)a.m_rows * K, a0 * K));
+    const __amdgpu_buffer_rsrc_t sr =
+        make_rsrc(a.s + a0 * spr, rsrc_bytes((uint64_t)a.m_rows * spr * 4, a0 * spr * 4));
+    auto act_row = [&](uint32_t r) -> uint32_t {  // resource-relative activation row of tile row r
+        if constexpr (GRP) {
+            if ((int)r >= m_valid) return (uint32_t)a.m_rows;
+            const int p = pbeg + n0 + (int)r;
+            return (uint32_t)(a.grp.pair_row ? a.grp.pair_row[p] : p);
+        } else {
+            return r;
+        }
+    };
 
     // DMA chunk c = wave * kDma + i covers LDS bytes [1024c, 1024c + 1024): lane L writes physical slot L % 16 of
     // row 4c + L / 16, which holds logical slot (L % 16) ^ (row % 16).
@@ -311,8 +365,9 @@ __global__ __launch_bounds__(256, 2) void kquant_mfma_kernel(const MArgs a) {
 #pragma unroll
     for (int i = 0; i < kDma; i++) {
         const uint32_t row = 4u * (uint32_t)(wave * kDma + i) + ((uint32_t)lane >> 4);
-        dma_src[i] = row * K + 16u * F::src_piece(((uint32_t)lane & 15u) ^ (row & 15u));
+        dma_src[i] = act_row(row) * K + 16u * F::src_piece(((uint32_t)lane & 15u) ^ (row & 15u));
     }
+    const uint32_t s_src = wave * 64 < NT ? act_row(threadIdx.x) * (uint32_t)spr * 4u : 0u;
     // Reads past the last super-block of a row land in the next row or past the resource: harmless (not used).
     auto stage = [&](int sb, int buf) {
 #pragma unroll
@@ -323,7 +378,7 @@ __global__ __launch_bounds__(256, 2) void kquant_mfma_kernel(const MArgs a) {
         if (wave * 64 < NT)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 sr, (__attribute__((address_space(3))) void*)&act_s[buf][wave * 64], 4,
-                (int)(((uint32_t)threadIdx.x * (uint32_t)spr + (uint32_t)sb) * 4u), 0, 0, 0);
+                (int)(s_src + (uint32_t)sb * 4u), 0, 0, 0);
     };
     // A-operand byte offset of logical slot 4t + g in row r16 of a sub-tile: ((4t + g) ^ r16) = 4t ^ (g ^ r16).
     uint32_t a_off[4];
@@ -415,18 +470,16 @@ __global__ __launch_bounds__(256, 2) void kquant_mfma_kernel(const MArgs a) {
         }
     }
 
-    // y[n][o] = biasO + sum   (RT/Q4KDotKernel.cs:951, RT/Q6KDotKernel.cs:507)
+    // y[n][o] = biasO + sum   (RT/Q4KDotKernel.cs:951, RT/Q6KDotKernel.cs:507); grouped: output row pbeg + n
     const int o = o0 + r16;
     if (o >= n_out) return;
-    const float* bias = a.job[j].bias;
-    float* y = a.job[j].y;
     const float bias_o = bias ? bias[o] : 0.0f;
 #pragma unroll
     for (int s = 0; s < kSub; s++)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const int n = n0 + s * 16 + 4 * g + i;
-            if (n < a.m_rows) y[(size_t)n * n_out + o] = bias_o + out[s][i];
+            const int n = s * 16 + 4 * g + i;
+            if (n < m_valid) y[(size_t)(pbeg + n0 + n) * n_out + o] = bias_o + out[s][i];
         }
 }
 
@@ -436,11 +489,42 @@ static hipError_t launch_mfma(MArgs& ma, bool pre, hipStream_t st) {
     const int grid = (ma.o_tiles + 7) / 8 * 8 * ma.n_tiles;
     if constexpr (F::kNumMfma == 2) {  // only Q6_K weights carry the MFMA-ready copy
         if (pre) {
-            hipLaunchKernelGGL((kquant_mfma_kernel<F, NT, true>), dim3(grid), dim3(256), 0, st, ma);
+            hipLaunchKernelGGL((kquant_mfma_kernel<F, NT, true, false>), dim3(grid), dim3(256), 0, st, ma);
             return hipGetLastError();
         }
     }
-    hipLaunchKernelGGL((kquant_mfma_kernel<F, NT, false>), dim3(grid), dim3(256), 0, st, ma);
+    hipLaunchKernelGGL((kquant_mfma_kernel<F, NT, false, false>), dim3(grid), dim3(256), 0, st, ma);
+    return hipGetLastError();
+}
+
+hipError_t launch_mfma_grouped(int type, const GroupLaunch& L, const int* tiles, const int* tile_count,
+                               int max_tiles, hipStream_t st) {
+    MArgs ma{};
+    const int o1 = (L.n_rows + 63) / 64;
+    ma.o_tiles = o1 * (L.w1 ? 2 : 1);
+    ma.n_tiles = max_tiles;
+    ma.m_rows = L.rows;
+    ma.spr = L.in / kQK;
+    ma.q = L.act.q;
+    ma.s = L.act.s;
+    for (int e = 0; e < L.experts; e++) {
+        ma.grp.w0[e] = L.w0[e];
+        ma.grp.w1[e] = L.w1 ? L.w1[e] : nullptr;
+    }
+    ma.grp.expert_off = L.expert_off;
+    ma.grp.pair_row = L.pair_row;
+    ma.grp.tiles = tiles;
+    ma.grp.tile_count = tile_count;
+    ma.grp.y0 = L.y0;
+    ma.grp.y1 = L.y1;
+    ma.grp.n_rows = L.n_rows;
+    ma.grp.o_tiles1 = o1;
+    const int grid = (ma.o_tiles + 7) / 8 * 8 * max_tiles;
+    constexpr int NT = kGroupedTileRows;
+    if (type == 12)
+        hipLaunchKernelGGL((kquant_mfma_kernel<Q4KMfma, NT, false, true>), dim3(grid), dim3(256), 0, st, ma);
+    else
+        hipLaunchKernelGGL((kquant_mfma_kernel<Q6KMfma, NT, false, true>), dim3(grid), dim3(256), 0, st, ma);
     return hipGetLastError();
 }
 

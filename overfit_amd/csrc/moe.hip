@@ -81,9 +81,12 @@ __global__ __launch_bounds__(64) void moe_topk_kernel(const float* __restrict__ 
 // the per-wave count and each token's rank among the wave's claimers (popcount of the lower lanes), so a pair's
 // position is expert_off[e] + (claimers of e in earlier chunks) + (in earlier waves of this chunk) + rank. The
 // routing table is staged in LDS when it fits (rows * k ints <= 48 KB).
+// With `tiles`, it also lists the experts' pair ranges in tiles of `nt` rows, expert-major: entry t = expert | (tile
+// index within the expert << 8), with the list's length at *tile_count.
 __global__ __launch_bounds__(256) void moe_plan_kernel(const int* __restrict__ idx_g, int rows, int k, int n_experts,
                                                        int* __restrict__ expert_off, int* __restrict__ pair_row,
-                                                       int* __restrict__ pair_of, int staged) {
+                                                       int* __restrict__ pair_of, int staged, int nt,
+                                                       int* __restrict__ tiles, int* __restrict__ tile_count) {
     extern __shared__ int sidx[];
     __shared__ int run[kMaxExperts];        // first position of the current chunk's claimers, per expert
     __shared__ int wcnt[4][kMaxExperts];    // claimers per wave of the current chunk, per expert
@@ -113,17 +116,26 @@ __global__ __launch_bounds__(256) void moe_plan_kernel(const int* __restrict__ i
         if (tid < n_experts) run[tid] += wcnt[0][tid] + wcnt[1][tid] + wcnt[2][tid] + wcnt[3][tid];
         __syncthreads();
     }
+    __shared__ int tbase[kMaxExperts + 1];  // first tile-list entry per expert
     if (tid == 0) {
-        int acc = 0;
+        int acc = 0, tacc = 0;
         for (int e = 0; e < n_experts; e++) {
             const int c = run[e];
             run[e] = acc;
             expert_off[e] = acc;
             acc += c;
+            tbase[e] = tacc;
+            tacc += (c + nt - 1) / nt;
         }
         expert_off[n_experts] = acc;
+        tbase[n_experts] = tacc;
+        if (tiles) *tile_count = tacc;
     }
     __syncthreads();
+    if (tiles) {
+        for (int e = 0; e < n_experts; e++)
+            for (int i = tid; i < tbase[e + 1] - tbase[e]; i += blockDim.x) tiles[tbase[e] + i] = e | (i << 8);
+    }
     // pass 2: positions, tokens ascending within each expert
     for (int c0 = 0; c0 < rows; c0 += 256) {
         const int n = c0 + tid;
@@ -215,11 +227,11 @@ hipError_t launch_moe_topk(const float* logits, int rows, int n_experts, int k, 
 }
 
 hipError_t launch_moe_plan(const int* idx, int rows, int k, int n_experts, int* expert_off, int* pair_row,
-                           int* pair_of, hipStream_t st) {
+                           int* pair_of, int nt, int* tiles, int* tile_count, hipStream_t st) {
     const size_t bytes = (size_t)rows * k * sizeof(int);
     const int staged = bytes <= 48 * 1024;
     hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(256), staged ? bytes : 0, st, idx, rows, k, n_experts, expert_off,
-                       pair_row, pair_of, staged);
+                       pair_row, pair_of, staged, nt, tiles, tile_count);
     return hipGetLastError();
 }
 

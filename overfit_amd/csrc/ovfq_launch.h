@@ -70,8 +70,16 @@ hipError_t launch_mfma_prepare(int type, const uint8_t* w, int in, int out, uint
 // Routed MoE (moe.hip).
 hipError_t launch_moe_topk(const float* logits, int rows, int n_experts, int k, int stride, int normalize, int* idx,
                            float* w, hipStream_t st);
+// `tiles` (optional, else NULL): the experts' pair ranges in tiles of `nt` rows (expert | tile << 8), the count at
+// *tile_count; at most ceil(rows * k / nt) + n_experts entries.
 hipError_t launch_moe_plan(const int* idx, int rows, int k, int n_experts, int* expert_off, int* pair_row,
-                           int* pair_of, hipStream_t st);
+                           int* pair_of, int nt, int* tiles, int* tile_count, hipStream_t st);
+// The batched int8-MFMA kernel over expert groups: tile list entry t covers rows [64 i, 64 i + 64) of expert e's
+// pairs; gate/up pairs (w1 set) share the launch. Activation rows are gathered through pair_row (NULL: pair p reads
+// row p); outputs are pair-major.
+hipError_t launch_mfma_grouped(int type, const GroupLaunch& launch, const int* tiles, const int* tile_count,
+                               int max_tiles, hipStream_t st);
+constexpr int kGroupedTileRows = 64;
 hipError_t launch_swiglu_q8k(const float* gate, const float* up, const int* expert_off, int n_experts, int max_pairs,
                              int dff, int8_t* q, float* s, int16_t* b, hipStream_t st);
 hipError_t launch_moe_combine(const float* out, const int* pair_of, const float* w, int rows, int k, int dmodel,

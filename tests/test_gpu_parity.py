@@ -498,6 +498,28 @@ def test_moe_ffn_many_tokens(orc):
     _moe_check(y.cpu().numpy(), ref, "300 tokens top-3")
 
 
+def test_moe_ffn_grouped_tile_boundaries(orc):
+    """Many pairs per expert take the batched MFMA kernel over 64-row expert tiles: an expert with exactly 64 pairs
+    (one full tile), one with 66 (a full tile and a 2-row tile), one with none."""
+    case("moe grouped tiles", 130)
+    rng = np.random.default_rng(130)
+    E, dm, dff, rows, k = 3, 256, 256, 130, 1
+    gb = [orc.quantize_q4k(normal(rng, (dff, dm), 0.05)) for _ in range(E)]
+    ub = [orc.quantize_q4k(normal(rng, (dff, dm), 0.05)) for _ in range(E)]
+    db = [orc.quantize_q4k(normal(rng, (dm, dff), 0.05)) for _ in range(E)]
+    gw = [ov.Q4KWeight(b, dm, dff) for b in gb]
+    uw = [ov.Q4KWeight(b, dm, dff) for b in ub]
+    dw = [ov.Q4KWeight(b, dff, dm) for b in db]
+    x = normal(rng, (rows, dm))
+    idx = np.array([2] * 64 + [0] * 66, np.int32).reshape(rows, k)
+    rng.shuffle(idx)
+    w = rng.random((rows, k)).astype(np.float32)
+    ref = orc.moe_ffn_batched(gb, ub, db, ov.TYPE_Q4_K, ov.TYPE_Q4_K, x, rows, dm, dff, k, idx, w)
+    y = ov.moe_ffn(gw, uw, dw, t(x), rows, k, t(idx), t(w))
+    torch.cuda.synchronize()
+    _moe_check(y.cpu().numpy(), ref, "grouped tiles 64/66/0")
+
+
 def test_moe_config5_full_size(orc):
     """benchmark config 5: 8 Mixtral-shaped experts (gate/up 14336x4096, down 4096x14336, Q4_K), 16 tokens, top-2 of
     seeded uniform router logits, routed on the device; checked against the oracle's DecodeBatched restatement."""
