@@ -829,9 +829,14 @@ static int moe_impl(ovfq_ctx* ctx, int E, const ovfq_weight* const* gate, const 
     HIP_TRY(hipSetDevice(ctx->device));
     // scratch layout (sizes first, then the pointers into one buffer)
     // Many pairs per expert: the batched int8-MFMA kernel over expert groups (64-row tiles, operand build amortised
-    // over the tile); few: the small-M kernel (16-row tiles, super-block-parallel waves). Measured crossover about
-    // 32 pairs per expert on average.
-    const bool grouped_big = P >= (size_t)32 * E;
+    // over the tile); few: the small-M kernel (16-row tiles, super-block-parallel waves). Measured on MI355X with 8
+    // Mixtral-shaped experts, top-2: small-M wins at 8 pairs per expert on average (304 vs 352 us), the grouped
+    // kernel from 12 (354 vs 365 us; 64 tokens 362 vs 469 us).
+    static const int grouped_min = [] {
+        const char* v = getenv("OVFQ_MOE_GROUPED_MIN_PAIRS");
+        return v && *v ? atoi(v) : 12;
+    }();
+    const bool grouped_big = P >= (size_t)grouped_min * E;
     const int max_tiles = (int)((P + ovfq::kGroupedTileRows - 1) / ovfq::kGroupedTileRows) + E;
     auto carve = [&](Carver& c, int** off, int** prow, int** pof, float** g, float** u, int8_t** iq, float** is,
                      int16_t** ib, float** out, float** hx, int** hidx, float** hw, float** hy) {
