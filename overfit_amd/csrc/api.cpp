@@ -820,8 +820,6 @@ static int moe_impl(ovfq_ctx* ctx, int E, const ovfq_weight* const* gate, const 
             down[e]->in != dff || down[e]->out != dmodel)
             return fail(OVFQ_ERR_SIZE, "expert %d shapes differ (gate/up [d_ff][d_model], down [d_model][d_ff])", e);
     }
-    if (!ovfq::mfma_small_supported(gt, dmodel) || !ovfq::mfma_small_supported(dt, dff))
-        return fail(OVFQ_ERR_SIZE, "d_model / d_ff above 16384");
     if (!host && (rc_align(x) || rc_align(idx) || rc_align(w) || rc_align(y)))
         return fail(OVFQ_ERR_SIZE, "device pointers must be 4-byte aligned");
     const size_t P = (size_t)rows * k;
@@ -836,7 +834,9 @@ static int moe_impl(ovfq_ctx* ctx, int E, const ovfq_weight* const* gate, const 
         const char* v = getenv("OVFQ_MOE_GROUPED_MIN_PAIRS");
         return v && *v ? atoi(v) : 12;
     }();
-    const bool grouped_big = P >= (size_t)grouped_min * E;
+    // the small-M kernel keeps a row's block values in LDS (d_model, d_ff <= 16384); past that, always grouped
+    const bool small_ok = ovfq::mfma_small_supported(gt, dmodel) && ovfq::mfma_small_supported(dt, dff);
+    const bool grouped_big = !small_ok || P >= (size_t)grouped_min * E;
     const int max_tiles = (int)((P + ovfq::kGroupedTileRows - 1) / ovfq::kGroupedTileRows) + E;
     auto carve = [&](Carver& c, int** off, int** prow, int** pof, float** g, float** u, int8_t** iq, float** is,
                      int16_t** ib, float** out, float** hx, int** hidx, float** hw, float** hy) {

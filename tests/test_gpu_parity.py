@@ -520,6 +520,25 @@ def test_moe_ffn_grouped_tile_boundaries(orc):
     _moe_check(y.cpu().numpy(), ref, "grouped tiles 64/66/0")
 
 
+def test_moe_ffn_wide_intermediate(orc):
+    """d_ff = 16640 (65 super-blocks, past the small-M kernel's limit) with few tokens: the grouped batched kernel
+    takes it."""
+    case("moe wide d_ff", 16640)
+    rng = np.random.default_rng(65)
+    E, dm, dff, rows, k = 2, 256, 16640, 3, 1
+    gb = [orc.quantize_q4k(normal(rng, (dff, dm), 0.05)) for _ in range(E)]
+    ub = [orc.quantize_q4k(normal(rng, (dff, dm), 0.05)) for _ in range(E)]
+    db = [orc.quantize_q6k(normal(rng, (dm, dff), 0.05)) for _ in range(E)]
+    gw = [ov.Q4KWeight(b, dm, dff) for b in gb]
+    uw = [ov.Q4KWeight(b, dm, dff) for b in ub]
+    dw = [ov.Q6KWeight(b, dff, dm) for b in db]
+    x = normal(rng, (rows, dm))
+    idx = np.array([[1], [0], [1]], np.int32)
+    w = rng.random((rows, k)).astype(np.float32)
+    ref = orc.moe_ffn_batched(gb, ub, db, ov.TYPE_Q4_K, ov.TYPE_Q6_K, x, rows, dm, dff, k, idx, w)
+    _moe_check(ov.moe_ffn(gw, uw, dw, x, rows, k, idx, w), ref, "d_ff 16640")
+
+
 def test_moe_config5_full_size(orc):
     """benchmark config 5: 8 Mixtral-shaped experts (gate/up 14336x4096, down 4096x14336, Q4_K), 16 tokens, top-2 of
     seeded uniform router logits, routed on the device; checked against the oracle's DecodeBatched restatement."""
