@@ -32,6 +32,7 @@ SIGNATURES = {
     "ovfq_ctx_set_stream": (ci, [vp, vp]),
     "ovfq_ctx_reset_stream": (ci, [vp]),
     "ovfq_ctx_synchronize": (ci, [vp]),
+    "ovfq_ctx_set_batched_kernel": (ci, [vp, ci]),
     "ovfq_last_error": (ctypes.c_char_p, []),
     "ovfq_version": (ctypes.c_char_p, []),
     "ovfq_weight_create": (ci, [vp, ci, vp, sz, vp, ci, ci, PP]),

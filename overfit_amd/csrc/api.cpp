@@ -52,6 +52,7 @@ struct ovfq_ctx {
     int device = 0;
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
+    int batched_kernel = OVFQ_BATCHED_AUTO;  // ovfq_ctx_set_batched_kernel
     std::mutex mu;
     // Activation quantisation scratch (Q8_K / Q8_0) and host-call staging.
     DevBuf act_q, act_s, act_b, x_stage, y_stage, y2_stage, bias_stage;
@@ -187,14 +188,31 @@ bool gemv_enabled() {
     return on;
 }
 
-// Kernel for 3 <= M < 32: the super-block-parallel MFMA kernel, unless OVFQ_SMALL_KERNEL=general (for
-// measurements). At M = 2 the general kernel is faster on MI355X for every Llama-3-8B shape.
+// The small-M MFMA kernel serves M >= 3 unless OVFQ_SMALL_KERNEL=general (for measurements). At M = 2 the
+// general kernel is faster on MI355X for every Llama-3-8B shape.
 bool small_mfma_enabled(int rows) {
     static const bool general = [] {
         const char* v = getenv("OVFQ_SMALL_KERNEL");
         return v && !strcmp(v, "general");
     }();
     return rows >= 3 && !general;
+}
+
+// Batched K-quant launch of rows >= 3: the 64-row-tiled MFMA kernel (true), else the small-M kernel where it takes
+// the shape, else the general kernel. OVFQ_BATCHED_SMALL / _TILED force a kernel; automatic is the shape rule of
+// mfma_tiled_preferred, and the old M >= 32 bound where the small-M kernel cannot run.
+bool use_tiled_mfma(const ovfq_ctx* c, int type, const ovfq::ProjJob* jobs, int count, int in, int rows) {
+    if (!ovfq::mfma_supported(type) || rows < 3) return false;
+    if (c->batched_kernel == OVFQ_BATCHED_TILED) return true;
+    if (!small_mfma_enabled(rows) || !ovfq::mfma_small_supported(type, in)) return rows >= ovfq::kMfmaMinRows;
+    if (c->batched_kernel == OVFQ_BATCHED_SMALL) return false;
+    int o_tiles = 0;
+    long out_rows = 0;
+    for (int i = 0; i < count; i++) {
+        o_tiles += (jobs[i].n_rows + 63) / 64;
+        out_rows += jobs[i].n_rows;
+    }
+    return ovfq::mfma_tiled_preferred(type, rows, o_tiles, out_rows);
 }
 
 // One launch for `count` weights sharing an activation: either the fp32 activation x (quantised inside the
@@ -216,7 +234,7 @@ int launch_projection(ovfq_ctx* c, const ovfq_weight* const* ws, int count, cons
         HIP_TRY(ovfq::launch_project_q8_0(jobs, count, in, rows, act, c->stream));
     } else if (rows == 1 && gemv_enabled() && ovfq::gemv_supported(in)) {
         HIP_TRY(ovfq::launch_gemv_kquant(type, jobs, count, in, x, act, c->stream));
-    } else if (ovfq::mfma_supported(type, rows)) {
+    } else if (use_tiled_mfma(c, type, jobs, count, in, rows)) {
         HIP_TRY(ovfq::launch_project_mfma(type, jobs, count, in, rows, act, c->stream));
     } else if (small_mfma_enabled(rows) && ovfq::mfma_small_supported(type, in)) {
         // Few rows: 16-row MFMA tiles with super-block-parallel waves; a gate/up-shaped pair shares one launch.
@@ -333,6 +351,15 @@ int ovfq_ctx_reset_stream(ovfq_ctx* c) {
     HIP_TRY(hipSetDevice(c->device));
     HIP_TRY(hipStreamSynchronize(c->stream));
     c->stream = c->own_stream;
+    return ok();
+}
+
+int ovfq_ctx_set_batched_kernel(ovfq_ctx* c, int kernel) {
+    if (!c) return fail(OVFQ_ERR_NULL, "ctx is NULL");
+    if (kernel != OVFQ_BATCHED_AUTO && kernel != OVFQ_BATCHED_SMALL && kernel != OVFQ_BATCHED_TILED)
+        return fail(OVFQ_ERR_RANGE, "unknown batched kernel choice %d", kernel);
+    std::lock_guard<std::mutex> lk(c->mu);
+    c->batched_kernel = kernel;
     return ok();
 }
 
@@ -836,7 +863,8 @@ static int moe_impl(ovfq_ctx* ctx, int E, const ovfq_weight* const* gate, const 
     }();
     // the small-M kernel keeps a row's block values in LDS (d_model, d_ff <= 16384); past that, always grouped
     const bool small_ok = ovfq::mfma_small_supported(gt, dmodel) && ovfq::mfma_small_supported(dt, dff);
-    const bool grouped_big = !small_ok || P >= (size_t)grouped_min * E;
+    const bool grouped_big = !small_ok || ctx->batched_kernel == OVFQ_BATCHED_TILED ||
+                             (ctx->batched_kernel == OVFQ_BATCHED_AUTO && P >= (size_t)grouped_min * E);
     const int max_tiles = (int)((P + ovfq::kGroupedTileRows - 1) / ovfq::kGroupedTileRows) + E;
     auto carve = [&](Carver& c, int** off, int** prow, int** pof, float** g, float** u, int8_t** iq, float** is,
                      int16_t** ib, float** out, float** hx, int** hidx, float** hw, float** hy) {

@@ -528,14 +528,6 @@ hipError_t launch_mfma_grouped(int type, const GroupLaunch& L, const int* tiles,
     return hipGetLastError();
 }
 
-int mfma_min_rows() {
-    static const int v = [] {
-        const char* e = getenv("OVFQ_MFMA_MIN_ROWS");
-        return e && *e ? atoi(e) : 32;
-    }();
-    return v;
-}
-
 // 128 activation rows per workgroup halve the operand-build cost per output but allow only two workgroups per CU;
 // 64 rows fit four, which hides more latency. Measured on MI355X (Llama-3-8B layer shapes): 64 is faster up to
 // M = 512, 128 from M = 2048.
@@ -548,7 +540,21 @@ static int mfma_tile_rows(int rows) {
     return rows >= 1024 ? 128 : 64;
 }
 
-bool mfma_supported(int type, int rows) { return (type == 12 || type == 14) && rows >= mfma_min_rows(); }
+bool mfma_supported(int type) { return type == 12 || type == 14; }
+
+// The small-M kernel's time grows with every 16 activation rows (it streams the weights once per 16-row tile);
+// the tiled kernel's stays flat while its grid (64-row weight tiles x 64-row activation tiles) leaves CUs idle,
+// each workgroup walking the whole input dimension. Measured on MI355X (graph replay, weights rotated past the
+// cache, Llama-3-8B shapes, us small-M vs tiled): at 16 rows small-M wins everywhere (gate/up pair 34.6 vs 35.7);
+// from 17 rows the tiled kernel wins once its grid reaches 96 workgroups (14336x4096 Q4_K at 24 rows 31.2 vs
+// 25.9, fused q/k/v 32.8 vs 25.0) and loses below it (4096x4096 Q4_K at 64 rows 20.9 vs 25.4, at 96 rows and 128
+// workgroups 29.4 vs 25.5). Q6_K operands cost the tiled kernel more per workgroup: 4096x14336 stays on small-M
+// at 96 rows (109 vs 120) and switches at 128 (144 vs 123), i.e. from rows x out_rows >= 448 Ki.
+bool mfma_tiled_preferred(int type, int rows, int o_tiles, long out_rows) {
+    if (rows <= 16) return false;
+    if ((long)o_tiles * ((rows + 63) / 64) < 96) return false;
+    return type != 14 || (long)rows * out_rows >= 448L * 1024;
+}
 
 hipError_t launch_project_mfma(int type, const ProjJob* jobs, int njobs, int in, int rows, ActQ act,
                                hipStream_t st) {

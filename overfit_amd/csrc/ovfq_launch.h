@@ -38,8 +38,14 @@ bool gemv_supported(int in);
 bool gemv_quantize_inside(int in);
 hipError_t launch_gemv_kquant(int type, const ProjJob* jobs, int njobs, int in, const float* x, ActQ act,
                               hipStream_t st);
-// Batched (M >= mfma_min_rows) K-quant projection on int8 MFMA; bit-identical to launch_project_kquant.
-bool mfma_supported(int type, int rows);
+// Batched K-quant projection on int8 MFMA over 64-row weight tiles x 64/128-row activation tiles; bit-identical
+// to launch_project_kquant at any rows.
+bool mfma_supported(int type);
+// Automatic choice of that kernel over the small-M kernel for `rows` activation rows against weights of `o_tiles`
+// 64-row tiles and `out_rows` output rows in all (both kernels able to run).
+bool mfma_tiled_preferred(int type, int rows, int o_tiles, long out_rows);
+// Rows from which the tiled kernel runs where the small-M kernel cannot (input sizes past 16384).
+constexpr int kMfmaMinRows = 32;
 hipError_t launch_project_mfma(int type, const ProjJob* jobs, int njobs, int in, int rows, ActQ act,
                                hipStream_t st);
 // Small-batch / grouped-expert K-quant projection. One or two matrices per expert (gate, up) of equal shape;

@@ -100,6 +100,17 @@ class Context:
     def synchronize(self):
         self.check(self.lib.ovfq_ctx_synchronize(self.handle))
 
+    BATCHED_KERNELS = {"auto": 0, "small": 1, "tiled": 2}
+
+    def set_batched_kernel(self, kind: str):
+        """Kernel for batched K-quant work of 3+ rows: "auto" (by shape), "small" (super-block-parallel small-M
+        kernel where it takes the shape) or "tiled" (64-row-tiled kernel); outputs are bit-identical. The
+        reference's test-only BatchedQuantProjection.UseWeightStationaryQ4K toggle
+        (RT/BatchedQuantProjection.cs:21-24) plays this part there."""
+        if kind not in self.BATCHED_KERNELS:
+            raise ValueError(f"batched kernel must be one of {sorted(self.BATCHED_KERNELS)}, not {kind!r}")
+        self.check(self.lib.ovfq_ctx_set_batched_kernel(self.handle, self.BATCHED_KERNELS[kind]))
+
     def close(self):
         if self.handle:
             self.lib.ovfq_ctx_destroy(self.handle)

@@ -33,6 +33,7 @@ def test_null_arguments_are_rejected_before_device_work():
     assert lib.ovfq_project(None, None, None, 1, None, None) == _lib.OVFQ_ERR_NULL
     assert lib.ovfq_quantize_q8k(None, None, 1, 256, None, None, None) == _lib.OVFQ_ERR_NULL
     assert lib.ovfq_ctx_destroy(None) == _lib.OVFQ_ERR_NULL
+    assert lib.ovfq_ctx_set_batched_kernel(None, 0) == _lib.OVFQ_ERR_NULL
     assert lib.ovfq_weight_destroy(None) == _lib.OVFQ_ERR_NULL
 
 

@@ -16,6 +16,7 @@ pytestmark = pytest.mark.gpu
 
 torch = pytest.importorskip("torch")
 ov = pytest.importorskip("overfit_amd")
+from overfit_amd import _lib  # noqa: E402
 
 DEV = "cuda:0"
 
@@ -47,6 +48,19 @@ def t(a):
 @pytest.fixture(scope="module")
 def ctx():
     return ov.default_context()
+
+
+@pytest.fixture
+def batched(ctx):
+    """Forces the batched K-quant kernel ("small" / "tiled") for one test; automatic again afterwards."""
+    yield ctx.set_batched_kernel
+    ctx.set_batched_kernel("auto")
+
+
+def test_batched_kernel_choice_rejects_unknown(ctx):
+    with pytest.raises(ValueError):
+        ctx.set_batched_kernel("fast")
+    assert ctx.lib.ovfq_ctx_set_batched_kernel(ctx.handle, 3) == _lib.OVFQ_ERR_RANGE
 
 
 # ------------------------------------------------------------------------------------------------ quantizers
@@ -155,10 +169,12 @@ def test_kquant_project_bit_exact(orc, ctx, fmt, k, n, with_bias):
     assert_bit_exact(ov.project(w, x, bias), ref, f"{fmt} {k}x{n} host")
 
 
+@pytest.mark.parametrize("kernel", ["small", "tiled"])
 @pytest.mark.parametrize("fmt", ["q4k", "q6k"])
 @pytest.mark.parametrize("rows", [2, 3, 16, 17, 70])
-def test_kquant_batched_bit_exact(orc, fmt, rows):
-    case("batched", fmt, rows)
+def test_kquant_batched_bit_exact(orc, batched, kernel, fmt, rows):
+    case("batched", kernel, fmt, rows)
+    batched(kernel)
     rng = np.random.default_rng(rows * 13)
     k, n = 1024, 96
     blocks = _kq_blocks(rng, fmt, n, k)
@@ -174,16 +190,19 @@ def test_kquant_batched_bit_exact(orc, fmt, rows):
 
 # ------------------------------------------------------------------------------------------------ prefill (MFMA)
 
-# rows >= 32 run on the int8-MFMA kernel: partial activation tiles (33, 70, 200), partial 64-row weight tiles
-# (n = 130, 200, 1000), an odd super-block count (k = 2304: Q6_K rows only 2-byte aligned), one super-block.
-PREFILL_SHAPES = [(32, 256, 64), (33, 768, 1000), (64, 1024, 96), (70, 512, 200), (128, 4096, 130),
-                  (200, 2304, 64)]
+# Both batched int8-MFMA kernels on every shape (the 64-row-tiled one and the small-M one, forced): partial
+# activation tiles (17, 24, 33, 70, 200), partial 64-row weight tiles (n = 130, 200, 1000), an odd super-block
+# count (k = 2304: Q6_K rows only 2-byte aligned), one super-block.
+PREFILL_SHAPES = [(17, 512, 200), (24, 1024, 64), (32, 256, 64), (33, 768, 1000), (64, 1024, 96), (70, 512, 200),
+                  (128, 4096, 130), (200, 2304, 64)]
 
 
+@pytest.mark.parametrize("kernel", ["tiled", "small"])
 @pytest.mark.parametrize("fmt", ["q4k", "q6k"])
 @pytest.mark.parametrize("rows,k,n", PREFILL_SHAPES)
-def test_kquant_prefill_bit_exact(orc, ctx, fmt, rows, k, n):
-    case("prefill", fmt, rows, k, n)
+def test_kquant_prefill_bit_exact(orc, ctx, batched, kernel, fmt, rows, k, n):
+    case("prefill", kernel, fmt, rows, k, n)
+    batched(kernel)
     rng = np.random.default_rng(rows * 7 + k + n)
     blocks = _kq_blocks(rng, fmt, n, k)
     x = normal(rng, (rows, k))
@@ -200,11 +219,12 @@ def test_kquant_prefill_bit_exact(orc, ctx, fmt, rows, k, n):
 
 @pytest.mark.parametrize("fmt", ["q4k", "q6k"])
 @pytest.mark.parametrize("rows,k,n", [(32, 256, 64), (70, 512, 200), (128, 4096, 130), (200, 2304, 64)])
-def test_prepared_mfma_prefill_bit_exact(orc, ctx, fmt, rows, k, n):
-    """The opt-in MFMA-ready copy (ovfq_weight_prepare_mfma; Q6_K, a no-op for Q4_K): batched projections read the
-    prepared operands and stay bit-exact (n not a multiple of 64: the last tile's absent rows), before and after
-    preparing, repeatedly."""
+def test_prepared_mfma_prefill_bit_exact(orc, ctx, batched, fmt, rows, k, n):
+    """The opt-in MFMA-ready copy (ovfq_weight_prepare_mfma; Q6_K, a no-op for Q4_K): batched projections on the
+    tiled kernel read the prepared operands and stay bit-exact (n not a multiple of 64: the last tile's absent
+    rows), before and after preparing, repeatedly."""
     case("prepared prefill", fmt, rows, k, n)
+    batched("tiled")
     rng = np.random.default_rng(rows * 11 + k + n)
     blocks = _kq_blocks(rng, fmt, n, k)
     x = normal(rng, (rows, k))
@@ -221,10 +241,12 @@ def test_prepared_mfma_prefill_bit_exact(orc, ctx, fmt, rows, k, n):
         assert_bit_exact(yd.cpu().numpy().reshape(rows, n), ref, f"{fmt} {rows}x{k}x{n} prepared rep {rep}")
 
 
-def test_prepared_mfma_multi_job_and_mixed(orc, ctx):
-    """A fused q/k/v-style launch of Q6_K weights over M = 48 rows with every weight prepared (the prepared kernel
-    variant), with one weight unprepared (the GGUF-operand variant for the whole launch), and Q8_0 rejected."""
+def test_prepared_mfma_multi_job_and_mixed(orc, ctx, batched):
+    """A fused q/k/v-style launch of Q6_K weights over M = 48 rows on the tiled kernel with every weight prepared
+    (the prepared kernel variant), with one weight unprepared (the GGUF-operand variant for the whole launch), and
+    Q8_0 rejected."""
     case("prepared multi", 48)
+    batched("tiled")
     rng = np.random.default_rng(48)
     rows, k, shapes = 48, 1024, [192, 64, 80]
     blocks = [_kq_blocks(rng, "q6k", n, k) for n in shapes]
@@ -244,11 +266,12 @@ def test_prepared_mfma_multi_job_and_mixed(orc, ctx):
         ov.Q8Weight(wq, wsc, 64, 8).prepare_mfma()
 
 
-@pytest.mark.parametrize("rows", [5, 40])
-def test_multi_projection_rows_bit_exact(orc, ctx, rows):
-    """Fused q/k/v-style launch over `rows` activation rows (rows = 40 takes the MFMA kernel's multi-job grid,
-    rows = 5 the small-M kernel), from the fp32 input and from a shared prequantised activation."""
-    case("multi rows", rows)
+@pytest.mark.parametrize("rows,kernel", [(5, "auto"), (40, "tiled"), (40, "small")])
+def test_multi_projection_rows_bit_exact(orc, ctx, batched, rows, kernel):
+    """Fused q/k/v-style launch over `rows` activation rows (the tiled kernel's multi-job grid, or the small-M
+    kernel per weight), from the fp32 input and from a shared prequantised activation."""
+    case("multi rows", rows, kernel)
+    batched(kernel)
     rng = np.random.default_rng(400 + rows)
     k, shapes = 1024, [192, 64, 80]
     blocks = [_kq_blocks(rng, "q4k", n, k) for n in shapes]
@@ -407,11 +430,12 @@ def _moe_check(y, ref, what):
     assert cos >= 0.99999 and err <= 1e-3 * scale, what
 
 
-@pytest.mark.parametrize("rows", [1, 5, 40])
-def test_ffn_swiglu_matches_oracle(orc, rows):
+@pytest.mark.parametrize("rows,kernel", [(1, "auto"), (5, "auto"), (40, "tiled"), (40, "small")])
+def test_ffn_swiglu_matches_oracle(orc, batched, rows, kernel):
     """The fused decode/prefill FFN (gate/up -> SiLU*up + Q8_K -> down) against the oracle's
-    DecodeSwiGluBatchedDispatched restatement: rows 1 (GEMV), 5 (small-M MFMA), 40 (prefill MFMA)."""
-    case("ffn swiglu", rows)
+    DecodeSwiGluBatchedDispatched restatement: rows 1 (GEMV), 5 (small-M MFMA), 40 (both batched MFMA kernels)."""
+    case("ffn swiglu", rows, kernel)
+    batched(kernel)
     rng = np.random.default_rng(70 + rows)
     dm, dff = 1024, 2048
     gb, ub = orc.quantize_q4k(normal(rng, (dff, dm), 0.05)), orc.quantize_q4k(normal(rng, (dff, dm), 0.05))
@@ -609,9 +633,11 @@ def test_kquant_long_rows_bit_exact(orc, fmt, rows):
     assert_bit_exact(y, ref, f"{fmt} K={k} rows={rows}")
 
 
+@pytest.mark.parametrize("kernel", ["tiled", "small"])
 @pytest.mark.parametrize("fmt", ["q4k", "q6k"])
-def test_kquant_prefill_range_extremes(orc, fmt):
-    case("prefill extremes", fmt)
+def test_kquant_prefill_range_extremes(orc, batched, kernel, fmt):
+    case("prefill extremes", kernel, fmt)
+    batched(kernel)
     rows, k, n = 48, 1024, 64
     blocks = _extreme_blocks(fmt, n, k)
     rng = np.random.default_rng(5)
