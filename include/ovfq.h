@@ -67,16 +67,19 @@ OVFQ_API int ovfq_ctx_set_stream(ovfq_ctx* ctx, void* stream);
 /* Returns the context to its own stream. */
 OVFQ_API int ovfq_ctx_reset_stream(ovfq_ctx* ctx);
 OVFQ_API int ovfq_ctx_synchronize(ovfq_ctx* ctx);
-/* Kernel choice for batched K-quant work of 3 or more activation rows (projections, fused q/k/v and gate/up
+/* Kernel choice for batched K-quant work of 2 or more activation rows (projections, fused q/k/v and gate/up
  * launches, the SwiGLU FFN, routed expert groups). OVFQ_BATCHED_AUTO (the default) picks by shape;
- * OVFQ_BATCHED_SMALL forces the super-block-parallel small-M kernel wherever it takes the shape (input sizes up
- * to 16384; larger ones keep the automatic choice); OVFQ_BATCHED_TILED forces the 64-row-tiled kernel. Every
- * choice gives bit-identical outputs. Counterpart of the reference's test-only A/B toggle
+ * OVFQ_BATCHED_SMALL forces the super-block-parallel small-M MFMA kernel wherever it takes the shape (3 or more
+ * rows, input sizes up to 16384); OVFQ_BATCHED_TILED the 64-row-tiled MFMA kernel (3 or more rows);
+ * OVFQ_BATCHED_ROWS the multi-row decode kernel (2 to 8 rows, rows * input_size <= 32768). Shapes a forced
+ * kernel does not take keep the automatic choice (routed experts: only SMALL / TILED apply). Every choice gives
+ * bit-identical outputs. Counterpart of the reference's test-only A/B toggle
  * BatchedQuantProjection.UseWeightStationaryQ4K (RT/BatchedQuantProjection.cs:21-24): for parity tests and
- * benches that cover both kernels on one shape. */
+ * benches that cover every kernel on one shape. */
 #define OVFQ_BATCHED_AUTO 0
 #define OVFQ_BATCHED_SMALL 1
 #define OVFQ_BATCHED_TILED 2
+#define OVFQ_BATCHED_ROWS 3
 OVFQ_API int ovfq_ctx_set_batched_kernel(ovfq_ctx* ctx, int kernel);
 /* Message for the last non-zero status returned on the calling thread ("" if none). */
 OVFQ_API const char* ovfq_last_error(void);

@@ -215,6 +215,18 @@ bool use_tiled_mfma(const ovfq_ctx* c, int type, const ovfq::ProjJob* jobs, int 
     return ovfq::mfma_tiled_preferred(type, rows, o_tiles, out_rows);
 }
 
+// Few activation rows: the multi-row decode kernel (each weight block unpacked once, one int8 dot per row). Its
+// cost grows by about one block dot per row, the small-M MFMA kernel's hardly at all (MI355X, graph replay, us,
+// multi-row / previous kernel): 2 rows 14336x4096 Q4_K 10.8 / 13.7, Q6_K 4096x14336 16.6 / 19.5; 4 rows 13.0 /
+// 14.9; 8 rows 17.8 / 16.3. A fused q/k/v launch (three weights, which the small-M kernel runs one by one) is
+// 7.0 / 19.1 at 3 rows and 10.1 / 20.0 at 8. Automatic: up to 4 rows, and up to 8 for three or more weights.
+bool use_gemv_rows(const ovfq_ctx* c, int type, int in, int rows, int count) {
+    if ((type != OVFQ_TYPE_Q4_K && type != OVFQ_TYPE_Q6_K) || !ovfq::gemv_rows_supported(in, rows)) return false;
+    if (c->batched_kernel == OVFQ_BATCHED_ROWS) return true;
+    if (c->batched_kernel != OVFQ_BATCHED_AUTO) return false;
+    return rows <= 4 || count >= 3;
+}
+
 // One launch for `count` weights sharing an activation: either the fp32 activation x (quantised inside the
 // decode kernel) or an already-quantised `act`.
 int launch_projection(ovfq_ctx* c, const ovfq_weight* const* ws, int count, const float* const* biases,
@@ -234,6 +246,8 @@ int launch_projection(ovfq_ctx* c, const ovfq_weight* const* ws, int count, cons
         HIP_TRY(ovfq::launch_project_q8_0(jobs, count, in, rows, act, c->stream));
     } else if (rows == 1 && gemv_enabled() && ovfq::gemv_supported(in)) {
         HIP_TRY(ovfq::launch_gemv_kquant(type, jobs, count, in, x, act, c->stream));
+    } else if (use_gemv_rows(c, type, in, rows, count)) {
+        HIP_TRY(ovfq::launch_gemv_rows_kquant(type, jobs, count, in, rows, act, c->stream));
     } else if (use_tiled_mfma(c, type, jobs, count, in, rows)) {
         HIP_TRY(ovfq::launch_project_mfma(type, jobs, count, in, rows, act, c->stream));
     } else if (small_mfma_enabled(rows) && ovfq::mfma_small_supported(type, in)) {
@@ -356,7 +370,8 @@ int ovfq_ctx_reset_stream(ovfq_ctx* c) {
 
 int ovfq_ctx_set_batched_kernel(ovfq_ctx* c, int kernel) {
     if (!c) return fail(OVFQ_ERR_NULL, "ctx is NULL");
-    if (kernel != OVFQ_BATCHED_AUTO && kernel != OVFQ_BATCHED_SMALL && kernel != OVFQ_BATCHED_TILED)
+    if (kernel != OVFQ_BATCHED_AUTO && kernel != OVFQ_BATCHED_SMALL && kernel != OVFQ_BATCHED_TILED &&
+        kernel != OVFQ_BATCHED_ROWS)
         return fail(OVFQ_ERR_RANGE, "unknown batched kernel choice %d", kernel);
     std::lock_guard<std::mutex> lk(c->mu);
     c->batched_kernel = kernel;

@@ -278,6 +278,223 @@ hipError_t launch_gemv(GArgs& ga, const ProjJob* jobs, int njobs, hipStream_t st
 
 bool gemv_supported(int in) { return in % kQK == 0 && in / kQK <= kGemvMaxSpr; }
 
+// ------------------------------------------------------------------------------------------ several rows
+// 2 .. kRowsMax activation rows (small batches, speculative verification): the decode kernel's persistent,
+// double-buffered weight stream, each weight block unpacked once per item (F::prep) and dotted with every
+// activation row (F::dot_p) from the rows' prequantised Q8_K copy in LDS. Per (activation row, output row) one
+// lane adds the block values in ascending block order, so outputs stay bit-identical to the reference's loop.
+constexpr int kRowsMax = 8;
+constexpr int kRowsSlots = 128;  // rows * super-blocks per row staged in LDS (<= 50 KB per workgroup)
+
+struct RArgs {
+    GJob job[kMaxJobs];
+    int njobs;
+    int total_groups;
+    int spr;
+    int rows;
+    const int8_t* q;
+    const float* s;
+    const int16_t* b;
+};
+
+template <class F, int R>
+__global__ __launch_bounds__(256) void kquant_gemv_rows_kernel(const RArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int spr = a.spr, rows = a.rows, slots = rows * spr;
+    uint8_t* lq = smem;                                                      // [rows][spr] activation slots
+    int16_t* lb = reinterpret_cast<int16_t*>(smem + slots * kLdsSlot);       // [rows][spr][16] bsums
+    float* ls = reinterpret_cast<float*>(smem + slots * (kLdsSlot + 32));    // [rows][spr] scales
+    float* red = reinterpret_cast<float*>(smem + ((slots * (kLdsSlot + 36) + 15) & ~15));
+    const int wave = wave_id();
+    const int lane = threadIdx.x & 63;
+    const int q = lane >> 2, t = lane & 3;
+    const int nchunks = (spr + 15) >> 4;
+    const int stride = gridDim.x * 4;
+    const int total = a.total_groups;
+    const uint32_t row_bytes = (uint32_t)spr * F::kBytes;
+    float* rw = red + wave * (R * kRowsMax * 17);
+
+    struct Item {
+        typename F::W w[R];
+        uint32_t bias;
+    };
+    struct Cur {
+        const uint8_t* w;
+        const float* bias;
+        float* y;
+        int n_rows;
+        int row0;
+    };
+    // job of row group g, chosen with compile-time indices (the table stays in scalar registers)
+    auto locate = [&](int g) -> Cur {
+        Cur c{a.job[0].w, a.job[0].bias, a.job[0].y, a.job[0].n_rows, a.job[0].g_begin};
+#pragma unroll
+        for (int i = 1; i < kMaxJobs; i++) {
+            const bool take = i < a.njobs && g >= a.job[i].g_begin;
+            c.w = take ? a.job[i].w : c.w;
+            c.bias = take ? a.job[i].bias : c.bias;
+            c.y = take ? a.job[i].y : c.y;
+            c.n_rows = take ? a.job[i].n_rows : c.n_rows;
+            c.row0 = take ? a.job[i].g_begin : c.row0;
+        }
+        c.row0 = (g - c.row0) * R;
+        return c;
+    };
+    // loads of item (g, c); past the end the resources have zero length (the loads return 0)
+    auto load_item = [&](int g, int c, bool valid, Item& it) {
+        const Cur jb = locate(valid ? g : 0);
+        const int row0 = jb.row0;
+        const uint64_t base_off = (uint64_t)row0 * row_bytes;
+        const uint64_t al = base_off & ~3ull;
+        const uint32_t extra = (uint32_t)(base_off & 3ull);
+        const uint64_t end = (uint64_t)min(row0 + R, jb.n_rows) * row_bytes;
+        const __amdgpu_buffer_rsrc_t wr = make_rsrc(jb.w + al, valid ? rsrc_bytes(end, al) : 0u);
+        const uint32_t sb = (uint32_t)(c * 16 + q);
+#pragma unroll
+        for (int r = 0; r < R; r++) it.w[r] = F::load_w(wr, extra + r * row_bytes + sb * F::kBytes, t);
+        const float* bias = jb.bias;
+        const bool want_bias = valid && bias != nullptr && c == nchunks - 1;
+        const __amdgpu_buffer_rsrc_t bsr = make_rsrc(bias, want_bias ? (uint32_t)jb.n_rows * 4 : 0u);
+        it.bias = ld1(bsr, (uint32_t)(row0 + lane % R) * 4);
+    };
+
+    int g = blockIdx.x * 4 + wave;
+    int c = 0;
+    Item ia, ib;
+    {
+        // Activation slots i = m * spr + sb (the LDS and the global layout agree): each 16-lane row of a wave takes
+        // one slot per pass, lane l16 its 16 quants and bsum group l16; rounds of four passes, each round's loads
+        // issued before its stores (the first item's weights go out after the first round's loads).
+        constexpr int kPasses = 4;
+        const int l16 = lane & 15, hrow = lane >> 4;
+        const int pos = F::lds_pos(16 * l16);
+        const __amdgpu_buffer_rsrc_t qr = make_rsrc(a.q, (uint32_t)slots * kQK);
+        const __amdgpu_buffer_rsrc_t br = make_rsrc(a.b, (uint32_t)slots * 32);
+        const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.s, (uint32_t)slots * 4);
+#pragma unroll 1
+        for (int base = 0; base < slots; base += 16 * kPasses) {
+            u32x4 qv[kPasses];
+            uint32_t bv[kPasses], sv[kPasses];
+#pragma unroll
+            for (int p = 0; p < kPasses; p++) {
+                const uint32_t i = (uint32_t)(base + p * 16 + wave * 4 + hrow);  // past the slots: reads return 0
+                qv[p] = ld4(qr, i * kQK + l16 * 16);
+                bv[p] = __builtin_amdgcn_raw_buffer_load_b16(br, (int)(i * 32 + l16 * 2), 0, 0);
+                sv[p] = ld1(sr, i * 4);
+            }
+            if (base == 0) load_item(g, 0, g < total, ia);
+#pragma unroll
+            for (int p = 0; p < kPasses; p++) {
+                const int i = base + p * 16 + wave * 4 + hrow;
+                if (i < slots) {
+                    *reinterpret_cast<u32x4*>(lq + i * kLdsSlot + pos) = qv[p];
+                    lb[i * 16 + l16] = (int16_t)bv[p];
+                    if (l16 == 0) ls[i] = as_float(sv[p]);
+                }
+            }
+        }
+    }
+    __syncthreads();
+    if (g >= total) return;
+
+    float acc = 0.0f;
+    auto step = [&](Item& cur, Item& nxt) -> bool {
+        int ng = g, nc = c + 1;
+        if (nc == nchunks) {
+            nc = 0;
+            ng += stride;
+        }
+        const bool more = ng < total;
+        load_item(ng, nc, more, nxt);
+        const int sb = c * 16 + q;
+        const bool live = sb < spr;
+        const int sbl = live ? sb : 0;
+        typename F::P pw[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) pw[r] = F::prep(cur.w[r], t);
+        // one activation row at a time: the rows' operands are not all held in registers at once
+#pragma unroll 1
+        for (int m = 0; m < rows; m++) {
+            const typename F::A av = F::load_a_lds(lq + m * spr * kLdsSlot, lb + m * spr * 16, ls + m * spr, sbl, t);
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const float v = F::dot_p(pw[r], av);
+                if (t == 0 && live) rw[(m * R + r) * 17 + q] = v;
+            }
+        }
+        wave_sync();
+        if (lane < rows * R) {
+            const int nq = min(16, spr - c * 16);
+            for (int qq = 0; qq < nq; qq++) acc += rw[lane * 17 + qq];
+        }
+        wave_sync();
+        if (c == nchunks - 1) {
+            const Cur jb = locate(g);
+            const int m = lane / R, r = lane % R;
+            if (lane < rows * R && jb.row0 + r < jb.n_rows) {
+                // bias[o] + sum (RT/Q4KDotKernel.cs:473); no add at all without a bias
+                jb.y[(size_t)m * jb.n_rows + jb.row0 + r] = jb.bias ? as_float(cur.bias) + acc : acc;
+            }
+            acc = 0.0f;
+        }
+        g = ng;
+        c = nc;
+        return more;
+    };
+    while (step(ia, ib) && step(ib, ia)) {
+    }
+}
+
+bool gemv_rows_supported(int in, int rows) {
+    return rows >= 2 && rows <= kRowsMax && in % kQK == 0 && rows * (in / kQK) <= kRowsSlots;
+}
+
+namespace {
+
+template <class F, int R>
+hipError_t launch_gemv_rows(RArgs& ra, const ProjJob* jobs, int njobs, hipStream_t st) {
+    int groups = 0;
+    for (int i = 0; i < njobs; i++) {
+        ra.job[i].g_begin = groups;
+        groups += (jobs[i].n_rows + R - 1) / R;
+    }
+    ra.total_groups = groups;
+    static const int forced_wg = env_int("OVFQ_GEMV_ROWS_WG_PER_CU", 0);
+    const int wg_per_cu = forced_wg > 0 ? forced_wg : 2;
+    int wgs = (groups + 3) / 4;
+    const int cap = cu_count() * wg_per_cu;
+    if (wgs > cap) wgs = cap;
+    const int slots = ra.rows * ra.spr;
+    const size_t lds = (size_t)((slots * (kLdsSlot + 36) + 15) & ~15) + 4 * R * kRowsMax * 17 * sizeof(float);
+    hipLaunchKernelGGL((kquant_gemv_rows_kernel<F, R>), dim3(wgs), dim3(256), lds, st, ra);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_gemv_rows_kquant(int type, const ProjJob* jobs, int njobs, int in, int rows, ActQ act,
+                                   hipStream_t st) {
+    if (!gemv_rows_supported(in, rows)) return hipErrorInvalidValue;
+    RArgs ra{};
+    for (int i = 0; i < kMaxJobs; i++) {
+        if (i < njobs) {
+            ra.job[i] = GJob{jobs[i].w, jobs[i].bias, jobs[i].y, jobs[i].n_rows, 0};
+        } else {
+            ra.job[i] = GJob{nullptr, nullptr, nullptr, 0, 0x7fffffff};
+        }
+    }
+    ra.njobs = njobs;
+    ra.spr = in / kQK;
+    ra.rows = rows;
+    ra.q = act.q;
+    ra.s = act.s;
+    ra.b = act.b;
+    static const int forced_r = env_int("OVFQ_GEMV_ROWS_R", 0);
+    const int R = forced_r == 1 || forced_r == 2 ? forced_r : (ra.spr <= 16 ? 2 : 1);
+    if (type == 12) return R == 2 ? launch_gemv_rows<Q4K, 2>(ra, jobs, njobs, st) : launch_gemv_rows<Q4K, 1>(ra, jobs, njobs, st);
+    return R == 2 ? launch_gemv_rows<Q6K, 2>(ra, jobs, njobs, st) : launch_gemv_rows<Q6K, 1>(ra, jobs, njobs, st);
+}
+
 // Every workgroup of the decode kernel quantises the whole activation; past 32 super-blocks (K > 8192) that
 // prologue costs more than one standalone quantise launch, so long rows are quantised once beforehand.
 bool gemv_quantize_inside(int in) {

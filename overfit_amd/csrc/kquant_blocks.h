@@ -89,6 +89,46 @@ struct Q4K {
         // q8Scale * (d * mainAcc - dmin * minAcc)
         return a.s * (d * (float)main_acc - dmin * (float)min_acc);
     }
+    // The same Dot split in two for several activation rows against one block: prep() unpacks the lane's scales,
+    // mins and nibbles once; dot_p() is the per-row remainder (identical arithmetic to dot()).
+    struct P {
+        uint32_t lo[8], hi[8];
+        uint32_t sc01, m01;
+        uint32_t dd;  // fp16 d | fp16 dmin << 16
+    };
+    __device__ __forceinline__ static P prep(const W& w, int t) {
+        P p;
+        const uint32_t sh = (t & 1) * 16;
+        const uint32_t A16 = (w.h.y >> sh) & 0xffffu, B16 = (w.h.z >> sh) & 0xffffu, C16 = (w.h.w >> sh) & 0xffffu;
+        const bool upper = t >= 2;
+        p.sc01 = upper ? ((C16 & 0x0f0fu) | ((A16 >> 2) & 0x3030u)) : (A16 & 0x3f3fu);
+        p.m01 = upper ? (((C16 >> 4) & 0x0f0fu) | ((B16 >> 2) & 0x3030u)) : (B16 & 0x3f3fu);
+        const uint32_t qw[8] = {w.a.x, w.a.y, w.a.z, w.a.w, w.b.x, w.b.y, w.b.z, w.b.w};
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            p.lo[k] = qw[k] & 0x0f0f0f0fu;
+            p.hi[k] = (qw[k] >> 4) & 0x0f0f0f0fu;
+        }
+        p.dd = w.h.x;
+        return p;
+    }
+    __device__ __forceinline__ static float dot_p(const P& p, const A& a) {
+        const uint32_t aw[16] = {a.q[0].x, a.q[0].y, a.q[0].z, a.q[0].w, a.q[1].x, a.q[1].y, a.q[1].z, a.q[1].w,
+                                 a.q[2].x, a.q[2].y, a.q[2].z, a.q[2].w, a.q[3].x, a.q[3].y, a.q[3].z, a.q[3].w};
+        int dlo = 0, dhi = 0;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            dlo = sdot4(p.lo[k], aw[k], dlo);
+            dhi = sdot4(p.hi[k], aw[8 + k], dhi);
+        }
+        int main_acc = (int)(p.sc01 & 0xffu) * dlo + (int)(p.sc01 >> 8) * dhi;
+        int min_acc = sdot2_k(a.bs.x, (int)(p.m01 & 0xffu), 0);
+        min_acc = sdot2_k(a.bs.y, (int)(p.m01 >> 8), min_acc);
+        main_acc = quad_sum(main_acc);
+        min_acc = quad_sum(min_acc);
+        const float d = half_lo(p.dd), dmin = half_hi(p.dd);
+        return a.s * (d * (float)main_acc - dmin * (float)min_acc);
+    }
 };
 
 // ------------------------------------------------------------------------------------------ Q6_K block
@@ -188,6 +228,53 @@ struct Q6K {
         part = quad_sum(part);
         const float d = half_lo(w.d);
         // d * q8Scale * mainAcc
+        return d * a.s * (float)part;
+    }
+    // prep() / dot_p(): dot() split for several activation rows against one block (see Q4K).
+    struct P {
+        uint32_t q[4][4];  // q1..q4 runs, 6-bit values
+        int s[4];
+        uint32_t d;
+        int lh;
+    };
+    __device__ __forceinline__ static P prep(const W& w, int t) {
+        P p;
+        const uint32_t m4 = 0x0f0f0f0fu, m3 = 0x30303030u;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            p.q[0][k] = (w.a[k] & m4) | ((w.h[k] << 4) & m3);
+            p.q[1][k] = (w.b[k] & m4) | ((w.h[k] << 2) & m3);
+            p.q[2][k] = ((w.a[k] >> 4) & m4) | (w.h[k] & m3);
+            p.q[3][k] = ((w.b[k] >> 4) & m4) | ((w.h[k] >> 2) & m3);
+        }
+        p.lh = t & 1;
+        const uint32_t bo = 8 * p.lh;
+        p.s[0] = __builtin_amdgcn_sbfe((int)w.s0, bo, 8);
+        p.s[1] = __builtin_amdgcn_sbfe((int)w.s0, bo + 16, 8);
+        p.s[2] = __builtin_amdgcn_sbfe((int)w.s1, bo, 8);
+        p.s[3] = __builtin_amdgcn_sbfe((int)w.s1, bo + 16, 8);
+        p.d = w.d;
+        return p;
+    }
+    __device__ __forceinline__ static float dot_p(const P& p, const A& a) {
+        const uint32_t aw[16] = {a.q[0].x, a.q[0].y, a.q[0].z, a.q[0].w, a.q[1].x, a.q[1].y, a.q[1].z, a.q[1].w,
+                                 a.q[2].x, a.q[2].y, a.q[2].z, a.q[2].w, a.q[3].x, a.q[3].y, a.q[3].z, a.q[3].w};
+        int d1 = 0, d2 = 0, d3 = 0, d4 = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            d1 = sdot4(p.q[0][k], aw[k], d1);
+            d2 = sdot4(p.q[1][k], aw[4 + k], d2);
+            d3 = sdot4(p.q[2][k], aw[8 + k], d3);
+            d4 = sdot4(p.q[3][k], aw[12 + k], d4);
+        }
+        const uint32_t hs = 16 * p.lh;
+        const int b1 = __builtin_amdgcn_sbfe((int)a.bs.x, hs, 16);
+        const int b2 = __builtin_amdgcn_sbfe((int)a.bs.y, hs, 16);
+        const int b3 = __builtin_amdgcn_sbfe((int)a.bs.z, hs, 16);
+        const int b4 = __builtin_amdgcn_sbfe((int)a.bs.w, hs, 16);
+        int part = p.s[0] * (d1 - 32 * b1) + p.s[1] * (d2 - 32 * b2) + p.s[2] * (d3 - 32 * b3) + p.s[3] * (d4 - 32 * b4);
+        part = quad_sum(part);
+        const float d = half_lo(p.d);
         return d * a.s * (float)part;
     }
 };

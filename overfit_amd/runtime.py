@@ -100,11 +100,12 @@ class Context:
     def synchronize(self):
         self.check(self.lib.ovfq_ctx_synchronize(self.handle))
 
-    BATCHED_KERNELS = {"auto": 0, "small": 1, "tiled": 2}
+    BATCHED_KERNELS = {"auto": 0, "small": 1, "tiled": 2, "rows": 3}
 
     def set_batched_kernel(self, kind: str):
-        """Kernel for batched K-quant work of 3+ rows: "auto" (by shape), "small" (super-block-parallel small-M
-        kernel where it takes the shape) or "tiled" (64-row-tiled kernel); outputs are bit-identical. The
+        """Kernel for batched K-quant work of 2+ rows: "auto" (by shape), "small" (small-M MFMA kernel), "tiled"
+        (64-row-tiled MFMA kernel) or "rows" (multi-row decode kernel), each where it takes the shape; outputs are
+        bit-identical. The
         reference's test-only BatchedQuantProjection.UseWeightStationaryQ4K toggle
         (RT/BatchedQuantProjection.cs:21-24) plays this part there."""
         if kind not in self.BATCHED_KERNELS:

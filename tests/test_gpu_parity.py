@@ -60,7 +60,7 @@ def batched(ctx):
 def test_batched_kernel_choice_rejects_unknown(ctx):
     with pytest.raises(ValueError):
         ctx.set_batched_kernel("fast")
-    assert ctx.lib.ovfq_ctx_set_batched_kernel(ctx.handle, 3) == _lib.OVFQ_ERR_RANGE
+    assert ctx.lib.ovfq_ctx_set_batched_kernel(ctx.handle, 4) == _lib.OVFQ_ERR_RANGE
 
 
 # ------------------------------------------------------------------------------------------------ quantizers
@@ -169,9 +169,9 @@ def test_kquant_project_bit_exact(orc, ctx, fmt, k, n, with_bias):
     assert_bit_exact(ov.project(w, x, bias), ref, f"{fmt} {k}x{n} host")
 
 
-@pytest.mark.parametrize("kernel", ["small", "tiled"])
+@pytest.mark.parametrize("kernel", ["small", "tiled", "rows"])
 @pytest.mark.parametrize("fmt", ["q4k", "q6k"])
-@pytest.mark.parametrize("rows", [2, 3, 16, 17, 70])
+@pytest.mark.parametrize("rows", [2, 3, 8, 16, 17, 70])
 def test_kquant_batched_bit_exact(orc, batched, kernel, fmt, rows):
     case("batched", kernel, fmt, rows)
     batched(kernel)
@@ -369,10 +369,52 @@ def test_gguf_upload_q8_0_q4k_q6k(orc, on_device):
 
 # ------------------------------------------------------------------------------------------------ small batch
 
-# 2 <= rows < 32 stream the weights with the rows staged in LDS (passes of 4): long rows (R = 1 path), the
-# largest K (64 super-blocks), an odd super-block count with 2-byte-aligned Q6_K rows, partial passes.
+# Small batches on the automatic kernel choice: long rows, the largest K (64 super-blocks), an odd super-block
+# count with 2-byte-aligned Q6_K rows, few output rows.
 SMALL_SHAPES = [("q4k", 4, 14336, 300), ("q6k", 7, 2304, 130), ("q4k", 31, 4096, 64), ("q6k", 9, 16384, 70),
                 ("q4k", 2, 256, 3)]
+
+# The multi-row decode kernel, forced: 2..8 activation rows staged in LDS (one and two staging rounds), two rows
+# per wave (K <= 4096) and one (longer rows), partial 16-block chunks (K = 2304, 4352), odd output counts.
+ROWS_SHAPES = [("q6k", 2, 16384, 70), ("q4k", 3, 4352, 129), ("q6k", 5, 2304, 33), ("q4k", 8, 4096, 130),
+               ("q6k", 8, 4096, 97), ("q4k", 4, 8192, 64), ("q4k", 7, 256, 5)]
+
+
+@pytest.mark.parametrize("fmt,rows,k,n", ROWS_SHAPES)
+def test_multi_row_decode_bit_exact(orc, batched, fmt, rows, k, n):
+    case("multi-row decode", fmt, rows, k, n)
+    batched("rows")
+    rng = np.random.default_rng(rows * 17 + n)
+    blocks = _kq_blocks(rng, fmt, n, k)
+    x = normal(rng, (rows, k))
+    bias = normal(rng, n)
+    w = (ov.Q4KWeight if fmt == "q4k" else ov.Q6KWeight)(blocks, k, n)
+    batched_ref = orc.q4k_project_batched if fmt == "q4k" else orc.q6k_project_batched
+    y = ov.project(w, t(x), t(bias), rows=rows)
+    torch.cuda.synchronize()
+    assert_bit_exact(y.cpu().numpy().reshape(rows, n), batched_ref(x, rows, blocks, k, n, bias), f"{fmt} rows {rows}")
+    assert_bit_exact(ov.project(w, x, None, rows=rows).reshape(rows, n), batched_ref(x, rows, blocks, k, n, None),
+                     f"{fmt} rows {rows} no bias")
+
+
+@pytest.mark.parametrize("rows", [2, 6])
+def test_multi_row_decode_fused_jobs(orc, ctx, rows):
+    """A q/k/v-shaped launch of three Q4_K weights over 2 and 6 rows on the automatic choice (the multi-row decode
+    kernel runs fused launches of three or more weights up to 8 rows), with a bias on one weight."""
+    case("multi-row fused", rows)
+    rng = np.random.default_rng(900 + rows)
+    k, shapes = 2048, [256, 64, 70]
+    blocks = [_kq_blocks(rng, "q4k", n, k) for n in shapes]
+    ws = [ov.Q4KWeight(b, k, n) for b, n in zip(blocks, shapes)]
+    x = normal(rng, (rows, k))
+    bias = normal(rng, shapes[1])
+    refs = [orc.q4k_project_batched(x, rows, b, k, n, bias if i == 1 else None)
+            for i, (b, n) in enumerate(zip(blocks, shapes))]
+    ys = [torch.empty(rows * n, device=DEV) for n in shapes]
+    ctx.project_multi_dev(ws, t(x), ys, [None, t(bias), None], rows=rows)
+    torch.cuda.synchronize()
+    for i, (y, ref) in enumerate(zip(ys, refs)):
+        assert_bit_exact(y.cpu().numpy().reshape(rows, -1), ref, f"fused rows={rows} job {i}")
 
 
 @pytest.mark.parametrize("fmt,rows,k,n", SMALL_SHAPES)
