@@ -425,14 +425,33 @@ __global__ __launch_bounds__(256, 2) void kquant_mfma_kernel(const MArgs a) {
         stage(0, 0);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        for (int sb = 0; sb < spr; sb++) {
-            // next super-block's weights (registers) and activation (LDS DMA) in flight during this one's compute
-            const typename F::W wnxt = F::load(wr, woff + (uint32_t)(sb + 1) * F::kBytes, g);  // past the row: unused
-            if (sb + 1 < spr) stage(sb + 1, (sb + 1) & 1);
-            compute(sb & 1, wcur);
-            wcur = wnxt;
-            __builtin_amdgcn_s_waitcnt(0);  // the DMA writes to LDS are complete before the barrier publishes them
-            __syncthreads();
+        if constexpr (F::kNumMfma == 3) {
+            // Q4_K: two super-blocks per iteration, the weight registers alternating without copies (3-5 % faster
+            // on MI355X; the Q6_K build is slower unrolled). Same loads, waits and barriers as the loop below.
+            typename F::W walt;
+            for (int sb = 0; sb < spr; sb += 2) {
+                walt = F::load(wr, woff + (uint32_t)(sb + 1) * F::kBytes, g);  // past the row: unused
+                if (sb + 1 < spr) stage(sb + 1, 1);
+                compute(0, wcur);
+                __builtin_amdgcn_s_waitcnt(0);
+                __syncthreads();
+                if (sb + 1 >= spr) break;
+                wcur = F::load(wr, woff + (uint32_t)(sb + 2) * F::kBytes, g);
+                if (sb + 2 < spr) stage(sb + 2, 0);
+                compute(1, walt);
+                __builtin_amdgcn_s_waitcnt(0);
+                __syncthreads();
+            }
+        } else {
+            for (int sb = 0; sb < spr; sb++) {
+                // next super-block's weights (registers) and activation (LDS DMA) in flight during this one's compute
+                const typename F::W wnxt = F::load(wr, woff + (uint32_t)(sb + 1) * F::kBytes, g);  // past the row: unused
+                if (sb + 1 < spr) stage(sb + 1, (sb + 1) & 1);
+                compute(sb & 1, wcur);
+                wcur = wnxt;
+                __builtin_amdgcn_s_waitcnt(0);  // the DMA writes to LDS are complete before the barrier publishes them
+                __syncthreads();
+            }
         }
     } else {
         auto load_pre = [&](int sb) {
