@@ -472,10 +472,11 @@ def _moe_check(y, ref, what):
     assert cos >= 0.99999 and err <= 1e-3 * scale, what
 
 
-@pytest.mark.parametrize("rows,kernel", [(1, "auto"), (5, "auto"), (40, "tiled"), (40, "small")])
+@pytest.mark.parametrize("rows,kernel", [(1, "auto"), (3, "auto"), (5, "auto"), (40, "tiled"), (40, "small")])
 def test_ffn_swiglu_matches_oracle(orc, batched, rows, kernel):
     """The fused decode/prefill FFN (gate/up -> SiLU*up + Q8_K -> down) against the oracle's
-    DecodeSwiGluBatchedDispatched restatement: rows 1 (GEMV), 5 (small-M MFMA), 40 (both batched MFMA kernels)."""
+    DecodeSwiGluBatchedDispatched restatement: rows 1 (GEMV), 3 (multi-row decode kernel), 5 (small-M MFMA), 40 (both
+    batched MFMA kernels)."""
     case("ffn swiglu", rows, kernel)
     batched(kernel)
     rng = np.random.default_rng(70 + rows)
