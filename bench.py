@@ -232,10 +232,9 @@ def main():
                 "pct_peak": round(100 * nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 2), "algorithmic_bytes": nbytes,
                 "copies": n_copies, "what": label}
 
-    def prefill_line(m=512, n_layers=2):
-        """benchmark config 3: the layer's seven projections at M = m rows on the int8-MFMA kernel, in four launches
-        (fused q/k/v, o, fused gate/up, down; each quantises its fp32 input to Q8_K first), graph-replayed over
-        n_layers weight copies."""
+    def rows_layer(m):
+        """fp32 inputs / outputs for the layer's four projection launches at m rows, and the step over one copy:
+        fused q/k/v, o, fused gate/up, down, each quantising its fp32 input to Q8_K first."""
         gen2 = torch.Generator(device="cuda:0").manual_seed(9)
         xp = {name: torch.randn(m * k, generator=gen2, device=dev) for name, k in
               (("attn", 4096), ("o", 4096), ("ffn", 4096), ("down", 14336))}
@@ -246,7 +245,29 @@ def main():
             ctx.project_multi_dev([ws["o"]], xp["o"], [yp["o"]], rows=m)
             ctx.project_multi_dev([ws["gate"], ws["up"]], xp["ffn"], [yp["gate"], yp["up"]], rows=m)
             ctx.project_multi_dev([ws["down"]], xp["down"], [yp["down"]], rows=m)
+        return pstep, xp, yp
 
+    def small_batch_line(ms=(2, 4, 8)):
+        """Small batches (speculative verification, batched decode): the layer's four projection launches at M
+        rows on the automatic kernel choice (multi-row decode / small-M MFMA), graph-replayed over the copies."""
+        wb = sum(weight_bytes(n, k, fmt) for _, n, k, fmt in LAYER)
+        out = {"what": "Llama-3-8B layer projections (4 launches) at a few activation rows", "weight_bytes": wb,
+               "timing": "HIP graph replay over %d layer copies x 4, per layer" % len(copies)}
+        for m in ms:
+            pstep, xp, yp = rows_layer(m)
+            g = capture([(lambda ws=ws: pstep(ws)) for ws in copies] * 4)
+            us = replay_us(g, 4 * len(copies), 8)
+            del g, xp, yp
+            out["m%d" % m] = {"us_per_layer": round(us, 2), "tokens_per_s": round(m / (us * 1e-6), 1),
+                              "GB_s": round(wb / (us * 1e-6) / 1e9, 1)}
+        torch.cuda.empty_cache()
+        return out
+
+    def prefill_line(m=512, n_layers=2):
+        """benchmark config 3: the layer's seven projections at M = m rows on the int8-MFMA kernel, in four launches
+        (fused q/k/v, o, fused gate/up, down; each quantises its fp32 input to Q8_K first), graph-replayed over
+        n_layers weight copies."""
+        pstep, xp, yp = rows_layer(m)
         g = capture([(lambda ws=ws: pstep(ws)) for ws in copies[:n_layers]])
         us = replay_us(g, n_layers, 8)
         del g
@@ -412,6 +433,7 @@ def main():
     config1 = gemv_line(4096, 4096, "q4k", 64, "benchmark config 1: Q4_K 4096x4096 GEMV (quantise in-launch)")
     large_q4k = gemv_line(128256, 4096, "q4k", 2, "Q4_K GEMV at LM-head size (asymptotic efficiency)")
     lm_head = gemv_line(128256, 4096, "q6k", 2, "Llama-3-8B Q6_K LM head 128256x4096 (config 4)")
+    small = small_batch_line()  # before config 3, which gives the weights their MFMA-ready copies
     config3 = prefill_line()
     config4 = model_line()
     config5 = moe_line()
@@ -449,6 +471,7 @@ def main():
         "config4_32_layers_lm_head": config4,
         "config5_moe_mixtral_16tok_top2": config5,
         "ffn_swiglu_decode": ffn,
+        "small_batch_layer": small,
         "q4k_gemv_128256x4096": large_q4k,
         "q6k_lm_head_128256x4096": lm_head,
         "cpu_baseline": cpu,
