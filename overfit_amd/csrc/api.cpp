@@ -227,6 +227,14 @@ bool use_gemv_rows(const ovfq_ctx* c, int type, int in, int rows, int count) {
     return rows <= 4 || count >= 3;
 }
 
+// Whether the projection launch quantises its fp32 input itself instead of a separate Q8_K launch: one row on the
+// decode kernel (K <= 8192), or up to 64 super-blocks of rows on the multi-row decode kernel.
+bool quantize_in_launch(const ovfq_ctx* c, int type, int in, int rows, int count) {
+    if (type == OVFQ_TYPE_Q8_0) return false;
+    if (rows == 1) return gemv_enabled() && ovfq::gemv_supported(in) && ovfq::gemv_quantize_inside(in);
+    return use_gemv_rows(c, type, in, rows, count) && ovfq::gemv_rows_quantize_inside(in, rows);
+}
+
 // One launch for `count` weights sharing an activation: either the fp32 activation x (quantised inside the
 // decode kernel) or an already-quantised `act`.
 int launch_projection(ovfq_ctx* c, const ovfq_weight* const* ws, int count, const float* const* biases,
@@ -242,12 +250,14 @@ int launch_projection(ovfq_ctx* c, const ovfq_weight* const* ws, int count, cons
     }
     const int type = ws[0]->type;
     const int in = ws[0]->in;
+    if (x && rows > 1 && !use_gemv_rows(c, type, in, rows, count))
+        return fail(OVFQ_ERR_SIZE, "in-launch quantisation of %d rows needs the multi-row decode kernel", rows);
     if (type == OVFQ_TYPE_Q8_0) {
         HIP_TRY(ovfq::launch_project_q8_0(jobs, count, in, rows, act, c->stream));
     } else if (rows == 1 && gemv_enabled() && ovfq::gemv_supported(in)) {
         HIP_TRY(ovfq::launch_gemv_kquant(type, jobs, count, in, x, act, c->stream));
     } else if (use_gemv_rows(c, type, in, rows, count)) {
-        HIP_TRY(ovfq::launch_gemv_rows_kquant(type, jobs, count, in, rows, act, c->stream));
+        HIP_TRY(ovfq::launch_gemv_rows_kquant(type, jobs, count, in, rows, x, act, c->stream));
     } else if (use_tiled_mfma(c, type, jobs, count, in, rows)) {
         HIP_TRY(ovfq::launch_project_mfma(type, jobs, count, in, rows, act, c->stream));
     } else if (small_mfma_enabled(rows) && ovfq::mfma_small_supported(type, in)) {
@@ -650,8 +660,7 @@ static int project_impl(ovfq_ctx* ctx, int count, const ovfq_weight* const* ws, 
             bd[i] = biases ? biases[i] : nullptr;
         }
     }
-    if (rows == 1 && ws[0]->type != OVFQ_TYPE_Q8_0 && gemv_enabled() && ovfq::gemv_supported(in) &&
-        ovfq::gemv_quantize_inside(in)) {
+    if (quantize_in_launch(ctx, ws[0]->type, in, rows, count)) {
         // Decode: the Q8_K quantisation happens inside the projection launch.
         if ((rc = launch_projection(ctx, ws, count, bd, yd, rows, ovfq::ActQ{nullptr, nullptr, nullptr}, xd)))
             return rc;
@@ -1020,10 +1029,10 @@ static int ffn_impl(ovfq_ctx* ctx, const ovfq_weight* gate, const ovfq_weight* u
         xd = hx;
         yd = hy;
     }
-    // gate/up (one launch; for one row the Q8_K quantisation runs inside it)
+    // gate/up (one launch; for one or a few short rows the Q8_K quantisation runs inside it)
     const ovfq_weight* gu[2] = {gate, up};
     float* gu_out[2] = {g, u};
-    if (rows == 1 && gemv_enabled() && ovfq::gemv_supported(dmodel) && ovfq::gemv_quantize_inside(dmodel)) {
+    if (quantize_in_launch(ctx, gate->type, dmodel, rows, 2)) {
         if ((rc = launch_projection(ctx, gu, 2, nullptr, gu_out, rows, ovfq::ActQ{nullptr, nullptr, nullptr}, xd)))
             return rc;
     } else {
