@@ -281,8 +281,9 @@ bool gemv_supported(int in) { return in % kQK == 0 && in / kQK <= kGemvMaxSpr; }
 // ------------------------------------------------------------------------------------------ several rows
 // 2 .. kRowsMax activation rows (small batches, speculative verification): the decode kernel's persistent,
 // double-buffered weight stream, each weight block unpacked once per item (F::prep) and dotted with every
-// activation row (F::dot_p) from the rows' prequantised Q8_K copy in LDS. Per (activation row, output row) one
-// lane adds the block values in ascending block order, so outputs stay bit-identical to the reference's loop.
+// activation row (F::dot_p) from the rows' Q8_K copy in LDS (quantised in the launch from fp32 rows, or copied
+// from a prequantised activation). Per (activation row, output row) one lane adds the block values in ascending
+// block order, so outputs stay bit-identical to the reference's loop.
 constexpr int kRowsMax = 8;
 constexpr int kRowsSlots = 128;  // rows * super-blocks per row staged in LDS (<= 50 KB per workgroup)
 
