@@ -222,6 +222,10 @@ bool use_tiled_mfma(const ovfq_ctx* c, int type, const ovfq::ProjJob* jobs, int 
 // 7.0 / 19.1 at 3 rows and 10.1 / 20.0 at 8. Automatic: up to 4 rows, and up to 8 for three or more weights.
 bool use_gemv_rows(const ovfq_ctx* c, int type, int in, int rows, int count) {
     if ((type != OVFQ_TYPE_Q4_K && type != OVFQ_TYPE_Q6_K) || !ovfq::gemv_rows_supported(in, rows)) return false;
+    // Decode rows of 16384 < K <= 32768, past the one-row kernel (which is faster wherever it runs: MI355X, us, one-row
+    // / multi-row kernel at M = 1: 4096x4096 Q4_K 4.8 / 5.5, 4096x14336 Q6_K 14.0 / 14.3). At K = 28672 it
+    // replaces the general kernel: 8192 rows Q4_K 31.1 -> 28.7, Q6_K 51.7 -> 40.4.
+    if (rows == 1) return gemv_enabled() && !ovfq::gemv_supported(in);
     if (c->batched_kernel == OVFQ_BATCHED_ROWS) return true;
     if (c->batched_kernel != OVFQ_BATCHED_AUTO) return false;
     return rows <= 4 || count >= 3;
@@ -231,7 +235,7 @@ bool use_gemv_rows(const ovfq_ctx* c, int type, int in, int rows, int count) {
 // decode kernel (K <= 8192), or up to 64 super-blocks of rows on the multi-row decode kernel.
 bool quantize_in_launch(const ovfq_ctx* c, int type, int in, int rows, int count) {
     if (type == OVFQ_TYPE_Q8_0) return false;
-    if (rows == 1) return gemv_enabled() && ovfq::gemv_supported(in) && ovfq::gemv_quantize_inside(in);
+    if (rows == 1 && ovfq::gemv_supported(in)) return gemv_enabled() && ovfq::gemv_quantize_inside(in);
     return use_gemv_rows(c, type, in, rows, count) && ovfq::gemv_rows_quantize_inside(in, rows);
 }
 

@@ -484,7 +484,7 @@ __global__ __launch_bounds__(256) void kquant_gemv_rows_kernel(const RArgs a) {
 }
 
 bool gemv_rows_supported(int in, int rows) {
-    return rows >= 2 && rows <= kRowsMax && in % kQK == 0 && rows * (in / kQK) <= kRowsSlots;
+    return rows >= 1 && rows <= kRowsMax && in % kQK == 0 && rows * (in / kQK) <= kRowsSlots;
 }
 
 // Every workgroup quantises all rows of its activation; up to 64 super-blocks in all (four 4096-element rows) that
@@ -505,8 +505,10 @@ hipError_t launch_gemv_rows(RArgs& ra, const ProjJob* jobs, int njobs, hipStream
         groups += (jobs[i].n_rows + R - 1) / R;
     }
     ra.total_groups = groups;
+    // Workgroups per CU: 2; one long row (K > 16384, past the one-row decode kernel) takes 3 like that kernel's
+    // long rows.
     static const int forced_wg = env_int("OVFQ_GEMV_ROWS_WG_PER_CU", 0);
-    const int wg_per_cu = forced_wg > 0 ? forced_wg : 2;
+    const int wg_per_cu = forced_wg > 0 ? forced_wg : (ra.rows == 1 && ra.spr > 16 ? 3 : 2);
     int wgs = (groups + 3) / 4;
     const int cap = cu_count() * wg_per_cu;
     if (wgs > cap) wgs = cap;

@@ -36,8 +36,9 @@ hipError_t launch_project_kquant(int type, const ProjJob* jobs, int njobs, int i
 // inside the launch; x == NULL copies the prequantised `act`. Requires gemv_supported(in).
 bool gemv_supported(int in);
 bool gemv_quantize_inside(int in);
-// Decode kernel over 2 .. 8 activation rows (rows * in / 256 <= 128): from the fp32 rows x, quantised inside the
-// launch (requires gemv_rows_quantize_inside), or, x == NULL, from the prequantised `act`.
+// Decode kernel over 1 .. 8 activation rows (rows * in / 256 <= 128; one row only where gemv_supported fails): from
+// the fp32 rows x, quantised inside the launch (requires gemv_rows_quantize_inside), or, x == NULL, from the
+// prequantised `act`.
 bool gemv_rows_supported(int in, int rows);
 bool gemv_rows_quantize_inside(int in, int rows);
 hipError_t launch_gemv_rows_kquant(int type, const ProjJob* jobs, int njobs, int in, int rows, const float* x,
