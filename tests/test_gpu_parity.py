@@ -937,7 +937,8 @@ def test_graph_replay_moe_and_ffn(orc, ctx):
 
 def test_graph_replay_matches_eager(orc, ctx):
     """The bench replays captured decode steps; every replay must reproduce the eager outputs bit-for-bit
-    (replays interleaved with eager work and synchronisations)."""
+    (replays interleaved with eager work and synchronisations): one-row launches, a 3-row launch on the multi-row
+    kernel (quantised inside the launch) and a 3-row Q6_K launch of long rows (separate quantise launch)."""
     case("graph replay")
     rng = np.random.default_rng(12)
     k, n, k2 = 4096, 512, 14336
@@ -945,11 +946,15 @@ def test_graph_replay_matches_eager(orc, ctx):
     wu = ov.Q4KWeight(_kq_blocks(rng, "q4k", n, k), k, n)
     wd = ov.Q6KWeight(_kq_blocks(rng, "q6k", 256, k2), k2, 256)
     x, xd = t(normal(rng, k)), t(normal(rng, k2))
-    ys = [torch.empty(n, device=DEV), torch.empty(n, device=DEV), torch.empty(256, device=DEV)]
+    x3, xd3 = t(normal(rng, (3, k))), t(normal(rng, (3, k2)))
+    ys = [torch.empty(n, device=DEV), torch.empty(n, device=DEV), torch.empty(256, device=DEV),
+          torch.empty(3 * n, device=DEV), torch.empty(3 * n, device=DEV), torch.empty(3 * 256, device=DEV)]
 
     def step():
         ctx.project_multi_dev([wq, wu], x, ys[:2])
-        ctx.project_multi_dev([wd], xd, ys[2:])
+        ctx.project_multi_dev([wd], xd, ys[2:3])
+        ctx.project_multi_dev([wq, wu], x3, ys[3:5], rows=3)
+        ctx.project_multi_dev([wd], xd3, ys[5:], rows=3)
 
     step()
     torch.cuda.synchronize()
