@@ -978,3 +978,41 @@ def test_graph_replay_matches_eager(orc, ctx):
             assert np.array_equal(y.cpu().numpy().view(np.uint32), e.view(np.uint32)), f"replay {rep}"
         step()  # eager work between replays
         torch.cuda.synchronize()
+
+
+def test_concurrent_calls_on_one_context(orc, ctx):
+    """The reference calls Project / ProjectPreQuantized from several worker threads at once
+    (RT/CachedMultiHeadAttention.cs:280, :876-907), each with its own activation. Four threads share one context
+    (host-pointer calls: staging, launch, copy back and wait happen under the context's lock), over one-row,
+    multi-row and prefill shapes, and every output stays bit-exact."""
+    import threading
+    case("concurrent calls")
+    rng = np.random.default_rng(31)
+    k, n = 1024, 160
+    blocks = {fmt: _kq_blocks(rng, fmt, n, k) for fmt in ("q4k", "q6k")}
+    ws = {"q4k": ov.Q4KWeight(blocks["q4k"], k, n), "q6k": ov.Q6KWeight(blocks["q6k"], k, n)}
+    jobs = []
+    for i, (fmt, rows) in enumerate([("q4k", 1), ("q6k", 3), ("q4k", 40), ("q6k", 1), ("q4k", 2), ("q6k", 17)]):
+        x = normal(rng, (rows, k))
+        ref = (orc.q4k_project_batched if fmt == "q4k" else orc.q6k_project_batched)(x, rows, blocks[fmt], k, n, None)
+        jobs.append((fmt, rows, x, ref))
+    errors = []
+
+    def worker(tid):
+        try:
+            for it in range(6):
+                fmt, rows, x, ref = jobs[(tid + it) % len(jobs)]
+                y = ov.project(ws[fmt], x, None, rows=rows).reshape(rows, n)
+                if not np.array_equal(y.view(np.uint32), ref.view(np.uint32)):
+                    errors.append(f"thread {tid} iteration {it}: {fmt} rows={rows} differs")
+        except Exception as e:  # noqa: BLE001 - reported below
+            errors.append(f"thread {tid}: {e!r}")
+
+    threads = [threading.Thread(target=worker, args=(tid,)) for tid in range(4)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(timeout=60)
+    assert not any(th.is_alive() for th in threads), "a worker did not finish"
+    assert not errors, errors
+
