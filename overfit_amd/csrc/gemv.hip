@@ -263,9 +263,9 @@ hipError_t launch_gemv(GArgs& ga, const ProjJob* jobs, int njobs, hipStream_t st
         groups += (jobs[i].n_rows + R - 1) / R;
     }
     ga.total_groups = groups;
-    // Workgroups per CU (measured on MI355X): 2 for rows of up to 16 blocks, 3 for longer rows.
+    // Workgroups per CU (measured on MI355X): 2 with two rows per wave (Q4_K rows of up to 16 blocks), else 3.
     static const int forced_wg = env_int("OVFQ_GEMV_WG_PER_CU", 0);
-    const int wg_per_cu = forced_wg > 0 ? forced_wg : (ga.spr <= 16 ? 2 : 3);
+    const int wg_per_cu = forced_wg > 0 ? forced_wg : (R == 2 ? 2 : 3);
     int wgs = (groups + 3) / 4;
     const int cap = cu_count() * wg_per_cu;
     if (wgs > cap) wgs = cap;
@@ -569,8 +569,10 @@ hipError_t launch_gemv_kquant(int type, const ProjJob* jobs, int njobs, int in, 
     ga.b = act.b;
     static const int forced_r = env_int("OVFQ_GEMV_ROWS_PER_WAVE", 0);
     int R = forced_r;
-    // Rows per wave (measured on MI355X): 2 for rows of up to 16 blocks (K <= 4096), 1 for longer rows.
-    if (R != 1 && R != 2 && R != 4) R = ga.spr <= 16 ? 2 : 1;
+    // Rows per wave (measured on MI355X): 2 for Q4_K rows of up to 16 blocks (K <= 4096), else 1. Q6_K at K = 4096
+    // is 7-11 % faster with one row per wave and three workgroups per CU (4096 rows 7.05 -> 6.29 us, 14336 rows
+    // 14.3 -> 12.7 us; the 128256-row LM head 85.3 -> 84.3 us).
+    if (R != 1 && R != 2 && R != 4) R = type == 12 && ga.spr <= 16 ? 2 : 1;
     if (type == 12) {
         if (R == 4) return launch_gemv<Q4K, 4>(ga, jobs, njobs, st);
         if (R == 2) return launch_gemv<Q4K, 2>(ga, jobs, njobs, st);
