@@ -371,10 +371,10 @@ def main():
         del g, sets
         torch.cuda.empty_cache()
         return {"what": "benchmark config 5: Mixtral-8x7B experts (Q4_K gate/up/down), 16 tokens, top-2, one MoE "
-                        "step (route + group + 2 grouped projections + SwiGLU + combine, 7 launches)",
+                        "step (route + group/quantise + 2 grouped projections + SwiGLU + combine, 6 launches)",
                 "us": round(us, 1), "experts_used": used, "weight_bytes": wb,
                 "GB_s": round(wb / (us * 1e-6) / 1e9, 1), "pct_peak": round(100 * wb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 2),
-                "timing": "HIP graph replay over %d expert sets, per step" % n_sets}
+                "timing": "HIP graph replay of 8 steps over %d expert sets, per step" % n_sets}
 
     def ffn_line():
         """The fused decode FFN: gate/up -> SiLU*up + Q8_K -> down for one token, 3 launches, over the

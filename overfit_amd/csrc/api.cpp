@@ -934,12 +934,18 @@ static int moe_impl(ovfq_ctx* ctx, int E, const ovfq_weight* const* gate, const 
         wd = hw;
         yd = hy;
     }
-    ovfq::ActQ act;
-    if ((rc = quantize_into_scratch(ctx, gt, xd, rows, dmodel, &act))) return rc;
+    // the grouping plan and the Q8_K quantisation of x share one launch (neither depends on the other)
+    const size_t n_x = (size_t)rows * dmodel;
+    if ((rc = ensure(ctx, ctx->act_q, n_x)) || (rc = ensure(ctx, ctx->act_s, n_x / OVFQ_QK * sizeof(float))) ||
+        (rc = ensure(ctx, ctx->act_b, n_x / 16 * sizeof(int16_t))))
+        return rc;
+    const ovfq::ActQ act{(const int8_t*)ctx->act_q.p, (const float*)ctx->act_s.p, (const int16_t*)ctx->act_b.p};
     int* tile_count = off + E + 1;
     int* tiles = off + E + 2;
     HIP_TRY(ovfq::launch_moe_plan(idxd, rows, k, E, off, prow, pof, ovfq::kGroupedTileRows,
-                                  grouped_big ? tiles : nullptr, tile_count, ctx->stream));
+                                  grouped_big ? tiles : nullptr, tile_count, xd, (int64_t)(n_x / OVFQ_QK),
+                                  (int8_t*)ctx->act_q.p, (float*)ctx->act_s.p, (int16_t*)ctx->act_b.p,
+                                  ctx->stream));
     const uint8_t* gw[OVFQ_MAX_EXPERTS];
     const uint8_t* uw[OVFQ_MAX_EXPERTS];
     const uint8_t* dw[OVFQ_MAX_EXPERTS];

@@ -2,7 +2,8 @@
 //
 // MoeFeedForwardBlock.DecodeBatched (RT/MoeFeedForwardBlock.cs:140-241) without its router projection:
 //   1. MoeRouter.SelectTopK per token (RT/MoeRouter.cs:40-128)                       -> moe_topk_kernel
-//   2. group the (token, top-k slot) pairs by expert, tokens ascending               -> moe_plan_kernel
+//   2. group the (token, top-k slot) pairs by expert, tokens ascending, and quantise
+//      the tokens' activation to Q8_K in the same launch                            -> moe_plan_kernel
 //   3. per expert: gate/up = batched projections of its tokens                   (mfma.hip, grid.y = expert)
 //   4. SiLU(gate) * up, quantised to Q8_K for the down projection                    -> swiglu_q8k_kernel
 //   5. per expert: down projection of its pairs                                  (mfma.hip)
@@ -83,10 +84,20 @@ __global__ __launch_bounds__(64) void moe_topk_kernel(const float* __restrict__ 
 // routing table is staged in LDS when it fits (rows * k ints <= 48 KB).
 // With `tiles`, it also lists the experts' pair ranges in tiles of `nt` rows, expert-major: entry t = expert | (tile
 // index within the expert << 8), with the list's length at *tile_count.
+// Workgroup 0 does all of the above; workgroups 1.. quantise the tokens' activation x to Q8_K (one wave per
+// 256-element block, the standalone quantiser's arithmetic), which the plan does not depend on: one launch for both.
 __global__ __launch_bounds__(256) void moe_plan_kernel(const int* __restrict__ idx_g, int rows, int k, int n_experts,
                                                        int* __restrict__ expert_off, int* __restrict__ pair_row,
                                                        int* __restrict__ pair_of, int staged, int nt,
-                                                       int* __restrict__ tiles, int* __restrict__ tile_count) {
+                                                       int* __restrict__ tiles, int* __restrict__ tile_count,
+                                                       const float* __restrict__ x, int64_t n_blocks,
+                                                       int8_t* __restrict__ xq, float* __restrict__ xs,
+                                                       int16_t* __restrict__ xb) {
+    if (blockIdx.x > 0) {
+        const int64_t blk = (int64_t)(blockIdx.x - 1) * 4 + wave_id();
+        if (blk < n_blocks) q8k_quantize_block(x, blk, xq, xs, xb);
+        return;
+    }
     extern __shared__ int sidx[];
     __shared__ int run[kMaxExperts];        // first position of the current chunk's claimers, per expert
     __shared__ int wcnt[4][kMaxExperts];    // claimers per wave of the current chunk, per expert
@@ -227,11 +238,14 @@ hipError_t launch_moe_topk(const float* logits, int rows, int n_experts, int k, 
 }
 
 hipError_t launch_moe_plan(const int* idx, int rows, int k, int n_experts, int* expert_off, int* pair_row,
-                           int* pair_of, int nt, int* tiles, int* tile_count, hipStream_t st) {
+                           int* pair_of, int nt, int* tiles, int* tile_count, const float* x, int64_t n_blocks,
+                           int8_t* xq, float* xs, int16_t* xb, hipStream_t st) {
     const size_t bytes = (size_t)rows * k * sizeof(int);
     const int staged = bytes <= 48 * 1024;
-    hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(256), staged ? bytes : 0, st, idx, rows, k, n_experts, expert_off,
-                       pair_row, pair_of, staged, nt, tiles, tile_count);
+    const int64_t grid = 1 + (n_blocks + 3) / 4;
+    hipLaunchKernelGGL(moe_plan_kernel, dim3((unsigned)grid), dim3(256), staged ? bytes : 0, st, idx, rows, k,
+                       n_experts, expert_off, pair_row, pair_of, staged, nt, tiles, tile_count, x, n_blocks, xq, xs,
+                       xb);
     return hipGetLastError();
 }
 

@@ -141,6 +141,18 @@ __device__ __forceinline__ Q8KLane q8k_quantize_wave(float v0, float v1, float v
     return r;
 }
 
+// Q8_K block `blk` of x (256 floats) quantised by one wave: quants, bsums and scale written to q, bs, s.
+__device__ __forceinline__ void q8k_quantize_block(const float* __restrict__ x, int64_t blk, int8_t* __restrict__ q,
+                                                   float* __restrict__ s, int16_t* __restrict__ bs) {
+    const int lane = threadIdx.x & 63;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(x + blk * kQK, kQK * 4);
+    const u32x4 raw = ld4(xr, lane * 16);
+    const Q8KLane r = q8k_quantize_wave(as_float(raw.x), as_float(raw.y), as_float(raw.z), as_float(raw.w));
+    reinterpret_cast<uint32_t*>(q + blk * kQK)[lane] = r.packed;
+    if ((lane & 3) == 0) bs[blk * 16 + (lane >> 2)] = (int16_t)r.group_sum;
+    if (lane == 0) s[blk] = r.scale;
+}
+
 // Max over the 16 lanes of a DPP row; every lane of the row receives it. Used on the bit patterns of
 // non-negative floats, whose unsigned integer order is their numeric order.
 __device__ __forceinline__ uint32_t row16_max_u32(uint32_t v) {

@@ -84,9 +84,11 @@ hipError_t launch_mfma_prepare(int type, const uint8_t* w, int in, int out, uint
 hipError_t launch_moe_topk(const float* logits, int rows, int n_experts, int k, int stride, int normalize, int* idx,
                            float* w, hipStream_t st);
 // `tiles` (optional, else NULL): the experts' pair ranges in tiles of `nt` rows (expert | tile << 8), the count at
-// *tile_count; at most ceil(rows * k / nt) + n_experts entries.
+// *tile_count; at most ceil(rows * k / nt) + n_experts entries. The same launch quantises the n_blocks Q8_K blocks
+// of x into xq / xs / xb (n_blocks may be 0).
 hipError_t launch_moe_plan(const int* idx, int rows, int k, int n_experts, int* expert_off, int* pair_row,
-                           int* pair_of, int nt, int* tiles, int* tile_count, hipStream_t st);
+                           int* pair_of, int nt, int* tiles, int* tile_count, const float* x, int64_t n_blocks,
+                           int8_t* xq, float* xs, int16_t* xb, hipStream_t st);
 // The batched int8-MFMA kernel over expert groups: tile list entry t covers rows [64 i, 64 i + 64) of expert e's
 // pairs; gate/up pairs (w1 set) share the launch. Activation rows are gathered through pair_row (NULL: pair p reads
 // row p); outputs are pair-major.

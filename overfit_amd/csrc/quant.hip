@@ -20,13 +20,7 @@ __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float* __restri
     // wave_id() is a readfirstlane value, so the buffer resource below is provably wave-uniform (SGPRs).
     const int64_t blk = (int64_t)blockIdx.x * 4 + wave_id();
     if (blk >= n_blocks) return;
-    const int lane = threadIdx.x & 63;
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(x + blk * kQK, kQK * 4);
-    const u32x4 raw = ld4(xr, lane * 16);
-    const Q8KLane r = q8k_quantize_wave(as_float(raw.x), as_float(raw.y), as_float(raw.z), as_float(raw.w));
-    reinterpret_cast<uint32_t*>(q + blk * kQK)[lane] = r.packed;
-    if ((lane & 3) == 0) bs[blk * 16 + (lane >> 2)] = (int16_t)r.group_sum;
-    if (lane == 0) s[blk] = r.scale;
+    q8k_quantize_block(x, blk, q, s, bs);
 }
 
 // ------------------------------------------------------------------------------------------ Q8_0 activation
