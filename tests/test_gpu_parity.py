@@ -676,12 +676,15 @@ def test_kquant_long_rows_bit_exact(orc, fmt, rows):
     assert_bit_exact(y, ref, f"{fmt} K={k} rows={rows}")
 
 
-@pytest.mark.parametrize("kernel", ["tiled", "small"])
+@pytest.mark.parametrize("kernel,rows,k", [("tiled", 48, 1024), ("small", 48, 1024), ("rows", 8, 1024),
+                                           ("auto", 1, 28672)])
 @pytest.mark.parametrize("fmt", ["q4k", "q6k"])
-def test_kquant_prefill_range_extremes(orc, batched, kernel, fmt):
-    case("prefill extremes", kernel, fmt)
+def test_kquant_prefill_range_extremes(orc, batched, kernel, rows, k, fmt):
+    """Operand range extremes (every quant +-127, the largest scales and mins) on both MFMA kernels, the multi-row
+    decode kernel (8 rows) and its one-row use for long rows (K = 28672)."""
+    case("prefill extremes", kernel, rows, k, fmt)
     batched(kernel)
-    rows, k, n = 48, 1024, 64
+    n = 64
     blocks = _extreme_blocks(fmt, n, k)
     rng = np.random.default_rng(5)
     x = np.sign(normal(rng, (rows, k))).astype(np.float32)  # every quant +-127
