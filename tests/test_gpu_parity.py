@@ -218,6 +218,26 @@ def test_kquant_prefill_bit_exact(orc, ctx, batched, kernel, fmt, rows, k, n):
 
 
 @pytest.mark.parametrize("fmt", ["q4k", "q6k"])
+def test_kquant_prefill_128_row_tiles(orc, ctx, fmt):
+    """From 1024 rows the tiled kernel stages 128 activation rows per workgroup: 1100 rows (a partial last tile),
+    130 outputs (a partial 64-row weight tile), with a bias, before and after the MFMA-ready copy (Q6_K)."""
+    case("prefill 128-row tiles", fmt)
+    rows, k, n = 1100, 512, 130
+    rng = np.random.default_rng(1100)
+    blocks = _kq_blocks(rng, fmt, n, k)
+    x = normal(rng, (rows, k))
+    bias = normal(rng, n)
+    w = (ov.Q4KWeight if fmt == "q4k" else ov.Q6KWeight)(blocks, k, n)
+    ref = (orc.q4k_project_batched if fmt == "q4k" else orc.q6k_project_batched)(x, rows, blocks, k, n, bias)
+    for prepared in (False, True):
+        if prepared:
+            w.prepare_mfma()
+        yd = ov.project(w, t(x), t(bias), rows=rows)
+        torch.cuda.synchronize()
+        assert_bit_exact(yd.cpu().numpy().reshape(rows, n), ref, f"{fmt} 1100 rows prepared={prepared}")
+
+
+@pytest.mark.parametrize("fmt", ["q4k", "q6k"])
 @pytest.mark.parametrize("rows,k,n", [(32, 256, 64), (70, 512, 200), (128, 4096, 130), (200, 2304, 64)])
 def test_prepared_mfma_prefill_bit_exact(orc, ctx, batched, fmt, rows, k, n):
     """The opt-in MFMA-ready copy (ovfq_weight_prepare_mfma; Q6_K, a no-op for Q4_K): batched projections on the
