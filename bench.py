@@ -119,8 +119,9 @@ def run_cpu_baseline(layer0_host, budget_s=2.5):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=10)
+    # 2000 timed steps of ~38 us (under 0.1 s): a 200-step window still carries start-up effects (~1 % slower)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--copies", type=int, default=4, help="layer copies rotated to defeat the 256 MB cache")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile", choices=["layer", "prefill", "moe", "small"], default=None,
