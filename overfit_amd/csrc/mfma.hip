@@ -569,8 +569,14 @@ bool mfma_supported(int type) { return type == 12 || type == 14; }
 // 25.9, fused q/k/v 32.8 vs 25.0) and loses below it (4096x4096 Q4_K at 64 rows 20.9 vs 25.4, at 96 rows and 128
 // workgroups 29.4 vs 25.5). Q6_K operands cost the tiled kernel more per workgroup: 4096x14336 stays on small-M
 // at 96 rows (109 vs 120) and switches at 128 (144 vs 123), i.e. from rows x out_rows >= 448 Ki.
+// Whatever the grid, one wave of tiled workgroups costs about as much as 6 (Q4_K) or 7 (Q6_K) small-M passes at the
+// same input size, because both walk the whole input: at 256 / 1024 output rows, us small-M vs tiled, Q4_K K = 4096
+// at 80 rows 23.9 vs 23.9 and 96 rows 28.2 vs 23.9, K = 14336 at 80 rows 68.2 vs 73.8 and 96 rows 81.2 vs 73.8;
+// Q6_K K = 4096 at 96 rows 33.9 vs 34.5 and 112 rows 39.1 vs 34.8, K = 14336 at 96 rows 105.1 vs 111.5 and 112
+// rows 122.3 vs 111.0; at 512 rows and 128 output rows 138 vs 24.
 bool mfma_tiled_preferred(int type, int rows, int o_tiles, long out_rows) {
     if (rows <= 16) return false;
+    if ((rows + 15) / 16 >= (type == 14 ? 7 : 6)) return true;
     if ((long)o_tiles * ((rows + 63) / 64) < 96) return false;
     return type != 14 || (long)rows * out_rows >= 448L * 1024;
 }
