@@ -430,7 +430,7 @@ def main():
         traffic = json.load(open(tfile)).get("bytes_per_launch")
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                "kernel": "kquant_gemv_kernel<Q4K,2> (Q8_K quantise + fused gate+up GEMV, 2x14336x4096)",
+                "kernel": "kquant_gemv_kernel<Q4K,2,true> (Q8_K quantise + fused gate+up GEMV, 2x14336x4096)",
                 "avg_us": round(gu_avg, 3), "algorithmic_bytes": gu_bytes,
                 "timing": "HIP graph replay of 4x%d launches over %d weight copies, /launch" % (len(copies), len(copies))}
 

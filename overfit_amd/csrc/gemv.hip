@@ -114,7 +114,8 @@ __device__ __forceinline__ void stage_activation(const GArgs& a, uint8_t* lq, in
     }
 }
 
-template <class F, int R>
+// kMulti: the launch has several jobs (fused projections); with one, no job lookup is needed.
+template <class F, int R, bool kMulti>
 __global__ __launch_bounds__(256) void kquant_gemv_kernel(const GArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int spr = a.spr;
@@ -149,24 +150,26 @@ __global__ __launch_bounds__(256) void kquant_gemv_kernel(const GArgs a) {
         int row0;
     };
     auto locate = [&](int g) -> Cur {
-        Cur c{a.job[0].w, a.job[0].bias, a.job[0].y, a.job[0].n_rows, a.job[0].g_begin};
+        Cur c{a.job[0].w, a.job[0].bias, a.job[0].y, a.job[0].n_rows, 0};
+        if constexpr (kMulti) {
 #pragma unroll
-        for (int i = 1; i < kMaxJobs; i++) {
-            const bool take = i < a.njobs && g >= a.job[i].g_begin;
-            c.w = take ? a.job[i].w : c.w;
-            c.bias = take ? a.job[i].bias : c.bias;
-            c.y = take ? a.job[i].y : c.y;
-            c.n_rows = take ? a.job[i].n_rows : c.n_rows;
-            c.row0 = take ? a.job[i].g_begin : c.row0;
+            for (int i = 1; i < kMaxJobs; i++) {
+                const bool take = i < a.njobs && g >= a.job[i].g_begin;
+                c.w = take ? a.job[i].w : c.w;
+                c.bias = take ? a.job[i].bias : c.bias;
+                c.y = take ? a.job[i].y : c.y;
+                c.n_rows = take ? a.job[i].n_rows : c.n_rows;
+                c.row0 = take ? a.job[i].g_begin : c.row0;
+            }
         }
         c.row0 = (g - c.row0) * R;
         return c;
     };
-    // Issues the loads of item (g, c). The instruction stream is the same whether or not the item exists (past
-    // the end the resources have zero length, so the loads return 0 without touching memory): the compiler's
-    // wait counts then see a fixed number of younger loads and the prefetch overlaps the current item's math.
-    auto load_item = [&](int g, int c, bool valid, Item& it) {
-        const Cur jb = locate(valid ? g : 0);
+    // Issues the loads of item (row group of job record jb, chunk c). The instruction stream is the same whether
+    // or not the item exists (past the end the resources have zero length, so the loads return 0 without touching
+    // memory): the compiler's wait counts then see a fixed number of younger loads and the prefetch overlaps the
+    // current item's math.
+    auto load_item = [&](const Cur& jb, int c, bool valid, Item& it) {
         const int row0 = jb.row0;
         const uint64_t base_off = (uint64_t)row0 * row_bytes;
         const uint64_t al = base_off & ~3ull;
@@ -187,9 +190,12 @@ __global__ __launch_bounds__(256) void kquant_gemv_kernel(const GArgs a) {
     int g = blockIdx.x * 4 + wave;
     int c = 0;
     Item ia, ib;
-    stage_activation<F>(a, lq, lb, ls, wave, lane, [&] { load_item(g, 0, g < total, ia); });
+    // The first item's lookup runs inside the prefetch, after the activation loads have gone out (they, not the
+    // weights, bound the start of the first item).
+    stage_activation<F>(a, lq, lb, ls, wave, lane, [&] { load_item(locate(g < total ? g : 0), 0, g < total, ia); });
     __syncthreads();
     if (g >= total) return;
+    Cur cj = locate(g);  // job record of row group g, looked up once per row group
 
     float acc = 0.0f;
     int a_chunk = -1;
@@ -202,7 +208,9 @@ __global__ __launch_bounds__(256) void kquant_gemv_kernel(const GArgs a) {
             ng += stride;
         }
         const bool more = ng < total;
-        load_item(ng, nc, more, nxt);
+        Cur nj = cj;
+        if (nc == 0) nj = locate(more ? ng : 0);
+        load_item(nj, nc, more, nxt);
         const int sb = c * 16 + q;
         const bool live = sb < spr;
         if (c != a_chunk) {
@@ -221,15 +229,15 @@ __global__ __launch_bounds__(256) void kquant_gemv_kernel(const GArgs a) {
         }
         wave_sync();
         if (c == nchunks - 1) {
-            const Cur jb = locate(g);
-            if (lane < R && jb.row0 + lane < jb.n_rows) {
+            if (lane < R && cj.row0 + lane < cj.n_rows) {
                 // bias[o] + sum (RT/Q4KDotKernel.cs:473); no add at all without a bias
-                jb.y[jb.row0 + lane] = jb.bias ? as_float(cur.bias) + acc : acc;
+                cj.y[cj.row0 + lane] = cj.bias ? as_float(cur.bias) + acc : acc;
             }
             acc = 0.0f;
         }
         g = ng;
         c = nc;
+        cj = nj;
         return more;
     };
     while (step(ia, ib) && step(ib, ia)) {
@@ -270,7 +278,10 @@ hipError_t launch_gemv(GArgs& ga, const ProjJob* jobs, int njobs, hipStream_t st
     const int cap = cu_count() * wg_per_cu;
     if (wgs > cap) wgs = cap;
     const size_t lds = (size_t)((ga.spr * (kLdsSlot + 36) + 15) & ~15) + 4 * R * 17 * sizeof(float);
-    hipLaunchKernelGGL((kquant_gemv_kernel<F, R>), dim3(wgs), dim3(256), lds, st, ga);
+    if (njobs > 1)
+        hipLaunchKernelGGL((kquant_gemv_kernel<F, R, true>), dim3(wgs), dim3(256), lds, st, ga);
+    else
+        hipLaunchKernelGGL((kquant_gemv_kernel<F, R, false>), dim3(wgs), dim3(256), lds, st, ga);
     return hipGetLastError();
 }
 
