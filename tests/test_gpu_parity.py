@@ -169,9 +169,11 @@ def test_kquant_project_bit_exact(orc, ctx, fmt, k, n, with_bias):
     assert_bit_exact(ov.project(w, x, bias), ref, f"{fmt} {k}x{n} host")
 
 
-@pytest.mark.parametrize("kernel", ["small", "tiled", "rows"])
+# "auto" at 97 and 512 rows over 96 outputs: the automatic choice takes the tiled kernel for its small grid once the
+# small-M kernel would make 6 (Q4_K) / 7 (Q6_K) passes of 16 rows.
+@pytest.mark.parametrize("kernel", ["small", "tiled", "rows", "auto"])
 @pytest.mark.parametrize("fmt", ["q4k", "q6k"])
-@pytest.mark.parametrize("rows", [2, 3, 8, 16, 17, 70])
+@pytest.mark.parametrize("rows", [2, 3, 8, 16, 17, 70, 97, 512])
 def test_kquant_batched_bit_exact(orc, batched, kernel, fmt, rows):
     case("batched", kernel, fmt, rows)
     batched(kernel)
