@@ -698,6 +698,32 @@ def test_kquant_long_rows_bit_exact(orc, fmt, rows):
     assert_bit_exact(y, ref, f"{fmt} K={k} rows={rows}")
 
 
+# Row counts on both sides of every threshold of the automatic kernel choice: one-row GEMV, multi-row decode kernel
+# (up to 4 rows; 8 for fused launches), small-M MFMA kernel, tiled MFMA kernel (grid >= 96 workgroups, or from 81 /
+# 97 rows), and past K = 16384 the general kernel below 32 rows.
+DISPATCH_ROWS = {2304: [1, 2, 3, 4, 5, 8, 9, 15, 16, 17, 31, 32, 33, 64, 65, 80, 81, 96, 97, 112, 113, 129],
+                 16640: [1, 2, 4, 9, 31, 32, 33, 70]}
+
+
+@pytest.mark.parametrize("fmt", ["q4k", "q6k"])
+@pytest.mark.parametrize("k", sorted(DISPATCH_ROWS))
+def test_automatic_choice_boundaries_bit_exact(orc, ctx, fmt, k):
+    """Every row count of DISPATCH_ROWS through the automatic choice, 70 outputs (a partial 64-row tile), a bias:
+    bit-exact against the oracle's batched restatement."""
+    n = 70
+    rng = np.random.default_rng(k + (1 if fmt == "q6k" else 0))
+    blocks = _kq_blocks(rng, fmt, n, k)
+    w = (ov.Q4KWeight if fmt == "q4k" else ov.Q6KWeight)(blocks, k, n)
+    bias = normal(rng, n)
+    batched = orc.q4k_project_batched if fmt == "q4k" else orc.q6k_project_batched
+    for rows in DISPATCH_ROWS[k]:
+        case("automatic choice", fmt, k, rows)
+        x = normal(rng, (rows, k))
+        ref = batched(x, rows, blocks, k, n, bias)
+        y = ov.project(w, x, bias, rows=rows).reshape(rows, n)
+        assert_bit_exact(y, ref, f"{fmt} K={k} rows={rows} automatic")
+
+
 @pytest.mark.parametrize("kernel,rows,k", [("tiled", 48, 1024), ("small", 48, 1024), ("rows", 8, 1024),
                                            ("auto", 1, 28672)])
 @pytest.mark.parametrize("fmt", ["q4k", "q6k"])
