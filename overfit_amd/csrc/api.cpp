@@ -188,8 +188,9 @@ bool gemv_enabled() {
     return on;
 }
 
-// The small-M MFMA kernel serves M >= 3 unless OVFQ_SMALL_KERNEL=general (for measurements). At M = 2 the
-// general kernel is faster on MI355X for every Llama-3-8B shape.
+// The small-M MFMA kernel serves M >= 3 unless OVFQ_SMALL_KERNEL=general (for measurements). M = 2 takes the
+// multi-row decode kernel, or the general kernel where that cannot run: the small-M kernel was slower than the
+// general one at M = 2 on MI355X for every Llama-3-8B shape.
 bool small_mfma_enabled(int rows) {
     static const bool general = [] {
         const char* v = getenv("OVFQ_SMALL_KERNEL");
@@ -200,7 +201,7 @@ bool small_mfma_enabled(int rows) {
 
 // Batched K-quant launch of rows >= 3: the 64-row-tiled MFMA kernel (true), else the small-M kernel where it takes
 // the shape, else the general kernel. OVFQ_BATCHED_SMALL / _TILED force a kernel; automatic is the shape rule of
-// mfma_tiled_preferred, and the old M >= 32 bound where the small-M kernel cannot run.
+// mfma_tiled_preferred, and M >= 32 where the small-M kernel cannot run (input sizes past 16384).
 bool use_tiled_mfma(const ovfq_ctx* c, int type, const ovfq::ProjJob* jobs, int count, int in, int rows) {
     if (!ovfq::mfma_supported(type) || rows < 3) return false;
     if (c->batched_kernel == OVFQ_BATCHED_TILED) return true;
