@@ -235,6 +235,42 @@ def main():
                 "pct_peak": round(100 * nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 2), "algorithmic_bytes": nbytes,
                 "copies": n_copies, "what": label}
 
+    def q8_line():
+        """Q8_0 projections (the reference's Q8DotKernel path) on a 4096x4096 weight: the decode call (M = 1: Q8_0
+        quantise + row kernel) and M = 512 (the int8-MFMA kernel), graph-replayed over copies past the cache."""
+        n = k = 4096
+        gen3 = torch.Generator(device="cuda:0").manual_seed(88)
+        ws = []
+        for _ in range(32):
+            wf = torch.randn(n, k, generator=gen3, device=dev) * 0.02
+            q, s = ov.quantize_weight(wf, ov.TYPE_Q8_0)
+            del wf
+            ws.append(ov.Q8Weight(q, s, k, n))
+            del q, s
+        wbytes = n * k + 4 * (n * k // 32)
+        out = {"shape": "4096x4096 q8_0", "weight_bytes": wbytes}
+        for m, copies in ((1, 32), (512, 4)):
+            x = torch.randn(m * k, generator=gen3, device=dev)
+            y = torch.empty(m * n, device=dev)
+            per_graph = copies * max(1, 16 // copies)
+            g = capture([(lambda w=w: ctx.project_multi_dev([w], x, [y], rows=m)) for w in ws[:copies]]
+                        * (per_graph // copies))
+            us = replay_us(g, per_graph, max(2, 128 // per_graph))
+            del g
+            if m == 1:
+                nbytes = wbytes + 4 * k + 4 * n
+                out["m1"] = {"us": round(us, 3), "GB_s": round(nbytes / (us * 1e-6) / 1e9, 1),
+                             "pct_peak": round(100 * nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 2),
+                             "what": "decode: Q8_0 quantise of x + the row kernel (2 launches)"}
+            else:
+                tops = 2.0 * m * n * k / (us * 1e-6) / 1e12
+                out["m512"] = {"us": round(us, 2), "useful_TOPS": round(tops, 1), "tokens_per_s": round(m / (us * 1e-6), 1),
+                               "what": "prefill: Q8_0 quantise of x + the int8-MFMA kernel (one 16x16x32 MFMA per block)"}
+        del ws
+        torch.cuda.empty_cache()
+        out["timing"] = "HIP graph replay over weight copies, per call"
+        return out
+
     def rows_layer(m):
         """fp32 inputs / outputs for the layer's four projection launches at m rows, and the step over one copy:
         fused q/k/v, o, fused gate/up, down, each quantising its fp32 input to Q8_K first."""
@@ -442,6 +478,7 @@ def main():
     config4 = model_line()
     config5 = moe_line()
     ffn = ffn_line()
+    q8 = q8_line()
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -478,6 +515,7 @@ def main():
         "small_batch_layer": small,
         "q4k_gemv_128256x4096": large_q4k,
         "q6k_lm_head_128256x4096": lm_head,
+        "q8_0_4096x4096": q8,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

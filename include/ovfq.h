@@ -72,8 +72,9 @@ OVFQ_API int ovfq_ctx_synchronize(ovfq_ctx* ctx);
  * OVFQ_BATCHED_SMALL forces the super-block-parallel small-M MFMA kernel wherever it takes the shape (3 or more
  * rows, input sizes up to 16384); OVFQ_BATCHED_TILED the 64-row-tiled MFMA kernel (3 or more rows);
  * OVFQ_BATCHED_ROWS the multi-row decode kernel (2 to 8 rows, rows * input_size <= 32768). Shapes a forced
- * kernel does not take keep the automatic choice (routed experts: only SMALL / TILED apply). Every choice gives
- * bit-identical outputs. Counterpart of the reference's test-only A/B toggle
+ * kernel does not take keep the automatic choice (routed experts: only SMALL / TILED apply). For Q8_0 weights,
+ * TILED forces the 64x64-tiled int8-MFMA kernel from 2 rows and SMALL / ROWS the row kernel (automatic: the MFMA
+ * kernel from 32 rows, or from 16 rows for 8192 outputs or more). Every choice gives bit-identical outputs. Counterpart of the reference's test-only A/B toggle
  * BatchedQuantProjection.UseWeightStationaryQ4K (RT/BatchedQuantProjection.cs:21-24): for parity tests and
  * benches that cover every kernel on one shape. */
 #define OVFQ_BATCHED_AUTO 0

@@ -258,7 +258,23 @@ int launch_projection(ovfq_ctx* c, const ovfq_weight* const* ws, int count, cons
     if (x && rows > 1 && !use_gemv_rows(c, type, in, rows, count))
         return fail(OVFQ_ERR_SIZE, "in-launch quantisation of %d rows needs the multi-row decode kernel", rows);
     if (type == OVFQ_TYPE_Q8_0) {
-        HIP_TRY(ovfq::launch_project_q8_0(jobs, count, in, rows, act, c->stream));
+        // The int8-MFMA kernel from 32 rows, or from 16 rows for 8192 outputs or more (MI355X, graph replay, us,
+        // row kernel / MFMA kernel): 4096x4096 at 16 rows 63.6 / 76.7, 24 rows 91.5 / 80.4, 64 rows 235 / 102;
+        // 14336x4096 at 16 rows 149 / 78.6; 4096x14336 at 24 rows 234 / 276, 32 rows 304 / 287; 512 rows of
+        // 4096x4096 181 us on the MFMA kernel. OVFQ_Q8_MFMA_MIN_ROWS sets a plain row bound instead (measurements).
+        static const int q8_mfma_min = [] {
+            const char* v = getenv("OVFQ_Q8_MFMA_MIN_ROWS");
+            return v && *v ? atoi(v) : 0;
+        }();
+        long outs = 0;
+        for (int i = 0; i < count; i++) outs += jobs[i].n_rows;
+        bool q8_mfma = q8_mfma_min > 0 ? rows >= q8_mfma_min : rows >= 32 || (rows >= 16 && outs >= 8192);
+        if (c->batched_kernel == OVFQ_BATCHED_TILED) q8_mfma = rows >= 2;
+        else if (c->batched_kernel != OVFQ_BATCHED_AUTO) q8_mfma = false;
+        if (q8_mfma && ovfq::q8_0_mfma_supported(in, rows))
+            HIP_TRY(ovfq::launch_project_q8_0_mfma(jobs, count, in, rows, act, c->stream));
+        else
+            HIP_TRY(ovfq::launch_project_q8_0(jobs, count, in, rows, act, c->stream));
     } else if (rows == 1 && gemv_enabled() && ovfq::gemv_supported(in)) {
         HIP_TRY(ovfq::launch_gemv_kquant(type, jobs, count, in, x, act, c->stream));
     } else if (use_gemv_rows(c, type, in, rows, count)) {

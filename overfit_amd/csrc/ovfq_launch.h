@@ -101,6 +101,10 @@ hipError_t launch_moe_combine(const float* out, const int* pair_of, const float*
                               float* y, hipStream_t st);
 
 hipError_t launch_project_q8_0(const ProjJob* jobs, int njobs, int in, int rows, ActQ act, hipStream_t st);
+// Q8_0 over several activation rows on int8 MFMA (one 16x16x32 MFMA per 32-element block), bit-identical to
+// launch_project_q8_0.
+bool q8_0_mfma_supported(int in, int rows);
+hipError_t launch_project_q8_0_mfma(const ProjJob* jobs, int njobs, int in, int rows, ActQ act, hipStream_t st);
 
 // GGUF Q8_0 (34-byte blocks) -> int8 quant plane + f32 scale plane.
 hipError_t launch_q8_0_deinterleave(const void* gguf, int64_t n_blocks, int8_t* q, float* s, hipStream_t st);

@@ -259,4 +259,118 @@ hipError_t launch_project_q8_0(const ProjJob* jobs, int njobs, int in, int rows,
     return hipGetLastError();
 }
 
+// ------------------------------------------------------------------------------------------ Q8_0 on int8 MFMA
+// Q8DotKernel.ProjectBatched (RT/Q8DotKernel.cs:352-445) for several activation rows. The weights are int8 already,
+// so each 32-element block is one v_mfma_i32_16x16x32_i8 per 16 x 16 (activation row, output) tile, giving the
+// block's exact int32 dot; the reference's tail (wScale * aScale) * dot is then added per (row, output) in
+// ascending block order from +0 (Dot, RT/Q8DotKernel.cs:127-137), and bias + sum is written.
+// Workgroup: 64 outputs (wave w: outputs 16w .. 16w + 15, the B operand, column o = lane % 16) x 64 activation
+// rows (four 16-row A tiles). Lane group g = lane / 16 carries K bytes 8g .. 8g + 7 of the block in both operands;
+// the four results a lane holds, D[4g + i][lane % 16], are (activation row 4g + i of the tile, its own output).
+// Blocks go in groups of four: the lane's four weight scales and, per tile row 4g + i, four activation scales are
+// one 16-byte load each.
+struct Q8MArgs {
+    const int8_t* w;
+    const float* ws;
+    const float* bias;
+    float* y;
+    int n_out;
+    int in;
+    int rows;
+    const int8_t* q;
+    const float* s;
+};
+
+typedef int i32x4m __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256) void q8_0_mfma_kernel(const Q8MArgs a) {
+    const int wave = wave_id();
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4, c16 = lane & 15;
+    const int o0 = (int)blockIdx.x * 64 + wave * 16;
+    const int m0 = (int)blockIdx.y * 64;
+    if (o0 >= a.n_out) return;  // wave-uniform; the kernel has no barrier
+    const uint32_t K = (uint32_t)a.in, nb = K / 32;
+    // Resources over this wave's weight rows and the workgroup's activation rows: rows past the end read zeros.
+    const uint32_t wrows = (uint32_t)min(16, a.n_out - o0), arows = (uint32_t)min(64, a.rows - m0);
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w + (uint64_t)o0 * K, wrows * K);
+    const __amdgpu_buffer_rsrc_t wsr = make_rsrc(a.ws + (uint64_t)o0 * nb, wrows * nb * 4);
+    const __amdgpu_buffer_rsrc_t qr = make_rsrc(a.q + (uint64_t)m0 * K, arows * K);
+    const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.s + (uint64_t)m0 * nb, arows * nb * 4);
+    const uint32_t woff = (uint32_t)c16 * K + 8u * g;
+    float acc[4][4];
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[t][i] = 0.0f;
+    for (uint32_t b4 = 0; b4 < nb; b4 += 4) {
+        // scales of blocks b4 .. b4 + 3 (past the row's last block: unused)
+        const u32x4 wsv = ld4(wsr, ((uint32_t)c16 * nb + b4) * 4);
+        u32x4 xs[4][4];
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) xs[t][i] = ld4(sr, ((uint32_t)(16 * t + 4 * g + i) * nb + b4) * 4);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t b = b4 + j;
+            if (b < nb) {  // wave-uniform
+                const u32x2 wv = ld2(wr, woff + 32 * b);
+                const long bop = (long)(((uint64_t)wv.y << 32) | wv.x);
+                const uint32_t wsw = j == 0 ? wsv.x : j == 1 ? wsv.y : j == 2 ? wsv.z : wsv.w;
+                const float wsc = as_float(wsw);
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    const u32x2 av = ld2(qr, (uint32_t)(16 * t + c16) * K + 32 * b + 8u * g);
+                    const long aop = (long)(((uint64_t)av.y << 32) | av.x);
+                    const i32x4m d = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, i32x4m{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const u32x4 xv = xs[t][i];
+                        const uint32_t xw = j == 0 ? xv.x : j == 1 ? xv.y : j == 2 ? xv.z : xv.w;
+                        // (wScale * aScale) * blockDot, then the ascending sum
+                        acc[t][i] += (wsc * as_float(xw)) * (float)d[i];
+                    }
+                }
+            }
+        }
+    }
+    const int o = o0 + c16;
+    if (o < a.n_out) {
+        const float bo = a.bias ? a.bias[o] : 0.0f;
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int m = m0 + 16 * t + 4 * g + i;
+                if (m < a.rows) a.y[(size_t)m * a.n_out + o] = a.bias ? bo + acc[t][i] : acc[t][i];
+            }
+    }
+}
+
+bool q8_0_mfma_supported(int in, int rows) {
+    // 32-bit resource offsets: 64 activation rows and 16 weight rows of K bytes, and the whole activation
+    return in % 32 == 0 && (uint64_t)in * 64 < (1ull << 31) && (uint64_t)in * (uint64_t)rows < (1ull << 31);
+}
+
+hipError_t launch_project_q8_0_mfma(const ProjJob* jobs, int njobs, int in, int rows, ActQ act, hipStream_t st) {
+    for (int i = 0; i < njobs; i++) {
+        Q8MArgs ma{};
+        ma.w = reinterpret_cast<const int8_t*>(jobs[i].w);
+        ma.ws = jobs[i].ws;
+        ma.bias = jobs[i].bias;
+        ma.y = jobs[i].y;
+        ma.n_out = jobs[i].n_rows;
+        ma.in = in;
+        ma.rows = rows;
+        ma.q = act.q;
+        ma.s = act.s;
+        const dim3 grid((jobs[i].n_rows + 63) / 64, (rows + 63) / 64);
+        hipLaunchKernelGGL(q8_0_mfma_kernel, grid, dim3(256), 0, st, ma);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
 }  // namespace ovfq

@@ -318,6 +318,27 @@ def test_multi_projection_rows_bit_exact(orc, ctx, batched, rows, kernel):
         assert_bit_exact(y.cpu().numpy().reshape(rows, -1), ref, f"multi prequantized rows={rows} job {i}")
 
 
+@pytest.mark.parametrize("rows,kernel", [(1, "auto"), (5, "auto"), (5, "tiled"), (70, "auto")])
+def test_q8_0_multi_projection_rows_bit_exact(orc, ctx, batched, rows, kernel):
+    """Fused Q8_0 q/k/v-style call over `rows` activation rows (the row kernel, or the int8-MFMA kernel with one
+    launch per weight): every output bit-exact, with a bias on the last weight."""
+    case("q8_0 multi rows", rows, kernel)
+    batched(kernel)
+    rng = np.random.default_rng(500 + rows)
+    k, shapes = 1024, [192, 64, 80]
+    planes = [orc.q8_quantize_rows(normal(rng, (n, k), 0.05)) for n in shapes]
+    ws = [ov.Q8Weight(wq, wsc, k, n) for (wq, wsc), n in zip(planes, shapes)]
+    x = normal(rng, (rows, k))
+    bias = normal(rng, shapes[2])
+    refs = [orc.q8_project_batched(x, rows, wq, wsc, k, n, bias if i == 2 else None)
+            for i, ((wq, wsc), n) in enumerate(zip(planes, shapes))]
+    ys = [torch.empty(rows * n, device=DEV) for n in shapes]
+    ctx.project_multi_dev(ws, t(x), ys, [None, None, t(bias)], rows=rows)
+    torch.cuda.synchronize()
+    for i, (y, ref) in enumerate(zip(ys, refs)):
+        assert_bit_exact(y.cpu().numpy().reshape(rows, -1), ref, f"q8_0 multi rows={rows} job {i}")
+
+
 def test_bound_multi_call_matches_oracle(orc, ctx):
     """A prepared multi-projection call (pointer arrays built once) replayed over new inputs: every call reads the
     bound tensors' current contents and is bit-exact, with and without a bias, M = 1 (decode GEMV) and M = 3."""
@@ -768,10 +789,16 @@ def test_llama3_8b_layer_prefill_sampled_rows(orc):
         assert rel <= 1e-3 and cos >= 0.99999
 
 
-@pytest.mark.parametrize("k,n", [(32, 5), (128, 4096), (4096, 300), (14336, 40)])
-@pytest.mark.parametrize("rows", [1, 2, 3, 7, 16])
-def test_q8_0_project_bit_exact(orc, k, n, rows):
-    case("q8_0 project", k, n, rows)
+# Automatic choice (the row kernel below 32 rows, 16 with 8192 outputs or more; the int8-MFMA kernel above), and each
+# kernel forced ("tiled": the MFMA kernel from 2 rows, "rows": the row kernel): partial 64-row activation tiles
+# (2 .. 16, 65, 130), a partial 64-output tile (70), 129 blocks per row (four-block groups with a short last one),
+# one block per row.
+@pytest.mark.parametrize("kernel", ["auto", "tiled", "rows"])
+@pytest.mark.parametrize("k,n", [(32, 5), (128, 4096), (4096, 300), (14336, 40), (4128, 70)])
+@pytest.mark.parametrize("rows", [1, 2, 3, 7, 16, 65, 130])
+def test_q8_0_project_bit_exact(orc, batched, kernel, k, n, rows):
+    case("q8_0 project", kernel, k, n, rows)
+    batched(kernel)
     rng = np.random.default_rng(k + n + rows)
     wq, ws = orc.q8_quantize_rows(normal(rng, (n, k), 0.05))
     wq[0, :32] = -128                               # GGUF Q8_0 weights may hold -128
