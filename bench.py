@@ -236,8 +236,9 @@ def main():
                 "copies": n_copies, "what": label}
 
     def q8_line():
-        """Q8_0 projections (the reference's Q8DotKernel path) on a 4096x4096 weight: the decode call (M = 1: Q8_0
-        quantise + row kernel) and M = 512 (the int8-MFMA kernel), graph-replayed over copies past the cache."""
+        """Q8_0 projections (the reference's Q8DotKernel path) on a 4096x4096 weight: the decode call (M = 1: the
+        persistent decode GEMV, quantising x inside the launch) and M = 512 (Q8_0 quantise + the int8-MFMA kernel),
+        graph-replayed over copies past the cache."""
         n = k = 4096
         gen3 = torch.Generator(device="cuda:0").manual_seed(88)
         ws = []
@@ -261,7 +262,7 @@ def main():
                 nbytes = wbytes + 4 * k + 4 * n
                 out["m1"] = {"us": round(us, 3), "GB_s": round(nbytes / (us * 1e-6) / 1e9, 1),
                              "pct_peak": round(100 * nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 2),
-                             "what": "decode: Q8_0 quantise of x + the row kernel (2 launches)"}
+                             "what": "decode: one launch, Q8_0 quantisation of x inside the persistent decode GEMV"}
             else:
                 tops = 2.0 * m * n * k / (us * 1e-6) / 1e12
                 out["m512"] = {"us": round(us, 2), "useful_TOPS": round(tops, 1), "tokens_per_s": round(m / (us * 1e-6), 1),

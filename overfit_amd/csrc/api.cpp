@@ -232,10 +232,10 @@ bool use_gemv_rows(const ovfq_ctx* c, int type, int in, int rows, int count) {
     return rows <= 4 || count >= 3;
 }
 
-// Whether the projection launch quantises its fp32 input itself instead of a separate Q8_K launch: one row on the
-// decode kernel (K <= 8192), or up to 64 super-blocks of rows on the multi-row decode kernel.
+// Whether the projection launch quantises its fp32 input itself instead of a separate Q8_K / Q8_0 launch: one row on
+// a decode kernel (K <= 8192), or up to 64 super-blocks of rows on the multi-row decode kernel.
 bool quantize_in_launch(const ovfq_ctx* c, int type, int in, int rows, int count) {
-    if (type == OVFQ_TYPE_Q8_0) return false;
+    if (type == OVFQ_TYPE_Q8_0) return rows == 1 && gemv_enabled() && ovfq::q8_0_gemv_quantize_inside(in);
     if (rows == 1 && ovfq::gemv_supported(in)) return gemv_enabled() && ovfq::gemv_quantize_inside(in);
     return use_gemv_rows(c, type, in, rows, count) && ovfq::gemv_rows_quantize_inside(in, rows);
 }
@@ -271,7 +271,9 @@ int launch_projection(ovfq_ctx* c, const ovfq_weight* const* ws, int count, cons
         bool q8_mfma = q8_mfma_min > 0 ? rows >= q8_mfma_min : rows >= 32 || (rows >= 16 && outs >= 8192);
         if (c->batched_kernel == OVFQ_BATCHED_TILED) q8_mfma = rows >= 2;
         else if (c->batched_kernel != OVFQ_BATCHED_AUTO) q8_mfma = false;
-        if (q8_mfma && ovfq::q8_0_mfma_supported(in, rows))
+        if (rows == 1 && gemv_enabled() && ovfq::q8_0_gemv_supported(in))
+            HIP_TRY(ovfq::launch_q8_0_gemv(jobs, count, in, x, act, c->stream));
+        else if (q8_mfma && ovfq::q8_0_mfma_supported(in, rows))
             HIP_TRY(ovfq::launch_project_q8_0_mfma(jobs, count, in, rows, act, c->stream));
         else
             HIP_TRY(ovfq::launch_project_q8_0(jobs, count, in, rows, act, c->stream));

@@ -82,6 +82,32 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Q8DotKernel.Quantize (RT/Q8DotKernel.cs:42-91) for one 32-element block held by 8 consecutive lanes (lane & 7 =
+// sub holds elements 4 sub .. 4 sub + 3 in `raw`): absmax over the 8 lanes, scale = absmax / 127, quants
+// round-half-even(v / scale) clamped to [-127, 127] (0 for an all-zero block), packed in element order. Every lane
+// of the wave must take part (the absmax uses cross-lane swaps).
+struct Q80Lane {
+    uint32_t packed;
+    float scale;
+};
+__device__ __forceinline__ Q80Lane q8_0_quantize_lane(u32x4 raw) {
+    const float v0 = as_float(raw.x), v1 = as_float(raw.y);
+    const float v2 = as_float(raw.z), v3 = as_float(raw.w);
+    float am = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
+    am = fmaxf(am, __shfl_xor(am, 1, 64));
+    am = fmaxf(am, __shfl_xor(am, 2, 64));
+    am = fmaxf(am, __shfl_xor(am, 4, 64));
+    const float scale = am / 127.0f;
+    const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+    const int q0 = (int)fminf(fmaxf(rintf(v0 * inv), -127.0f), 127.0f);
+    const int q1 = (int)fminf(fmaxf(rintf(v1 * inv), -127.0f), 127.0f);
+    const int q2 = (int)fminf(fmaxf(rintf(v2 * inv), -127.0f), 127.0f);
+    const int q3 = (int)fminf(fmaxf(rintf(v3 * inv), -127.0f), 127.0f);
+    return Q80Lane{(uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) |
+                       ((uint32_t)(q3 & 0xff) << 24),
+                   scale};
+}
+
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 
 // fp32 -> fp16 bits, round to nearest even, overflow to infinity: the (Half)x conversion of .NET, written out

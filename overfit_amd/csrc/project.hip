@@ -13,6 +13,8 @@
 // Dot does, and the per-row sum over super-blocks is accumulated in ascending block order by one lane per
 // row (through a small LDS transpose), so every output float is bit-identical to the reference's sequential
 // `sum += Dot(...)` loop.
+#include <cstdlib>
+
 #include "ovfq_device.h"
 #include "ovfq_launch.h"
 #include "kquant_blocks.h"
@@ -257,6 +259,267 @@ hipError_t launch_project_q8_0(const ProjJob* jobs, int njobs, int in, int rows,
     const size_t lds = (size_t)4 * rw * (bpr + 1) * sizeof(float);
     hipLaunchKernelGGL(q8_0_project_kernel, dim3(wg), dim3(256), lds, st, ka);
     return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------------------------ Q8_0 decode GEMV
+// Q8DotKernel.Project / ProjectParallel (RT/Q8DotKernel.cs:155-350) at M = 1 on a persistent grid. Each workgroup
+// copies the Q8_0 activation (K int8 + K/32 f32 scales) into LDS once; its waves then walk row groups of R rows
+// in items of 64 blocks: lane l takes block 64c + l of each row (its 32 weight bytes and scale; the wave reads
+// 64 consecutive blocks of a row), and the next item's loads are issued before the current item is computed. The
+// lane forms the reference's (wScale * aScale) * dot; per row, one lane adds the item's 64 block values in
+// ascending order (RT/Q8DotKernel.cs:127-137), and bias + sum is written after the row's last item.
+struct Q8GJob {
+    const int8_t* w;
+    const float* ws;
+    const float* bias;
+    float* y;
+    int n_rows;
+    int g_begin;  // first row group of this job
+};
+
+struct Q8GArgs {
+    Q8GJob job[kMaxJobs];
+    int njobs;
+    int total_groups;
+    int in;
+    int nb;          // blocks per row
+    const float* x;  // fp32 activation, quantised in the kernel (in <= kQ8GemvQuantMaxIn); NULL -> use q / s
+    const int8_t* q;
+    const float* s;
+};
+
+constexpr int kQ8GemvMaxIn = 32768;       // LDS copy of the activation: 32 KB + 4 KB of scales
+constexpr int kQ8GemvQuantMaxIn = 8192;   // in-launch quantisation (every workgroup quantises the whole input)
+
+template <int R, bool kMulti>
+__global__ __launch_bounds__(256) void q8_0_gemv_kernel(const Q8GArgs a) {
+    extern __shared__ __align__(16) uint8_t smem8[];
+    const int K = a.in, nb = a.nb;
+    uint8_t* lq = smem8;                                          // [K] activation quants
+    float* ls = reinterpret_cast<float*>(smem8 + K);              // [nb] activation scales
+    float* red = ls + ((nb + 3) & ~3);                            // per wave [R][65] block values
+    const int wave = wave_id();
+    const int lane = threadIdx.x & 63;
+    const int nchunks = (nb + 63) >> 6;
+    const int stride = gridDim.x * 4;
+    const int total = a.total_groups;
+    float* rw = red + wave * R * 65;
+
+    struct Item {
+        u32x4 w[R][2];
+        uint32_t ws[R];
+        uint32_t bias;
+    };
+    struct Cur {
+        const int8_t* w;
+        const float* ws;
+        const float* bias;
+        float* y;
+        int n_rows;
+        int row0;
+    };
+    auto locate = [&](int g) -> Cur {
+        Cur c{a.job[0].w, a.job[0].ws, a.job[0].bias, a.job[0].y, a.job[0].n_rows, 0};
+        if constexpr (kMulti) {
+#pragma unroll
+            for (int i = 1; i < kMaxJobs; i++) {
+                const bool take = i < a.njobs && g >= a.job[i].g_begin;
+                c.w = take ? a.job[i].w : c.w;
+                c.ws = take ? a.job[i].ws : c.ws;
+                c.bias = take ? a.job[i].bias : c.bias;
+                c.y = take ? a.job[i].y : c.y;
+                c.n_rows = take ? a.job[i].n_rows : c.n_rows;
+                c.row0 = take ? a.job[i].g_begin : c.row0;
+            }
+        }
+        c.row0 = (g - c.row0) * R;
+        return c;
+    };
+    // Loads of item (row group of jb, chunk c); an invalid item reads through zero-length resources. Lanes past the
+    // row's last block read the next row's bytes (or zeros past the group) and are not used.
+    auto load_item = [&](const Cur& jb, int c, bool valid, Item& it) {
+        const int rows = min(R, jb.n_rows - jb.row0);
+        const __amdgpu_buffer_rsrc_t wr =
+            make_rsrc(jb.w + (uint64_t)jb.row0 * K, valid ? (uint32_t)rows * (uint32_t)K : 0u);
+        const __amdgpu_buffer_rsrc_t wsr =
+            make_rsrc(jb.ws + (uint64_t)jb.row0 * nb, valid ? (uint32_t)rows * (uint32_t)nb * 4u : 0u);
+        const uint32_t blk = (uint32_t)(c * 64 + lane);
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t off = (uint32_t)r * (uint32_t)K + blk * 32u;
+            it.w[r][0] = ld4(wr, off);
+            it.w[r][1] = ld4(wr, off + 16);
+            it.ws[r] = ld1(wsr, ((uint32_t)r * (uint32_t)nb + blk) * 4u);
+        }
+        const bool want_bias = valid && jb.bias != nullptr && c == nchunks - 1;
+        const __amdgpu_buffer_rsrc_t bsr = make_rsrc(jb.bias, want_bias ? (uint32_t)jb.n_rows * 4u : 0u);
+        it.bias = ld1(bsr, (uint32_t)(jb.row0 + (lane < R ? lane : 0)) * 4u);
+    };
+
+    int g = blockIdx.x * 4 + wave;
+    int c = 0;
+    Item ia, ib;
+    if (a.x) {
+        // Q8DotKernel.Quantize of the fp32 activation into LDS (the standalone quantiser's device function): pass p
+        // covers 1024 floats, 8 lanes per block; loads first, then the first item's weights, then the quantisation.
+        constexpr int kPasses = kQ8GemvQuantMaxIn / 1024;
+        const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)K * 4u);
+        u32x4 xv[kPasses];
+#pragma unroll
+        for (int p = 0; p < kPasses; p++) xv[p] = ld4(xr, (uint32_t)(p * 1024 + threadIdx.x * 4) * 4u);  // past K: 0
+        load_item(locate(g < total ? g : 0), 0, g < total, ia);
+#pragma unroll
+        for (int p = 0; p < kPasses; p++) {
+            const Q80Lane r = q8_0_quantize_lane(xv[p]);  // every lane takes part
+            const int blk = p * 32 + (int)(threadIdx.x >> 3), sub = (int)(threadIdx.x & 7);
+            if (blk < nb) {
+                reinterpret_cast<uint32_t*>(lq + blk * 32)[sub] = r.packed;
+                if (sub == 0) ls[blk] = r.scale;
+            }
+        }
+    } else {
+        // activation -> LDS: the quant loads go out first, then the first item's weights, then the LDS stores
+        constexpr int kPasses = kQ8GemvMaxIn / 4096;
+        const __amdgpu_buffer_rsrc_t qr = make_rsrc(a.q, (uint32_t)K);
+        const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.s, (uint32_t)nb * 4u);
+        // unconditional: offsets past K (or past the scales) read zeros through the resources' bounds
+        u32x4 qv[kPasses];
+#pragma unroll
+        for (int p = 0; p < kPasses; p++) qv[p] = ld4(qr, (uint32_t)(p * 4096 + threadIdx.x * 16));
+        uint32_t sv[kQ8GemvMaxIn / 32 / 256];
+#pragma unroll
+        for (int p = 0; p < kQ8GemvMaxIn / 32 / 256; p++) sv[p] = ld1(sr, (uint32_t)(p * 256 + threadIdx.x) * 4u);
+        load_item(locate(g < total ? g : 0), 0, g < total, ia);
+#pragma unroll
+        for (int p = 0; p < kPasses; p++) {
+            const int i = p * 4096 + (int)threadIdx.x * 16;
+            if (i < K) *reinterpret_cast<u32x4*>(lq + i) = qv[p];
+        }
+#pragma unroll
+        for (int p = 0; p < kQ8GemvMaxIn / 32 / 256; p++) {
+            const int i = p * 256 + (int)threadIdx.x;
+            if (i < nb) ls[i] = as_float(sv[p]);
+        }
+    }
+    __syncthreads();
+    if (g >= total) return;
+    Cur cj = locate(g);
+
+    float acc = 0.0f;
+    auto step = [&](Item& cur, Item& nxt) -> bool {
+        int ng = g, nc = c + 1;
+        if (nc == nchunks) {
+            nc = 0;
+            ng += stride;
+        }
+        const bool more = ng < total;
+        Cur nj = cj;
+        if (nc == 0) nj = locate(more ? ng : 0);
+        load_item(nj, nc, more, nxt);
+        const int blk = c * 64 + lane;
+        const bool live = blk < nb;
+        const int ab = live ? blk : 0;
+        const u32x4 x0 = *reinterpret_cast<const u32x4*>(lq + ab * 32);
+        const u32x4 x1 = *reinterpret_cast<const u32x4*>(lq + ab * 32 + 16);
+        const float xs = ls[ab];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            int dot = 0;
+            dot = sdot4(cur.w[r][0].x, x0.x, dot);
+            dot = sdot4(cur.w[r][0].y, x0.y, dot);
+            dot = sdot4(cur.w[r][0].z, x0.z, dot);
+            dot = sdot4(cur.w[r][0].w, x0.w, dot);
+            dot = sdot4(cur.w[r][1].x, x1.x, dot);
+            dot = sdot4(cur.w[r][1].y, x1.y, dot);
+            dot = sdot4(cur.w[r][1].z, x1.z, dot);
+            dot = sdot4(cur.w[r][1].w, x1.w, dot);
+            if (live) rw[r * 65 + lane] = as_float(cur.ws[r]) * xs * (float)dot;  // (wScale * aScale) * dot
+        }
+        wave_sync();
+        if (lane < R) {
+            const int nv = min(64, nb - c * 64);
+            for (int j = 0; j < nv; j++) acc += rw[lane * 65 + j];
+        }
+        wave_sync();
+        if (c == nchunks - 1) {
+            if (lane < R && cj.row0 + lane < cj.n_rows)
+                cj.y[cj.row0 + lane] = cj.bias ? as_float(cur.bias) + acc : acc;
+            acc = 0.0f;
+        }
+        g = ng;
+        c = nc;
+        cj = nj;
+        return more;
+    };
+    while (step(ia, ib) && step(ib, ia)) {
+    }
+}
+
+bool q8_0_gemv_supported(int in) { return in % 32 == 0 && in <= kQ8GemvMaxIn; }
+bool q8_0_gemv_quantize_inside(int in) { return q8_0_gemv_supported(in) && in <= kQ8GemvQuantMaxIn; }
+
+namespace {
+int q8_cu_count() {
+    static int cus[16] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return 256;
+    if (!cus[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
+template <int R>
+hipError_t launch_q8g(Q8GArgs& ga, const ProjJob* jobs, int njobs, hipStream_t st) {
+    int groups = 0;
+    for (int i = 0; i < njobs; i++) {
+        ga.job[i].g_begin = groups;
+        groups += (jobs[i].n_rows + R - 1) / R;
+    }
+    ga.total_groups = groups;
+    static const int forced_wg = [] {
+        const char* v = getenv("OVFQ_Q8_GEMV_WG_PER_CU");
+        return v && *v ? atoi(v) : 0;
+    }();
+    const int wg_per_cu = forced_wg > 0 ? forced_wg : 2;
+    int wgs = (groups + 3) / 4;
+    const int cap = q8_cu_count() * wg_per_cu;
+    if (wgs > cap) wgs = cap;
+    const size_t lds = (size_t)ga.in + 4 * (size_t)((ga.nb + 3) & ~3) + 4 * (size_t)4 * R * 65;
+    if (njobs > 1)
+        hipLaunchKernelGGL((q8_0_gemv_kernel<R, true>), dim3(wgs), dim3(256), lds, st, ga);
+    else
+        hipLaunchKernelGGL((q8_0_gemv_kernel<R, false>), dim3(wgs), dim3(256), lds, st, ga);
+    return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_q8_0_gemv(const ProjJob* jobs, int njobs, int in, const float* x, ActQ act, hipStream_t st) {
+    if (x && !q8_0_gemv_quantize_inside(in)) return hipErrorInvalidValue;
+    Q8GArgs ga{};
+    for (int i = 0; i < kMaxJobs; i++) {
+        if (i < njobs)
+            ga.job[i] = Q8GJob{reinterpret_cast<const int8_t*>(jobs[i].w), jobs[i].ws, jobs[i].bias, jobs[i].y,
+                               jobs[i].n_rows, 0};
+        else
+            ga.job[i] = Q8GJob{nullptr, nullptr, nullptr, nullptr, 0, 0x7fffffff};
+    }
+    ga.njobs = njobs;
+    ga.in = in;
+    ga.nb = in / 32;
+    ga.x = x;
+    ga.q = act.q;
+    ga.s = act.s;
+    static const int forced_r = [] {
+        const char* v = getenv("OVFQ_Q8_GEMV_ROWS_PER_WAVE");
+        return v && *v ? atoi(v) : 0;
+    }();
+    const int R = forced_r == 1 || forced_r == 2 || forced_r == 4 ? forced_r : 2;
+    if (R == 4) return launch_q8g<4>(ga, jobs, njobs, st);
+    if (R == 1) return launch_q8g<1>(ga, jobs, njobs, st);
+    return launch_q8g<2>(ga, jobs, njobs, st);
 }
 
 // ------------------------------------------------------------------------------------------ Q8_0 on int8 MFMA

@@ -34,24 +34,10 @@ __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float* __restr
     if (wblk >= n_blocks) return;
     const int sub = lane & 7;
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(x + wblk * 32, rsrc_bytes((uint64_t)n_blocks * 128, (uint64_t)wblk * 128));
-    const u32x4 raw = ld4(xr, lane * 16);
-    const float v0 = as_float(raw.x), v1 = as_float(raw.y);
-    const float v2 = as_float(raw.z), v3 = as_float(raw.w);
-    float am = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
-    am = fmaxf(am, __shfl_xor(am, 1, 64));
-    am = fmaxf(am, __shfl_xor(am, 2, 64));
-    am = fmaxf(am, __shfl_xor(am, 4, 64));
-    const float scale = am / 127.0f;
-    const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
-    const int q0 = (int)fminf(fmaxf(rintf(v0 * inv), -127.0f), 127.0f);
-    const int q1 = (int)fminf(fmaxf(rintf(v1 * inv), -127.0f), 127.0f);
-    const int q2 = (int)fminf(fmaxf(rintf(v2 * inv), -127.0f), 127.0f);
-    const int q3 = (int)fminf(fmaxf(rintf(v3 * inv), -127.0f), 127.0f);
-    const uint32_t packed = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) |
-                            ((uint32_t)(q3 & 0xff) << 24);
+    const Q80Lane r = q8_0_quantize_lane(ld4(xr, lane * 16));
     if (blk < n_blocks) {
-        reinterpret_cast<uint32_t*>(q + blk * 32)[sub] = packed;
-        if (sub == 0) s[blk] = scale;
+        reinterpret_cast<uint32_t*>(q + blk * 32)[sub] = r.packed;
+        if (sub == 0) s[blk] = r.scale;
     }
 }
 
