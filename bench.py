@@ -124,9 +124,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--copies", type=int, default=4, help="layer copies rotated to defeat the 256 MB cache")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--profile", choices=["layer", "prefill", "moe", "small"], default=None,
+    ap.add_argument("--profile", choices=["layer", "prefill", "moe", "small", "q8"], default=None,
                     help="for rocprof runs: only the timed decode-layer loop, the config-3 prefill line, the "
-                         "config-5 MoE line, or the small-batch layer line")
+                         "config-5 MoE line, the small-batch layer line, or the Q8_0 line")
     ap.add_argument("--pmc", action="store_true",
                     help="for rocprofv3 --pmc runs: 16 gate/up launches, then 16 plain 64 MiB device copies "
                          "(the counter calibration reference)")
@@ -427,8 +427,8 @@ def main():
                 "us": round(us, 2), "weight_bytes": wb, "GB_s": round(wb / (us * 1e-6) / 1e9, 1),
                 "timing": "HIP graph replay over %d layer copies x 4" % len(copies)}
 
-    if args.profile in ("prefill", "moe", "small"):
-        only = {"prefill": prefill_line, "moe": moe_line, "small": small_batch_line}[args.profile]
+    if args.profile in ("prefill", "moe", "small", "q8"):
+        only = {"prefill": prefill_line, "moe": moe_line, "small": small_batch_line, "q8": q8_line}[args.profile]
         print(json.dumps(only()), flush=True)
         return
 
