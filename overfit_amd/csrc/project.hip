@@ -14,6 +14,7 @@
 // row (through a small LDS transpose), so every output float is bit-identical to the reference's sequential
 // `sum += Dot(...)` loop.
 #include <cstdlib>
+#include <type_traits>
 
 #include "ovfq_device.h"
 #include "ovfq_launch.h"
@@ -546,57 +547,122 @@ struct Q8MArgs {
 
 typedef int i32x4m __attribute__((ext_vector_type(4)));
 
-__global__ __launch_bounds__(256) void q8_0_mfma_kernel(const Q8MArgs a) {
+// LDS staging of one four-block group (128 K bytes): row r, piece g (bytes 8g .. 8g + 7 of a block) and block j sit
+// at r * kQ8Row + 32 g + 8 j, so a lane's operand pieces of all four blocks are 32 contiguous bytes (two 16-byte
+// reads); rows are padded to 144 bytes so the 16 rows one read instruction covers start on different banks.
+constexpr int kQ8Row = 144;
+
+__device__ __forceinline__ void q8_stage_block(uint8_t* base, int row, int j, u32x4 lo, u32x4 hi) {
+    uint8_t* p = base + row * kQ8Row + 8 * j;
+    *reinterpret_cast<u32x2*>(p) = u32x2{lo.x, lo.y};
+    *reinterpret_cast<u32x2*>(p + 32) = u32x2{lo.z, lo.w};
+    *reinterpret_cast<u32x2*>(p + 64) = u32x2{hi.x, hi.y};
+    *reinterpret_cast<u32x2*>(p + 96) = u32x2{hi.z, hi.w};
+}
+
+__global__ __launch_bounds__(256, 2) void q8_0_mfma_kernel(const Q8MArgs a) {
+    __shared__ __align__(16) uint8_t la[2][64 * kQ8Row];     // activation tile, double-buffered
+    __shared__ __align__(16) float lxs[2][64 * 4];            // its scales [row][block]
+    __shared__ __align__(16) uint8_t lw[4][2][16 * kQ8Row];  // each wave's weight rows, double-buffered
+    const int tid = (int)threadIdx.x;
     const int wave = wave_id();
-    const int lane = threadIdx.x & 63;
+    const int lane = tid & 63;
     const int g = lane >> 4, c16 = lane & 15;
-    const int o0 = (int)blockIdx.x * 64 + wave * 16;
+    const int o0 = (int)blockIdx.x * 64 + wave * 16;  // this wave's outputs (past n_out: read zeros, store nothing)
     const int m0 = (int)blockIdx.y * 64;
-    if (o0 >= a.n_out) return;  // wave-uniform; the kernel has no barrier
     const uint32_t K = (uint32_t)a.in, nb = K / 32;
-    // Resources over this wave's weight rows and the workgroup's activation rows: rows past the end read zeros.
-    const uint32_t wrows = (uint32_t)min(16, a.n_out - o0), arows = (uint32_t)min(64, a.rows - m0);
-    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w + (uint64_t)o0 * K, wrows * K);
-    const __amdgpu_buffer_rsrc_t wsr = make_rsrc(a.ws + (uint64_t)o0 * nb, wrows * nb * 4);
+    const uint32_t wrows = (uint32_t)max(0, min(16, a.n_out - o0)), arows = (uint32_t)min(64, a.rows - m0);
+    const uint64_t obase = o0 < a.n_out ? (uint64_t)o0 : 0;
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w + obase * K, wrows * K);
+    const __amdgpu_buffer_rsrc_t wsr = make_rsrc(a.ws + obase * nb, wrows * nb * 4);
     const __amdgpu_buffer_rsrc_t qr = make_rsrc(a.q + (uint64_t)m0 * K, arows * K);
     const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.s + (uint64_t)m0 * nb, arows * nb * 4);
-    const uint32_t woff = (uint32_t)c16 * K + 8u * g;
+    // staging assignments: thread tid copies block (tid & 3) of activation row tid >> 2 and its scale; lane copies
+    // block (lane & 3) of the wave's weight row lane >> 2
+    const int ar = tid >> 2, aj = tid & 3, wrow = lane >> 2, wj = lane & 3;
+    struct Stage {
+        u32x4 a0, a1, w0, w1;
+        uint32_t xs;
+    };
+    auto fetch = [&](uint32_t b4, Stage& st) {  // past the row's blocks: the next row's bytes or zeros, unused
+        const uint32_t ao = (uint32_t)ar * K + (b4 + aj) * 32;
+        st.a0 = ld4(qr, ao);
+        st.a1 = ld4(qr, ao + 16);
+        st.xs = ld1(sr, ((uint32_t)ar * nb + b4 + aj) * 4);
+        const uint32_t wo = (uint32_t)wrow * K + (b4 + wj) * 32;
+        st.w0 = ld4(wr, wo);
+        st.w1 = ld4(wr, wo + 16);
+    };
+    auto stage = [&](int buf, const Stage& st) {
+        q8_stage_block(la[buf], ar, aj, st.a0, st.a1);
+        lxs[buf][ar * 4 + aj] = as_float(st.xs);
+        q8_stage_block(lw[wave][buf], wrow, wj, st.w0, st.w1);
+    };
     float acc[4][4];
 #pragma unroll
     for (int t = 0; t < 4; t++)
 #pragma unroll
         for (int i = 0; i < 4; i++) acc[t][i] = 0.0f;
-    for (uint32_t b4 = 0; b4 < nb; b4 += 4) {
-        // scales of blocks b4 .. b4 + 3 (past the row's last block: unused)
-        const u32x4 wsv = ld4(wsr, ((uint32_t)c16 * nb + b4) * 4);
-        u32x4 xs[4][4];
+    // Two groups in flight: while group k is computed from LDS, group k + 1 (fetched during group k - 1) waits in
+    // registers for its LDS stores and group k + 2's loads are issued.
+    Stage sa, sb;
+    fetch(0, sa);
+    stage(0, sa);
+    if (4 < nb) fetch(4, sb);
+    __syncthreads();
+    int buf = 0;
+    uint32_t b4 = 0;
+    // next: group k + 1 (in registers); after: free. A full group (four blocks) has no per-block test, so the
+    // compiler can interleave its 16 MFMAs with the fp32 tails; only the row's last group can be partial.
+    auto group = [&](auto full_tag, Stage& next, Stage& after) -> bool {
+        constexpr bool kFull = decltype(full_tag)::value;
+        if (b4 + 8 < nb) fetch(b4 + 8, after);
+        const u32x4 wsv = ld4(wsr, ((uint32_t)c16 * nb + b4) * 4);  // the lane's weight scales of the four blocks
+        const uint8_t* wp = lw[wave][buf] + c16 * kQ8Row + 32 * g;
+        const u32x4 wlo = *reinterpret_cast<const u32x4*>(wp), whi = *reinterpret_cast<const u32x4*>(wp + 16);
+        const uint32_t bw[8] = {wlo.x, wlo.y, wlo.z, wlo.w, whi.x, whi.y, whi.z, whi.w};
 #pragma unroll
-        for (int t = 0; t < 4; t++)
+        for (int t = 0; t < 4; t++) {
+            const uint8_t* ap = la[buf] + (16 * t + c16) * kQ8Row + 32 * g;
+            const u32x4 alo = *reinterpret_cast<const u32x4*>(ap), ahi = *reinterpret_cast<const u32x4*>(ap + 16);
+            const uint32_t aw[8] = {alo.x, alo.y, alo.z, alo.w, ahi.x, ahi.y, ahi.z, ahi.w};
+            u32x4 xv[4];  // scales of rows 16t + 4g + i, blocks b4 .. b4 + 3
 #pragma unroll
-            for (int i = 0; i < 4; i++) xs[t][i] = ld4(sr, ((uint32_t)(16 * t + 4 * g + i) * nb + b4) * 4);
+            for (int i = 0; i < 4; i++) xv[i] = *reinterpret_cast<const u32x4*>(&lxs[buf][(16 * t + 4 * g + i) * 4]);
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const uint32_t b = b4 + j;
-            if (b < nb) {  // wave-uniform
-                const u32x2 wv = ld2(wr, woff + 32 * b);
-                const long bop = (long)(((uint64_t)wv.y << 32) | wv.x);
-                const uint32_t wsw = j == 0 ? wsv.x : j == 1 ? wsv.y : j == 2 ? wsv.z : wsv.w;
-                const float wsc = as_float(wsw);
-#pragma unroll
-                for (int t = 0; t < 4; t++) {
-                    const u32x2 av = ld2(qr, (uint32_t)(16 * t + c16) * K + 32 * b + 8u * g);
-                    const long aop = (long)(((uint64_t)av.y << 32) | av.x);
+            for (int j = 0; j < 4; j++) {
+                if (kFull || b4 + j < nb) {  // wave-uniform
+                    const long aop = (long)(((uint64_t)aw[2 * j + 1] << 32) | aw[2 * j]);
+                    const long bop = (long)(((uint64_t)bw[2 * j + 1] << 32) | bw[2 * j]);
                     const i32x4m d = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, i32x4m{0, 0, 0, 0}, 0, 0, 0);
+                    const uint32_t wsw = j == 0 ? wsv.x : j == 1 ? wsv.y : j == 2 ? wsv.z : wsv.w;
+                    const float wsc = as_float(wsw);
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
-                        const u32x4 xv = xs[t][i];
-                        const uint32_t xw = j == 0 ? xv.x : j == 1 ? xv.y : j == 2 ? xv.z : xv.w;
+                        const uint32_t xw = j == 0 ? xv[i].x : j == 1 ? xv[i].y : j == 2 ? xv[i].z : xv[i].w;
                         // (wScale * aScale) * blockDot, then the ascending sum
                         acc[t][i] += (wsc * as_float(xw)) * (float)d[i];
                     }
                 }
             }
         }
+        if (b4 + 4 < nb) stage(buf ^ 1, next);
+        __syncthreads();  // the other buffer is complete; this one is free for the group after next
+        buf ^= 1;
+        b4 += 4;
+        return b4 < nb;
+    };
+    for (;;) {
+        if (b4 + 4 > nb) {
+            group(std::false_type{}, sb, sa);
+            break;
+        }
+        if (!group(std::true_type{}, sb, sa)) break;
+        if (b4 + 4 > nb) {
+            group(std::false_type{}, sa, sb);
+            break;
+        }
+        if (!group(std::true_type{}, sa, sb)) break;
     }
     const int o = o0 + c16;
     if (o < a.n_out) {
