@@ -528,8 +528,8 @@ hipError_t launch_q8_0_gemv(const ProjJob* jobs, int njobs, int in, const float*
 // so each 32-element block is one v_mfma_i32_16x16x32_i8 per 16 x 16 (activation row, output) tile, giving the
 // block's exact int32 dot; the reference's tail (wScale * aScale) * dot is then added per (row, output) in
 // ascending block order from +0 (Dot, RT/Q8DotKernel.cs:127-137), and bias + sum is written.
-// Workgroup: 64 outputs (wave w: outputs 16w .. 16w + 15, the B operand, column o = lane % 16) x 64 activation
-// rows (four 16-row A tiles). Lane group g = lane / 16 carries K bytes 8g .. 8g + 7 of the block in both operands;
+// Workgroup: 64 outputs (wave w: outputs 16w .. 16w + 15, the B operand, column o = lane % 16) x 16 T activation
+// rows (T 16-row A tiles: 1 or 2 for batches of up to 16 or 32 rows, else 4). Lane group g = lane / 16 carries K bytes 8g .. 8g + 7 of the block in both operands;
 // the four results a lane holds, D[4g + i][lane % 16], are (activation row 4g + i of the tile, its own output).
 // Blocks go in groups of four: the lane's four weight scales and, per tile row 4g + i, four activation scales are
 // one 16-byte load each.
@@ -560,47 +560,54 @@ __device__ __forceinline__ void q8_stage_block(uint8_t* base, int row, int j, u3
     *reinterpret_cast<u32x2*>(p + 96) = u32x2{hi.z, hi.w};
 }
 
+// T: 16-row activation tiles per workgroup (1 or 2 when the whole batch has at most 16 / 32 rows, else 4).
+template <int T>
 __global__ __launch_bounds__(256, 2) void q8_0_mfma_kernel(const Q8MArgs a) {
-    __shared__ __align__(16) uint8_t la[2][64 * kQ8Row];     // activation tile, double-buffered
-    __shared__ __align__(16) float lxs[2][64 * 4];            // its scales [row][block]
+    __shared__ __align__(16) uint8_t la[2][16 * T * kQ8Row];  // activation tile, double-buffered
+    __shared__ __align__(16) float lxs[2][16 * T * 4];         // its scales [row][block]
     __shared__ __align__(16) uint8_t lw[4][2][16 * kQ8Row];  // each wave's weight rows, double-buffered
     const int tid = (int)threadIdx.x;
     const int wave = wave_id();
     const int lane = tid & 63;
     const int g = lane >> 4, c16 = lane & 15;
     const int o0 = (int)blockIdx.x * 64 + wave * 16;  // this wave's outputs (past n_out: read zeros, store nothing)
-    const int m0 = (int)blockIdx.y * 64;
+    const int m0 = (int)blockIdx.y * 16 * T;
     const uint32_t K = (uint32_t)a.in, nb = K / 32;
-    const uint32_t wrows = (uint32_t)max(0, min(16, a.n_out - o0)), arows = (uint32_t)min(64, a.rows - m0);
+    const uint32_t wrows = (uint32_t)max(0, min(16, a.n_out - o0)), arows = (uint32_t)min(16 * T, a.rows - m0);
     const uint64_t obase = o0 < a.n_out ? (uint64_t)o0 : 0;
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w + obase * K, wrows * K);
     const __amdgpu_buffer_rsrc_t wsr = make_rsrc(a.ws + obase * nb, wrows * nb * 4);
     const __amdgpu_buffer_rsrc_t qr = make_rsrc(a.q + (uint64_t)m0 * K, arows * K);
     const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.s + (uint64_t)m0 * nb, arows * nb * 4);
-    // staging assignments: thread tid copies block (tid & 3) of activation row tid >> 2 and its scale; lane copies
-    // block (lane & 3) of the wave's weight row lane >> 2
+    // staging assignments: thread tid < 64 T copies block (tid & 3) of activation row tid >> 2 and its scale; lane
+    // copies block (lane & 3) of the wave's weight row lane >> 2
     const int ar = tid >> 2, aj = tid & 3, wrow = lane >> 2, wj = lane & 3;
+    const bool astage = tid < 64 * T;  // wave-uniform
     struct Stage {
         u32x4 a0, a1, w0, w1;
         uint32_t xs;
     };
     auto fetch = [&](uint32_t b4, Stage& st) {  // past the row's blocks: the next row's bytes or zeros, unused
-        const uint32_t ao = (uint32_t)ar * K + (b4 + aj) * 32;
-        st.a0 = ld4(qr, ao);
-        st.a1 = ld4(qr, ao + 16);
-        st.xs = ld1(sr, ((uint32_t)ar * nb + b4 + aj) * 4);
+        if (astage) {
+            const uint32_t ao = (uint32_t)ar * K + (b4 + aj) * 32;
+            st.a0 = ld4(qr, ao);
+            st.a1 = ld4(qr, ao + 16);
+            st.xs = ld1(sr, ((uint32_t)ar * nb + b4 + aj) * 4);
+        }
         const uint32_t wo = (uint32_t)wrow * K + (b4 + wj) * 32;
         st.w0 = ld4(wr, wo);
         st.w1 = ld4(wr, wo + 16);
     };
     auto stage = [&](int buf, const Stage& st) {
-        q8_stage_block(la[buf], ar, aj, st.a0, st.a1);
-        lxs[buf][ar * 4 + aj] = as_float(st.xs);
+        if (astage) {
+            q8_stage_block(la[buf], ar, aj, st.a0, st.a1);
+            lxs[buf][ar * 4 + aj] = as_float(st.xs);
+        }
         q8_stage_block(lw[wave][buf], wrow, wj, st.w0, st.w1);
     };
-    float acc[4][4];
+    float acc[T][4];
 #pragma unroll
-    for (int t = 0; t < 4; t++)
+    for (int t = 0; t < T; t++)
 #pragma unroll
         for (int i = 0; i < 4; i++) acc[t][i] = 0.0f;
     // Two groups in flight: while group k is computed from LDS, group k + 1 (fetched during group k - 1) waits in
@@ -622,7 +629,7 @@ __global__ __launch_bounds__(256, 2) void q8_0_mfma_kernel(const Q8MArgs a) {
         const u32x4 wlo = *reinterpret_cast<const u32x4*>(wp), whi = *reinterpret_cast<const u32x4*>(wp + 16);
         const uint32_t bw[8] = {wlo.x, wlo.y, wlo.z, wlo.w, whi.x, whi.y, whi.z, whi.w};
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
+        for (int t = 0; t < T; t++) {
             const uint8_t* ap = la[buf] + (16 * t + c16) * kQ8Row + 32 * g;
             const u32x4 alo = *reinterpret_cast<const u32x4*>(ap), ahi = *reinterpret_cast<const u32x4*>(ap + 16);
             const uint32_t aw[8] = {alo.x, alo.y, alo.z, alo.w, ahi.x, ahi.y, ahi.z, ahi.w};
@@ -668,7 +675,7 @@ __global__ __launch_bounds__(256, 2) void q8_0_mfma_kernel(const Q8MArgs a) {
     if (o < a.n_out) {
         const float bo = a.bias ? a.bias[o] : 0.0f;
 #pragma unroll
-        for (int t = 0; t < 4; t++)
+        for (int t = 0; t < T; t++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int m = m0 + 16 * t + 4 * g + i;
@@ -694,8 +701,14 @@ hipError_t launch_project_q8_0_mfma(const ProjJob* jobs, int njobs, int in, int 
         ma.rows = rows;
         ma.q = act.q;
         ma.s = act.s;
-        const dim3 grid((jobs[i].n_rows + 63) / 64, (rows + 63) / 64);
-        hipLaunchKernelGGL(q8_0_mfma_kernel, grid, dim3(256), 0, st, ma);
+        const int T = rows <= 16 ? 1 : rows <= 32 ? 2 : 4;
+        const dim3 grid((jobs[i].n_rows + 63) / 64, (rows + 16 * T - 1) / (16 * T));
+        if (T == 1)
+            hipLaunchKernelGGL(q8_0_mfma_kernel<1>, grid, dim3(256), 0, st, ma);
+        else if (T == 2)
+            hipLaunchKernelGGL(q8_0_mfma_kernel<2>, grid, dim3(256), 0, st, ma);
+        else
+            hipLaunchKernelGGL(q8_0_mfma_kernel<4>, grid, dim3(256), 0, st, ma);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }

@@ -790,14 +790,14 @@ def test_llama3_8b_layer_prefill_sampled_rows(orc):
 
 
 # One row on the decode GEMV (activation in LDS up to K = 32768; 32800 takes the row kernel). More rows: automatic
-# choice (the row kernel for few rows, the int8-MFMA kernel from 16 rows or fewer for short inputs), and each kernel
-# forced ("tiled": the MFMA kernel from 2 rows, "rows": the row kernel): partial 64-row activation tiles (2 .. 16,
-# 65, 130), a partial 64-output tile (70), 129 blocks per row (four-block groups with a short last one; a partial
+# choice (the row kernel for few rows, the int8-MFMA kernel from 12 rows or fewer for short inputs), and each kernel
+# forced ("tiled": the MFMA kernel from 2 rows, "rows": the row kernel): partial 16/32/64-row activation tiles (2 .. 16,
+# 24, 65, 130), a partial 64-output tile (70), 129 blocks per row (four-block groups with a short last one; a partial
 # 64-block GEMV item), one block per row.
 @pytest.mark.parametrize("kernel", ["auto", "tiled", "rows"])
 @pytest.mark.parametrize("k,n", [(32, 5), (128, 4096), (4096, 300), (14336, 40), (4128, 70), (32768, 24),
                                  (32800, 9)])
-@pytest.mark.parametrize("rows", [1, 2, 3, 7, 16, 65, 130])
+@pytest.mark.parametrize("rows", [1, 2, 3, 7, 16, 24, 65, 130])
 def test_q8_0_project_bit_exact(orc, batched, kernel, k, n, rows):
     case("q8_0 project", kernel, k, n, rows)
     batched(kernel)
