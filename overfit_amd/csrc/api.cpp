@@ -258,12 +258,12 @@ int launch_projection(ovfq_ctx* c, const ovfq_weight* const* ws, int count, cons
     if (x && rows > 1 && !use_gemv_rows(c, type, in, rows, count))
         return fail(OVFQ_ERR_SIZE, "in-launch quantisation of %d rows needs the multi-row decode kernel", rows);
     if (type == OVFQ_TYPE_Q8_0) {
-        // The int8-MFMA kernel from 12 rows; for inputs up to 8192 from 8 rows, and from 4 rows for 8192 outputs or
-        // more. Its time is flat up to 16 rows (one 16-row tile per workgroup), the row kernel's grows by a pass
-        // over the weights per row (MI355X, graph replay, us, row kernel / MFMA kernel): 4096x4096 at 4 rows 21.6 /
-        // 31.9, 16 rows 63.6 / 31.9, 64 rows 235 / 46.0, 512 rows - / 52.0; 14336x4096 at 4 rows 43.0 / 33.9, 16 rows
-        // 149 / 34.0; 4096x14336 at 16 rows 164 / 106, 24 rows 234 / 122, 512 rows - / 168. OVFQ_Q8_MFMA_MIN_ROWS
-        // sets a plain row bound instead (measurements).
+        // The int8-MFMA kernel from 8 rows; for inputs up to 8192 from 6 rows, and from 4 rows for 8192 outputs or
+        // more. Its time is flat up to 16 rows (one 16-row tile, one-wave workgroups of 16 outputs), the row
+        // kernel's grows by a pass over the weights per row (MI355X, graph replay, us, row kernel / MFMA kernel):
+        // 4096x4096 at 4 rows 21.6 / 25.7, 16 rows 63.6 / 25.8, 64 rows 235 / 46.0, 512 rows - / 52.0; 14336x4096 at
+        // 4 rows 43.0 / 31.6, 16 rows 149 / 31.6; 4096x14336 at 16 rows 164 / 84.3, 24 rows 234 / 122, 512 rows - /
+        // 168. OVFQ_Q8_MFMA_MIN_ROWS sets a plain row bound instead (measurements).
         static const int q8_mfma_min = [] {
             const char* v = getenv("OVFQ_Q8_MFMA_MIN_ROWS");
             return v && *v ? atoi(v) : 0;
@@ -271,7 +271,7 @@ int launch_projection(ovfq_ctx* c, const ovfq_weight* const* ws, int count, cons
         long outs = 0;
         for (int i = 0; i < count; i++) outs += jobs[i].n_rows;
         bool q8_mfma = q8_mfma_min > 0 ? rows >= q8_mfma_min
-                                       : rows >= 12 || (in <= 8192 && (rows >= 8 || (rows >= 4 && outs >= 8192)));
+                                       : rows >= 8 || (in <= 8192 && (rows >= 6 || (rows >= 4 && outs >= 8192)));
         if (c->batched_kernel == OVFQ_BATCHED_TILED) q8_mfma = rows >= 2;
         else if (c->batched_kernel != OVFQ_BATCHED_AUTO) q8_mfma = false;
         if (rows == 1 && gemv_enabled() && ovfq::q8_0_gemv_supported(in))

@@ -561,16 +561,19 @@ __device__ __forceinline__ void q8_stage_block(uint8_t* base, int row, int j, u3
 }
 
 // T: 16-row activation tiles per workgroup (1 or 2 when the whole batch has at most 16 / 32 rows, else 4).
-template <int T>
+// kW: waves per workgroup (16 outputs each): 4, or 1 for one-tile batches, so that few outputs still spread over
+// every CU (each wave then stages its own 16-row activation tile).
+template <int T, int kW>
 __global__ __launch_bounds__(256, 2) void q8_0_mfma_kernel(const Q8MArgs a) {
+    static_assert(kW == 4 || T == 1, "a one-wave workgroup stages one 16-row tile");
     __shared__ __align__(16) uint8_t la[2][16 * T * kQ8Row];  // activation tile, double-buffered
     __shared__ __align__(16) float lxs[2][16 * T * 4];         // its scales [row][block]
-    __shared__ __align__(16) uint8_t lw[4][2][16 * kQ8Row];  // each wave's weight rows, double-buffered
+    __shared__ __align__(16) uint8_t lw[kW][2][16 * kQ8Row];  // each wave's weight rows, double-buffered
     const int tid = (int)threadIdx.x;
     const int wave = wave_id();
     const int lane = tid & 63;
     const int g = lane >> 4, c16 = lane & 15;
-    const int o0 = (int)blockIdx.x * 64 + wave * 16;  // this wave's outputs (past n_out: read zeros, store nothing)
+    const int o0 = (int)blockIdx.x * 16 * kW + wave * 16;  // this wave's outputs (past n_out: zeros, no store)
     const int m0 = (int)blockIdx.y * 16 * T;
     const uint32_t K = (uint32_t)a.in, nb = K / 32;
     const uint32_t wrows = (uint32_t)max(0, min(16, a.n_out - o0)), arows = (uint32_t)min(16 * T, a.rows - m0);
@@ -702,13 +705,13 @@ hipError_t launch_project_q8_0_mfma(const ProjJob* jobs, int njobs, int in, int 
         ma.q = act.q;
         ma.s = act.s;
         const int T = rows <= 16 ? 1 : rows <= 32 ? 2 : 4;
-        const dim3 grid((jobs[i].n_rows + 63) / 64, (rows + 16 * T - 1) / (16 * T));
+        const dim3 grid4((jobs[i].n_rows + 63) / 64, (rows + 16 * T - 1) / (16 * T));
         if (T == 1)
-            hipLaunchKernelGGL(q8_0_mfma_kernel<1>, grid, dim3(256), 0, st, ma);
+            hipLaunchKernelGGL((q8_0_mfma_kernel<1, 1>), dim3((jobs[i].n_rows + 15) / 16, 1), dim3(64), 0, st, ma);
         else if (T == 2)
-            hipLaunchKernelGGL(q8_0_mfma_kernel<2>, grid, dim3(256), 0, st, ma);
+            hipLaunchKernelGGL((q8_0_mfma_kernel<2, 4>), grid4, dim3(256), 0, st, ma);
         else
-            hipLaunchKernelGGL(q8_0_mfma_kernel<4>, grid, dim3(256), 0, st, ma);
+            hipLaunchKernelGGL((q8_0_mfma_kernel<4, 4>), grid4, dim3(256), 0, st, ma);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }

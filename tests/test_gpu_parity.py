@@ -790,7 +790,7 @@ def test_llama3_8b_layer_prefill_sampled_rows(orc):
 
 
 # One row on the decode GEMV (activation in LDS up to K = 32768; 32800 takes the row kernel). More rows: automatic
-# choice (the row kernel for few rows, the int8-MFMA kernel from 12 rows or fewer for short inputs), and each kernel
+# choice (the row kernel for few rows, the int8-MFMA kernel from 8 rows or fewer for short inputs), and each kernel
 # forced ("tiled": the MFMA kernel from 2 rows, "rows": the row kernel): partial 16/32/64-row activation tiles (2 .. 16,
 # 24, 65, 130), a partial 64-output tile (70), 129 blocks per row (four-block groups with a short last one; a partial
 # 64-block GEMV item), one block per row.
