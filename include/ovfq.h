@@ -73,7 +73,8 @@ OVFQ_API int ovfq_ctx_synchronize(ovfq_ctx* ctx);
  * rows, input sizes up to 16384); OVFQ_BATCHED_TILED the 64-row-tiled MFMA kernel (3 or more rows);
  * OVFQ_BATCHED_ROWS the multi-row decode kernel (2 to 8 rows, rows * input_size <= 32768). Shapes a forced
  * kernel does not take keep the automatic choice (routed experts: only SMALL / TILED apply). For Q8_0 weights,
- * TILED forces the 64x64-tiled int8-MFMA kernel from 2 rows and SMALL / ROWS the row kernel (automatic: the MFMA
+ * TILED forces the tiled int8-MFMA kernel from 2 rows, ROWS the multi-row decode kernel (up to 8 rows, rows *
+ * input_size <= 32768) and SMALL the row kernel (automatic: the decode kernel where it takes the shape, else the MFMA
  * kernel from 8 rows, for inputs up to 8192 from 6 rows, or from 4 with 8192 outputs or more). Every choice gives
  * bit-identical outputs. Counterpart of the reference's test-only A/B toggle
  * BatchedQuantProjection.UseWeightStationaryQ4K (RT/BatchedQuantProjection.cs:21-24): for parity tests and

@@ -257,6 +257,8 @@ int launch_projection(ovfq_ctx* c, const ovfq_weight* const* ws, int count, cons
     const int in = ws[0]->in;
     if (x && rows > 1 && !use_gemv_rows(c, type, in, rows, count))
         return fail(OVFQ_ERR_SIZE, "in-launch quantisation of %d rows needs the multi-row decode kernel", rows);
+    // Every kernel below reads either the fp32 input (decode kernels that quantise it) or the quantised activation.
+    if (!x && (!act.q || !act.s)) return fail(OVFQ_ERR_NULL, "projection launch without a quantised activation");
     if (type == OVFQ_TYPE_Q8_0) {
         // The int8-MFMA kernel from 8 rows; for inputs up to 8192 from 6 rows, and from 4 rows for 8192 outputs or
         // more. Its time is flat up to 16 rows (one 16-row tile, one-wave workgroups of 16 outputs), the row
@@ -274,8 +276,16 @@ int launch_projection(ovfq_ctx* c, const ovfq_weight* const* ws, int count, cons
                                        : rows >= 8 || (in <= 8192 && (rows >= 6 || (rows >= 4 && outs >= 8192)));
         if (c->batched_kernel == OVFQ_BATCHED_TILED) q8_mfma = rows >= 2;
         else if (c->batched_kernel != OVFQ_BATCHED_AUTO) q8_mfma = false;
-        if (rows == 1 && gemv_enabled() && ovfq::q8_0_gemv_supported(in))
-            HIP_TRY(ovfq::launch_q8_0_gemv(jobs, count, in, x, act, c->stream));
+        // The decode GEMV over 1 .. 8 rows where rows * K fits its LDS copy (it loads each block once for all rows:
+        // 4096x4096 at 2 / 4 rows 7.2 / 7.8 us against the row kernel's 14.1 / 21.5 and the MFMA kernel's 25.6 / 25.8;
+        // 14336x4096 at 4 rows 16.6 against 43.1 / 31.9). One row always takes it where it runs (the batched-kernel
+        // choice is for 2 or more rows, and the caller may have left the quantisation to it); forced SMALL sends
+        // 2 .. 8 rows to the row kernel, forced TILED to the MFMA kernel.
+        const bool q8_choice = c->batched_kernel == OVFQ_BATCHED_AUTO || c->batched_kernel == OVFQ_BATCHED_ROWS;
+        const bool q8_rows = gemv_enabled() && ovfq::q8_0_gemv_rows_supported(in, rows) && (rows == 1 || q8_choice);
+        if (x && !q8_rows) return fail(OVFQ_ERR_SIZE, "in-launch Q8_0 quantisation needs the decode kernel");
+        if (q8_rows)
+            HIP_TRY(ovfq::launch_q8_0_gemv(jobs, count, in, rows, x, act, c->stream));
         else if (q8_mfma && ovfq::q8_0_mfma_supported(in, rows))
             HIP_TRY(ovfq::launch_project_q8_0_mfma(jobs, count, in, rows, act, c->stream));
         else

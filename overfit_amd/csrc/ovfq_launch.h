@@ -104,9 +104,13 @@ hipError_t launch_project_q8_0(const ProjJob* jobs, int njobs, int in, int rows,
 // Q8_0 decode (M = 1) on a persistent grid with the activation in LDS (K <= 32768), bit-identical to
 // launch_project_q8_0: from the fp32 x, quantised inside the launch (requires q8_0_gemv_quantize_inside), or,
 // x == NULL, from the prequantised `act`.
+// With 2 .. 8 activation rows (rows * in <= 32768) from the prequantised `act` only: each block is loaded once and
+// dotted with every row.
 bool q8_0_gemv_supported(int in);
+bool q8_0_gemv_rows_supported(int in, int rows);
 bool q8_0_gemv_quantize_inside(int in);
-hipError_t launch_q8_0_gemv(const ProjJob* jobs, int njobs, int in, const float* x, ActQ act, hipStream_t st);
+hipError_t launch_q8_0_gemv(const ProjJob* jobs, int njobs, int in, int rows, const float* x, ActQ act,
+                            hipStream_t st);
 // Q8_0 over several activation rows on int8 MFMA (one 16x16x32 MFMA per 32-element block), bit-identical to
 // launch_project_q8_0.
 bool q8_0_mfma_supported(int in, int rows);

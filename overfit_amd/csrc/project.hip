@@ -263,12 +263,13 @@ hipError_t launch_project_q8_0(const ProjJob* jobs, int njobs, int in, int rows,
 }
 
 // ------------------------------------------------------------------------------------------ Q8_0 decode GEMV
-// Q8DotKernel.Project / ProjectParallel (RT/Q8DotKernel.cs:155-350) at M = 1 on a persistent grid. Each workgroup
-// copies the Q8_0 activation (K int8 + K/32 f32 scales) into LDS once; its waves then walk row groups of R rows
+// Q8DotKernel.Project / ProjectParallel (RT/Q8DotKernel.cs:155-350) at M = 1 (and ProjectBatched at 2 .. 8 rows) on
+// a persistent grid. Each workgroup copies the Q8_0 activation rows (K int8 + K/32 f32 scales each) into LDS once; its waves then walk row groups of R rows
 // in items of 64 blocks: lane l takes block 64c + l of each row (its 32 weight bytes and scale; the wave reads
 // 64 consecutive blocks of a row), and the next item's loads are issued before the current item is computed. The
-// lane forms the reference's (wScale * aScale) * dot; per row, one lane adds the item's 64 block values in
-// ascending order (RT/Q8DotKernel.cs:127-137), and bias + sum is written after the row's last item.
+// lane forms the reference's (wScale * aScale) * dot for every activation row; per (activation row, output row), one
+// lane adds the item's 64 block values in ascending order (RT/Q8DotKernel.cs:127-137), and bias + sum is written
+// after the row's last item.
 struct Q8GJob {
     const int8_t* w;
     const float* ws;
@@ -284,27 +285,29 @@ struct Q8GArgs {
     int total_groups;
     int in;
     int nb;          // blocks per row
-    const float* x;  // fp32 activation, quantised in the kernel (in <= kQ8GemvQuantMaxIn); NULL -> use q / s
+    int m_rows;      // activation rows (1 .. kQ8GemvMaxRows), outputs [m_rows][n_rows] per job
+    const float* x;  // fp32 activation (one row), quantised in the kernel (in <= kQ8GemvQuantMaxIn); NULL -> q / s
     const int8_t* q;
     const float* s;
 };
 
-constexpr int kQ8GemvMaxIn = 32768;       // LDS copy of the activation: 32 KB + 4 KB of scales
+constexpr int kQ8GemvMaxIn = 32768;       // LDS copy of the activation rows: 32 KB + 4 KB of scales
+constexpr int kQ8GemvMaxRows = 8;         // activation rows per launch
 constexpr int kQ8GemvQuantMaxIn = 8192;   // in-launch quantisation (every workgroup quantises the whole input)
 
 template <int R, bool kMulti>
 __global__ __launch_bounds__(256) void q8_0_gemv_kernel(const Q8GArgs a) {
     extern __shared__ __align__(16) uint8_t smem8[];
-    const int K = a.in, nb = a.nb;
-    uint8_t* lq = smem8;                                          // [K] activation quants
-    float* ls = reinterpret_cast<float*>(smem8 + K);              // [nb] activation scales
-    float* red = ls + ((nb + 3) & ~3);                            // per wave [R][65] block values
+    const int K = a.in, nb = a.nb, M = a.m_rows;
+    uint8_t* lq = smem8;                                          // [M][K] activation quants
+    float* ls = reinterpret_cast<float*>(smem8 + M * K);          // [M][nb] activation scales
+    float* red = ls + ((M * nb + 3) & ~3);                        // per wave [R][M][65] block values
     const int wave = wave_id();
     const int lane = threadIdx.x & 63;
     const int nchunks = (nb + 63) >> 6;
     const int stride = gridDim.x * 4;
     const int total = a.total_groups;
-    float* rw = red + wave * R * 65;
+    float* rw = red + wave * R * kQ8GemvMaxRows * 65;
 
     struct Item {
         u32x4 w[R][2];
@@ -354,7 +357,7 @@ __global__ __launch_bounds__(256) void q8_0_gemv_kernel(const Q8GArgs a) {
         }
         const bool want_bias = valid && jb.bias != nullptr && c == nchunks - 1;
         const __amdgpu_buffer_rsrc_t bsr = make_rsrc(jb.bias, want_bias ? (uint32_t)jb.n_rows * 4u : 0u);
-        it.bias = ld1(bsr, (uint32_t)(jb.row0 + (lane < R ? lane : 0)) * 4u);
+        it.bias = ld1(bsr, (uint32_t)(jb.row0 + (lane < R * M ? lane / M : 0)) * 4u);
     };
 
     int g = blockIdx.x * 4 + wave;
@@ -381,8 +384,8 @@ __global__ __launch_bounds__(256) void q8_0_gemv_kernel(const Q8GArgs a) {
     } else {
         // activation -> LDS: the quant loads go out first, then the first item's weights, then the LDS stores
         constexpr int kPasses = kQ8GemvMaxIn / 4096;
-        const __amdgpu_buffer_rsrc_t qr = make_rsrc(a.q, (uint32_t)K);
-        const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.s, (uint32_t)nb * 4u);
+        const __amdgpu_buffer_rsrc_t qr = make_rsrc(a.q, (uint32_t)(M * K));  // [M][K]: the LDS layout
+        const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.s, (uint32_t)(M * nb) * 4u);
         // unconditional: offsets past K (or past the scales) read zeros through the resources' bounds
         u32x4 qv[kPasses];
 #pragma unroll
@@ -394,12 +397,12 @@ __global__ __launch_bounds__(256) void q8_0_gemv_kernel(const Q8GArgs a) {
 #pragma unroll
         for (int p = 0; p < kPasses; p++) {
             const int i = p * 4096 + (int)threadIdx.x * 16;
-            if (i < K) *reinterpret_cast<u32x4*>(lq + i) = qv[p];
+            if (i < M * K) *reinterpret_cast<u32x4*>(lq + i) = qv[p];
         }
 #pragma unroll
         for (int p = 0; p < kQ8GemvMaxIn / 32 / 256; p++) {
             const int i = p * 256 + (int)threadIdx.x;
-            if (i < nb) ls[i] = as_float(sv[p]);
+            if (i < M * nb) ls[i] = as_float(sv[p]);
         }
     }
     __syncthreads();
@@ -420,31 +423,37 @@ __global__ __launch_bounds__(256) void q8_0_gemv_kernel(const Q8GArgs a) {
         const int blk = c * 64 + lane;
         const bool live = blk < nb;
         const int ab = live ? blk : 0;
-        const u32x4 x0 = *reinterpret_cast<const u32x4*>(lq + ab * 32);
-        const u32x4 x1 = *reinterpret_cast<const u32x4*>(lq + ab * 32 + 16);
-        const float xs = ls[ab];
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            int dot = 0;
-            dot = sdot4(cur.w[r][0].x, x0.x, dot);
-            dot = sdot4(cur.w[r][0].y, x0.y, dot);
-            dot = sdot4(cur.w[r][0].z, x0.z, dot);
-            dot = sdot4(cur.w[r][0].w, x0.w, dot);
-            dot = sdot4(cur.w[r][1].x, x1.x, dot);
-            dot = sdot4(cur.w[r][1].y, x1.y, dot);
-            dot = sdot4(cur.w[r][1].z, x1.z, dot);
-            dot = sdot4(cur.w[r][1].w, x1.w, dot);
-            if (live) rw[r * 65 + lane] = as_float(cur.ws[r]) * xs * (float)dot;  // (wScale * aScale) * dot
+        for (int m = 0; m < kQ8GemvMaxRows; m++) {
+            if (m >= M) break;  // uniform
+            const u32x4 x0 = *reinterpret_cast<const u32x4*>(lq + m * K + ab * 32);
+            const u32x4 x1 = *reinterpret_cast<const u32x4*>(lq + m * K + ab * 32 + 16);
+            const float xs = ls[m * nb + ab];
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                int dot = 0;
+                dot = sdot4(cur.w[r][0].x, x0.x, dot);
+                dot = sdot4(cur.w[r][0].y, x0.y, dot);
+                dot = sdot4(cur.w[r][0].z, x0.z, dot);
+                dot = sdot4(cur.w[r][0].w, x0.w, dot);
+                dot = sdot4(cur.w[r][1].x, x1.x, dot);
+                dot = sdot4(cur.w[r][1].y, x1.y, dot);
+                dot = sdot4(cur.w[r][1].z, x1.z, dot);
+                dot = sdot4(cur.w[r][1].w, x1.w, dot);
+                // (wScale * aScale) * dot
+                if (live) rw[(r * M + m) * 65 + lane] = as_float(cur.ws[r]) * xs * (float)dot;
+            }
         }
         wave_sync();
-        if (lane < R) {
+        if (lane < R * M) {  // lane = r * M + m: weight row r, activation row m
             const int nv = min(64, nb - c * 64);
             for (int j = 0; j < nv; j++) acc += rw[lane * 65 + j];
         }
         wave_sync();
         if (c == nchunks - 1) {
-            if (lane < R && cj.row0 + lane < cj.n_rows)
-                cj.y[cj.row0 + lane] = cj.bias ? as_float(cur.bias) + acc : acc;
+            const int row = cj.row0 + lane / M, m = lane % M;
+            if (lane < R * M && row < cj.n_rows)
+                cj.y[(size_t)m * cj.n_rows + row] = cj.bias ? as_float(cur.bias) + acc : acc;
             acc = 0.0f;
         }
         g = ng;
@@ -457,6 +466,9 @@ __global__ __launch_bounds__(256) void q8_0_gemv_kernel(const Q8GArgs a) {
 }
 
 bool q8_0_gemv_supported(int in) { return in % 32 == 0 && in <= kQ8GemvMaxIn; }
+bool q8_0_gemv_rows_supported(int in, int rows) {
+    return rows >= 1 && rows <= kQ8GemvMaxRows && in % 32 == 0 && (long)rows * in <= kQ8GemvMaxIn;
+}
 bool q8_0_gemv_quantize_inside(int in) { return q8_0_gemv_supported(in) && in <= kQ8GemvQuantMaxIn; }
 
 namespace {
@@ -488,7 +500,8 @@ hipError_t launch_q8g(Q8GArgs& ga, const ProjJob* jobs, int njobs, hipStream_t s
     int wgs = (groups + 3) / 4;
     const int cap = q8_cu_count() * wg_per_cu;
     if (wgs > cap) wgs = cap;
-    const size_t lds = (size_t)ga.in + 4 * (size_t)((ga.nb + 3) & ~3) + 4 * (size_t)4 * R * 65;
+    const size_t lds = (size_t)ga.m_rows * ga.in + 4 * (size_t)((ga.m_rows * ga.nb + 3) & ~3) +
+                       4 * (size_t)4 * R * kQ8GemvMaxRows * 65;
     if (njobs > 1)
         hipLaunchKernelGGL((q8_0_gemv_kernel<R, true>), dim3(wgs), dim3(256), lds, st, ga);
     else
@@ -497,8 +510,10 @@ hipError_t launch_q8g(Q8GArgs& ga, const ProjJob* jobs, int njobs, hipStream_t s
 }
 }  // namespace
 
-hipError_t launch_q8_0_gemv(const ProjJob* jobs, int njobs, int in, const float* x, ActQ act, hipStream_t st) {
-    if (x && !q8_0_gemv_quantize_inside(in)) return hipErrorInvalidValue;
+hipError_t launch_q8_0_gemv(const ProjJob* jobs, int njobs, int in, int rows, const float* x, ActQ act,
+                            hipStream_t st) {
+    if ((x && (rows != 1 || !q8_0_gemv_quantize_inside(in))) || !q8_0_gemv_rows_supported(in, rows))
+        return hipErrorInvalidValue;
     Q8GArgs ga{};
     for (int i = 0; i < kMaxJobs; i++) {
         if (i < njobs)
@@ -510,6 +525,7 @@ hipError_t launch_q8_0_gemv(const ProjJob* jobs, int njobs, int in, const float*
     ga.njobs = njobs;
     ga.in = in;
     ga.nb = in / 32;
+    ga.m_rows = rows;
     ga.x = x;
     ga.q = act.q;
     ga.s = act.s;

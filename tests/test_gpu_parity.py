@@ -790,11 +790,12 @@ def test_llama3_8b_layer_prefill_sampled_rows(orc):
 
 
 # One row on the decode GEMV (activation in LDS up to K = 32768; 32800 takes the row kernel). More rows: automatic
-# choice (the row kernel for few rows, the int8-MFMA kernel from 8 rows or fewer for short inputs), and each kernel
-# forced ("tiled": the MFMA kernel from 2 rows, "rows": the row kernel): partial 16/32/64-row activation tiles (2 .. 16,
+# choice (the decode kernel over up to 4 rows, the row kernel, the int8-MFMA kernel from 8 rows or fewer for short
+# inputs), and each kernel forced ("tiled": the MFMA kernel from 2 rows, "rows": the multi-row decode kernel where it
+# takes the shape, "small": the row kernel): partial 16/32/64-row activation tiles (2 .. 16,
 # 24, 65, 130), a partial 64-output tile (70), 129 blocks per row (four-block groups with a short last one; a partial
 # 64-block GEMV item), one block per row.
-@pytest.mark.parametrize("kernel", ["auto", "tiled", "rows"])
+@pytest.mark.parametrize("kernel", ["auto", "tiled", "rows", "small"])
 @pytest.mark.parametrize("k,n", [(32, 5), (128, 4096), (4096, 300), (14336, 40), (4128, 70), (32768, 24),
                                  (32800, 9)])
 @pytest.mark.parametrize("rows", [1, 2, 3, 7, 16, 24, 65, 130])
