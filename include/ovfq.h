@@ -19,6 +19,14 @@
  *  - Thread safety: any number of host threads may call into one context; calls are serialised by a
  *    per-context lock and run in order on the context's stream (the reference calls Project concurrently from
  *    its head-parallel workers, RT/CachedMultiHeadAttention.cs:280, :876-907).
+ *  - Lifetime: a weight belongs to the context it was created on, and that context must outlive it
+ *    (ovfq_ctx_destroy returns OVFQ_ERR_SIZE, destroying nothing, while any of its weights is alive).
+ *  - Sizes: every activation and output plane (rows x its width) stays below 2^31 elements, the length limit
+ *    of the reference's Span<T> scratch and outputs; larger calls return OVFQ_ERR_SIZE.
+ *  - Scratch and HIP graphs: the context grows its device scratch on demand (activation quantisation, FFN and
+ *    MoE intermediates, host staging) and never frees a superseded buffer before ovfq_ctx_destroy, so a graph
+ *    captured from _dev calls stays valid after later, larger calls on the same context. Work captured into a
+ *    graph and work issued eagerly on the same context share that scratch: they must not run concurrently.
  */
 #ifndef OVFQ_H
 #define OVFQ_H
@@ -163,7 +171,12 @@ OVFQ_API int ovfq_project_dev(ovfq_ctx* ctx, const ovfq_weight* w, const float* 
 
 /* Q4KDotKernel.ProjectPreQuantized (RT/Q4KDotKernel.cs:445-476) / Q6KDotKernel.ProjectPreQuantized
  * (RT/Q6KDotKernel.cs:274-305), for `rows` rows of an already-quantised Q8_K activation in the layout
- * ovfq_quantize_q8k writes. For Q8_0 weights pass the Q8_0 activation scales in `scales` and NULL bsums. */
+ * ovfq_quantize_q8k writes. For Q8_0 weights pass the Q8_0 activation scales in `scales` and NULL bsums.
+ * Precondition, as in the reference: bsums[g] is the sum of the 16 quants of group g (QuantizeActivationQ8K's
+ * definition, RT/Q4KDotKernel.cs:122-135), which every quantiser here writes. The decode kernels (1 to 8 rows)
+ * read the bsums plane as the reference's Dot does; the MFMA kernels that take larger batches form the same
+ * sums from the quants themselves. Bsums that are not those sums therefore give results that depend on the
+ * row count. */
 OVFQ_API int ovfq_project_prequantized(ovfq_ctx* ctx, const ovfq_weight* w, const int8_t* quants,
                                        const float* scales, const int16_t* bsums, int rows, const float* bias,
                                        float* y);

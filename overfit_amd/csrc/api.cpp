@@ -11,6 +11,7 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "../../include/ovfq.h"
 #include "ovfq_launch.h"
@@ -58,6 +59,11 @@ struct ovfq_ctx {
     DevBuf act_q, act_s, act_b, x_stage, y_stage, y2_stage, bias_stage;
     // Routed-MoE scratch (plan, gate/up/intermediate/expert outputs, host staging), carved from one buffer.
     DevBuf moe;
+    // Scratch buffers replaced by larger ones. A HIP graph captured from _dev calls keeps the addresses it
+    // was recorded with, so a superseded buffer stays allocated until the context is destroyed.
+    std::vector<void*> retired;
+    // Live weights created on this context (ovfq_ctx_destroy refuses while any remain).
+    int live_weights = 0;
 };
 
 struct ovfq_weight {
@@ -73,18 +79,18 @@ struct ovfq_weight {
 
 namespace {
 
-// Grows `b` to at least `bytes`, waiting for queued work that may still read the old buffer.
+// Grows `b` to at least `bytes`. The old buffer is not freed: queued work and any HIP graph captured from
+// earlier calls may still address it, so it is kept in `retired` until ovfq_ctx_destroy. Capacities at least
+// double on growth, which bounds the retired bytes by the live buffer's size.
 int ensure(ovfq_ctx* c, DevBuf& b, size_t bytes) {
     if (b.cap >= bytes) return OVFQ_OK;
-    if (b.p) {
-        HIP_TRY(hipStreamSynchronize(c->stream));
-        HIP_TRY(hipFree(b.p));
-        b.p = nullptr;
-        b.cap = 0;
-    }
     size_t cap = bytes < 4096 ? 4096 : bytes;
+    if (cap < 2 * b.cap) cap = 2 * b.cap;
     cap = (cap + 255) & ~size_t(255);
-    HIP_TRY(hipMalloc(&b.p, cap));
+    void* p = nullptr;
+    HIP_TRY(hipMalloc(&p, cap));
+    if (b.p) c->retired.push_back(b.p);
+    b.p = p;
     b.cap = cap;
     return OVFQ_OK;
 }
@@ -152,6 +158,7 @@ int weight_create(ovfq_ctx* ctx, int type, const void* blocks, size_t nbytes, co
         return fail(OVFQ_ERR_HIP, "weight upload failed: %s", hipGetErrorString(e));
     }
     w->nbytes = expected + scale_bytes;
+    ctx->live_weights++;
     *res = w;
     return ok();
 }
@@ -334,6 +341,16 @@ int check_rows(int rows) {
     return OVFQ_OK;
 }
 
+// An activation or output plane of `rows` x `cols` elements must stay below 2^31 elements, the length limit of
+// the reference's spans (its scratch and outputs are Span<T>); the kernels index such planes with 32-bit
+// offsets.
+int check_plane(int64_t rows, int64_t cols, const char* what) {
+    if (rows * cols >= ((int64_t)1 << 31))
+        return fail(OVFQ_ERR_SIZE, "%s of %lld x %lld elements exceeds 2^31 - 1", what, (long long)rows,
+                    (long long)cols);
+    return OVFQ_OK;
+}
+
 // Device pointers handed to the _dev entry points must keep the kernels' 4-byte (quants/bsums) alignment.
 // Carves 256-byte-aligned pieces off a base pointer.
 struct Carver {
@@ -384,12 +401,16 @@ int ovfq_ctx_destroy(ovfq_ctx* c) {
     if (!c) return fail(OVFQ_ERR_NULL, "ctx is NULL");
     {
         std::lock_guard<std::mutex> lk(c->mu);
+        // A weight locks its context when destroyed, so the context must outlive every weight made on it.
+        if (c->live_weights > 0)
+            return fail(OVFQ_ERR_SIZE, "context still owns %d weight(s): destroy them first", c->live_weights);
         (void)hipSetDevice(c->device);
         (void)hipStreamSynchronize(c->stream);
         DevBuf* bufs[] = {&c->act_q,   &c->act_s,   &c->act_b,      &c->x_stage,
                           &c->y_stage, &c->y2_stage, &c->bias_stage, &c->moe};
         for (DevBuf* b : bufs)
             if (b->p) (void)hipFree(b->p);
+        for (void* p : c->retired) (void)hipFree(p);
         if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
     }
     delete c;
@@ -486,6 +507,7 @@ static int weight_create_gguf(ovfq_ctx* ctx, int type, const void* src, size_t n
         return fail(OVFQ_ERR_HIP, "Q8_0 GGUF upload failed: %s", hipGetErrorString(e));
     }
     w->nbytes = (size_t)n_blocks * (OVFQ_Q8_BLOCK + sizeof(float));
+    ctx->live_weights++;
     *res = w;
     return ok();
 }
@@ -509,6 +531,7 @@ int ovfq_weight_destroy(ovfq_weight* w) {
         if (w->blocks) (void)hipFree(w->blocks);
         if (w->scales) (void)hipFree(w->scales);
         if (w->mfma) (void)hipFree(w->mfma);
+        w->ctx->live_weights--;
     }
     delete w;
     return ok();
@@ -592,6 +615,7 @@ static int quantize_impl(ovfq_ctx* ctx, bool k_quant, const float* x, int rows, 
     const int blk = k_quant ? OVFQ_QK : OVFQ_Q8_BLOCK;
     if (k <= 0 || k % blk)
         return fail(OVFQ_ERR_SIZE, "Source length (%d) must be a multiple of %d.", k, blk);
+    if ((rc = check_plane(rows, k, "activation"))) return rc;
     if (!host) {
         if ((rc = check_dev_align(x, "x")) || (rc = check_dev_align(q, "quants")) ||
             (rc = check_dev_align(s, "scales")) || (rc = check_dev_align(b, "bsums")))
@@ -659,9 +683,11 @@ static int project_impl(ovfq_ctx* ctx, int count, const ovfq_weight* const* ws, 
         if (ws[i]->type != ws[0]->type) return fail(OVFQ_ERR_TYPE, "fused weights must share a type");
         if (ws[i]->in != ws[0]->in) return fail(OVFQ_ERR_SIZE, "fused weights must share inputSize");
         if (!host && (rc = check_dev_align(ys[i], "output"))) return rc;
+        if ((rc = check_plane(rows, ws[i]->out, "output"))) return rc;
     }
     if (!host && (rc = check_dev_align(x, "input"))) return rc;
     const int in = ws[0]->in;
+    if ((rc = check_plane(rows, in, "activation"))) return rc;
     std::lock_guard<std::mutex> lk(ctx->mu);
     HIP_TRY(hipSetDevice(ctx->device));
     const float* xd = x;
@@ -758,6 +784,7 @@ static int prequant_impl(ovfq_ctx* ctx, const ovfq_weight* w, const int8_t* q, c
     const bool kq = w->type != OVFQ_TYPE_Q8_0;
     if (!q || !s || (kq && !b) || !y) return fail(OVFQ_ERR_NULL, "activation scratch or output is NULL");
     if ((rc = check_rows(rows))) return rc;
+    if ((rc = check_plane(rows, w->in, "activation")) || (rc = check_plane(rows, w->out, "output"))) return rc;
     if (!host) {
         if ((rc = check_dev_align(q, "quants")) || (rc = check_dev_align(s, "scales")) ||
             (rc = check_dev_align(b, "bsums")) || (rc = check_dev_align(y, "output")))
@@ -825,6 +852,9 @@ int ovfq_project_multi_prequantized_dev(ovfq_ctx* ctx, int count, const ovfq_wei
         if ((rc = check_dev_align(ys[i], "output"))) return rc;
     }
     if ((rc = check_rows(rows))) return rc;
+    if ((rc = check_plane(rows, ws[0]->in, "activation"))) return rc;
+    for (int i = 0; i < count; i++)
+        if ((rc = check_plane(rows, ws[i]->out, "output"))) return rc;
     if ((rc = check_dev_align(q, "quants")) || (rc = check_dev_align(s, "scales")) || (rc = check_dev_align(b, "bsums")))
         return rc;
     std::lock_guard<std::mutex> lk(ctx->mu);
@@ -844,6 +874,7 @@ static int topk_impl(ovfq_ctx* ctx, const float* logits, int rows, int n_experts
         return fail(OVFQ_ERR_SIZE, "n_experts (%d) above %d", n_experts, OVFQ_MAX_EXPERTS);
     if (top_k < 1) return fail(OVFQ_ERR_RANGE, "top_k (%d) must be positive", top_k);
     if (rows < 1) return fail(OVFQ_ERR_RANGE, "rows (%d) must be positive", rows);
+    if (check_plane(rows, n_experts, "logits") || check_plane(rows, top_k, "expert_indices")) return OVFQ_ERR_SIZE;
     if (!host && (rc_align(logits) || rc_align(idx) || rc_align(w)))
         return fail(OVFQ_ERR_SIZE, "device pointers must be 4-byte aligned");
     const int k = top_k < n_experts ? top_k : n_experts;
@@ -888,9 +919,9 @@ static int moe_impl(ovfq_ctx* ctx, int E, const ovfq_weight* const* gate, const 
     if (!gate || !up || !down) return fail(OVFQ_ERR_NULL, "expert weight arrays are NULL");
     if (!x || !idx || !w || !y) return fail(OVFQ_ERR_NULL, "x / expert_indices / expert_weights / y is NULL");
     if (E < 1 || E > OVFQ_MAX_EXPERTS) return fail(OVFQ_ERR_RANGE, "n_experts (%d) must be in [1, %d]", E, OVFQ_MAX_EXPERTS);
-    if (rows < 1) return fail(OVFQ_ERR_RANGE, "rows (%d) must be positive", rows);
-    if (k < 1 || k > E) return fail(OVFQ_ERR_RANGE, "top_k (%d) must be in [1, n_experts]", k);
     int rc;
+    if ((rc = check_rows(rows))) return rc;
+    if (k < 1 || k > E) return fail(OVFQ_ERR_RANGE, "top_k (%d) must be in [1, n_experts]", k);
     for (int e = 0; e < E; e++) {
         if (!gate[e] || !up[e] || !down[e]) return fail(OVFQ_ERR_NULL, "expert %d has a NULL weight", e);
         if ((rc = check_weight(ctx, gate[e])) || (rc = check_weight(ctx, up[e])) || (rc = check_weight(ctx, down[e])))
@@ -909,6 +940,10 @@ static int moe_impl(ovfq_ctx* ctx, int E, const ovfq_weight* const* gate, const 
     }
     if (!host && (rc_align(x) || rc_align(idx) || rc_align(w) || rc_align(y)))
         return fail(OVFQ_ERR_SIZE, "device pointers must be 4-byte aligned");
+    // token rows and (token, slot) pair rows of the activation, gate/up and expert-output planes
+    if ((rc = check_plane(rows, dmodel, "activation")) || (rc = check_plane((int64_t)rows * k, dff, "gate/up output")) ||
+        (rc = check_plane((int64_t)rows * k, dmodel, "expert output")))
+        return rc;
     const size_t P = (size_t)rows * k;
     std::lock_guard<std::mutex> lk(ctx->mu);
     HIP_TRY(hipSetDevice(ctx->device));
@@ -1042,6 +1077,7 @@ static int ffn_impl(ovfq_ctx* ctx, const ovfq_weight* gate, const ovfq_weight* u
     if (up->in != dmodel || up->out != dff || down->in != dff || down->out != dmodel)
         return fail(OVFQ_ERR_SIZE, "shapes must be gate/up [d_ff][d_model] and down [d_model][d_ff]");
     if (!host && (rc_align(x) || rc_align(y))) return fail(OVFQ_ERR_SIZE, "device pointers must be 4-byte aligned");
+    if ((rc = check_plane(rows, dmodel, "activation")) || (rc = check_plane(rows, dff, "gate/up output"))) return rc;
     std::lock_guard<std::mutex> lk(ctx->mu);
     HIP_TRY(hipSetDevice(ctx->device));
     const size_t R = (size_t)rows;

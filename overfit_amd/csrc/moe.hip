@@ -21,6 +21,12 @@ namespace ovfq {
 // One thread per token: insertion of each logit into a descending top-k list (ties keep the lower index), then
 // softmax over the k kept logits (normalize) or the full softmax evaluated at them. The workgroup's 64 logit rows
 // are first copied to LDS with coalesced loads, so the sequential scan reads LDS, not memory.
+//
+// The list has KM >= k entries, every one indexed at compile time so that it lives in registers (a list indexed
+// at run time would sit in scratch memory). One insertion is the reference's loop written as a selection per
+// entry: with pos0 = min(filled, k - 1), the entries j in (p, pos0] take entry j - 1 and entry p takes the new
+// logit, where p is where the reference's `while (pos > 0 && w[pos - 1] < l) pos--` stops (RT/MoeRouter.cs:70-91).
+template <int KM>
 __global__ __launch_bounds__(64) void moe_topk_kernel(const float* __restrict__ logits, int rows, int n_experts,
                                                       int k, int stride, int normalize, int* __restrict__ idx_out,
                                                       float* __restrict__ w_out) {
@@ -32,45 +38,67 @@ __global__ __launch_bounds__(64) void moe_topk_kernel(const float* __restrict__ 
     const int n = row0 + threadIdx.x;
     if (n >= rows) return;
     const float* l = sl + threadIdx.x * n_experts;
-    int idx[kMaxExperts];
-    float wv[kMaxExperts];
-    for (int i = 0; i < k; i++) {
+    int idx[KM];
+    float wv[KM];
+#pragma unroll
+    for (int i = 0; i < KM; i++) {
         idx[i] = -1;
         wv[i] = -INFINITY;
     }
     int filled = 0;
     for (int e = 0; e < n_experts; e++) {
         const float v = l[e];
-        if (filled == k && v <= wv[k - 1]) continue;
-        int pos = filled < k ? filled : k - 1;
-        while (pos > 0 && wv[pos - 1] < v) {
-            wv[pos] = wv[pos - 1];
-            idx[pos] = idx[pos - 1];
-            pos--;
+        float last = wv[0];
+#pragma unroll
+        for (int i = 1; i < KM; i++) last = i == k - 1 ? wv[i] : last;
+        if (filled == k && v <= last) continue;
+        const int pos0 = filled < k ? filled : k - 1;
+        float nw[KM];
+        int ni[KM];
+        bool shift_above = false;  // entry j + 1 takes entry j
+#pragma unroll
+        for (int j = KM - 1; j >= 0; j--) {
+            const bool in_run = j <= pos0 && (j == pos0 || shift_above);
+            const bool shift = j > 0 && in_run && wv[j > 0 ? j - 1 : 0] < v;
+            const bool place = in_run && !shift;
+            nw[j] = shift ? wv[j > 0 ? j - 1 : 0] : (place ? v : wv[j]);
+            ni[j] = shift ? idx[j > 0 ? j - 1 : 0] : (place ? e : idx[j]);
+            shift_above = shift;
         }
-        wv[pos] = v;
-        idx[pos] = e;
+#pragma unroll
+        for (int j = 0; j < KM; j++) {
+            wv[j] = nw[j];
+            idx[j] = ni[j];
+        }
         if (filled < k) filled++;
     }
     const float mx = wv[0];
     if (normalize) {
         float sum = 0.0f;
-        for (int i = 0; i < k; i++) {
-            const float w = expf(wv[i] - mx);
-            wv[i] = w;
-            sum += w;
+#pragma unroll
+        for (int i = 0; i < KM; i++) {
+            if (i < k) {
+                const float w = expf(wv[i] - mx);
+                wv[i] = w;
+                sum += w;
+            }
         }
         const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
-        for (int i = 0; i < k; i++) wv[i] *= inv;
+#pragma unroll
+        for (int i = 0; i < KM; i++) wv[i] *= inv;
     } else {
         float total = 0.0f;
         for (int e = 0; e < n_experts; e++) total += expf(l[e] - mx);
         const float inv = total > 0.0f ? 1.0f / total : 0.0f;
-        for (int i = 0; i < k; i++) wv[i] = expf(wv[i] - mx) * inv;
+#pragma unroll
+        for (int i = 0; i < KM; i++) wv[i] = expf(wv[i] - mx) * inv;
     }
-    for (int i = 0; i < k; i++) {
-        idx_out[(size_t)n * stride + i] = idx[i];
-        w_out[(size_t)n * stride + i] = wv[i];
+#pragma unroll
+    for (int i = 0; i < KM; i++) {
+        if (i < k) {
+            idx_out[(size_t)n * stride + i] = idx[i];
+            w_out[(size_t)n * stride + i] = wv[i];
+        }
     }
 }
 
@@ -232,8 +260,18 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
 
 hipError_t launch_moe_topk(const float* logits, int rows, int n_experts, int k, int stride, int normalize, int* idx,
                            float* w, hipStream_t st) {
-    hipLaunchKernelGGL(moe_topk_kernel, dim3((rows + 63) / 64), dim3(64), 0, st, logits, rows, n_experts, k, stride,
-                       normalize, idx, w);
+    const dim3 grid((rows + 63) / 64), block(64);
+    if (k <= 2)
+        hipLaunchKernelGGL(moe_topk_kernel<2>, grid, block, 0, st, logits, rows, n_experts, k, stride, normalize, idx, w);
+    else if (k <= 4)
+        hipLaunchKernelGGL(moe_topk_kernel<4>, grid, block, 0, st, logits, rows, n_experts, k, stride, normalize, idx, w);
+    else if (k <= 8)
+        hipLaunchKernelGGL(moe_topk_kernel<8>, grid, block, 0, st, logits, rows, n_experts, k, stride, normalize, idx, w);
+    else if (k <= 16)
+        hipLaunchKernelGGL(moe_topk_kernel<16>, grid, block, 0, st, logits, rows, n_experts, k, stride, normalize, idx, w);
+    else
+        hipLaunchKernelGGL(moe_topk_kernel<kMaxExperts>, grid, block, 0, st, logits, rows, n_experts, k, stride, normalize,
+                           idx, w);
     return hipGetLastError();
 }
 

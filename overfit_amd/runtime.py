@@ -113,8 +113,10 @@ class Context:
         self.check(self.lib.ovfq_ctx_set_batched_kernel(self.handle, self.BATCHED_KERNELS[kind]))
 
     def close(self):
+        """Destroys the context. Every weight created on it must have been destroyed first (the library refuses
+        otherwise, and the context stays usable)."""
         if self.handle:
-            self.lib.ovfq_ctx_destroy(self.handle)
+            self.check(self.lib.ovfq_ctx_destroy(self.handle))
             self.handle = None
 
     # ---------------------------------------------------------------- device-pointer conveniences

@@ -1,0 +1,181 @@
+"""API edges of libovfq on the device: lifetime rules, span-size bounds, the router's register top-k over many
+list sizes, and HIP-graph replay after the context's scratch has grown.
+
+Every refusal here happens in the host-side validation, before any device work (the reference throws before
+work, RT/Q4KDotKernel.cs:77-97); the buffers passed with them are small and never read.
+"""
+import ctypes
+import sys
+
+import numpy as np
+import pytest
+
+from qdata import normal, random_q4k_blocks, random_q6k_blocks
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+ov = pytest.importorskip("overfit_amd")
+from overfit_amd import _lib  # noqa: E402
+
+DEV = "cuda:0"
+
+
+def case(*what):
+    print("[case]", *what, flush=True, file=sys.stderr)
+
+
+def t(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def vp(x):
+    return ctypes.c_void_p(x.data_ptr())
+
+
+def test_context_outlives_its_weights(orc):
+    """ovfq_ctx_destroy refuses while a weight made on the context is alive (a weight locks its context when it is
+    destroyed), and succeeds once the weights are gone."""
+    case("ctx lifetime")
+    ctx = ov.Context(0)
+    rng = np.random.default_rng(1)
+    blocks = random_q4k_blocks(rng, 4).reshape(2, -1)
+    w = ov.Q4KWeight(blocks, 512, 2, ctx=ctx)
+    rc = ctx.lib.ovfq_ctx_destroy(ctx.handle)
+    assert rc == _lib.OVFQ_ERR_SIZE and b"destroy them first" in ctx.lib.ovfq_last_error()
+    x = normal(rng, 512)
+    y = ov.project(w, x)  # the context is still usable
+    assert np.array_equal(y.view(np.uint32), orc.q4k_project(x, blocks, 512, 2).view(np.uint32))
+    del w
+    import gc
+    gc.collect()
+    ctx.close()
+    assert ctx.handle is None
+
+
+def test_plane_bounds_are_refused_before_work():
+    """Activation / output planes of 2^31 elements or more (the reference's Span<T> limit) are refused with
+    OVFQ_ERR_SIZE by every projection entry point; the kernels' 32-bit offsets never see them."""
+    ctx = ov.default_context()
+    lib = ctx.lib
+    rng = np.random.default_rng(2)
+    k = 32768
+    w = ov.Q4KWeight(random_q4k_blocks(rng, k // 256).reshape(1, -1), k, 1)
+    w8 = ov.Q8Weight(np.zeros(k, np.int8), np.zeros(k // 32, np.float32), k, 1)
+    buf = torch.zeros(1024, device=DEV)
+    q = torch.zeros(1024, dtype=torch.int8, device=DEV)
+    b = torch.zeros(1024, dtype=torch.int16, device=DEV)
+    rows = 65536  # rows x 32768 = 2^31
+    case("plane bounds", rows, k)
+    assert lib.ovfq_project_dev(ctx.handle, w.handle, vp(buf), rows, None, vp(buf)) == _lib.OVFQ_ERR_SIZE
+    assert b"exceeds 2^31" in lib.ovfq_last_error()
+    assert lib.ovfq_project_dev(ctx.handle, w8.handle, vp(buf), rows, None, vp(buf)) == _lib.OVFQ_ERR_SIZE
+    assert lib.ovfq_project_prequantized_dev(ctx.handle, w.handle, vp(q), vp(buf), vp(b), rows, None,
+                                             vp(buf)) == _lib.OVFQ_ERR_SIZE
+    assert lib.ovfq_quantize_q8k_dev(ctx.handle, vp(buf), rows, k, vp(q), vp(buf), vp(b)) == _lib.OVFQ_ERR_SIZE
+    assert lib.ovfq_quantize_q8_0_dev(ctx.handle, vp(buf), rows, k, vp(q), vp(buf)) == _lib.OVFQ_ERR_SIZE
+    W = (ctypes.c_void_p * 1)(w.handle.value)
+    Y = (ctypes.c_void_p * 1)(buf.data_ptr())
+    assert lib.ovfq_project_multi_prequantized_dev(ctx.handle, 1, W, vp(q), vp(buf), vp(b), rows, None,
+                                                   Y) == _lib.OVFQ_ERR_SIZE
+    # one row below the bound passes validation (not run: rows - 1 rows of 32768 would need 8 GB of input)
+
+
+def test_moe_rows_and_pair_planes_are_refused_before_work():
+    """ovfq_moe_ffn_dev validates rows like every other entry point (1 .. 65536) and keeps the (token, slot) pair
+    planes (pairs x d_ff of gate/up outputs and of the Q8_K intermediate) below 2^31 elements."""
+    ctx = ov.default_context()
+    lib = ctx.lib
+    rng = np.random.default_rng(3)
+    E, dm, dff = 2, 256, 16384
+    gate = [ov.Q4KWeight(random_q4k_blocks(rng, dff).reshape(dff, -1), dm, dff) for _ in range(E)]
+    up = [ov.Q4KWeight(random_q4k_blocks(rng, dff).reshape(dff, -1), dm, dff) for _ in range(E)]
+    down = [ov.Q6KWeight(random_q6k_blocks(rng, dm * dff // 256).reshape(dm, -1), dff, dm) for _ in range(E)]
+    G, U, D = [(ctypes.c_void_p * E)(*[x.handle.value for x in ws]) for ws in (gate, up, down)]
+    buf = torch.zeros(1024, device=DEV)
+    idx = torch.zeros(1024, dtype=torch.int32, device=DEV)
+    for rows, k, want in [(0, 1, _lib.OVFQ_ERR_RANGE), (65537, 1, _lib.OVFQ_ERR_RANGE),
+                          (65536, 2, _lib.OVFQ_ERR_SIZE)]:
+        case("moe bounds", rows, k)
+        rc = lib.ovfq_moe_ffn_dev(ctx.handle, E, G, U, D, vp(buf), rows, k, vp(idx), vp(buf), vp(buf))
+        assert rc == want, (rows, k, rc, lib.ovfq_last_error())
+
+
+@pytest.mark.parametrize("E,k", [(8, 1), (8, 2), (8, 3), (16, 4), (16, 5), (60, 8), (64, 9), (64, 16), (64, 17),
+                                 (40, 33), (64, 64)])
+@pytest.mark.parametrize("normalize", [True, False])
+def test_topk_register_list_every_size(orc, E, k, normalize):
+    """MoeRouter.SelectTopK for list sizes across every compiled bucket (2, 4, 8, 16 and the 64-entry list), with
+    ties (the lower index wins) and -inf logits: indices exact, weights within a few ULP (expf)."""
+    case("topk", E, k, normalize)
+    rng = np.random.default_rng(E * 100 + k)
+    rows = 70
+    logits = (rng.integers(0, 12, size=(rows, E)) / 4.0).astype(np.float32)  # many ties
+    logits[5, :] = -np.inf
+    logits[6, : E // 2] = -np.inf
+    logits[7] = rng.standard_normal(E).astype(np.float32)
+    idx = torch.full((rows * k,), -9, dtype=torch.int32, device=DEV)
+    w = torch.zeros(rows * k, dtype=torch.float32, device=DEV)
+    assert ov.MoeRouter.SelectTopK(t(logits), k, idx, w, normalize, rows=rows) == min(k, E)
+    torch.cuda.synchronize()
+    gi, gw = idx.cpu().numpy(), w.cpu().numpy()
+    for n in range(rows):
+        ri, rw = orc.moe_select_topk(logits[n], k, normalize)
+        assert np.array_equal(gi[n * k:(n + 1) * k], ri), n
+        np.testing.assert_allclose(gw[n * k:(n + 1) * k], rw, rtol=4e-7, atol=0, err_msg=str(n))
+
+
+def test_graph_replay_after_scratch_growth(orc):
+    """A graph captured from _dev calls at one size keeps the scratch addresses it was recorded with. A larger eager
+    call afterwards grows the context's scratch; the superseded buffers stay allocated, so later replays still
+    reproduce the eager outputs bit-for-bit (and the larger call is itself exact)."""
+    case("graph replay after growth")
+    ctx = ov.Context(0)
+    rng = np.random.default_rng(21)
+    k, n, k2 = 4096, 256, 14336
+    bq = random_q4k_blocks(rng, n * k // 256).reshape(n, -1)
+    bd = random_q6k_blocks(rng, n * k2 // 256).reshape(n, -1)
+    wq = ov.Q4KWeight(bq, k, n, ctx=ctx)
+    wd = ov.Q6KWeight(bd, k2, n, ctx=ctx)
+    x1 = t(normal(rng, (40, k)))   # batched: quantised into the context scratch
+    x2 = t(normal(rng, (1, k2)))   # long decode row: quantised into the context scratch
+    ys = [torch.empty(40 * n, device=DEV), torch.empty(n, device=DEV)]
+
+    def step():
+        ctx.project_dev(wq, x1, ys[0], rows=40)
+        ctx.project_dev(wd, x2, ys[1], rows=1)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        ctx.set_stream(side.cuda_stream)
+        step()
+        side.synchronize()
+        eager = [y.cpu().numpy().copy() for y in ys]
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=side):
+            step()
+    ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+    big_rows = 300
+    xb = normal(rng, (big_rows, k2))
+    yb = torch.empty(big_rows * n, device=DEV)
+    for rep in range(3):
+        # a larger eager call each time: grows the activation scratch past what the graph was captured with
+        rows = big_rows if rep == 0 else big_rows // (rep + 1)
+        ctx.project_dev(wd, t(xb[:rows]), yb, rows=rows)
+        torch.cuda.synchronize()
+        if rep == 0:
+            ref = orc.q6k_project_batched(xb[:rows], rows, bd, k2, n, None)
+            got = yb[: rows * n].cpu().numpy()
+            assert np.array_equal(got.view(np.uint32), ref.reshape(-1).view(np.uint32)), "large eager call"
+        for y in ys:
+            y.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        for y, e in zip(ys, eager):
+            assert np.array_equal(y.cpu().numpy().view(np.uint32), e.view(np.uint32)), f"replay {rep}"
+    del g
+    del wq, wd
+    import gc
+    gc.collect()
+    ctx.close()
