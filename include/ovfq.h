@@ -169,6 +169,18 @@ OVFQ_API int ovfq_project(ovfq_ctx* ctx, const ovfq_weight* w, const float* x, i
 OVFQ_API int ovfq_project_dev(ovfq_ctx* ctx, const ovfq_weight* w, const float* x, int rows,
                               const float* bias, float* y);
 
+/* ovfq_project_dev that allocates nothing. No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, kernels and bit-identical outputs as ovfq_project_dev; where that entry point quantises the
+ * activation into the context's growable scratch, this one uses a fixed device array of 2.5 MiB that the
+ * library holds on every GPU it runs on until the process ends. rows * input_size is limited to 2^21
+ * (OVFQ_NOALLOC_MAX_ELEMS; e.g. 512 rows of 4096); larger calls return OVFQ_ERR_SIZE. Every call on one GPU
+ * uses that GPU's one array, through any context: calls that may overlap on a GPU (two contexts, or two
+ * streams) race and must be serialised by the caller. */
+#define OVFQ_NOALLOC_MAX_ELEMS (1 << 21)
+OVFQ_API int ovfq_project_noalloc_dev(ovfq_ctx* ctx, const ovfq_weight* w, const float* x, int rows,
+                                      const float* bias, float* y);
+
 /* Q4KDotKernel.ProjectPreQuantized (RT/Q4KDotKernel.cs:445-476) / Q6KDotKernel.ProjectPreQuantized
  * (RT/Q6KDotKernel.cs:274-305), for `rows` rows of an already-quantised Q8_K activation in the layout
  * ovfq_quantize_q8k writes. For Q8_0 weights pass the Q8_0 activation scales in `scales` and NULL bsums.

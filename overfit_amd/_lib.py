@@ -49,6 +49,7 @@ SIGNATURES = {
     "ovfq_quantize_q8_0_dev": (ci, [vp, vp, ci, ci, vp, vp]),
     "ovfq_project": (ci, [vp, vp, vp, ci, vp, vp]),
     "ovfq_project_dev": (ci, [vp, vp, vp, ci, vp, vp]),
+    "ovfq_project_noalloc_dev": (ci, [vp, vp, vp, ci, vp, vp]),
     "ovfq_project_prequantized": (ci, [vp, vp, vp, vp, vp, ci, vp, vp]),
     "ovfq_project_prequantized_dev": (ci, [vp, vp, vp, vp, vp, ci, vp, vp]),
     "ovfq_project_gate_up": (ci, [vp, vp, vp, vp, vp, vp]),

@@ -95,6 +95,8 @@ int ensure(ovfq_ctx* c, DevBuf& b, size_t bytes) {
     return OVFQ_OK;
 }
 
+static_assert(ovfq::kNoAllocMaxElems == OVFQ_NOALLOC_MAX_ELEMS, "header and library disagree on the fixed scratch");
+
 bool valid_type(int t) { return t == OVFQ_TYPE_Q4_K || t == OVFQ_TYPE_Q6_K || t == OVFQ_TYPE_Q8_0; }
 
 size_t block_bytes_per_row(int type, int in) {
@@ -385,6 +387,8 @@ int ovfq_ctx_create(int device, ovfq_ctx** out) {
     HIP_TRY(hipGetDeviceCount(&n));
     if (device < 0 || device >= n) return fail(OVFQ_ERR_RANGE, "device %d out of range (%d devices)", device, n);
     HIP_TRY(hipSetDevice(device));
+    // The allocation-free entry point's fixed scratch: resolve this device's copy once, with it current.
+    HIP_TRY(ovfq::noalloc_scratch_init(device));
     ovfq_ctx* c = new ovfq_ctx();
     c->device = device;
     hipError_t e = hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking);
@@ -751,6 +755,57 @@ int ovfq_project_dev(ovfq_ctx* ctx, const ovfq_weight* w, const float* x, int ro
     const float* biases[1] = {bias};
     float* ys[1] = {y};
     return project_impl(ctx, 1, &w, x, rows, biases, ys, false);
+}
+
+int ovfq_project_noalloc_dev(ovfq_ctx* ctx, const ovfq_weight* w, const float* x, int rows, const float* bias,
+                             float* y) {
+    if (!ctx) return fail(OVFQ_ERR_NULL, "ctx is NULL");
+    int rc = check_weight(ctx, w);
+    if (rc) return rc;
+    if (!x || !y) return fail(OVFQ_ERR_NULL, "input or output is NULL");
+    if ((rc = check_rows(rows))) return rc;
+    if ((rc = check_dev_align(x, "input")) || (rc = check_dev_align(y, "output"))) return rc;
+    if ((rc = check_plane(rows, w->out, "output"))) return rc;
+    const int in = w->in;
+    if ((int64_t)rows * in > ovfq::kNoAllocMaxElems)
+        return fail(OVFQ_ERR_SIZE, "rows x inputSize (%lld) above the fixed scratch's %lld elements",
+                    (long long)rows * in, (long long)ovfq::kNoAllocMaxElems);
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    HIP_TRY(hipSetDevice(ctx->device));
+    const ovfq_weight* ws[1] = {w};
+    const float* bs[1] = {bias};
+    float* ys[1] = {y};
+    if (quantize_in_launch(ctx, w->type, in, rows, 1)) {
+        if ((rc = launch_projection(ctx, ws, 1, bs, ys, rows, ovfq::ActQ{nullptr, nullptr, nullptr}, x))) return rc;
+        return ok();
+    }
+    // The activation's quantised form goes to this device's fixed scratch (resolved when a context was created
+    // on it): quants, then scales, then (Q8_K) bsums, each 256-byte aligned. The quantiser writes every byte
+    // the projection reads, so nothing is cleared first.
+    const bool q80 = w->type == OVFQ_TYPE_Q8_0;
+    const size_t n = (size_t)rows * in;
+    auto carve = [&](Carver& cv, int8_t** q, float** s, int16_t** b) {
+        *q = cv.take<int8_t>(n);
+        *s = cv.take<float>(n / (q80 ? OVFQ_Q8_BLOCK : OVFQ_QK) * sizeof(float));
+        *b = q80 ? nullptr : cv.take<int16_t>(n / OVFQ_GROUP * sizeof(int16_t));
+    };
+    int8_t* q;
+    float* s;
+    int16_t* b;
+    Carver sizing{nullptr};
+    carve(sizing, &q, &s, &b);
+    if (sizing.used > ovfq::kNoAllocScratchBytes)  // cannot happen up to kNoAllocMaxElems; checked all the same
+        return fail(OVFQ_ERR_SIZE, "fixed scratch too small (%zu B needed)", sizing.used);
+    char* base = static_cast<char*>(ovfq::noalloc_scratch(ctx->device));
+    if (!base) return fail(OVFQ_ERR_HIP, "fixed scratch of device %d is not resolved", ctx->device);
+    Carver cv{base};
+    carve(cv, &q, &s, &b);
+    if (q80)
+        HIP_TRY(ovfq::launch_quantize_q8_0(x, (int64_t)(n / OVFQ_Q8_BLOCK), q, s, ctx->stream));
+    else
+        HIP_TRY(ovfq::launch_quantize_q8k(x, (int64_t)(n / OVFQ_QK), q, s, b, ctx->stream));
+    if ((rc = launch_projection(ctx, ws, 1, bs, ys, rows, ovfq::ActQ{q, s, b}))) return rc;
+    return ok();
 }
 
 int ovfq_project_gate_up(ovfq_ctx* ctx, const ovfq_weight* gate, const ovfq_weight* up, const float* x,

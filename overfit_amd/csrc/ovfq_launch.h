@@ -116,6 +116,16 @@ hipError_t launch_q8_0_gemv(const ProjJob* jobs, int njobs, int in, int rows, co
 bool q8_0_mfma_supported(int in, int rows);
 hipError_t launch_project_q8_0_mfma(const ProjJob* jobs, int njobs, int in, int rows, ActQ act, hipStream_t st);
 
+// Fixed device scratch of ovfq_project_noalloc_dev (noalloc.hip): one copy per GPU, kNoAllocScratchBytes long.
+// noalloc_scratch_init(device) resolves the current device's copy (call with `device` current, once per
+// device; later calls return at once); noalloc_scratch(device) returns its device address, NULL before init.
+// Activation rows x input size up to kNoAllocMaxElems fit (Q8_K: n + n/8 + n/64 bytes, Q8_0: n + n/8, each
+// piece 256-byte aligned).
+constexpr int64_t kNoAllocMaxElems = (int64_t)1 << 21;
+constexpr size_t kNoAllocScratchBytes = (size_t)5 << 19;  // 2.5 MiB
+hipError_t noalloc_scratch_init(int device);
+void* noalloc_scratch(int device);
+
 // GGUF Q8_0 (34-byte blocks) -> int8 quant plane + f32 scale plane.
 hipError_t launch_q8_0_deinterleave(const void* gguf, int64_t n_blocks, int8_t* q, float* s, hipStream_t st);
 hipError_t launch_encode_q4k(const float* w, int64_t n_blocks, uint8_t* dst, hipStream_t st);
