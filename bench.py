@@ -124,9 +124,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--copies", type=int, default=4, help="layer copies rotated to defeat the 256 MB cache")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--profile", choices=["layer", "prefill", "moe", "small", "q8"], default=None,
+    ap.add_argument("--profile", choices=["layer", "prefill", "moe", "small", "q8", "heads"], default=None,
                     help="for rocprof runs: only the timed decode-layer loop, the config-3 prefill line, the "
-                         "config-5 MoE line, the small-batch layer line, or the Q8_0 line")
+                         "config-5 MoE line, the small-batch layer line, the Q8_0 line or the per-head Q8_0 Wo line")
     ap.add_argument("--pmc", action="store_true",
                     help="for rocprofv3 --pmc runs: 16 gate/up launches, then 16 plain 64 MiB device copies "
                          "(the counter calibration reference)")
@@ -271,6 +271,43 @@ def main():
         torch.cuda.empty_cache()
         out["timing"] = "HIP graph replay over weight copies, per call"
         return out
+
+    def heads_line(n_heads=32, head_dim=128, d_model=4096, n_copies=16):
+        """The reference's default Llama decode o-path: Wo requantised per head to Q8_0 (32 heads x [4096][128]),
+        output = sum of the head projections in ascending head order, in one launch (ovfq_project_heads_q8_0_dev,
+        Q8_0 quantisation inside the launch), graph-replayed over copies past the cache; beside it the same work
+        as 32 single-head projection launches (the per-head calls without the fused reduction)."""
+        gen5 = torch.Generator(device="cuda:0").manual_seed(55)
+        sets = []
+        for _ in range(n_copies):
+            hs = []
+            for _ in range(n_heads):
+                wf = torch.randn(d_model, head_dim, generator=gen5, device=dev) * 0.02
+                q, s_ = ov.quantize_weight(wf, ov.TYPE_Q8_0)
+                del wf
+                hs.append(ov.Q8Weight(q, s_, head_dim, d_model))
+                del q, s_
+            sets.append(hs)
+        xh = torch.randn(n_heads * head_dim, generator=gen5, device=dev)
+        yh = torch.empty(d_model, device=dev)
+        g = capture([(lambda hs=hs: ov.project_heads_q8_0(hs, xh, out=yh)) for hs in sets])
+        us = replay_us(g, n_copies, 16)
+        del g
+        bands = torch.empty(n_heads * d_model, device=dev)
+        g = capture([(lambda hs=hs: [ctx.project_dev(hs[h], xh[h * head_dim:(h + 1) * head_dim],
+                                                     bands[h * d_model:(h + 1) * d_model])
+                                     for h in range(n_heads)]) for hs in sets[:4]])
+        us_sep = replay_us(g, 4, 8)
+        del g, sets
+        torch.cuda.empty_cache()
+        wb = n_heads * (d_model * head_dim + 4 * d_model * head_dim // 32)
+        nbytes = wb + 4 * n_heads * head_dim + 4 * d_model
+        return {"what": "Llama-3-8B decode o-projection with per-head Q8_0 Wo (32 x 4096x128), ascending head sum, "
+                        "one launch", "us": round(us, 3), "weight_bytes": wb,
+                "GB_s": round(nbytes / (us * 1e-6) / 1e9, 1),
+                "pct_peak": round(100 * nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 2),
+                "separate_launches_us": round(us_sep, 2),
+                "timing": "HIP graph replay over %d weight copies, per call (separate: 32 launches, 4 copies)" % n_copies}
 
     def rows_layer(m):
         """fp32 inputs / outputs for the layer's four projection launches at m rows, and the step over one copy:
@@ -427,8 +464,9 @@ def main():
                 "us": round(us, 2), "weight_bytes": wb, "GB_s": round(wb / (us * 1e-6) / 1e9, 1),
                 "timing": "HIP graph replay over %d layer copies x 4" % len(copies)}
 
-    if args.profile in ("prefill", "moe", "small", "q8"):
-        only = {"prefill": prefill_line, "moe": moe_line, "small": small_batch_line, "q8": q8_line}[args.profile]
+    if args.profile in ("prefill", "moe", "small", "q8", "heads"):
+        only = {"prefill": prefill_line, "moe": moe_line, "small": small_batch_line, "q8": q8_line,
+                "heads": heads_line}[args.profile]
         print(json.dumps(only()), flush=True)
         return
 
@@ -480,6 +518,7 @@ def main():
     config5 = moe_line()
     ffn = ffn_line()
     q8 = q8_line()
+    heads = heads_line()
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -517,6 +556,7 @@ def main():
         "q4k_gemv_128256x4096": large_q4k,
         "q6k_lm_head_128256x4096": lm_head,
         "q8_0_4096x4096": q8,
+        "q8_0_heads_o_proj": heads,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

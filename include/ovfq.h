@@ -219,6 +219,23 @@ OVFQ_API int ovfq_project_multi_prequantized_dev(ovfq_ctx* ctx, int count, const
                                                  const int8_t* quants, const float* scales, const int16_t* bsums,
                                                  int rows, const float* const* biases, float* const* ys);
 
+/* ---------------------------------------------------------------------------- per-head attention output */
+
+#define OVFQ_MAX_HEADS 128
+
+/* The attention output projection of the reference's default Llama decode path, where Wo is requantised per head to
+ * Q8_0 (LD/GgufLlamaLoader.cs:977-995, SplitOutput :1298-1336): wo[h] is head h's Q8_0 weight of input_size head_dim
+ * and output_size d_model (all heads one shape; head_dim <= 256, n_heads <= OVFQ_MAX_HEADS). For every row n of
+ * x [rows][n_heads * head_dim] (head h's attention output at columns h * head_dim ..):
+ *   y[n] = bias (or zero), then for h = 0, 1, ..., n_heads - 1:  y[n] += Q8DotKernel.Project(x[n][h], wo[h]) (no bias)
+ * — the per-head projections of RT/CachedSingleHeadAttention.cs:323-337 and the ascending head reduction of
+ * RT/CachedMultiHeadAttention.cs:185-194, :292-297 (prefill rows: :600-614, :703-711), bit-identical, in one launch
+ * for up to 8 rows (more rows take one launch per 8). Replaces the n_heads separate projections plus the host sum. */
+OVFQ_API int ovfq_project_heads_q8_0(ovfq_ctx* ctx, int n_heads, const ovfq_weight* const* wo, const float* x,
+                                     int rows, const float* bias, float* y);
+OVFQ_API int ovfq_project_heads_q8_0_dev(ovfq_ctx* ctx, int n_heads, const ovfq_weight* const* wo, const float* x,
+                                         int rows, const float* bias, float* y);
+
 /* ---------------------------------------------------------------------------------- SwiGLU FFN */
 
 /* CachedFeedForwardBlock.DecodeSwiGluDispatched / DecodeSwiGluBatchedDispatched (RT/CachedFeedForwardBlock.cs:

@@ -62,6 +62,8 @@ _SIGS = {
                                        c_f32p]),
     "orc_q8_project_batched_prequantized": (c_int, [c_int, c_i8p, c_f32p, c_int, c_int, c_f32p, c_f32p, c_i8p,
                                                     c_f32p]),
+    "orc_q8_project_heads": (c_int, [c_f32p, c_int, c_int, c_int, c_int, ctypes.c_void_p, ctypes.c_void_p, c_f32p,
+                                     c_f32p]),
     "orc_encode_q4k_block": (None, [c_f32p, c_u8p]),
     "orc_quantize_q4k": (c_int, [c_f32p, c_int, c_int, c_u8p]),
     "orc_encode_q6k_block": (None, [c_f32p, c_u8p]),
@@ -309,6 +311,22 @@ def q8_project_batched(x, rows, wq, ws, k, n, bias=None):
     s = np.zeros(rows * (k // 32), np.float32)
     y = np.zeros((rows, n), np.float32)
     _check(lib().orc_q8_project_batched(P(x), rows, P(wq), P(ws), k, n, P(bias), P(y), P(q), P(s)))
+    return y
+
+
+def q8_project_heads(x, rows, wqs, wss, head_dim, d_model, bias=None):
+    """Per-head Q8_0 attention output projection: y[rows][d_model] = (bias or 0) + sum over heads, ascending, of
+    Q8DotKernel.Project(x[n][h*head_dim : (h+1)*head_dim], Wo_h) (RT/CachedMultiHeadAttention.cs:185-194, :292-297).
+    wqs[h] int8 [d_model][head_dim], wss[h] f32 [d_model][head_dim/32]."""
+    H = len(wqs)
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(rows, H * head_dim)
+    wqs = [np.ascontiguousarray(w, dtype=np.int8) for w in wqs]
+    wss = [np.ascontiguousarray(w, dtype=np.float32) for w in wss]
+    QP = (ctypes.c_void_p * H)(*[w.ctypes.data for w in wqs])
+    SP = (ctypes.c_void_p * H)(*[w.ctypes.data for w in wss])
+    bias = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    y = np.zeros((rows, d_model), np.float32)
+    _check(lib().orc_q8_project_heads(P(x), rows, H, head_dim, d_model, QP, SP, P(bias), P(y)))
     return y
 
 

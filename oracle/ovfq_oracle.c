@@ -584,6 +584,49 @@ int orc_q8_project(const float* input, const int8_t* wq, const float* ws, int in
     return ORC_OK;
 }
 
+int orc_q8_project_heads(const float* x, int rows, int n_heads, int head_dim, int d_model,
+                         const int8_t* const* wq, const float* const* ws, const float* bias, float* y) {
+    if (!x || !wq || !ws || !y) return ORC_ERR_NULL;
+    if (rows <= 0 || n_heads <= 0 || head_dim <= 0 || d_model <= 0) return ORC_ERR_RANGE;
+    if (head_dim % ORC_Q8_BLOCK) return ORC_ERR_SIZE;
+    for (int h = 0; h < n_heads; h++)
+        if (!wq[h] || !ws[h]) return ORC_ERR_NULL;
+    const int nb = head_dim / ORC_Q8_BLOCK;
+    int8_t* q = (int8_t*)malloc((size_t)head_dim);
+    float* s = (float*)malloc((size_t)nb * sizeof(float));
+    float* band = (float*)malloc((size_t)d_model * sizeof(float));
+    if (!q || !s || !band) {
+        free(q);
+        free(s);
+        free(band);
+        return ORC_ERR_NULL;
+    }
+    for (int n = 0; n < rows; n++) {
+        float* out = y + (size_t)n * d_model;
+        /* output starts as the attention bias, or zero (CachedMultiHeadAttention.cs:185-194) */
+        for (int o = 0; o < d_model; o++) out[o] = bias == NULL ? 0.0f : bias[o];
+        for (int h = 0; h < n_heads; h++) {
+            /* the head's projection: Q8DotKernel.Project of its attention output, empty bias */
+            const float* xh = x + (size_t)n * n_heads * head_dim + (size_t)h * head_dim;
+            int rc = orc_quantize_q8_0(xh, head_dim, q, s);
+            if (rc) {
+                free(q);
+                free(s);
+                free(band);
+                return rc;
+            }
+            for (int o = 0; o < d_model; o++)
+                band[o] = orc_q8_dot(wq[h] + (size_t)o * head_dim, ws[h] + (size_t)o * nb, q, s, head_dim);
+            /* output += head output, heads ascending (AddInPlace, CachedMultiHeadAttention.cs:292-297, :946-955) */
+            for (int o = 0; o < d_model; o++) out[o] += band[o];
+        }
+    }
+    free(q);
+    free(s);
+    free(band);
+    return ORC_OK;
+}
+
 int orc_q8_project_batched_prequantized(int rows, const int8_t* wq, const float* ws, int in, int out,
                                         const float* bias, float* output, const int8_t* in_q,
                                         const float* in_s) {

@@ -117,6 +117,14 @@ int orc_q8_project_batched_prequantized(int rows, const int8_t* w_quants, const 
                                         int input_size, int output_size, const float* bias, float* output,
                                         const int8_t* in_q, const float* in_s);
 
+/* The Llama attention output projection with per-head Q8_0 Wo (LD/GgufLlamaLoader.cs:977-995 requantises Wo per
+ * head): y[n] = (bias or 0) then, heads ascending, y[n] += Q8DotKernel.Project(x[n][h*head_dim ..], Wo_h), where
+ * Wo_h is [d_model][head_dim] (wq[h], ws[h]). RT/CachedMultiHeadAttention.cs:185-194 and :292-297 (decode),
+ * :600-614 and :703-711 (prefill rows); each head's projection RT/CachedSingleHeadAttention.cs:323-337 /
+ * RT/Q8DotKernel.cs:155-215. x is [rows][n_heads * head_dim], y [rows][d_model]. */
+int orc_q8_project_heads(const float* x, int rows, int n_heads, int head_dim, int d_model,
+                         const int8_t* const* wq, const float* const* ws, const float* bias, float* y);
+
 /* a18: LD/GgmlQuant.cs:31-126 (EncodeQ4_KBlock) and :132-161 (QuantizeQ4_K) */
 void orc_encode_q4k_block(const float* src256, uint8_t* block144);
 int orc_quantize_q4k(const float* f32, int input_size, int output_size, uint8_t* dst);

@@ -8,7 +8,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libovfq.so")
-SOURCES = ["quant.hip", "project.hip", "gemv.hip", "mfma.hip", "moe.hip", "noalloc.hip", "api.cpp"]
+SOURCES = ["quant.hip", "project.hip", "gemv.hip", "mfma.hip", "moe.hip", "heads.hip", "noalloc.hip", "api.cpp"]
 
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 

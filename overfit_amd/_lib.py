@@ -63,6 +63,8 @@ SIGNATURES = {
     "ovfq_moe_ffn_dev": (ci, [vp, ci, PP, PP, PP, vp, ci, ci, vp, vp, vp]),
     "ovfq_project_gate_up_dev": (ci, [vp, vp, vp, vp, vp, vp]),
     "ovfq_project_multi_dev": (ci, [vp, ci, PP, vp, ci, PP, PP]),
+    "ovfq_project_heads_q8_0": (ci, [vp, ci, PP, vp, ci, vp, vp]),
+    "ovfq_project_heads_q8_0_dev": (ci, [vp, ci, PP, vp, ci, vp, vp]),
     "ovfq_project_multi_prequantized_dev": (ci, [vp, ci, PP, vp, vp, vp, ci, PP, PP]),
     "ovfq_quantize_weight_q4k_dev": (ci, [vp, vp, ci, ci, vp]),
     "ovfq_quantize_weight_q6k_dev": (ci, [vp, vp, ci, ci, vp]),

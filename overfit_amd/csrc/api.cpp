@@ -96,6 +96,7 @@ int ensure(ovfq_ctx* c, DevBuf& b, size_t bytes) {
 }
 
 static_assert(ovfq::kNoAllocMaxElems == OVFQ_NOALLOC_MAX_ELEMS, "header and library disagree on the fixed scratch");
+static_assert(ovfq::kHeadsMax == OVFQ_MAX_HEADS, "header and library disagree on the head count");
 
 bool valid_type(int t) { return t == OVFQ_TYPE_Q4_K || t == OVFQ_TYPE_Q6_K || t == OVFQ_TYPE_Q8_0; }
 
@@ -916,6 +917,83 @@ int ovfq_project_multi_prequantized_dev(ovfq_ctx* ctx, int count, const ovfq_wei
     HIP_TRY(hipSetDevice(ctx->device));
     if ((rc = launch_projection(ctx, ws, count, biases, ys, rows, ovfq::ActQ{q, s, b}))) return rc;
     return ok();
+}
+
+// ---------------------------------------------------------------------------------------- per-head Q8_0 Wo
+
+static int heads_impl(ovfq_ctx* ctx, int H, const ovfq_weight* const* wo, const float* x, int rows, const float* bias,
+                      float* y, bool host) {
+    if (!ctx) return fail(OVFQ_ERR_NULL, "ctx is NULL");
+    if (!wo) return fail(OVFQ_ERR_NULL, "head weight array is NULL");
+    if (!x || !y) return fail(OVFQ_ERR_NULL, "input or output is NULL");
+    if (H < 1 || H > ovfq::kHeadsMax) return fail(OVFQ_ERR_RANGE, "n_heads (%d) must be in [1, %d]", H, ovfq::kHeadsMax);
+    int rc;
+    for (int h = 0; h < H; h++) {
+        if ((rc = check_weight(ctx, wo[h]))) return rc;
+        if (wo[h]->type != OVFQ_TYPE_Q8_0) return fail(OVFQ_ERR_TYPE, "head %d: per-head Wo must be Q8_0", h);
+        if (wo[h]->in != wo[0]->in || wo[h]->out != wo[0]->out)
+            return fail(OVFQ_ERR_SIZE, "head %d: every head's Wo must be [d_model][head_dim] of one shape", h);
+    }
+    const int hd = wo[0]->in, dm = wo[0]->out, K = H * hd;
+    if (hd > ovfq::kHeadsMaxDim) return fail(OVFQ_ERR_SIZE, "head_dim (%d) above %d", hd, ovfq::kHeadsMaxDim);
+    if ((rc = check_rows(rows))) return rc;
+    if ((rc = check_plane(rows, K, "activation")) || (rc = check_plane(rows, dm, "output"))) return rc;
+    if (!host && ((rc = check_dev_align(x, "input")) || (rc = check_dev_align(y, "output")) ||
+                  (rc = check_dev_align(bias, "bias"))))
+        return rc;
+    // rows per launch: as many as the LDS copy of the activation and the head values allow (up to 8)
+    int R = 0;
+    for (int r = rows < ovfq::kHeadsMaxRows ? rows : ovfq::kHeadsMaxRows; r >= 1 && !R; r--)
+        if (ovfq::q8_0_heads_supported(H, hd, r)) R = r;
+    if (!R) return fail(OVFQ_ERR_SIZE, "n_heads x head_dim (%d) too large for one launch", K);
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    HIP_TRY(hipSetDevice(ctx->device));
+    const float* xd = x;
+    const float* bd = bias;
+    float* yd = y;
+    if (host) {
+        if ((rc = ensure(ctx, ctx->x_stage, (size_t)rows * K * 4)) || (rc = ensure(ctx, ctx->y_stage, (size_t)rows * dm * 4)))
+            return rc;
+        if (bias && (rc = ensure(ctx, ctx->bias_stage, (size_t)dm * 4))) return rc;
+        HIP_TRY(hipMemcpyAsync(ctx->x_stage.p, x, (size_t)rows * K * 4, hipMemcpyHostToDevice, ctx->stream));
+        if (bias) HIP_TRY(hipMemcpyAsync(ctx->bias_stage.p, bias, (size_t)dm * 4, hipMemcpyHostToDevice, ctx->stream));
+        xd = (const float*)ctx->x_stage.p;
+        bd = bias ? (const float*)ctx->bias_stage.p : nullptr;
+        yd = (float*)ctx->y_stage.p;
+    }
+    const int8_t* wq[ovfq::kHeadsMax];
+    const float* ws[ovfq::kHeadsMax];
+    for (int h = 0; h < H; h++) {
+        wq[h] = static_cast<const int8_t*>(wo[h]->blocks);
+        ws[h] = wo[h]->scales;
+    }
+    // One launch per R rows; the Q8_0 quantisation of the heads' inputs runs inside it when the rows are short, else
+    // once for all rows beforehand.
+    ovfq::ActQ act{nullptr, nullptr, nullptr};
+    const bool inside = ovfq::q8_0_heads_quantize_inside(H, hd, R);
+    if (!inside && (rc = quantize_into_scratch(ctx, OVFQ_TYPE_Q8_0, xd, rows, K, &act))) return rc;
+    for (int r0 = 0; r0 < rows; r0 += R) {
+        const int n = rows - r0 < R ? rows - r0 : R;
+        const ovfq::ActQ a = inside ? ovfq::ActQ{nullptr, nullptr, nullptr}
+                                    : ovfq::ActQ{act.q + (size_t)r0 * K, act.s + (size_t)r0 * (K / OVFQ_Q8_BLOCK), nullptr};
+        HIP_TRY(ovfq::launch_q8_0_heads(wq, ws, H, hd, dm, n, bd, inside ? xd + (size_t)r0 * K : nullptr, a,
+                                        yd + (size_t)r0 * dm, ctx->stream));
+    }
+    if (host) {
+        HIP_TRY(hipMemcpyAsync(y, yd, (size_t)rows * dm * 4, hipMemcpyDeviceToHost, ctx->stream));
+        HIP_TRY(hipStreamSynchronize(ctx->stream));
+    }
+    return ok();
+}
+
+int ovfq_project_heads_q8_0(ovfq_ctx* ctx, int n_heads, const ovfq_weight* const* wo, const float* x, int rows,
+                            const float* bias, float* y) {
+    return heads_impl(ctx, n_heads, wo, x, rows, bias, y, true);
+}
+
+int ovfq_project_heads_q8_0_dev(ovfq_ctx* ctx, int n_heads, const ovfq_weight* const* wo, const float* x, int rows,
+                                const float* bias, float* y) {
+    return heads_impl(ctx, n_heads, wo, x, rows, bias, y, false);
 }
 
 // ---------------------------------------------------------------------------------------- routed MoE

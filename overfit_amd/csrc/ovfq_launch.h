@@ -126,6 +126,23 @@ constexpr size_t kNoAllocScratchBytes = (size_t)5 << 19;  // 2.5 MiB
 hipError_t noalloc_scratch_init(int device);
 void* noalloc_scratch(int device);
 
+// Attention output projection with per-head Q8_0 Wo (heads.hip): y[rows][d_model] = (bias or 0) + the heads'
+// projections of their head_dim slices of x, added in ascending head order, in one launch. wq[h] / ws[h] are head h's
+// int8 [d_model][head_dim] and f32 [d_model][head_dim / 32] planes. From the fp32 x (quantised to Q8_0 inside the
+// launch; requires q8_0_heads_quantize_inside) or, x == NULL, a Q8_0 activation [rows][n_heads * head_dim].
+constexpr int kHeadsMax = 128;          // heads per launch
+constexpr int kHeadsMaxDim = 256;       // head_dim
+constexpr int kHeadsMaxRows = 8;        // activation rows per launch
+constexpr int kHeadsMaxIn = 32768;      // rows * n_heads * head_dim staged in LDS
+constexpr int kHeadsMaxRowHeads = 256;  // rows * n_heads head values kept in LDS
+constexpr int kHeadsQuantMaxIn = 8192;  // in-launch quantisation (every workgroup quantises the whole input)
+constexpr size_t kHeadsMaxLds = 65536;
+bool q8_0_heads_supported(int n_heads, int head_dim, int rows);
+bool q8_0_heads_quantize_inside(int n_heads, int head_dim, int rows);
+size_t q8_0_heads_lds_bytes(int n_heads, int head_dim, int rows);
+hipError_t launch_q8_0_heads(const int8_t* const* wq, const float* const* ws, int n_heads, int head_dim, int d_model,
+                             int rows, const float* bias, const float* x, ActQ act, float* y, hipStream_t st);
+
 // GGUF Q8_0 (34-byte blocks) -> int8 quant plane + f32 scale plane.
 hipError_t launch_q8_0_deinterleave(const void* gguf, int64_t n_blocks, int8_t* q, float* s, hipStream_t st);
 hipError_t launch_encode_q4k(const float* w, int64_t n_blocks, uint8_t* dst, hipStream_t st);

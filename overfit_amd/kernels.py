@@ -423,6 +423,37 @@ def moe_ffn(gate_experts, up_experts, down_experts, x, rows, top_k, expert_indic
     return out
 
 
+def project_heads_q8_0(head_weights, x, rows=1, bias=None, out=None):
+    """The attention output projection with per-head Q8_0 Wo (ovfq_project_heads_q8_0[_dev]): for each of `rows`
+    rows of x [rows][n_heads * head_dim], out = bias (or zero) plus, heads ascending, each head's
+    Q8DotKernel.Project of its head_dim slice through head_weights[h] ([d_model][head_dim] Q8Weight) —
+    RT/CachedMultiHeadAttention.cs:185-194, :292-297 and RT/CachedSingleHeadAttention.cs:323-337, in one launch."""
+    H = len(head_weights)
+    if H == 0:
+        raise OverfitArgumentError("head_weights is empty")
+    inp = as_buf(x, np.float32, "x")
+    d_model = head_weights[0].OutputSize
+    if inp.size < rows * H * head_weights[0].InputSize:
+        raise OverfitArgumentError("x is smaller than rows * n_heads * head_dim")
+    if out is None:
+        if inp.device:
+            import torch
+
+            out = torch.empty(rows * d_model, dtype=torch.float32, device=inp.obj.device)
+        else:
+            out = np.zeros(rows * d_model, np.float32)
+    o = as_buf(out, np.float32, "out")
+    if o.size < rows * d_model:
+        raise OverfitArgumentError("out is smaller than rows * d_model")
+    bb = as_buf(bias, np.float32, "bias", allow_none=True)
+    same_side(inp, o, bb)
+    ctx = head_weights[0].context
+    W = (ctypes.c_void_p * H)(*[w.handle.value for w in head_weights])
+    fn = ctx.lib.ovfq_project_heads_q8_0_dev if inp.device else ctx.lib.ovfq_project_heads_q8_0
+    raise_for_status(fn(ctx.handle, H, W, inp.ptr, rows, None if is_empty(bb) else bb.ptr, o.ptr), ctx.lib)
+    return out
+
+
 def project(weight, x, bias=None, rows=1, out=None):
     """Convenience: y = (bias +) x @ W^T with the library's own activation scratch."""
     inp = as_buf(x, np.float32, "x")

@@ -364,6 +364,48 @@ def test_q8_project_matches_f32(orc):
         assert l2 < 0.03
 
 
+def _heads(orc, rng, H, hd, dm):
+    planes = [orc.q8_quantize_rows(normal(rng, (dm, hd), 0.05)) for _ in range(H)]
+    return [p[0] for p in planes], [p[1] for p in planes]
+
+
+@pytest.mark.parametrize("H,hd,dm,rows", [(1, 128, 96, 1), (32, 128, 256, 2), (8, 96, 64, 3), (4, 256, 40, 1)])
+def test_q8_project_heads_is_the_ascending_sum_of_head_projections(orc, H, hd, dm, rows):
+    """The per-head o-path (RT/CachedMultiHeadAttention.cs:185-194, :292-297, :600-614, :703-711): output starts as
+    the bias (or zero) and each head's Q8DotKernel.Project (already pinned) is added in ascending head order, one
+    float32 add per output and head. Restated here from the pinned single-head projection and numpy float32 adds;
+    the plausible mistakes (descending order, or one fused Q8 dot over all heads as a single [d_model][H*hd]
+    matrix) are shown to differ, so the check can tell them apart."""
+    rng = np.random.default_rng(H * 1000 + hd + rows)
+    wqs, wss = _heads(orc, rng, H, hd, dm)
+    x = normal(rng, (rows, H * hd))
+    bias = normal(rng, dm)
+    for b in (None, bias):
+        y = orc.q8_project_heads(x, rows, wqs, wss, hd, dm, b)
+        for n in range(rows):
+            ref = np.zeros(dm, np.float32) if b is None else b.copy()
+            for h in range(H):
+                ref = (ref + orc.q8_project(x[n, h * hd:(h + 1) * hd], wqs[h], wss[h], hd, dm)).astype(np.float32)
+            assert np.array_equal(y[n].view(np.uint32), ref.view(np.uint32)), (b is None, n)
+    if H == 1:  # one head and no bias is exactly the single projection
+        y = orc.q8_project_heads(x, rows, wqs, wss, hd, dm)
+        assert np.array_equal(y[0].view(np.uint32), orc.q8_project(x[0], wqs[0], wss[0], hd, dm).view(np.uint32))
+        return
+    y = orc.q8_project_heads(x, rows, wqs, wss, hd, dm, bias)
+    rev = bias.copy()
+    for h in reversed(range(H)):
+        rev = (rev + orc.q8_project(x[0, h * hd:(h + 1) * hd], wqs[h], wss[h], hd, dm)).astype(np.float32)
+    assert not np.array_equal(y[0].view(np.uint32), rev.view(np.uint32)), "order not distinguished"
+    whole_q = np.concatenate(wqs, axis=1)  # [dm][H*hd]: the heads as one Q8 matrix
+    whole_s = np.concatenate(wss, axis=1)
+    fused = orc.q8_project(x[0], whole_q, whole_s, H * hd, dm, bias)
+    assert not np.array_equal(y[0].view(np.uint32), fused.view(np.uint32)), "fused dot not distinguished"
+    # and the value itself: within Q8 noise of the float64 product with the dequantised weights
+    w64 = np.concatenate([q.astype(np.float64) * np.repeat(s, 32, axis=1) for q, s in zip(wqs, wss)], axis=1)
+    ref64 = w64 @ x[0].astype(np.float64) + bias
+    assert np.max(np.abs(y[0] - ref64)) <= 0.03 * np.max(np.abs(ref64))
+
+
 @pytest.mark.parametrize("rows", [1, 3, 16, 70])
 def test_batched_is_bit_identical_to_per_row_project(orc, rows):
     # TL/Runtime/Q4KDotKernelTests.cs:98-136, Parity/Q4KWeightStationaryParityTests.cs:19-71,
