@@ -60,10 +60,52 @@ def make_layer(ov, torch, seed):
     return ws
 
 
+def cpu_meta(L, workers):
+    """What the CPU baseline ran on and with: model, logical CPUs, the CPUs this process may use, worker threads,
+    compiler and flags of the AVX2 restatement."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except AttributeError:
+        allowed = os.cpu_count() or 1
+    info = L.cpub_build_info().decode()
+    compiler, _, flags = info.partition("; ")
+    return {"cpu_model": model, "nproc": os.cpu_count(), "cpus_allowed": allowed, "workers": workers,
+            "compiler": compiler, "flags": flags}
+
+
+def batched_workers():
+    """OverfitParallel.For uses every core (WorkerCount = ProcessorCount); here the CPUs this process may use,
+    capped at the 16 host CPUs one GPU's share of the box has."""
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except AttributeError:
+        allowed = os.cpu_count() or 1
+    return max(1, min(allowed, 16))
+
+
+def best_of(fn, budget_s, min_reps=3):
+    fn()
+    best, n = float("inf"), 0
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or n < min_reps:
+        t0 = time.perf_counter()
+        fn()
+        best = min(best, time.perf_counter() - t0)
+        n += 1
+    return best, n
+
+
 def run_cpu_baseline(layer0_host, budget_s=2.5):
     """Times the AVX2 C restatement of the reference's decode path on one layer step (7 projections)."""
-    import ctypes
-
     import numpy as np
 
     import oracle
@@ -71,8 +113,10 @@ def run_cpu_baseline(layer0_host, budget_s=2.5):
     L = oracle.lib()
     if not L.cpub_has_avx2():
         return None
-    workers = max(1, min(os.cpu_count() or 1, 10))  # OverfitParallel decode cap min(cores, 10)
-    L.cpub_set_workers(workers)
+    allowed = batched_workers()
+    workers = max(1, min(allowed, 10))  # OverfitParallel decode cap min(cores, 10)
+    L.cpub_set_workers(allowed)
+    L.cpub_set_decode_cap(workers)
     rng = np.random.default_rng(1)
     xs = {k: rng.standard_normal(k).astype(np.float32) for k in (4096, 14336)}
     q = np.zeros(14336, np.int8)
@@ -93,18 +137,9 @@ def run_cpu_baseline(layer0_host, budget_s=2.5):
         L.cpub_q6k_project_parallel(P(xs[14336]), P(layer0_host["down"]), 14336, 4096, None, P(out["down"]),
                                     P(q), P(s), P(b))
 
-    step()
-    step()
-    best = float("inf")
-    n = 0
-    t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or n < 3:
-        t0 = time.perf_counter()
-        step()
-        best = min(best, time.perf_counter() - t0)
-        n += 1
+    best, n = best_of(step, budget_s)
     _, alg = layer_algorithmic_bytes()
-    return {
+    line = {
         "value": round(alg / best / 1e9, 2),
         "unit": "GB/s",
         "tok_s": round(1.0 / best, 2),
@@ -112,8 +147,83 @@ def run_cpu_baseline(layer0_host, budget_s=2.5):
         "cores": workers,
         "kind": "port",
         "sample": f"best of {n} steps of the config-2 layer (7 projections, same Q4_K/Q6_K bytes as the GPU run), "
-                  f"AVX2 C restatement of Overfit's CPU path, {workers} row-band workers, ~{budget_s:.1f}s wall",
+                  f"AVX2 C restatement of Overfit's CPU path, {workers} row-band workers (ForDecode), "
+                  f"~{budget_s:.1f}s wall",
     }
+    line.update(cpu_meta(L, workers))
+    return line
+
+
+def run_cpu_configs(layer0_host, moe_host, budget_s=2.0):
+    """CPU baselines of the other benchmark configurations, on the same bytes as the GPU run: config 1 (a Q4_K
+    4096x4096 GEMV, ForDecode over min(cores, 10) bands), config 3 (the layer's seven projections at M = 512 through
+    BatchedQuantProjection.Dispatch: Q4_K weight-stationary 64-row tiles, Q6_K ProjectBatched, OverfitParallel.For over
+    every worker) and config 5 (MoeFeedForwardBlock.DecodeBatched over the routed tokens: per expert, the batched
+    SwiGLU through the same Dispatch). Bit-identical to the oracle (tests/test_oracle_pins.py)."""
+    import ctypes
+
+    import numpy as np
+
+    import oracle
+
+    L = oracle.lib()
+    if not L.cpub_has_avx2():
+        return None
+    P = oracle.P
+    allw = batched_workers()
+    dec = max(1, min(allw, 10))
+    L.cpub_set_workers(allw)
+    L.cpub_set_decode_cap(dec)
+    rng = np.random.default_rng(3)
+    out = {}
+
+    # config 1: Q4_K 4096x4096 GEMV (the layer's q weight has exactly this shape)
+    x1 = rng.standard_normal(4096).astype(np.float32)
+    y1 = np.zeros(4096, np.float32)
+    q = np.zeros(512 * 14336, np.int8)
+    s = np.zeros(512 * 14336 // 256, np.float32)
+    b = np.zeros(512 * 14336 // 16, np.int16)
+    best, n = best_of(lambda: L.cpub_q4k_project_parallel(P(x1), P(layer0_host["q"]), 4096, 4096, None, P(y1),
+                                                          P(q), P(s), P(b)), budget_s / 2)
+    nbytes = weight_bytes(4096, 4096, "q4k") + 4 * 4096 + 4 * 4096
+    out["config1_q4k_gemv_4096x4096"] = dict(
+        value=round(nbytes / best / 1e9, 2), unit="GB/s", us=round(best * 1e6, 1), cores=dec, kind="port",
+        sample=f"best of {n} Q4KDotKernel.ProjectParallel calls (quantise + {dec} row bands)", **cpu_meta(L, dec))
+
+    # config 3: the layer at M = 512, seven Dispatch calls (each quantises its input rows, as the reference does)
+    m = 512
+    xin = {kk: rng.standard_normal(m * kk).astype(np.float32) for kk in (4096, 14336)}
+    ys = {name: np.zeros(m * nn, np.float32) for name, nn, _, _ in LAYER}
+
+    def prefill():
+        for name, nn, kk, fmt in LAYER:
+            fn = L.cpub_q6k_project_batched if fmt == "q6k" else L.cpub_q4k_project_batched_ws
+            fn(P(xin[kk]), m, P(layer0_host[name]), kk, nn, None, P(ys[name]), P(q), P(s), P(b))
+
+    best, n = best_of(prefill, budget_s, min_reps=2)
+    ops = 2 * m * sum(nn * kk for _, nn, kk, _ in LAYER)
+    out["config3_prefill_m512"] = dict(
+        value=round(m / best, 1), unit="tokens/s", us_per_layer=round(best * 1e6, 1),
+        useful_TOPS=round(ops / best / 1e12, 3), cores=allw, kind="port",
+        sample=f"best of {n} layer steps at M={m} (7 BatchedQuantProjection.Dispatch calls: Q4_K weight-stationary, "
+               f"Q6_K batched; OverfitParallel.For over {allw} workers)", **cpu_meta(L, allw))
+
+    # config 5: the routed MoE step on the GPU run's expert bytes, routing and tokens
+    if moe_host is not None:
+        E = len(moe_host["gate"])
+        arr = lambda ms: (ctypes.c_void_p * E)(*[mm.ctypes.data for mm in ms])  # noqa: E731
+        G, U, D = arr(moe_host["gate"]), arr(moe_host["up"]), arr(moe_host["down"])
+        xm, idx, wts = moe_host["x"], moe_host["idx"], moe_host["w"]
+        tokens, top_k = moe_host["tokens"], moe_host["top_k"]
+        ym = np.zeros(tokens * 4096, np.float32)
+        best, n = best_of(lambda: L.cpub_moe_ffn_batched(E, G, U, D, 12, 12, P(xm), tokens, 4096, 14336, top_k,
+                                                         P(idx), P(wts), P(ym)), budget_s, min_reps=2)
+        wb = moe_host["weight_bytes"]
+        out["config5_moe_mixtral_16tok_top2"] = dict(
+            value=round(wb / best / 1e9, 2), unit="GB/s", us=round(best * 1e6, 1), cores=allw, kind="port",
+            sample=f"best of {n} MoE steps (16 tokens top-2 over {E} Q4_K experts, the GPU run's routing; per expert "
+                   f"the batched SwiGLU via Dispatch, OverfitParallel.For over {allw} workers)", **cpu_meta(L, allw))
+    return out
 
 
 def main():
@@ -414,20 +524,25 @@ def main():
                 "proj_tok_s_eager": round(1e6 / eager_us, 1), "proj_tok_s_graph": round(1e6 / graph_us, 1),
                 "GB_s_graph": round(w / (graph_us * 1e-6) / 1e9, 1)}
 
-    def moe_line(n_sets=2, tokens=16, top_k=2, n_experts=8):
+    def moe_line(n_sets=2, tokens=16, top_k=2, n_experts=8, keep_host=False):
         """benchmark config 5: Mixtral-8x7B-shaped experts (gate/up 14336x4096, down 4096x14336, Q4_K), 16 tokens
         routed top-2 on the device from seeded U[0,1) logits, grouped per-expert SwiGLU; graph-replayed over
-        n_sets independent expert sets (> 1.5 GB, past the 256 MB cache)."""
+        n_sets independent expert sets (> 1.5 GB, past the 256 MB cache). keep_host: also returns host copies of
+        the first set's blocks, the tokens and the routing, for the CPU baseline."""
         gen4 = torch.Generator(device="cuda:0").manual_seed(15)
         sets = []
-        for _ in range(n_sets):
+        host = {"gate": [], "up": [], "down": []} if keep_host else None
+        for si in range(n_sets):
             mats = {"gate": [], "up": [], "down": []}
             for name in ("gate", "up", "down"):
                 n, kk = (4096, 14336) if name == "down" else (14336, 4096)
                 for _ in range(n_experts):
                     wf = torch.randn(n, kk, generator=gen4, device=dev) * 0.02
-                    mats[name].append(ov.Q4KWeight(ov.quantize_weight(wf, ov.TYPE_Q4_K), kk, n))
-                    del wf
+                    blocks = ov.quantize_weight(wf, ov.TYPE_Q4_K)
+                    mats[name].append(ov.Q4KWeight(blocks, kk, n))
+                    if host is not None and si == 0:
+                        host[name].append(blocks.cpu().numpy().reshape(n, -1))
+                    del wf, blocks
             sets.append(mats)
         xm = torch.randn(tokens * 4096, generator=gen4, device=dev)
         logits = torch.rand(tokens * n_experts, generator=gen4, device=dev)
@@ -443,13 +558,17 @@ def main():
         us = replay_us(g, 4 * n_sets, 10)
         used = len(set(idx.cpu().numpy().tolist()))
         wb = used * (2 * weight_bytes(14336, 4096, "q4k") + weight_bytes(4096, 14336, "q4k"))
+        if host is not None:
+            host.update(x=xm.cpu().numpy(), idx=idx.cpu().numpy(), w=wts.cpu().numpy(), tokens=tokens,
+                        top_k=top_k, weight_bytes=wb)
         del g, sets
         torch.cuda.empty_cache()
-        return {"what": "benchmark config 5: Mixtral-8x7B experts (Q4_K gate/up/down), 16 tokens, top-2, one MoE "
+        line = {"what": "benchmark config 5: Mixtral-8x7B experts (Q4_K gate/up/down), 16 tokens, top-2, one MoE "
                         "step (route + group/quantise + 2 grouped projections + SwiGLU + combine, 6 launches)",
                 "us": round(us, 1), "experts_used": used, "weight_bytes": wb,
                 "GB_s": round(wb / (us * 1e-6) / 1e9, 1), "pct_peak": round(100 * wb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 2),
                 "timing": "HIP graph replay of 8 steps over %d expert sets, per step" % n_sets}
+        return (line, host) if keep_host else line
 
     def ffn_line():
         """The fused decode FFN: gate/up -> SiLU*up + Q8_K -> down for one token, 3 launches, over the
@@ -505,6 +624,9 @@ def main():
         traffic = json.load(open(tfile)).get("bytes_per_launch")
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                "traffic_source": "not measured in this run: the committed profiles/traffic_q4k_gate_up_gemv.json "
+                                  "(two rocprofv3 --pmc passes, FETCH_SIZE and WRITE_SIZE, calibrated by a 64 MiB "
+                                  "device copy)" if traffic is not None else None,
                 "kernel": "kquant_gemv_kernel<Q4K,2,true> (Q8_K quantise + fused gate+up GEMV, 2x14336x4096)",
                 "avg_us": round(gu_avg, 3), "algorithmic_bytes": gu_bytes,
                 "timing": "HIP graph replay of 4x%d launches over %d weight copies, /launch" % (len(copies), len(copies))}
@@ -515,15 +637,17 @@ def main():
     small = small_batch_line()  # before config 3, which gives the weights their MFMA-ready copies
     config3 = prefill_line()
     config4 = model_line()
-    config5 = moe_line()
+    config5, moe_host = moe_line(keep_host=not args.no_cpu_baseline)
     ffn = ffn_line()
     q8 = q8_line()
     heads = heads_line()
 
-    cpu = None
+    cpu = cpu_configs = None
     if not args.no_cpu_baseline:
         host = {name: copies[0][name + "_blocks"].cpu().numpy() for name, _, _, _ in LAYER}
         cpu = run_cpu_baseline(host)
+        cpu_configs = run_cpu_configs(host, moe_host)
+        del moe_host
 
     line = {
         "metric": METRIC,
@@ -558,6 +682,7 @@ def main():
         "q8_0_4096x4096": q8,
         "q8_0_heads_o_proj": heads,
         "cpu_baseline": cpu,
+        "cpu_baseline_configs": cpu_configs,
     }
     print(json.dumps(line), flush=True)
 

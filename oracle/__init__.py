@@ -85,6 +85,14 @@ _SIGS = {
                                          c_i16p]),
     "cpub_q6k_project_parallel": (c_int, [c_f32p, c_u8p, c_int, c_int, c_f32p, c_f32p, c_i8p, c_f32p, c_i16p]),
     "cpub_q8_project_parallel": (c_int, [c_f32p, c_i8p, c_f32p, c_int, c_int, c_f32p, c_f32p, c_i8p, c_f32p]),
+    "cpub_set_decode_cap": (c_int, [c_int]),
+    "cpub_q4k_project_batched_ws": (c_int, [c_f32p, c_int, c_u8p, c_int, c_int, c_f32p, c_f32p, c_i8p, c_f32p,
+                                            c_i16p]),
+    "cpub_q6k_project_batched": (c_int, [c_f32p, c_int, c_u8p, c_int, c_int, c_f32p, c_f32p, c_i8p, c_f32p,
+                                         c_i16p]),
+    "cpub_moe_ffn_batched": (c_int, [c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, c_int, c_int, c_f32p,
+                                     c_int, c_int, c_int, c_int, c_i32p, c_f32p, c_f32p]),
+    "cpub_build_info": (ctypes.c_char_p, []),
 }
 
 _NP_CTYPE = {

@@ -20,9 +20,10 @@ COMMON = ["-O2", "-fPIC", "-std=c11", "-ffp-contract=off", "-fno-fast-math", "-W
 
 def build(verbose: bool = False) -> str:
     objs = []
+    cpub_flags = [*COMMON, "-mavx2", "-mfma"]
     steps = [
         ("ovfq_oracle.c", []),
-        ("cpu_baseline.c", ["-mavx2", "-mfma"]),
+        ("cpu_baseline.c", ["-mavx2", "-mfma", '-DCPUB_FLAGS="%s"' % " ".join(cpub_flags)]),
     ]
     for src, extra in steps:
         obj = os.path.join(HERE, src.replace(".c", ".o"))

@@ -1,18 +1,27 @@
 /*
- * cpu_baseline.c — the reported CPU baseline: a C restatement of Overfit's AVX2 decode path, threaded like
- * the reference's OverfitParallel.ForDecode (contiguous row bands, caller participates). Test and bench
+ * cpu_baseline.c — the reported CPU baseline: a C restatement of Overfit's AVX2 decode and batched paths,
+ * threaded like the reference's OverfitParallel (contiguous row bands, caller participates). Test and bench
  * infrastructure only (bench.py's cpu_baseline leg); never part of the product library.
  *
  *   MainDot AVX2             RT/Q4KDotKernel.cs:270-302
  *   Q6_K UnsignedDotSuperBlock AVX2  RT/Q6KDotKernel.cs:129-184
  *   Q8 Int8BlockDot AVX2     RT/Q8DotKernel.cs:469-478
  *   QuantizeActivationQ8KAvx2 RT/Q4KDotKernel.cs:148-209
- *   ForDecode row bands      Sources/Main/Runtime/OverfitParallel.cs:494-580 (perChunk = ceil(n/chunks))
+ *   ForDecode row bands      Sources/Main/Runtime/OverfitParallel.cs:494-580 (perChunk = ceil(n/chunks), decode
+ *                            cap min(cores, 10))
+ *   For (batched)            Sources/Main/Runtime/OverfitParallel.cs:399-480 (chunkCount = min(workers, n),
+ *                            perChunk = ceil(n/chunkCount), the caller runs the last chunk)
+ *   ProjectBatchedWeightStationary  RT/Q4KDotKernel.cs:809-955 (each super-block decoded once per 64-row tile)
+ *   Q6KDotKernel.ProjectBatched     RT/Q6KDotKernel.cs:403-510 (rows innermost)
+ *   BatchedQuantProjection.Dispatch RT/BatchedQuantProjection.cs:26-87 (Q4_K -> weight-stationary)
+ *   DecodeSwiGluBatchedDispatched   RT/CachedFeedForwardBlock.cs:328-348
+ *   MoeFeedForwardBlock.DecodeBatched (after routing) RT/MoeFeedForwardBlock.cs:187-241
  *
  * Every kernel here is integer-identical to the scalar oracle (ovfq_oracle.c) and keeps the same float
  * tail and per-row summation order, so outputs are bit-identical to the oracle; tests check that.
  */
 #include <immintrin.h>
+#include <math.h>
 #include <pthread.h>
 #include <sched.h>
 #include <stdatomic.h>
@@ -38,12 +47,18 @@ static struct {
     void* ctx;
     int n;
     int per_chunk;
+    int chunks;
+    int caller_last;
     int started;
 } g_pool;
+
+/* OverfitParallel.DecodeMaxWorkers: single-token projections use at most min(cores, 10) chunks (PAR:184-195). */
+static int g_decode_cap = 10;
 
 static pthread_mutex_t g_pool_lock = PTHREAD_MUTEX_INITIALIZER;
 
 static void run_chunk(int idx) {
+    if (idx < 0 || idx >= g_pool.chunks) return;
     int start = idx * g_pool.per_chunk;
     int end = start + g_pool.per_chunk;
     if (end > g_pool.n) end = g_pool.n;
@@ -66,7 +81,9 @@ static void* worker_main(void* arg) {
             }
         }
         seen = gen;
-        run_chunk(idx);
+        /* with the caller on the last chunk, pool thread i takes chunk i - 1 of the first chunks - 1 */
+        if (g_pool.caller_last) run_chunk(idx - 1 < g_pool.chunks - 1 ? idx - 1 : -1);
+        else run_chunk(idx);
         atomic_fetch_sub_explicit(&g_pool.remaining, 1, memory_order_acq_rel);
     }
 }
@@ -94,22 +111,41 @@ int cpub_set_workers(int workers) {
     return workers;
 }
 
-/* OverfitParallel.ForDecode: split [0,n) into `workers` contiguous bands; the caller runs band 0. */
-static void parallel_for(int n, cpub_chunk_fn fn, void* ctx) {
+/* Split [0, n) into min(cap, workers, n) contiguous chunks of ceil(n / chunks); the calling thread runs the first
+ * chunk (ForDecode) or, with caller_last, the last one (For, PAR:472) and waits for the others. One chunk, or
+ * n < 2, runs inline. */
+static void parallel_for_capped(int n, cpub_chunk_fn fn, void* ctx, int cap, int caller_last) {
     if (!g_pool.started) cpub_set_workers(1);
     int w = g_pool.workers;
-    if (w == 1 || n < 2) {
+    int chunks = cap < w ? cap : w;
+    if (chunks > n) chunks = n;
+    if (chunks <= 1 || n < 2) {
         fn(0, n, ctx);
         return;
     }
     g_pool.fn = fn;
     g_pool.ctx = ctx;
     g_pool.n = n;
-    g_pool.per_chunk = (n + w - 1) / w;
+    g_pool.chunks = chunks;
+    g_pool.per_chunk = (n + chunks - 1) / chunks;
+    g_pool.caller_last = caller_last;
+    /* pool threads 1 .. w-1 take chunks 1 .. w-1 (caller_last: chunks 0 .. w-2); the caller the remaining one */
     atomic_store_explicit(&g_pool.remaining, w - 1, memory_order_release);
     atomic_fetch_add_explicit(&g_pool.generation, 1, memory_order_acq_rel);
-    run_chunk(0);
+    run_chunk(caller_last ? chunks - 1 : 0);
     while (atomic_load_explicit(&g_pool.remaining, memory_order_acquire) != 0) _mm_pause();
+}
+
+/* OverfitParallel.ForDecode (single-token projections). */
+static void parallel_for(int n, cpub_chunk_fn fn, void* ctx) { parallel_for_capped(n, fn, ctx, g_decode_cap, 0); }
+
+/* OverfitParallel.For over every worker (batched projections). */
+static void parallel_for_all(int n, cpub_chunk_fn fn, void* ctx) { parallel_for_capped(n, fn, ctx, 1 << 30, 1); }
+
+/* Chunk cap of the single-token (ForDecode) projections; the reference's is min(cores, 10). */
+int cpub_set_decode_cap(int cap) {
+    g_decode_cap = cap < 1 ? 1 : cap;
+    return g_decode_cap;
 }
 
 /* ---------------------------------------------------------------- AVX2 kernels */
@@ -369,6 +405,200 @@ int cpub_q8_project_parallel(const float* input, const int8_t* wq, const float* 
     q8_ctx c = {wq, ws, in_q, in_s, bias, output, in};
     parallel_for(out, q8_chunk, &c);
     return ORC_OK;
+}
+
+/* ---------------------------------------------------------------- batched projections (prefill, experts) */
+
+#define CPUB_WS_TILE 64 /* Q4KDotKernel.WeightStationaryTile (RT/Q4KDotKernel.cs:809) */
+
+typedef struct {
+    const uint8_t* blocks;
+    const int8_t* q;
+    const float* s;
+    const int16_t* b;
+    const float* bias;
+    float* out;
+    int spr;
+    int in;
+    int out_dim;
+    int rows;
+} batched_ctx;
+
+/* WeightStationaryChunk (RT/Q4KDotKernel.cs:894-955): per output, per 64-row tile, each super-block's d, dmin and
+ * scales/mins decoded once and contracted against every row of the tile; acc[t] += q8s * (d*main - dmin*min) in
+ * ascending super-block order, then output = biasO + acc[t]. */
+static void q4k_ws_chunk(int start, int end, void* vctx) {
+    batched_ctx* c = (batched_ctx*)vctx;
+    float acc[CPUB_WS_TILE];
+    for (int o = start; o < end; o++) {
+        const uint8_t* row = c->blocks + (size_t)o * c->spr * ORC_Q4K_BYTES;
+        const float bias_o = c->bias == NULL ? 0.0f : c->bias[o];
+        for (int t0 = 0; t0 < c->rows; t0 += CPUB_WS_TILE) {
+            const int tile = c->rows - t0 < CPUB_WS_TILE ? c->rows - t0 : CPUB_WS_TILE;
+            for (int t = 0; t < tile; t++) acc[t] = 0.0f;
+            for (int sb = 0; sb < c->spr; sb++) {
+                const uint8_t* blk = row + (size_t)sb * ORC_Q4K_BYTES;
+                const float d = orc_half_to_float(rd16(blk));
+                const float dmin = orc_half_to_float(rd16(blk + 2));
+                uint8_t sc[8], m[8];
+                orc_unpack_q4k_scales_mins(blk + 4, sc, m);
+                for (int t = 0; t < tile; t++) {
+                    const size_t n = (size_t)(t0 + t);
+                    const int32_t main_acc = q4k_main_dot_avx2(blk + 16, c->q + n * c->in + sb * 256, sc);
+                    const int16_t* bs = c->b + n * c->spr * 16 + sb * 16;
+                    int32_t min_acc = 0;
+                    for (int j = 0; j < 8; j++) min_acc += m[j] * (bs[2 * j] + bs[2 * j + 1]);
+                    acc[t] += c->s[n * c->spr + sb] * (d * (float)main_acc - dmin * (float)min_acc);
+                }
+            }
+            for (int t = 0; t < tile; t++) c->out[(size_t)(t0 + t) * c->out_dim + o] = bias_o + acc[t];
+        }
+    }
+}
+
+/* Q6KDotKernel.ProjectBatchedChunk (RT/Q6KDotKernel.cs:477-510): per output, rows innermost, each row's
+ * sum += Dot(...) in ascending super-block order; output = biasO + sum. */
+static void q6k_batched_chunk(int start, int end, void* vctx) {
+    batched_ctx* c = (batched_ctx*)vctx;
+    for (int o = start; o < end; o++) {
+        const uint8_t* row = c->blocks + (size_t)o * c->spr * ORC_Q6K_BYTES;
+        const float bias_o = c->bias == NULL ? 0.0f : c->bias[o];
+        for (int n = 0; n < c->rows; n++) {
+            const size_t nn = (size_t)n;
+            float sum = 0.0f;
+            for (int sb = 0; sb < c->spr; sb++)
+                sum += q6k_dot_avx2(row + (size_t)sb * ORC_Q6K_BYTES, c->q + nn * c->in + sb * 256,
+                                    c->s[nn * c->spr + sb], c->b + nn * c->spr * 16 + sb * 16);
+            c->out[nn * c->out_dim + o] = bias_o + sum;
+        }
+    }
+}
+
+/* Per-row QuantizeActivationQ8K on the calling thread (RT/Q4KDotKernel.cs:718-725, :856-863), then For over the
+ * outputs. */
+static int batched_project(int type, const float* x, int rows, const uint8_t* blocks, int in, int out,
+                           const float* bias, float* y, int8_t* q, float* s, int16_t* b) {
+    if (rows <= 0 || in <= 0 || out <= 0) return ORC_ERR_RANGE;
+    if (in % 256) return ORC_ERR_SIZE;
+    const int spr = in / 256;
+    for (int n = 0; n < rows; n++) {
+        int rc = cpub_quantize_q8k(x + (size_t)n * in, in, q + (size_t)n * in, s + (size_t)n * spr,
+                                   b + (size_t)n * spr * 16);
+        if (rc) return rc;
+    }
+    batched_ctx c = {blocks, q, s, b, bias, y, spr, in, out, rows};
+    if (type == 12) parallel_for_all(out, q4k_ws_chunk, &c);
+    else if (type == 14) parallel_for_all(out, q6k_batched_chunk, &c);
+    else return ORC_ERR_RANGE;
+    return ORC_OK;
+}
+
+/* Q4KDotKernel.ProjectBatchedWeightStationary (RT/Q4KDotKernel.cs:819-893). */
+int cpub_q4k_project_batched_ws(const float* x, int rows, const uint8_t* blocks, int in, int out, const float* bias,
+                                float* y, int8_t* q, float* s, int16_t* b) {
+    return batched_project(12, x, rows, blocks, in, out, bias, y, q, s, b);
+}
+
+/* Q6KDotKernel.ProjectBatched (RT/Q6KDotKernel.cs:403-475). */
+int cpub_q6k_project_batched(const float* x, int rows, const uint8_t* blocks, int in, int out, const float* bias,
+                             float* y, int8_t* q, float* s, int16_t* b) {
+    return batched_project(14, x, rows, blocks, in, out, bias, y, q, s, b);
+}
+
+/* DecodeSwiGluBatchedDispatched (RT/CachedFeedForwardBlock.cs:328-348) with BatchedQuantProjection.Dispatch for each
+ * projection (Q4_K weight-stationary, Q6_K batched): gate, SiLU (the oracle's 1 / (1 + expf(-g)) form), up,
+ * gate * up, down. Scratch: g, u [rows][d_ff]; q [rows][max(d_model, d_ff)], s, b to match. */
+static int swiglu_batched(const float* x, int rows, const uint8_t* gate, const uint8_t* up, const uint8_t* down,
+                          int gate_type, int down_type, int d_model, int d_ff, float* y, float* g, float* u, int8_t* q,
+                          float* s, int16_t* b) {
+    int rc = batched_project(gate_type, x, rows, gate, d_model, d_ff, NULL, g, q, s, b);
+    if (rc) return rc;
+    for (size_t i = 0; i < (size_t)rows * d_ff; i++) {
+        const float sig = 1.0f / (1.0f + expf(-g[i]));
+        g[i] = g[i] * sig;
+    }
+    if ((rc = batched_project(gate_type, x, rows, up, d_model, d_ff, NULL, u, q, s, b))) return rc;
+    for (size_t i = 0; i < (size_t)rows * d_ff; i++) u[i] = g[i] * u[i];
+    return batched_project(down_type, u, rows, down, d_ff, d_model, NULL, y, q, s, b);
+}
+
+/* MoeFeedForwardBlock.DecodeBatched after routing (RT/MoeFeedForwardBlock.cs:187-241): for each expert in order,
+ * its tokens (first matching slot, tokens ascending) gathered, the batched SwiGLU, outputs stashed at (token, slot);
+ * then each token's slots combined in slot order. Same grouping and combine as the oracle's orc_moe_ffn_batched. */
+int cpub_moe_ffn_batched(int n_experts, const uint8_t* const* gate, const uint8_t* const* up,
+                         const uint8_t* const* down, int gate_type, int down_type, const float* x, int rows,
+                         int d_model, int d_ff, int top_k, const int* idx, const float* w, float* y) {
+    if (!gate || !up || !down || !x || !idx || !w || !y) return ORC_ERR_NULL;
+    if (n_experts <= 0 || rows <= 0 || top_k <= 0) return ORC_ERR_RANGE;
+    if (d_model % 256 || d_ff % 256) return ORC_ERR_SIZE;
+    const size_t P = (size_t)rows * top_k;
+    const int kmax = d_model > d_ff ? d_model : d_ff;
+    int* row_buf = (int*)malloc(sizeof(int) * (size_t)rows);
+    int* slot_buf = (int*)malloc(sizeof(int) * (size_t)rows);
+    int* have = (int*)calloc(P, sizeof(int));
+    float* gathered = (float*)malloc(sizeof(float) * (size_t)rows * d_model);
+    float* expert_out = (float*)malloc(sizeof(float) * (size_t)rows * d_model);
+    float* slot_out = (float*)malloc(sizeof(float) * P * d_model);
+    float* g = (float*)malloc(sizeof(float) * (size_t)rows * d_ff);
+    float* u = (float*)malloc(sizeof(float) * (size_t)rows * d_ff);
+    int8_t* q = (int8_t*)malloc((size_t)rows * kmax);
+    float* s = (float*)malloc(sizeof(float) * (size_t)rows * (kmax / 256));
+    int16_t* b = (int16_t*)malloc(sizeof(int16_t) * (size_t)rows * (kmax / 16));
+    int rc = (row_buf && slot_buf && have && gathered && expert_out && slot_out && g && u && q && s && b) ? ORC_OK
+                                                                                                      : ORC_ERR_SIZE;
+    for (int e = 0; e < n_experts && !rc; e++) {
+        int count = 0;
+        for (int n = 0; n < rows; n++)
+            for (int j = 0; j < top_k; j++)
+                if (idx[n * top_k + j] == e) {
+                    row_buf[count] = n;
+                    slot_buf[count] = j;
+                    count++;
+                    break;
+                }
+        if (count == 0) continue;
+        for (int c = 0; c < count; c++)
+            memcpy(gathered + (size_t)c * d_model, x + (size_t)row_buf[c] * d_model, sizeof(float) * d_model);
+        rc = swiglu_batched(gathered, count, gate[e], up[e], down[e], gate_type, down_type, d_model, d_ff,
+                            expert_out, g, u, q, s, b);
+        for (int c = 0; c < count && !rc; c++) {
+            const size_t slot = (size_t)row_buf[c] * top_k + slot_buf[c];
+            memcpy(slot_out + slot * d_model, expert_out + (size_t)c * d_model, sizeof(float) * d_model);
+            have[slot] = 1;
+        }
+    }
+    for (int n = 0; n < rows && !rc; n++) {
+        float* dst = y + (size_t)n * d_model;
+        for (int d = 0; d < d_model; d++) dst[d] = 0.0f;
+        for (int j = 0; j < top_k; j++) {
+            const size_t slot = (size_t)n * top_k + j;
+            if (!have[slot]) continue;
+            const float wj = w[slot];
+            const float* src = slot_out + slot * d_model;
+            for (int d = 0; d < d_model; d++) dst[d] += wj * src[d];
+        }
+    }
+    free(row_buf);
+    free(slot_buf);
+    free(have);
+    free(gathered);
+    free(expert_out);
+    free(slot_out);
+    free(g);
+    free(u);
+    free(q);
+    free(s);
+    free(b);
+    return rc;
+}
+
+/* Compiler and flags this file was built with (for the baseline's report). */
+const char* cpub_build_info(void) {
+#ifdef CPUB_FLAGS
+    return "gcc " __VERSION__ "; " CPUB_FLAGS;
+#else
+    return "gcc " __VERSION__;
+#endif
 }
 
 int cpub_has_avx2(void) {

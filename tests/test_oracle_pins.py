@@ -675,3 +675,50 @@ def test_cpu_baseline_is_bit_identical_to_oracle(orc):
     s8 = np.zeros(k // 32, np.float32)
     L.cpub_q8_project_parallel(orc.P(x), orc.P(wq), orc.P(ws), k, n, orc.P(bias), orc.P(y), orc.P(q8), orc.P(s8))
     assert np.array_equal(y, orc.q8_project(x, wq, ws, k, n, bias))
+
+
+@pytest.mark.parametrize("workers", [1, 3, 8])
+def test_cpu_baseline_batched_paths_are_bit_identical_to_oracle(orc, workers):
+    """The batched CPU baseline (OverfitParallel.For over every worker, the caller on the last chunk; the Q4_K
+    weight-stationary 64-row tile; Q6_K ProjectBatched; the routed-MoE DecodeBatched) gives the oracle's bits for
+    any worker count, for row counts across the tile boundary and output counts not divisible by the chunks."""
+    L = orc.lib()
+    if not L.cpub_has_avx2():
+        pytest.skip("no AVX2 on this CPU")
+    L.cpub_set_workers(workers)
+    rng = np.random.default_rng(43 + workers)
+    k, n = 512, 37
+    b4 = random_q4k_blocks(rng, n * k // 256).reshape(n, -1)
+    b6 = random_q6k_blocks(rng, n * k // 256).reshape(n, -1)
+    bias = normal(rng, n)
+    for rows in (1, 5, 64, 131):
+        x = normal(rng, (rows, k))
+        q = np.zeros(rows * k, np.int8)
+        s = np.zeros(rows * k // 256, np.float32)
+        b = np.zeros(rows * k // 16, np.int16)
+        y = np.full((rows, n), np.nan, np.float32)
+        for bb in (None, bias):
+            assert L.cpub_q4k_project_batched_ws(orc.P(x), rows, orc.P(b4), k, n, orc.P(bb), orc.P(y), orc.P(q),
+                                                 orc.P(s), orc.P(b)) == 0
+            ref = orc.q4k_project_batched_ws(x, rows, b4, k, n, bb)
+            assert np.array_equal(y.view(np.uint32), ref.view(np.uint32)), ("q4k ws", rows)
+            assert L.cpub_q6k_project_batched(orc.P(x), rows, orc.P(b6), k, n, orc.P(bb), orc.P(y), orc.P(q),
+                                              orc.P(s), orc.P(b)) == 0
+            ref = orc.q6k_project_batched(x, rows, b6, k, n, bb)
+            assert np.array_equal(y.view(np.uint32), ref.view(np.uint32)), ("q6k", rows)
+    # routed MoE: 5 experts, 9 tokens, top-2 (Q4_K gate/up, Q6_K down)
+    import ctypes
+    E, dm, dff, rows, top_k = 5, 256, 512, 9, 2
+    gate = [orc.quantize_q4k(normal(rng, (dff, dm), 0.05)) for _ in range(E)]
+    up = [orc.quantize_q4k(normal(rng, (dff, dm), 0.05)) for _ in range(E)]
+    down = [orc.quantize_q6k(normal(rng, (dm, dff), 0.05)) for _ in range(E)]
+    x = normal(rng, (rows, dm))
+    idx = np.stack([rng.choice(E, top_k, replace=False) for _ in range(rows)]).astype(np.int32)
+    w = rng.random((rows, top_k)).astype(np.float32)
+    arr = lambda ms: (ctypes.c_void_p * E)(*[m.ctypes.data for m in ms])  # noqa: E731
+    y = np.zeros((rows, dm), np.float32)
+    assert L.cpub_moe_ffn_batched(E, arr(gate), arr(up), arr(down), 12, 14, orc.P(x), rows, dm, dff, top_k,
+                                  orc.P(idx), orc.P(w), orc.P(y)) == 0
+    ref = orc.moe_ffn_batched(gate, up, down, 12, 14, x, rows, dm, dff, top_k, idx, w)
+    assert np.array_equal(y.view(np.uint32), np.asarray(ref, np.float32).view(np.uint32))
+    L.cpub_set_workers(4)
