@@ -516,13 +516,55 @@ def main():
         g = capture([token])
         graph_us = replay_us(g, 1, 10)
         w = n_layers * layer_algorithmic_bytes()[0] + weight_bytes(128256, 4096, "q6k")
-        del g, layers[len(copies):], head
+        del g
+        host = host_token_line(layers, head)
+        del layers[len(copies):], head
         torch.cuda.empty_cache()
         return {"what": "benchmark config 4: %d Llama-3-8B Q4_K_M layers + Q6_K LM head, one decode token, "
                         "projections only (%d launches)" % (n_layers, 4 * n_layers + 1),
                 "weight_bytes": w, "eager_us": round(eager_us, 1), "graph_us": round(graph_us, 1),
                 "proj_tok_s_eager": round(1e6 / eager_us, 1), "proj_tok_s_graph": round(1e6 / graph_us, 1),
-                "GB_s_graph": round(w / (graph_us * 1e-6) / 1e9, 1)}
+                "GB_s_graph": round(w / (graph_us * 1e-6) / 1e9, 1), "host_pointer_calls": host}
+
+    def host_token_line(layers, head, reps=5):
+        """Config 4 end to end through the host-pointer entry points, as the C# drop-in issues them per layer:
+        ovfq_project for q, k and v, ovfq_project for o, ovfq_project_gate_up, ovfq_project for down, then the LM
+        head — each call synchronous, its fp32 input copied up from pageable host memory and its output copied back
+        (6 calls per layer, 193 per token). Timed on the host clock around whole tokens; the call arguments are
+        prepared ctypes objects, so Python adds about a microsecond per call. Attention, RMSNorm and RoPE (host-side
+        by the benchmark's definition) are not run."""
+        import ctypes
+
+        lib = ctx.lib
+        hx = {k: np.random.default_rng(k).standard_normal(k).astype(np.float32) for k in (4096, 14336)}
+        outs = {n: np.zeros(n, np.float32) for n in (4096, 1024, 14336, 128256)}
+        up_out = np.zeros(14336, np.float32)
+        P = lambda a: ctypes.c_void_p(a.ctypes.data)  # noqa: E731
+        calls = []
+        for ws in layers:
+            x4, x14 = P(hx[4096]), P(hx[14336])
+            for name, n in (("q", 4096), ("k", 1024), ("v", 1024), ("o", 4096)):
+                calls.append((lib.ovfq_project, (ctx.handle, ws[name].handle, x4, 1, None, P(outs[n]))))
+            calls.append((lib.ovfq_project_gate_up, (ctx.handle, ws["gate"].handle, ws["up"].handle, x4,
+                                                     P(outs[14336]), P(up_out))))
+            calls.append((lib.ovfq_project, (ctx.handle, ws["down"].handle, x14, 1, None, P(outs[4096]))))
+        calls.append((lib.ovfq_project, (ctx.handle, head.handle, P(hx[4096]), 1, None, P(outs[128256]))))
+
+        def token():
+            for fn, args in calls:
+                if fn(*args):
+                    raise RuntimeError(lib.ovfq_last_error())
+
+        token()
+        best = float("inf")
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            token()
+            best = min(best, time.perf_counter() - t0)
+        return {"what": "the same token through the synchronous host-pointer entry points (input up, output down per "
+                        "call, %d calls)" % len(calls),
+                "us": round(best * 1e6, 1), "proj_tok_s": round(1.0 / best, 1),
+                "timing": "host clock, best of %d tokens" % reps}
 
     def moe_line(n_sets=2, tokens=16, top_k=2, n_experts=8, keep_host=False):
         """benchmark config 5: Mixtral-8x7B-shaped experts (gate/up 14336x4096, down 4096x14336, Q4_K), 16 tokens

@@ -120,6 +120,20 @@ OVFQ_API int ovfq_weight_create_gguf(ovfq_ctx* ctx, int type, const void* gguf_b
 /* As ovfq_weight_create_gguf, from device memory. */
 OVFQ_API int ovfq_weight_create_gguf_dev(ovfq_ctx* ctx, int type, const void* gguf_bytes, size_t nbytes,
                                          int input_size, int output_size, ovfq_weight** out);
+/* Replaces GgufLlamaLoader.LoadExperts (LD/GgufLlamaLoader.cs:600-690) for Q4_K / Q6_K / Q8_0: a 3-D expert tensor
+ * (ffn_gate_exps / ffn_up_exps / ffn_down_exps) as stored in a GGUF file, dims [ne0 = input_size, ne1 = output_size,
+ * ne2 = n_experts] with the expert axis slowest, -> n_experts weights written to out[0 .. n_experts). Each expert is
+ * the contiguous slice e of the tensor: K-quant bytes verbatim, Q8_0 blocks de-interleaved per expert. All experts
+ * share one device allocation (each slice 256-byte aligned), freed when the last of them is destroyed; each is
+ * destroyed with ovfq_weight_destroy like any weight. `nbytes` must cover n_experts slices. 1 <= n_experts <=
+ * OVFQ_MAX_EXPERT_SLICES. The reference's Q5_0 / Q5_K re-quantisation to Q8_0 is not in this library
+ * (OVFQ_ERR_TYPE). */
+#define OVFQ_MAX_EXPERT_SLICES 4096
+OVFQ_API int ovfq_weight_create_experts_gguf(ovfq_ctx* ctx, int type, const void* gguf_bytes, size_t nbytes,
+                                             int input_size, int output_size, int n_experts, ovfq_weight** out);
+/* As ovfq_weight_create_experts_gguf, from device memory. */
+OVFQ_API int ovfq_weight_create_experts_gguf_dev(ovfq_ctx* ctx, int type, const void* gguf_bytes, size_t nbytes,
+                                                 int input_size, int output_size, int n_experts, ovfq_weight** out);
 OVFQ_API int ovfq_weight_destroy(ovfq_weight* w);
 /* Opt-in MFMA-ready copy of a Q6_K weight, written on the device: for every 16 output rows and super-block, the
  * int8 weight operands the batched (M >= 32) int8-MFMA kernel otherwise rebuilds from the GGUF bytes for every
@@ -236,7 +250,7 @@ OVFQ_API int ovfq_project_heads_q8_0(ovfq_ctx* ctx, int n_heads, const ovfq_weig
 OVFQ_API int ovfq_project_heads_q8_0_dev(ovfq_ctx* ctx, int n_heads, const ovfq_weight* const* wo, const float* x,
                                          int rows, const float* bias, float* y);
 
-/* ---------------------------------------------------------------------------------- SwiGLU FFN */
+/* ---------------------------------------------------------------------------------- gated FFN */
 
 /* CachedFeedForwardBlock.DecodeSwiGluDispatched / DecodeSwiGluBatchedDispatched (RT/CachedFeedForwardBlock.cs:
  * 261-344) on the device: y[rows][d_model] = down(SiLU(gate(x)) * up(x)) for x[rows][d_model], gate/up
@@ -248,6 +262,18 @@ OVFQ_API int ovfq_ffn_swiglu(ovfq_ctx* ctx, const ovfq_weight* gate, const ovfq_
                              const float* x, int rows, float* y);
 OVFQ_API int ovfq_ffn_swiglu_dev(ovfq_ctx* ctx, const ovfq_weight* gate, const ovfq_weight* up,
                                  const ovfq_weight* down, const float* x, int rows, float* y);
+
+/* FeedForwardActivation's gated values (Runtime/FeedForwardActivation.cs:27, :33). */
+#define OVFQ_FFN_SWIGLU 3 /* gate activation SiLU (Llama, Mistral, Qwen, Phi)      */
+#define OVFQ_FFN_GEGLU 4  /* gate activation GELU, tanh approximation (Gemma)      */
+
+/* The same FFN with the gate activation chosen as CachedFeedForwardBlock.ApplyGate does (RT/CachedFeedForwardBlock.cs:
+ * 474-485): OVFQ_FFN_SWIGLU is ovfq_ffn_swiglu; OVFQ_FFN_GEGLU applies 0.5 g (1 + tanh(sqrt(2/pi) (g + 0.044715
+ * g^3))) in ApplyGeLU's operation order (:498-517) with the device tanhf. Any other activation -> OVFQ_ERR_RANGE. */
+OVFQ_API int ovfq_ffn_gated(ovfq_ctx* ctx, const ovfq_weight* gate, const ovfq_weight* up, const ovfq_weight* down,
+                            const float* x, int rows, int activation, float* y);
+OVFQ_API int ovfq_ffn_gated_dev(ovfq_ctx* ctx, const ovfq_weight* gate, const ovfq_weight* up,
+                                const ovfq_weight* down, const float* x, int rows, int activation, float* y);
 
 /* ---------------------------------------------------------------------------------- routed MoE */
 

@@ -72,6 +72,7 @@ _SIGS = {
     "orc_moe_select_topk": (c_int, [c_f32p, c_int, c_int, c_i32p, c_f32p, c_int]),
     "orc_q8_0_deinterleave": (c_int, [c_u8p, ctypes.c_long, c_i8p, c_f32p]),
     "orc_swiglu_batched": (c_int, [c_f32p, c_int, c_u8p, c_u8p, c_u8p, c_int, c_int, c_int, c_int, c_f32p]),
+    "orc_gated_ffn_batched": (c_int, [c_f32p, c_int, c_u8p, c_u8p, c_u8p, c_int, c_int, c_int, c_int, c_int, c_f32p]),
     "orc_moe_ffn_batched": (c_int, [c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, c_int, c_int, c_f32p,
                                     c_int, c_int, c_int, c_int, c_i32p, c_f32p, c_f32p]),
     # CPU baseline (cpu_baseline.c)
@@ -366,6 +367,17 @@ def swiglu_batched(x, rows, gate, up, down, gate_type, down_type, d_model, d_ff)
     y = np.zeros((rows, d_model), np.float32)
     g, u, d = (np.ascontiguousarray(a, np.uint8) for a in (gate, up, down))
     _check(lib().orc_swiglu_batched(P(x), rows, P(g), P(u), P(d), gate_type, down_type, d_model, d_ff, P(y)))
+    return y
+
+
+def gated_ffn_batched(x, rows, gate, up, down, gate_type, down_type, d_model, d_ff, activation):
+    """The batched gated FFN with ApplyGate's activation (3 SwiGLU, 4 GeGLU: FeedForwardActivation's values)
+    (oracle): y[rows][d_model]."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(rows, d_model)
+    y = np.zeros((rows, d_model), np.float32)
+    g, u, d = (np.ascontiguousarray(a, np.uint8) for a in (gate, up, down))
+    _check(lib().orc_gated_ffn_batched(P(x), rows, P(g), P(u), P(d), gate_type, down_type, d_model, d_ff, activation,
+                                       P(y)))
     return y
 
 

@@ -884,12 +884,24 @@ static int batched_kq(int type, const float* x, int rows, const uint8_t* blocks,
     return ORC_ERR_RANGE;
 }
 
-int orc_swiglu_batched(const float* x, int rows, const uint8_t* gate, const uint8_t* up, const uint8_t* down,
-                       int gate_type, int down_type, int d_model, int d_ff, float* y) {
-    /* RT/CachedFeedForwardBlock.cs:328-344 (DecodeSwiGluBatchedDispatched): gate = ProjectBatched(x); gate *=
-     * sigmoid(gate) (ApplySiLU, :464-472); up = ProjectBatched(x); up = gate * up; y = ProjectBatched(up). */
+/* ApplyGeLU (RT/CachedFeedForwardBlock.cs:498-517): x3 = x*x*x; inner = sqrt(2/pi) * (x + 0.044715 * x3);
+ * 0.5f * x * (1 + tanh(inner)), in that operation order. */
+static float gelu_tanh(float x) {
+    const float sqrt_two_over_pi = 0.7978845608028654f;
+    const float coeff = 0.044715f;
+    const float x3 = x * x * x;
+    const float inner = sqrt_two_over_pi * (x + coeff * x3);
+    return 0.5f * x * (1.0f + tanhf(inner));
+}
+
+int orc_gated_ffn_batched(const float* x, int rows, const uint8_t* gate, const uint8_t* up, const uint8_t* down,
+                          int gate_type, int down_type, int d_model, int d_ff, int activation, float* y) {
+    /* RT/CachedFeedForwardBlock.cs:328-348 (DecodeSwiGluBatchedDispatched): gate = ProjectBatched(x); ApplyGate
+     * (SiLU: gate *= sigmoid(gate), ApplySiLU :464-472; GELU(tanh): ApplyGeLU :498-517); up = ProjectBatched(x);
+     * up = gate * up; y = ProjectBatched(up). */
     if (!x || !gate || !up || !down || !y) return ORC_ERR_NULL;
     if (rows <= 0 || d_model % 256 || d_ff % 256) return ORC_ERR_SIZE;
+    if (activation != 3 && activation != 4) return ORC_ERR_RANGE;
     const int kmax = d_model > d_ff ? d_model : d_ff;
     float* g = (float*)malloc(sizeof(float) * (size_t)rows * d_ff);
     float* u = (float*)malloc(sizeof(float) * (size_t)rows * d_ff);
@@ -900,8 +912,12 @@ int orc_swiglu_batched(const float* x, int rows, const uint8_t* gate, const uint
     if (!rc) rc = batched_kq(gate_type, x, rows, gate, d_model, d_ff, g, q, s, b);
     if (!rc) {
         for (size_t i = 0; i < (size_t)rows * d_ff; i++) {
-            const float sig = 1.0f / (1.0f + expf(-g[i]));
-            g[i] = g[i] * sig;
+            if (activation == 4) {
+                g[i] = gelu_tanh(g[i]);
+            } else {
+                const float sig = 1.0f / (1.0f + expf(-g[i]));
+                g[i] = g[i] * sig;
+            }
         }
         rc = batched_kq(gate_type, x, rows, up, d_model, d_ff, u, q, s, b);
     }
@@ -915,6 +931,11 @@ int orc_swiglu_batched(const float* x, int rows, const uint8_t* gate, const uint
     free(s);
     free(b);
     return rc;
+}
+
+int orc_swiglu_batched(const float* x, int rows, const uint8_t* gate, const uint8_t* up, const uint8_t* down,
+                       int gate_type, int down_type, int d_model, int d_ff, float* y) {
+    return orc_gated_ffn_batched(x, rows, gate, up, down, gate_type, down_type, d_model, d_ff, 3, y);
 }
 
 int orc_moe_ffn_batched(int n_experts, const uint8_t* const* gate, const uint8_t* const* up,

@@ -146,6 +146,11 @@ int orc_moe_select_topk(const float* logits, int n, int top_k, int* expert_indic
  * gate/up [d_ff][d_model], down [d_model][d_ff]; types 12 (Q4_K) or 14 (Q6_K). SiLU via expf. */
 int orc_swiglu_batched(const float* x, int rows, const uint8_t* gate, const uint8_t* up, const uint8_t* down,
                        int gate_type, int down_type, int d_model, int d_ff, float* y);
+/* The same with the gate activation of ApplyGate (RT/CachedFeedForwardBlock.cs:474-485), activation taking
+ * FeedForwardActivation's values (Runtime/FeedForwardActivation.cs:11-34): 3 = SwiGLU (SiLU), 4 = GeGLU (GELU with
+ * the tanh approximation, ApplyGeLU :498-517, MathF.Tanh via tanhf). */
+int orc_gated_ffn_batched(const float* x, int rows, const uint8_t* gate, const uint8_t* up, const uint8_t* down,
+                          int gate_type, int down_type, int d_model, int d_ff, int activation, float* y);
 /* RT/MoeFeedForwardBlock.cs:140-241 (DecodeBatched) after routing: idx/w [rows][top_k]. */
 int orc_moe_ffn_batched(int n_experts, const uint8_t* const* gate, const uint8_t* const* up,
                         const uint8_t* const* down, int gate_type, int down_type, const float* x, int rows,

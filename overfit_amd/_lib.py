@@ -15,6 +15,8 @@ OVFQ_ERR_SIZE = -2
 OVFQ_ERR_RANGE = -3
 OVFQ_ERR_TYPE = -4
 OVFQ_ERR_HIP = -10
+OVFQ_FFN_SWIGLU = 3
+OVFQ_FFN_GEGLU = 4
 
 TYPE_Q8_0 = 8
 TYPE_Q4_K = 12
@@ -55,8 +57,12 @@ SIGNATURES = {
     "ovfq_project_gate_up": (ci, [vp, vp, vp, vp, vp, vp]),
     "ovfq_weight_create_gguf": (ci, [vp, ci, vp, ctypes.c_size_t, ci, ci, ctypes.POINTER(vp)]),
     "ovfq_weight_create_gguf_dev": (ci, [vp, ci, vp, ctypes.c_size_t, ci, ci, ctypes.POINTER(vp)]),
+    "ovfq_weight_create_experts_gguf": (ci, [vp, ci, vp, ctypes.c_size_t, ci, ci, ci, ctypes.POINTER(vp)]),
+    "ovfq_weight_create_experts_gguf_dev": (ci, [vp, ci, vp, ctypes.c_size_t, ci, ci, ci, ctypes.POINTER(vp)]),
     "ovfq_ffn_swiglu": (ci, [vp, vp, vp, vp, vp, ci, vp]),
     "ovfq_ffn_swiglu_dev": (ci, [vp, vp, vp, vp, vp, ci, vp]),
+    "ovfq_ffn_gated": (ci, [vp, vp, vp, vp, vp, ci, ci, vp]),
+    "ovfq_ffn_gated_dev": (ci, [vp, vp, vp, vp, vp, ci, ci, vp]),
     "ovfq_moe_select_topk": (ci, [vp, vp, ci, ci, ci, ci, vp, vp]),
     "ovfq_moe_select_topk_dev": (ci, [vp, vp, ci, ci, ci, ci, vp, vp]),
     "ovfq_moe_ffn": (ci, [vp, ci, PP, PP, PP, vp, ci, ci, vp, vp, vp]),

@@ -66,6 +66,13 @@ struct ovfq_ctx {
     int live_weights = 0;
 };
 
+// One device allocation holding every expert sliced from a 3-D GGUF expert tensor; the last expert weight
+// destroyed frees it. Reference counts change under the owning context's mutex.
+struct SharedPlane {
+    void* p = nullptr;
+    int refs = 0;
+};
+
 struct ovfq_weight {
     ovfq_ctx* ctx = nullptr;
     int type = 0;
@@ -75,6 +82,7 @@ struct ovfq_weight {
     float* scales = nullptr; // Q8_0 scale plane
     size_t nbytes = 0;       // resident bytes (blocks + scales)
     void* mfma = nullptr;    // MFMA-ready copy (ovfq_weight_prepare_mfma), or NULL
+    SharedPlane* shared = nullptr; // set for expert slices: blocks/scales point into shared->p
 };
 
 namespace {
@@ -527,14 +535,106 @@ int ovfq_weight_create_gguf_dev(ovfq_ctx* ctx, int type, const void* gguf_bytes,
     return weight_create_gguf(ctx, type, gguf_bytes, nbytes, input_size, output_size, out, false);
 }
 
+// GgufLlamaLoader.LoadExperts (LD/GgufLlamaLoader.cs:600-690) for Q4_K / Q6_K / Q8_0: a 3-D expert tensor
+// [ne0 = in, ne1 = out, ne2 = n_experts] (expert axis slowest) -> one weight per expert. All experts live in one
+// device allocation, each slice starting on a 256-byte boundary (expert e at e * stride); Q4_K/Q6_K bytes are
+// copied verbatim, Q8_0 blocks de-interleaved per expert into quant planes [E][stride_q] then scale planes
+// [E][stride_s].
+static int experts_gguf_impl(ovfq_ctx* ctx, int type, const void* src, size_t nbytes, int in, int out,
+                             int n_experts, ovfq_weight** res, bool host) {
+    if (!ctx) return fail(OVFQ_ERR_NULL, "ctx is NULL");
+    if (!src) return fail(OVFQ_ERR_NULL, "gguf_bytes is NULL");
+    if (!res) return fail(OVFQ_ERR_NULL, "out is NULL");
+    int rc = check_weight_shape(type, in, out);
+    if (rc) return rc;
+    if (n_experts <= 0 || n_experts > OVFQ_MAX_EXPERT_SLICES)
+        return fail(OVFQ_ERR_RANGE, "n_experts (%d) must be in [1, %d]", n_experts, OVFQ_MAX_EXPERT_SLICES);
+    const bool q8 = type == OVFQ_TYPE_Q8_0;
+    const int64_t blocks_per_expert = (int64_t)out * (in / OVFQ_Q8_BLOCK);
+    const size_t src_expert = q8 ? (size_t)blocks_per_expert * 34 : block_bytes_per_row(type, in) * (size_t)out;
+    if (nbytes / (size_t)n_experts < src_expert)
+        return fail(OVFQ_ERR_SIZE, "expert tensor region (%zu B) is smaller than the expected %d x %zu B", nbytes,
+                    n_experts, src_expert);
+    if (!host && q8 && !aligned(src, 2)) return fail(OVFQ_ERR_SIZE, "device gguf_bytes must be 2-byte aligned");
+    auto pad = [](size_t b) { return (b + 255) & ~size_t(255); };
+    const size_t q_bytes = q8 ? (size_t)out * in : src_expert;
+    const size_t s_bytes = q8 ? (size_t)blocks_per_expert * sizeof(float) : 0;
+    const size_t q_stride = pad(q_bytes), s_stride = pad(s_bytes);
+    const size_t E = (size_t)n_experts;
+    const hipMemcpyKind kind = host ? hipMemcpyHostToDevice : hipMemcpyDeviceToDevice;
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    HIP_TRY(hipSetDevice(ctx->device));
+    char* base = nullptr;
+    void* staged = nullptr;
+    hipError_t e = hipMalloc((void**)&base, E * (q_stride + s_stride));
+    if (e == hipSuccess && !q8) {
+        for (size_t x = 0; x < E && e == hipSuccess; x++)
+            e = hipMemcpyAsync(base + x * q_stride, static_cast<const char*>(src) + x * src_expert, src_expert, kind,
+                               ctx->stream);
+    } else if (e == hipSuccess) {
+        const char* dsrc = static_cast<const char*>(src);
+        if (host) {
+            e = hipMalloc(&staged, E * src_expert);
+            if (e == hipSuccess) e = hipMemcpyAsync(staged, src, E * src_expert, hipMemcpyHostToDevice, ctx->stream);
+            dsrc = static_cast<const char*>(staged);
+        }
+        float* scales = reinterpret_cast<float*>(base + E * q_stride);
+        for (size_t x = 0; x < E && e == hipSuccess; x++)
+            e = ovfq::launch_q8_0_deinterleave(dsrc + x * src_expert, blocks_per_expert,
+                                               reinterpret_cast<int8_t*>(base + x * q_stride),
+                                               reinterpret_cast<float*>(reinterpret_cast<char*>(scales) + x * s_stride),
+                                               ctx->stream);
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (staged) (void)hipFree(staged);
+    if (e != hipSuccess) {
+        if (base) (void)hipFree(base);
+        return fail(OVFQ_ERR_HIP, "expert tensor upload failed: %s", hipGetErrorString(e));
+    }
+    SharedPlane* sp = new SharedPlane();
+    sp->p = base;
+    sp->refs = n_experts;
+    for (size_t x = 0; x < E; x++) {
+        ovfq_weight* w = new ovfq_weight();
+        w->ctx = ctx;
+        w->type = type;
+        w->in = in;
+        w->out = out;
+        w->blocks = base + x * q_stride;
+        w->scales = q8 ? reinterpret_cast<float*>(base + E * q_stride + x * s_stride) : nullptr;
+        w->nbytes = q_bytes + s_bytes;
+        w->shared = sp;
+        res[x] = w;
+    }
+    ctx->live_weights += n_experts;
+    return ok();
+}
+
+int ovfq_weight_create_experts_gguf(ovfq_ctx* ctx, int type, const void* gguf_bytes, size_t nbytes, int input_size,
+                                    int output_size, int n_experts, ovfq_weight** out) {
+    return experts_gguf_impl(ctx, type, gguf_bytes, nbytes, input_size, output_size, n_experts, out, true);
+}
+
+int ovfq_weight_create_experts_gguf_dev(ovfq_ctx* ctx, int type, const void* gguf_bytes, size_t nbytes,
+                                        int input_size, int output_size, int n_experts, ovfq_weight** out) {
+    return experts_gguf_impl(ctx, type, gguf_bytes, nbytes, input_size, output_size, n_experts, out, false);
+}
+
 int ovfq_weight_destroy(ovfq_weight* w) {
     if (!w) return fail(OVFQ_ERR_NULL, "weight is NULL");
     {
         std::lock_guard<std::mutex> lk(w->ctx->mu);
         (void)hipSetDevice(w->ctx->device);
         (void)hipStreamSynchronize(w->ctx->stream);
-        if (w->blocks) (void)hipFree(w->blocks);
-        if (w->scales) (void)hipFree(w->scales);
+        if (w->shared) {
+            if (--w->shared->refs == 0) {
+                (void)hipFree(w->shared->p);
+                delete w->shared;
+            }
+        } else {
+            if (w->blocks) (void)hipFree(w->blocks);
+            if (w->scales) (void)hipFree(w->scales);
+        }
         if (w->mfma) (void)hipFree(w->mfma);
         w->ctx->live_weights--;
     }
@@ -1170,7 +1270,7 @@ static int moe_impl(ovfq_ctx* ctx, int E, const ovfq_weight* const* gate, const 
         HIP_TRY(ovfq::launch_mfma_grouped(gt, L, tiles, tile_count, max_tiles, ctx->stream));
     else
         HIP_TRY(ovfq::launch_mfma_small(gt, L, ctx->stream));
-    HIP_TRY(ovfq::launch_swiglu_q8k(g, u, off, E, (int)P, dff, iq, is, ib, ctx->stream));
+    HIP_TRY(ovfq::launch_gate_up_q8k(g, u, off, E, (int)P, dff, false, iq, is, ib, ctx->stream));
     ovfq::GroupLaunch D{};
     D.w0 = dw;
     D.y0 = out;
@@ -1193,11 +1293,13 @@ static int moe_impl(ovfq_ctx* ctx, int E, const ovfq_weight* const* gate, const 
     return ok();
 }
 
-// ---------------------------------------------------------------------------------------- SwiGLU FFN
+// ---------------------------------------------------------------------------------------- gated FFN
 
 static int ffn_impl(ovfq_ctx* ctx, const ovfq_weight* gate, const ovfq_weight* up, const ovfq_weight* down,
-                    const float* x, int rows, float* y, bool host) {
+                    const float* x, int rows, int activation, float* y, bool host) {
     if (!ctx) return fail(OVFQ_ERR_NULL, "ctx is NULL");
+    if (activation != OVFQ_FFN_SWIGLU && activation != OVFQ_FFN_GEGLU)
+        return fail(OVFQ_ERR_RANGE, "activation %d is neither OVFQ_FFN_SWIGLU (3) nor OVFQ_FFN_GEGLU (4)", activation);
     if (!gate || !up || !down) return fail(OVFQ_ERR_NULL, "gate / up / down is NULL");
     if (!x || !y) return fail(OVFQ_ERR_NULL, "x / y is NULL");
     int rc;
@@ -1251,8 +1353,9 @@ static int ffn_impl(ovfq_ctx* ctx, const ovfq_weight* gate, const ovfq_weight* u
         if ((rc = quantize_into_scratch(ctx, gate->type, xd, rows, dmodel, &act))) return rc;
         if ((rc = launch_projection(ctx, gu, 2, nullptr, gu_out, rows, act))) return rc;
     }
-    // SiLU(gate) * up, quantised to Q8_K for the down projection
-    HIP_TRY(ovfq::launch_swiglu_q8k(g, u, nullptr, 0, rows, dff, iq, is, ib, ctx->stream));
+    // act(gate) * up, quantised to Q8_K for the down projection
+    HIP_TRY(ovfq::launch_gate_up_q8k(g, u, nullptr, 0, rows, dff, activation == OVFQ_FFN_GEGLU, iq, is, ib,
+                                     ctx->stream));
     const ovfq_weight* dw[1] = {down};
     float* dy[1] = {yd};
     if ((rc = launch_projection(ctx, dw, 1, nullptr, dy, rows, ovfq::ActQ{iq, is, ib}))) return rc;
@@ -1265,12 +1368,22 @@ static int ffn_impl(ovfq_ctx* ctx, const ovfq_weight* gate, const ovfq_weight* u
 
 int ovfq_ffn_swiglu(ovfq_ctx* ctx, const ovfq_weight* gate, const ovfq_weight* up, const ovfq_weight* down,
                     const float* x, int rows, float* y) {
-    return ffn_impl(ctx, gate, up, down, x, rows, y, true);
+    return ffn_impl(ctx, gate, up, down, x, rows, OVFQ_FFN_SWIGLU, y, true);
 }
 
 int ovfq_ffn_swiglu_dev(ovfq_ctx* ctx, const ovfq_weight* gate, const ovfq_weight* up, const ovfq_weight* down,
                         const float* x, int rows, float* y) {
-    return ffn_impl(ctx, gate, up, down, x, rows, y, false);
+    return ffn_impl(ctx, gate, up, down, x, rows, OVFQ_FFN_SWIGLU, y, false);
+}
+
+int ovfq_ffn_gated(ovfq_ctx* ctx, const ovfq_weight* gate, const ovfq_weight* up, const ovfq_weight* down,
+                   const float* x, int rows, int activation, float* y) {
+    return ffn_impl(ctx, gate, up, down, x, rows, activation, y, true);
+}
+
+int ovfq_ffn_gated_dev(ovfq_ctx* ctx, const ovfq_weight* gate, const ovfq_weight* up, const ovfq_weight* down,
+                       const float* x, int rows, int activation, float* y) {
+    return ffn_impl(ctx, gate, up, down, x, rows, activation, y, false);
 }
 
 int ovfq_moe_ffn(ovfq_ctx* ctx, int n_experts, const ovfq_weight* const* gate, const ovfq_weight* const* up,

@@ -5,7 +5,7 @@
 //   2. group the (token, top-k slot) pairs by expert, tokens ascending, and quantise
 //      the tokens' activation to Q8_K in the same launch                            -> moe_plan_kernel
 //   3. per expert: gate/up = batched projections of its tokens                   (mfma.hip, grid.y = expert)
-//   4. SiLU(gate) * up, quantised to Q8_K for the down projection                    -> swiglu_q8k_kernel
+//   4. SiLU(gate) * up, quantised to Q8_K for the down projection                    -> gate_up_q8k_kernel
 //   5. per expert: down projection of its pairs                                  (mfma.hip)
 //   6. y[token] = sum over top-k slots, in slot order, of weight * expert output     -> moe_combine_kernel
 // Pairs are numbered expert-major (expert 0's tokens first, ascending), which is the order the reference
@@ -201,12 +201,14 @@ __global__ __launch_bounds__(256) void moe_plan_kernel(const int* __restrict__ i
     }
 }
 
-// ------------------------------------------------------------------------------------------ SwiGLU
-// One wave per (pair, 256-element block) of the intermediate: gate <- gate * sigmoid(gate), up <- gate * up
-// (ApplySiLU + TensorPrimitives.Multiply, RT/CachedFeedForwardBlock.cs:339-343, :464-472), then the Q8_K
-// quantisation the down projection's BatchedQuantProjection.Dispatch applies to its input
-// (RT/Q4KDotKernel.cs:71-136). Pairs at or past expert_off[n_experts] are skipped.
-__global__ __launch_bounds__(256) void swiglu_q8k_kernel(const float* __restrict__ gate, const float* __restrict__ up,
+// ------------------------------------------------------------------------------------------ gate * up
+// One wave per (pair, 256-element block) of the intermediate: gate <- act(gate), up <- gate * up (ApplyGate +
+// TensorPrimitives.Multiply, RT/CachedFeedForwardBlock.cs:339-344, :474-485), then the Q8_K quantisation the down
+// projection's BatchedQuantProjection.Dispatch applies to its input (RT/Q4KDotKernel.cs:71-136). act is SiLU,
+// g * sigmoid(g) (ApplySiLU :464-472), or with GELU the tanh approximation 0.5 g (1 + tanh(sqrt(2/pi) (g + 0.044715
+// g^3))) in ApplyGeLU's operation order (:498-517). Pairs at or past expert_off[n_experts] are skipped.
+template <bool GELU>
+__global__ __launch_bounds__(256) void gate_up_q8k_kernel(const float* __restrict__ gate, const float* __restrict__ up,
                                                          const int* __restrict__ expert_off, int n_experts,
                                                          int max_pairs, int spr, int8_t* __restrict__ q,
                                                          float* __restrict__ s, int16_t* __restrict__ bs) {
@@ -223,8 +225,15 @@ __global__ __launch_bounds__(256) void swiglu_q8k_kernel(const float* __restrict
     float v[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const float sig = 1.0f / (1.0f + expf(-g[i]));
-        const float act = g[i] * sig;
+        float act;
+        if (GELU) {
+            const float x3 = g[i] * g[i] * g[i];
+            const float inner = 0.7978845608028654f * (g[i] + 0.044715f * x3);
+            act = 0.5f * g[i] * (1.0f + tanhf(inner));
+        } else {
+            const float sig = 1.0f / (1.0f + expf(-g[i]));
+            act = g[i] * sig;
+        }
         v[i] = act * u[i];
     }
     const Q8KLane r = q8k_quantize_wave(v[0], v[1], v[2], v[3]);
@@ -287,12 +296,17 @@ hipError_t launch_moe_plan(const int* idx, int rows, int k, int n_experts, int* 
     return hipGetLastError();
 }
 
-hipError_t launch_swiglu_q8k(const float* gate, const float* up, const int* expert_off, int n_experts, int max_pairs,
-                             int dff, int8_t* q, float* s, int16_t* b, hipStream_t st) {
+hipError_t launch_gate_up_q8k(const float* gate, const float* up, const int* expert_off, int n_experts, int max_pairs,
+                              int dff, bool gelu, int8_t* q, float* s, int16_t* b, hipStream_t st) {
     const int spr = dff / kQK;
     const int64_t waves = (int64_t)max_pairs * spr;
-    hipLaunchKernelGGL(swiglu_q8k_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, gate, up, expert_off,
-                       n_experts, max_pairs, spr, q, s, b);
+    const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
+    if (gelu)
+        hipLaunchKernelGGL(gate_up_q8k_kernel<true>, grid, block, 0, st, gate, up, expert_off, n_experts, max_pairs, spr,
+                           q, s, b);
+    else
+        hipLaunchKernelGGL(gate_up_q8k_kernel<false>, grid, block, 0, st, gate, up, expert_off, n_experts, max_pairs,
+                           spr, q, s, b);
     return hipGetLastError();
 }
 

@@ -95,8 +95,9 @@ hipError_t launch_moe_plan(const int* idx, int rows, int k, int n_experts, int* 
 hipError_t launch_mfma_grouped(int type, const GroupLaunch& launch, const int* tiles, const int* tile_count,
                                int max_tiles, hipStream_t st);
 constexpr int kGroupedTileRows = 64;
-hipError_t launch_swiglu_q8k(const float* gate, const float* up, const int* expert_off, int n_experts, int max_pairs,
-                             int dff, int8_t* q, float* s, int16_t* b, hipStream_t st);
+// act(gate) * up (act: SiLU, or GELU with the tanh approximation), quantised to Q8_K for the down projection.
+hipError_t launch_gate_up_q8k(const float* gate, const float* up, const int* expert_off, int n_experts, int max_pairs,
+                              int dff, bool gelu, int8_t* q, float* s, int16_t* b, hipStream_t st);
 hipError_t launch_moe_combine(const float* out, const int* pair_of, const float* w, int rows, int k, int dmodel,
                               float* y, hipStream_t st);
 

@@ -18,6 +18,8 @@ reference requires of its variants).
 """
 import ctypes
 
+import enum
+
 import numpy as np
 
 from . import _lib
@@ -376,9 +378,27 @@ class MoeRouter:
         return k
 
 
+class FeedForwardActivation(enum.IntEnum):
+    """Runtime/FeedForwardActivation.cs:11-34. The fused FFN takes the gated two: SwiGLU and GeGLU."""
+    None_ = 0
+    ReLU = 1
+    GeLU = 2
+    SwiGLU = 3
+    GeGLU = 4
+
+
 def ffn_swiglu(gate, up, down, x, rows=1, out=None):
     """CachedFeedForwardBlock.DecodeSwiGluDispatched / DecodeSwiGluBatchedDispatched (RT/CachedFeedForwardBlock.cs:
     261-344) on the device: down(SiLU(gate(x)) * up(x)) in three launches, no host round trip."""
+    return ffn_gated(gate, up, down, x, rows, FeedForwardActivation.SwiGLU, out)
+
+
+def ffn_gated(gate, up, down, x, rows=1, activation=FeedForwardActivation.SwiGLU, out=None):
+    """The gated FFN with ApplyGate's activation (RT/CachedFeedForwardBlock.cs:328-344, :474-485): SwiGLU (SiLU gate)
+    or GeGLU (GELU tanh-approximation gate, Gemma), down(act(gate(x)) * up(x)) in three launches."""
+    act = int(activation)
+    if act not in (FeedForwardActivation.SwiGLU, FeedForwardActivation.GeGLU):
+        raise OverfitArgumentError(f"the fused FFN is gated: activation must be SwiGLU or GeGLU, not {activation!r}")
     inp = as_buf(x, np.float32, "x")
     d_model = gate.InputSize
     if out is None:
@@ -391,8 +411,8 @@ def ffn_swiglu(gate, up, down, x, rows=1, out=None):
     o = as_buf(out, np.float32, "out")
     same_side(inp, o)
     ctx = gate.context
-    fn = ctx.lib.ovfq_ffn_swiglu_dev if inp.device else ctx.lib.ovfq_ffn_swiglu
-    raise_for_status(fn(ctx.handle, gate.handle, up.handle, down.handle, inp.ptr, rows, o.ptr), ctx.lib)
+    fn = ctx.lib.ovfq_ffn_gated_dev if inp.device else ctx.lib.ovfq_ffn_gated
+    raise_for_status(fn(ctx.handle, gate.handle, up.handle, down.handle, inp.ptr, rows, act, o.ptr), ctx.lib)
     return out
 
 

@@ -160,6 +160,30 @@ def load_gguf_tensor(type_id, data, input_size: int, output_size: int, ctx=None)
     return w
 
 
+def load_gguf_experts(type_id, data, input_size: int, output_size: int, n_experts: int, ctx=None):
+    """GgufLlamaLoader.LoadExperts (LD/GgufLlamaLoader.cs:600-690): a 3-D GGUF expert tensor [input_size,
+    output_size, n_experts] (expert axis slowest) -> one resident weight per expert, the experts sharing one device
+    allocation (freed with the last of them). Q4_K/Q6_K slices verbatim, Q8_0 de-interleaved per expert."""
+    cls = {_lib.TYPE_Q4_K: Q4KWeight, _lib.TYPE_Q6_K: Q6KWeight, _lib.TYPE_Q8_0: Q8Weight}.get(type_id)
+    if cls is None:
+        raise OverfitUnsupportedTypeError(f"type {type_id}")
+    buf = as_buf(data, np.uint8, "data")
+    ctx = ctx or default_context()
+    lib = ctx.lib
+    hs = (ctypes.c_void_p * max(int(n_experts), 1))()
+    fn = lib.ovfq_weight_create_experts_gguf_dev if buf.device else lib.ovfq_weight_create_experts_gguf
+    raise_for_status(fn(ctx.handle, type_id, buf.ptr, buf.size, input_size, output_size, n_experts, hs), lib)
+    experts = []
+    for h in hs[:n_experts]:
+        w = cls.__new__(cls)
+        w._ctx = ctx
+        w.handle = ctypes.c_void_p(h)
+        w._input_size = input_size
+        w._output_size = output_size
+        experts.append(w)
+    return experts
+
+
 class DecodeWeight:
     """The 4-way tagged union {F32 | Q8_0 | Q4_K | Q6_K} of RT/DecodeWeight.cs:28-177.
 

@@ -5,6 +5,7 @@ the fp32 tail and the per-row super-block sum are evaluated in the reference's o
 must equal the oracle's. The north-star tolerance (max relative error 1e-3, cosine >= 0.99999) is reported
 alongside as the outer bound.
 """
+import ctypes
 import sys
 
 import numpy as np
@@ -320,8 +321,9 @@ def test_multi_projection_rows_bit_exact(orc, ctx, batched, rows, kernel):
 
 @pytest.mark.parametrize("rows,kernel", [(1, "auto"), (5, "auto"), (5, "tiled"), (70, "auto")])
 def test_q8_0_multi_projection_rows_bit_exact(orc, ctx, batched, rows, kernel):
-    """Fused Q8_0 q/k/v-style call over `rows` activation rows (the row kernel, or the int8-MFMA kernel with one
-    launch per weight): every output bit-exact, with a bias on the last weight."""
+    """Fused Q8_0 q/k/v-style call over `rows` activation rows (the decode kernel up to 8 rows with rows x K <= 32768,
+    the int8-MFMA kernel beyond that or when forced, one launch per weight): every output bit-exact, with a bias on
+    the last weight."""
     case("q8_0 multi rows", rows, kernel)
     batched(kernel)
     rng = np.random.default_rng(500 + rows)
@@ -533,6 +535,41 @@ def test_ffn_swiglu_matches_oracle(orc, batched, rows, kernel):
     torch.cuda.synchronize()
     _moe_check(y.cpu().numpy(), ref, f"ffn rows={rows} device")
     _moe_check(ov.ffn_swiglu(g, u, d, x, rows), ref, f"ffn rows={rows} host")
+
+
+@pytest.mark.parametrize("rows,kernel,gtype", [(1, "auto", 12), (3, "auto", 12), (40, "tiled", 12), (2, "auto", 14)])
+def test_ffn_geglu_matches_oracle(orc, batched, rows, kernel, gtype):
+    """The GeGLU FFN (Gemma: GELU tanh-approximation gate, ApplyGeLU RT/CachedFeedForwardBlock.cs:498-517) against
+    the oracle at the FFN tolerance (tanhf on the device and on the host may differ by an ULP); the SwiGLU value of
+    the same entry point is bit-identical to ovfq_ffn_swiglu; non-gated activations are refused."""
+    case("ffn geglu", rows, kernel, gtype)
+    batched(kernel)
+    rng = np.random.default_rng(170 + rows)
+    dm, dff = 512, 1536
+    quant, W = (orc.quantize_q4k, ov.Q4KWeight) if gtype == 12 else (orc.quantize_q6k, ov.Q6KWeight)
+    gb, ub = quant(normal(rng, (dff, dm), 0.08)), quant(normal(rng, (dff, dm), 0.08))
+    db = orc.quantize_q6k(normal(rng, (dm, dff), 0.05))
+    g, u, d = W(gb, dm, dff), W(ub, dm, dff), ov.Q6KWeight(db, dff, dm)
+    x = normal(rng, (rows, dm))
+    ref = orc.gated_ffn_batched(x, rows, gb, ub, db, gtype, 14, dm, dff, 4)
+    y = ov.ffn_gated(g, u, d, t(x), rows, ov.FeedForwardActivation.GeGLU)
+    torch.cuda.synchronize()
+    _moe_check(y.cpu().numpy(), ref, f"geglu rows={rows} device")
+    _moe_check(ov.ffn_gated(g, u, d, x, rows, ov.FeedForwardActivation.GeGLU), ref, f"geglu rows={rows} host")
+    silu = orc.gated_ffn_batched(x, rows, gb, ub, db, gtype, 14, dm, dff, 3)
+    assert np.linalg.norm(y.cpu().numpy().reshape(ref.shape) - silu) > 10 * np.linalg.norm(
+        y.cpu().numpy().reshape(ref.shape) - ref)
+    a = ov.ffn_gated(g, u, d, t(x), rows, ov.FeedForwardActivation.SwiGLU)
+    b = ov.ffn_swiglu(g, u, d, t(x), rows)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+    with pytest.raises(ov.OverfitArgumentError):
+        ov.ffn_gated(g, u, d, t(x), rows, ov.FeedForwardActivation.GeLU)
+    ctx = g.context
+    out = torch.empty(rows * dm, device=DEV)
+    for bad in (0, 1, 2, 5, -1):
+        assert ctx.lib.ovfq_ffn_gated_dev(ctx.handle, g.handle, u.handle, d.handle, ctypes.c_void_p(t(x).data_ptr()),
+                                          rows, bad, ctypes.c_void_p(out.data_ptr())) == _lib.OVFQ_ERR_RANGE
 
 
 def test_ffn_swiglu_llama3_full_size(orc):
@@ -790,11 +827,11 @@ def test_llama3_8b_layer_prefill_sampled_rows(orc):
 
 
 # One row on the decode GEMV (activation in LDS up to K = 32768; 32800 takes the row kernel). More rows: automatic
-# choice (the decode kernel over up to 4 rows, the row kernel, the int8-MFMA kernel from 8 rows or fewer for short
-# inputs), and each kernel forced ("tiled": the MFMA kernel from 2 rows, "rows": the multi-row decode kernel where it
-# takes the shape, "small": the row kernel): partial 16/32/64-row activation tiles (2 .. 16,
-# 24, 65, 130), a partial 64-output tile (70), 129 blocks per row (four-block groups with a short last one; a partial
-# 64-block GEMV item), one block per row.
+# choice (the decode kernel over up to 8 rows where rows x K <= 32768, else the int8-MFMA kernel from 8 rows, or from
+# 4-6 rows for inputs up to 8192, else the row kernel), and each kernel forced ("tiled": the MFMA kernel from 2 rows,
+# "rows": the multi-row decode kernel where it takes the shape, "small": the row kernel): partial 16/32/64-row
+# activation tiles (2 .. 16, 24, 65, 130), a partial 64-output tile (70), 129 blocks per row (four-block groups with a
+# short last one; a partial 64-block GEMV item), one block per row.
 @pytest.mark.parametrize("kernel", ["auto", "tiled", "rows", "small"])
 @pytest.mark.parametrize("k,n", [(32, 5), (128, 4096), (4096, 300), (14336, 40), (4128, 70), (32768, 24),
                                  (32800, 9)])
@@ -811,6 +848,24 @@ def test_q8_0_project_bit_exact(orc, batched, kernel, k, n, rows):
     ref = orc.q8_project_batched(x, rows, wq, ws, k, n, bias)
     if rows == 1:
         assert np.array_equal(ref[0], orc.q8_project(x[0], wq, ws, k, n, bias))
+    y = ov.project(w, x, bias, rows=rows).reshape(rows, n)
+    assert_bit_exact(y, ref, f"q8_0 {k}x{n} rows={rows}")
+
+
+# The decode kernel's LDS copy of the activation exactly full (rows x K = 32768) at 4 and 8 rows, and 8 rows on
+# every kernel choice.
+@pytest.mark.parametrize("kernel", ["auto", "tiled", "rows", "small"])
+@pytest.mark.parametrize("k,n,rows", [(4096, 300, 8), (8192, 48, 4), (128, 4096, 8), (2048, 70, 8)])
+def test_q8_0_project_full_lds_and_eight_rows(orc, batched, kernel, k, n, rows):
+    case("q8_0 project full LDS", kernel, k, n, rows)
+    batched(kernel)
+    rng = np.random.default_rng(3 * k + n + rows)
+    wq, ws = orc.q8_quantize_rows(normal(rng, (n, k), 0.05))
+    wq[-1, -32:] = -128
+    x = normal(rng, (rows, k))
+    bias = normal(rng, n)
+    w = ov.Q8Weight(wq, ws, k, n)
+    ref = orc.q8_project_batched(x, rows, wq, ws, k, n, bias)
     y = ov.project(w, x, bias, rows=rows).reshape(rows, n)
     assert_bit_exact(y, ref, f"q8_0 {k}x{n} rows={rows}")
 

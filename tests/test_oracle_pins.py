@@ -596,6 +596,40 @@ def test_swiglu_batched_matches_f64_dequantised_ffn(orc):
     assert np.linalg.norm(y - bad) / np.linalg.norm(ref) > 5 * err
 
 
+def test_geglu_batched_matches_f64_dequantised_ffn(orc):
+    """The GeGLU gate (ApplyGeLU, RT/CachedFeedForwardBlock.cs:498-517: 0.5 x (1 + tanh(sqrt(2/pi)(x + 0.044715
+    x^3)))) against the float64 FFN on the dequantised weights with numpy's tanh: only the Q8_K quantisation separates
+    them; the SiLU FFN on the same weights is far away, and activation 3 (SwiGLU) is exactly orc_swiglu_batched."""
+    rng = np.random.default_rng(78)
+    dm, dff, rows = 512, 768, 3
+    (g,), (u,), (d,) = _small_experts(orc, rng, 1, dm, dff)
+    x = normal(rng, (rows, dm))
+    y = orc.gated_ffn_batched(x, rows, g, u, d, 12, 14, dm, dff, 4)
+    assert np.array_equal(orc.gated_ffn_batched(x, rows, g, u, d, 12, 14, dm, dff, 3).view(np.uint32),
+                          orc.swiglu_batched(x, rows, g, u, d, 12, 14, dm, dff).view(np.uint32))
+    dq = lambda blocks, k, n, fn: np.stack([fn(blocks, k, n, r) for r in range(n)]).astype(np.float64)  # noqa: E731
+    Wg, Wu = dq(g, dm, dff, orc.q4k_decode_row), dq(u, dm, dff, orc.q4k_decode_row)
+    Wd = dq(d, dff, dm, orc.q6k_decode_row)
+    a = x.astype(np.float64) @ Wg.T
+    gelu = 0.5 * a * (1 + np.tanh(np.sqrt(2 / np.pi) * (a + 0.044715 * a ** 3)))
+    ref = (gelu * (x.astype(np.float64) @ Wu.T)) @ Wd.T
+    err = np.linalg.norm(y - ref) / np.linalg.norm(ref)
+    assert err < 0.02, err
+    silu = ((a / (1 + np.exp(-a))) * (x.astype(np.float64) @ Wu.T)) @ Wd.T
+    assert np.linalg.norm(y - silu) / np.linalg.norm(ref) > 5 * err
+    # the elementwise GELU itself: float32 restatement vs float64 (tanh approximation) on a grid incl. large |x|
+    t = np.linspace(-12, 12, 4097).astype(np.float32)
+    g64 = 0.5 * t.astype(np.float64) * (1 + np.tanh(np.sqrt(2 / np.pi) * (t + 0.044715 * t.astype(np.float64) ** 3)))
+    assert np.max(np.abs(_gelu32(t) - g64)) < 2e-6 * max(1.0, np.max(np.abs(g64)))
+
+
+def _gelu32(t):
+    t = t.astype(np.float32)
+    x3 = t * t * t
+    inner = np.float32(0.7978845608028654) * (t + np.float32(0.044715) * x3)
+    return np.float32(0.5) * t * (np.float32(1.0) + np.tanh(inner).astype(np.float32))
+
+
 def test_moe_ffn_single_expert_is_the_swiglu_ffn(orc):
     rng = np.random.default_rng(5)
     dm, dff, rows = 256, 512, 4
