@@ -1266,6 +1266,7 @@ static int moe_impl(ovfq_ctx* ctx, int E, const ovfq_weight* const* gate, const 
     L.expert_off = off;
     L.pair_row = prow;
     L.act = act;
+    L.pairs = (int)P;
     if (grouped_big)
         HIP_TRY(ovfq::launch_mfma_grouped(gt, L, tiles, tile_count, max_tiles, ctx->stream));
     else
@@ -1281,6 +1282,7 @@ static int moe_impl(ovfq_ctx* ctx, int E, const ovfq_weight* const* gate, const 
     D.expert_off = off;
     D.pair_row = nullptr;  // the intermediate is already pair-major
     D.act = ovfq::ActQ{iq, is, ib};
+    D.pairs = (int)P;
     if (grouped_big)
         HIP_TRY(ovfq::launch_mfma_grouped(dt, D, tiles, tile_count, max_tiles, ctx->stream));
     else

@@ -25,6 +25,10 @@
 // keeps the 16 lanes reading one K slice on distinct banks) while the next super-block's weights and activation
 // are in flight. Workgroups are numbered XCD-aware: the workgroups of one weight tile run consecutively on the
 // same XCD (blockIdx % 8), so its bytes come from HBM once and from that XCD's L2 for the other activation tiles.
+#include <algorithm>
+#include <cstdlib>
+#include <type_traits>
+
 #include "kquant_blocks.h"
 #include "ovfq_device.h"
 #include "ovfq_launch.h"
@@ -762,6 +766,222 @@ __global__ __launch_bounds__(256) void kquant_mfma_small_kernel(const SArgs a) {
     }
 }
 
+// ------------------------------------------------------------------------------------------ expert stream
+// Grouped (MoE) Q4_K projections with few pairs per expert, on a persistent grid. A unit of work is (expert e,
+// matrix, 16-row weight tile, 16-pair chunk) and belongs to one wave: wave w of the launch takes units w,
+// w + (waves in the launch), ... (experts without pairs skipped) and walks each unit's super-blocks in ascending
+// order, one per step. A step's 16 weight rows (16 x 144 bytes) come into the wave's LDS ring slot by DMA two steps
+// ahead of use, crossing unit boundaries; its A operands (the chunk's pair rows, gathered from the Q8_K
+// activation) one step ahead in registers. The step runs the super-block's MFMAs and the reference's fp32 tail and
+// adds each block value to the lane's running sums: lane (g, r16) owns outputs (MFMA rows 4g + j, weight row r16),
+// so its sum is the reference's sequential sum over the row, with no exchange between waves. The unit's last step
+// stores biasO + sum.
+constexpr int kStreamDepth = 3;        // ring slots per wave: the weights of kStreamDepth - 1 steps in flight
+constexpr int kStreamSlot = 2304;      // 16 rows x 144 bytes: two 1 KiB DMA instructions and one of 256 bytes
+constexpr int kStreamMaxPairs = 1024;  // the pair -> activation row map is cached in LDS
+
+__global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int n_experts, int nmat, int pairs) {
+    using F = Q4KMfma;
+    // The ring's slots are separate objects, each named by a compile-time index below, so the compiler's wait
+    // insertion sees which DMA a slot read depends on (one array would make every read wait for every DMA).
+    __shared__ __align__(16) uint8_t ring0[4][kStreamSlot];
+    __shared__ __align__(16) uint8_t ring1[4][kStreamSlot];
+    __shared__ __align__(16) uint8_t ring2[4][kStreamSlot];
+    __shared__ int eoff[kMaxExperts + 1];
+    __shared__ int prow[kStreamMaxPairs];
+    const int tid = threadIdx.x, wave = wave_id(), lane = tid & 63;
+    const int g = lane >> 4, r16 = lane & 15;
+    for (int i = tid; i <= n_experts; i += 256) eoff[i] = a.expert_off[i];
+    for (int i = tid; i < pairs; i += 256) prow[i] = a.pair_row ? a.pair_row[i] : i;
+    __syncthreads();
+
+    const int spr = a.spr;
+    const int tiles = a.tiles, per_e = tiles * nmat, T = n_experts * per_e;
+    const int NW = (int)gridDim.x * 4;  // waves in the launch
+    const uint32_t K = (uint32_t)spr * kQK;
+    const uint32_t row_bytes = (uint32_t)spr * kQ4KBytes;
+    // MFMA row n of a chunk carries pair 4 (n % 4) + n / 4 of it: with up to 4 pairs they sit in rows 0, 4, 8,
+    // 12, the first of the four rows each lane's MFMA results cover, so the fp32 tail of the other three is skipped
+    // (8 pairs: two of four, ...). Lane (g, r16)'s result j is row 4g + j, i.e. pair 4j + g.
+    const int my_pair = 4 * (r16 & 3) + (r16 >> 2);  // pair (in the chunk) of A row r16
+
+    // The schedule: step (task t, pair chunk n0, super-block sb). A lead cursor walks it once; each step's fields
+    // are kept in a descriptor from the issue of its weights until it is computed.
+    struct Step {
+        int t, n0, sb;  // t >= T: past the end
+        int pbeg, cnt;  // the task's expert: first pair and pair count
+        int mat, o0;    // matrix (gate / up) and first weight row
+    };
+    // eoff is the same for every lane; reading it through readfirstlane lets the compiler keep every schedule field
+    // in scalar registers (a value it must assume per-lane would turn each buffer access into a waterfall loop).
+    auto eoff_u = [&](int i) { return __builtin_amdgcn_readfirstlane(eoff[i]); };
+    const uint8_t* wp = nullptr;  // the lead step's 16-row weight tile and the bytes to the end of its matrix
+    uint32_t wbytes = 0;
+    auto enter = [&](Step& c) {
+        const int e = c.t / per_e;
+        const int r = c.t - e * per_e;
+        c.mat = r >= tiles ? 1 : 0;
+        c.o0 = (r - c.mat * tiles) * 16;
+        c.pbeg = eoff_u(e);
+        c.cnt = eoff_u(e + 1) - c.pbeg;
+        const uint64_t base = (uint64_t)c.o0 * row_bytes;
+        wp = (c.mat ? a.w1[e] : a.w0[e]) + base;
+        wbytes = rsrc_bytes((uint64_t)a.n_rows * row_bytes, base);
+    };
+    auto seek = [&](Step& c, int t) {  // the first task from t on (stride NW) whose expert has pairs
+        for (; t < T; t += NW) {
+            const int e = t / per_e;
+            if (eoff_u(e + 1) > eoff_u(e)) break;
+        }
+        c.t = t;
+        c.n0 = 0;
+        c.sb = 0;
+        if (t < T) enter(c);
+    };
+    auto advance = [&](Step& c) {
+        if (c.t >= T) return;
+        if (++c.sb < spr) return;
+        c.sb = 0;
+        c.n0 += 16;
+        if (c.n0 < c.cnt) return;
+        seek(c, c.t + NW);
+    };
+
+    // DMA pieces of a step (16 rows x 9 pieces of 16 bytes): instruction i = 0, 1 moves pieces 64 i + lane (16
+    // bytes each), instruction 2 pieces 128 .. 143 as 4-byte words (lane L: word L % 4 of piece 128 + L / 4). The
+    // super-block's offset in the row goes in the scalar offset.
+    uint32_t lane_off[3];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const uint32_t p = 64u * i + (uint32_t)lane;
+        lane_off[i] = (p / 9u) * row_bytes + 16u * (p % 9u);
+    }
+    {
+        const uint32_t p = 128u + (uint32_t)lane / 4u;
+        lane_off[2] = (p / 9u) * row_bytes + 16u * (p % 9u) + 4u * ((uint32_t)lane & 3u);
+    }
+    auto slot = [&](auto j) -> uint8_t* {
+        if constexpr (decltype(j)::value == 0) return ring0[wave];
+        else if constexpr (decltype(j)::value == 1) return ring1[wave];
+        else return ring2[wave];
+    };
+    // The lead step's weights go to ring slot j. Past the end the resource is empty: the DMA still issues (a fixed
+    // instruction count keeps the waits below exact) and writes zeros.
+    auto issue_w = [&](const Step& c, auto j) {
+        // the descriptor from values marked uniform (else the compiler wraps each DMA in a waterfall loop)
+        const uint64_t wpi = (uint64_t)(uintptr_t)wp;
+        const uint64_t wpu = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(wpi >> 32)) << 32) |
+                             (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)wpi);
+        const uint32_t nb = __builtin_amdgcn_readfirstlane(c.t < T ? wbytes : 0u);
+        const __amdgpu_buffer_rsrc_t wr = make_rsrc(reinterpret_cast<const void*>((uintptr_t)wpu), nb);
+        const int soff = c.sb * kQ4KBytes;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (__attribute__((address_space(3))) void*)(slot(j)), 16,
+                                                 (int)lane_off[0], soff, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (__attribute__((address_space(3))) void*)(slot(j) + 1024), 16,
+                                                 (int)lane_off[1], soff, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (__attribute__((address_space(3))) void*)(slot(j) + 2048), 4,
+                                                 (int)lane_off[2], soff, 0, 0);
+    };
+    // A operands of a step: row r16 = pair my_pair of the chunk (an absent pair reads past the resource). The
+    // lane's K piece splits into a lane part (g) and a compile-time part, which goes in the immediate offset.
+    const uint32_t a_lane = 16u * (4u * ((uint32_t)g >> 1) + ((uint32_t)g & 1u));
+    const __amdgpu_buffer_rsrc_t qr = make_rsrc(a.q, (uint32_t)a.act_rows * K);
+    const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.s, (uint32_t)a.act_rows * (uint32_t)spr * 4u);
+    struct AOp {
+        u32x4 av[4];
+        uint32_t sv;
+    };
+    auto load_a = [&](const Step& c, AOp& A) {
+        uint32_t qb = 0x80000000u, sbase = 0x80000000u;
+        if (c.t < T && c.n0 + my_pair < c.cnt) {
+            const uint32_t arow = (uint32_t)prow[c.pbeg + c.n0 + my_pair];
+            qb = arow * K + a_lane;
+            sbase = arow * (uint32_t)spr * 4u;
+        }
+        const uint32_t o = qb + (uint32_t)c.sb * kQK;
+        A.av[0] = __builtin_amdgcn_raw_buffer_load_b128(qr, (int)o, 0, 0);
+        A.av[1] = __builtin_amdgcn_raw_buffer_load_b128(qr, (int)(o + 128u), 0, 0);
+        A.av[2] = __builtin_amdgcn_raw_buffer_load_b128(qr, (int)(o + 32u), 0, 0);
+        A.av[3] = __builtin_amdgcn_raw_buffer_load_b128(qr, (int)(o + 160u), 0, 0);
+        A.sv = ld1(sr, sbase + (uint32_t)c.sb * 4u);
+    };
+
+    Step lead;  // the next step whose weights go out
+    seek(lead, (int)blockIdx.x * 4 + wave);
+    if (lead.t >= T) {
+        // this wave has no unit; the other waves of the workgroup run on independently
+        return;
+    }
+    // Priming issues W(0), A(0), W(1): from then on step q issues A(q + 1) and W(q + 2), and everything younger
+    // than A(q) is W(q + 1), A(q + 1), W(q + 2): eleven instructions.
+    static_assert(kStreamDepth == 3, "three ring slots: the wait count and the unrolled loop below");
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    using S2 = std::integral_constant<int, 2>;
+    Step D0 = lead, D1, D2;
+    issue_w(lead, S0{});
+    advance(lead);
+    AOp A0, A1, A2;
+    load_a(D0, A0);
+    D1 = lead;
+    issue_w(lead, S1{});
+    advance(lead);
+
+    float run[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // sums of outputs (MFMA row 4g + j, weight row r16) so far
+    // Step q computes descriptor cur with ring slot q % 3 and A buffer q % 3, after loading the A operands of the
+    // next descriptor (nxt) and issuing the lead step's weights into the third slot, whose descriptor it records.
+    auto step = [&](const Step& cur, const Step& nxt, Step& rec, const AOp& acur, AOp& anxt, auto rd,
+                    auto wr_slot) -> bool {
+        load_a(nxt, anxt);
+        rec = lead;
+        issue_w(lead, wr_slot);
+        advance(lead);
+        asm volatile("s_waitcnt vmcnt(11)" ::: "memory");  // A(q) and, older, W(q) have landed
+        const uint8_t* rowp = slot(rd) + r16 * kQ4KBytes;
+        F::W w;
+        w.h = *reinterpret_cast<const u32x4*>(rowp);
+        w.q[0] = *reinterpret_cast<const u32x4*>(rowp + 16 + 16 * g);
+        w.q[1] = *reinterpret_cast<const u32x4*>(rowp + 16 + 64 + 16 * g);
+        // MFMAs of the super-block (as lohi_block_values), then the fp32 tail of the rows that hold pairs
+        i32x4 op[4][F::kNumMfma];
+        F::template operands<0>(w, g, op[0]);
+        F::template operands<1>(w, g, op[1]);
+        F::template operands<2>(w, g, op[2]);
+        F::template operands<3>(w, g, op[3]);
+        i32x4 acc[F::kNumMfma];
+#pragma unroll
+        for (int k = 0; k < F::kNumMfma; k++) acc[k] = i32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const i32x4 aop = i32x4{(int)acur.av[t].x, (int)acur.av[t].y, (int)acur.av[t].z, (int)acur.av[t].w};
+#pragma unroll
+            for (int k = 0; k < F::kNumMfma; k++) acc[k] = mfma16(aop, op[t][k], acc[k]);
+        }
+        const float d = F::d_of(w), dmin = F::dmin_of(w);
+        const int live = min(4, (cur.cnt - cur.n0 + 3) >> 2);  // results j < live hold pairs
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (j < live) run[j] += F::tail(acc, j, d, dmin, as_float(__shfl(acur.sv, 4 * g + j, 64)));
+        if (cur.sb == spr - 1) {
+            const int o = cur.o0 + r16;
+            const float* bias = cur.mat ? a.bias1 : a.bias0;
+            float* y = cur.mat ? a.y1 : a.y0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int pr = cur.n0 + 4 * j + g;
+                if (j < live && pr < cur.cnt && o < a.n_rows)
+                    y[(size_t)(cur.pbeg + pr) * a.n_rows + o] = bias ? bias[o] + run[j] : run[j];
+                run[j] = 0.0f;
+            }
+        }
+        return nxt.t < T;
+    };
+    while (step(D0, D1, D2, A0, A1, S0{}, S2{}) && step(D1, D2, D0, A1, A2, S1{}, S0{}) &&
+           step(D2, D0, D1, A2, A0, S2{}, S1{})) {
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the ring's last DMAs land before the wave ends
+}
+
 template <class F, int kBatch>
 static hipError_t launch_small(SArgs& sa, int nmat, int experts, hipStream_t st) {
     sa.tiles = (sa.n_rows + 15) / 16;
@@ -801,6 +1021,24 @@ hipError_t launch_mfma_small(int type, const GroupLaunch& L, hipStream_t st) {
     sa.q = L.act.q;
     sa.s = L.act.s;
     const int nmat = L.w1 ? 2 : 1;
+    static const int stream = [] {
+        const char* v = getenv("OVFQ_MOE_STREAM");
+        return v && *v ? atoi(v) : 1;
+    }();
+    if (stream && type == 12 && L.expert_off && L.pairs > 0 && L.pairs <= kStreamMaxPairs) {
+        sa.tiles = (sa.n_rows + 15) / 16;
+        const long units = (long)L.experts * nmat * sa.tiles;
+        int dev = 0, cus = 256;
+        if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        // workgroups per CU (measured on MI355X, config-5 MoE step: 3 / 4 / 5 / 6 -> 212 / 212 / 207 / 217 us)
+        static const int per_cu = [] {
+            const char* v = getenv("OVFQ_MOE_STREAM_WG");
+            return v && *v ? atoi(v) : 5;
+        }();
+        const int grid = (int)std::min<long>((units + 3) / 4, (long)cus * per_cu);
+        hipLaunchKernelGGL(q4k_mfma_stream_kernel, dim3(grid), dim3(256), 0, st, sa, L.experts, nmat, L.pairs);
+        return hipGetLastError();
+    }
     // super-blocks per wave batch (measured on MI355X: 2 beats 4 for every Llama/Mixtral shape)
     static const int forced = [] {
         const char* v = getenv("OVFQ_SMALL_BATCH");

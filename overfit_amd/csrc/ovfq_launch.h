@@ -72,6 +72,7 @@ struct GroupLaunch {
     const int* expert_off;
     const int* pair_row;
     ActQ act;
+    int pairs = 0;  // grouped launches: the pair count bound (rows x top_k), sizing the pair -> row map
 };
 // On MFMA with super-block-parallel waves (mfma.hip), 16 activation rows per tile.
 bool mfma_small_supported(int type, int in);
