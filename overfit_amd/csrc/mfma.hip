@@ -791,7 +791,8 @@ __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int
     __shared__ int prow[kStreamMaxPairs];
     const int tid = threadIdx.x, wave = wave_id(), lane = tid & 63;
     const int g = lane >> 4, r16 = lane & 15;
-    for (int i = tid; i <= n_experts; i += 256) eoff[i] = a.expert_off[i];
+    // without a pair list: one expert over activation rows 0 .. rows - 1 (a dense small batch)
+    for (int i = tid; i <= n_experts; i += 256) eoff[i] = a.expert_off ? a.expert_off[i] : (i == 0 ? 0 : a.rows);
     for (int i = tid; i < pairs; i += 256) prow[i] = a.pair_row ? a.pair_row[i] : i;
     __syncthreads();
 
@@ -1025,7 +1026,16 @@ hipError_t launch_mfma_small(int type, const GroupLaunch& L, hipStream_t st) {
         const char* v = getenv("OVFQ_MOE_STREAM");
         return v && *v ? atoi(v) : 1;
     }();
-    if (stream && type == 12 && L.expert_off && L.pairs > 0 && L.pairs <= kStreamMaxPairs) {
+    // A dense small batch takes the stream kernel only with many 16-row tiles: one wave per tile leaves most of
+    // the chip idle below that (MI355X, us, stream / super-block-parallel kernel: 14336x4096 at 16 rows 18.9 / 20.2,
+    // 32 rows 29.9 / 34.8; 4096x4096 at 16 rows 17.9 / 9.4; 4096x14336 at 16 rows 44.7 / 19.0).
+    static const int stream_dense_tiles = [] {
+        const char* v = getenv("OVFQ_SMALL_STREAM_MIN_TILES");
+        return v && *v ? atoi(v) : 768;
+    }();
+    const int pairs = L.expert_off ? L.pairs : L.rows;
+    const bool dense_ok = (long)nmat * ((sa.n_rows + 15) / 16) >= stream_dense_tiles;
+    if (stream && type == 12 && (L.expert_off || dense_ok) && pairs > 0 && pairs <= kStreamMaxPairs) {
         sa.tiles = (sa.n_rows + 15) / 16;
         const long units = (long)L.experts * nmat * sa.tiles;
         int dev = 0, cus = 256;
@@ -1036,7 +1046,7 @@ hipError_t launch_mfma_small(int type, const GroupLaunch& L, hipStream_t st) {
             return v && *v ? atoi(v) : 5;
         }();
         const int grid = (int)std::min<long>((units + 3) / 4, (long)cus * per_cu);
-        hipLaunchKernelGGL(q4k_mfma_stream_kernel, dim3(grid), dim3(256), 0, st, sa, L.experts, nmat, L.pairs);
+        hipLaunchKernelGGL(q4k_mfma_stream_kernel, dim3(grid), dim3(256), 0, st, sa, L.experts, nmat, pairs);
         return hipGetLastError();
     }
     // super-blocks per wave batch (measured on MI355X: 2 beats 4 for every Llama/Mixtral shape)

@@ -476,6 +476,61 @@ def test_small_batch_bit_exact(orc, fmt, rows, k, n):
     assert_bit_exact(y.cpu().numpy().reshape(rows, n), ref, f"{fmt} small batch {rows}x{k}x{n}")
 
 
+# Tall Q4_K matrices (768 16-row tiles or more) on the small-M path run on the expert-stream kernel: one wave per
+# 16-row tile walking every super-block in order, weights by LDS DMA. Shapes: 1, 9 and 16 rows (one pair chunk), 37
+# rows (three chunks, the last partial), a row count past the last full tile, gate/up pairs, a bias.
+STREAM_SHAPES = [(1, 256, 12288), (9, 512, 12290), (16, 256, 13000), (37, 256, 12300), (5, 768, 12304)]
+
+
+@pytest.mark.parametrize("rows,k,n", STREAM_SHAPES)
+def test_stream_kernel_dense_bit_exact(orc, batched, rows, k, n):
+    case("stream dense", rows, k, n)
+    batched("small")
+    rng = np.random.default_rng(rows * 13 + n)
+    blocks = _kq_blocks(rng, "q4k", n, k)
+    x = normal(rng, (rows, k))
+    bias = normal(rng, n)
+    w = ov.Q4KWeight(blocks, k, n)
+    y = ov.project(w, t(x), t(bias), rows=rows)
+    torch.cuda.synchronize()
+    assert_bit_exact(y.cpu().numpy().reshape(rows, n), orc.q4k_project_batched(x, rows, blocks, k, n, bias),
+                     f"stream {rows}x{k}x{n}")
+    if rows > 1:
+        # gate/up: two matrices in one launch (the units of both interleave on the persistent grid)
+        b2 = _kq_blocks(rng, "q4k", n, k)
+        w2 = ov.Q4KWeight(b2, k, n)
+        g = torch.empty(rows * n, device=DEV)
+        u = torch.empty(rows * n, device=DEV)
+        ov.default_context().project_multi_dev([w, w2], t(x), [g, u], rows=rows)
+        torch.cuda.synchronize()
+        assert_bit_exact(g.cpu().numpy().reshape(rows, n), orc.q4k_project_batched(x, rows, blocks, k, n, None),
+                         "stream gate")
+        assert_bit_exact(u.cpu().numpy().reshape(rows, n), orc.q4k_project_batched(x, rows, b2, k, n, None),
+                         "stream up")
+
+
+def test_moe_ffn_skewed_routing(orc):
+    """Few pairs in all (the expert-stream kernel) but one expert with 21 of them (two 16-pair chunks of its units),
+    one with a single pair, one with none: against the oracle at the FFN tolerance."""
+    case("moe skewed")
+    rng = np.random.default_rng(515)
+    E, dm, dff, rows, k = 8, 512, 768, 30, 1
+    gb = [orc.quantize_q4k(normal(rng, (dff, dm), 0.05)) for _ in range(E)]
+    ub = [orc.quantize_q4k(normal(rng, (dff, dm), 0.05)) for _ in range(E)]
+    db = [orc.quantize_q4k(normal(rng, (dm, dff), 0.05)) for _ in range(E)]
+    gw = [ov.Q4KWeight(b, dm, dff) for b in gb]
+    uw = [ov.Q4KWeight(b, dm, dff) for b in ub]
+    dw = [ov.Q4KWeight(b, dff, dm) for b in db]
+    x = normal(rng, (rows, dm))
+    idx = np.array([5] * 21 + [1] + [0, 2, 3, 4, 6, 0, 2, 3], np.int32).reshape(rows, k)  # expert 7: no pair
+    rng.shuffle(idx)
+    w = rng.random((rows, k)).astype(np.float32)
+    ref = orc.moe_ffn_batched(gb, ub, db, ov.TYPE_Q4_K, ov.TYPE_Q4_K, x, rows, dm, dff, k, idx, w)
+    y = ov.moe_ffn(gw, uw, dw, t(x), rows, k, t(idx), t(w))
+    torch.cuda.synchronize()
+    _moe_check(y.cpu().numpy(), ref, "skewed routing")
+
+
 # ------------------------------------------------------------------------------------------------ routed MoE
 
 @pytest.mark.parametrize("normalize", [True, False])
