@@ -234,9 +234,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--copies", type=int, default=4, help="layer copies rotated to defeat the 256 MB cache")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--profile", choices=["layer", "prefill", "moe", "small", "q8", "heads"], default=None,
+    ap.add_argument("--profile", choices=["layer", "prefill", "moe", "small", "q8", "heads", "config1"], default=None,
                     help="for rocprof runs: only the timed decode-layer loop, the config-3 prefill line, the "
-                         "config-5 MoE line, the small-batch layer line, the Q8_0 line or the per-head Q8_0 Wo line")
+                         "config-5 MoE line, the small-batch layer line, the Q8_0 line, the per-head Q8_0 Wo line "
+                         "or the config-1 Q4_K 4096x4096 GEMV line")
     ap.add_argument("--pmc", action="store_true",
                     help="for rocprofv3 --pmc runs: 16 gate/up launches, then 16 plain 64 MiB device copies "
                          "(the counter calibration reference)")
@@ -625,9 +626,11 @@ def main():
                 "us": round(us, 2), "weight_bytes": wb, "GB_s": round(wb / (us * 1e-6) / 1e9, 1),
                 "timing": "HIP graph replay over %d layer copies x 4" % len(copies)}
 
-    if args.profile in ("prefill", "moe", "small", "q8", "heads"):
+    if args.profile in ("prefill", "moe", "small", "q8", "heads", "config1"):
         only = {"prefill": prefill_line, "moe": moe_line, "small": small_batch_line, "q8": q8_line,
-                "heads": heads_line}[args.profile]
+                "heads": heads_line,
+                "config1": lambda: gemv_line(4096, 4096, "q4k", 64,
+                                             "benchmark config 1: Q4_K 4096x4096 GEMV (quantise in-launch)")}[args.profile]
         print(json.dumps(only()), flush=True)
         return
 
