@@ -26,12 +26,16 @@ FLAGS = [
     "-Wno-unused-function",
 ]
 
+# Per-file additions. The MFMA kernels accumulate in VGPRs instead of AGPRs: with AGPR accumulators the expert-stream
+# and small-M kernels copy every result out (v_accvgpr_read, 12 per super-block step) before the fp32 tail.
+FILE_FLAGS = {"mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"]}
+
 
 def build(verbose: bool = False) -> str:
     objs = []
     for src in SOURCES:
         obj = os.path.join(CSRC, src + ".o")
-        cmd = [HIPCC, *FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+        cmd = [HIPCC, *FLAGS, *FILE_FLAGS.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
         if verbose:
             print(" ".join(cmd), flush=True)
         subprocess.run(cmd, check=True)
