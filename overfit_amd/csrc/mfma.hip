@@ -28,6 +28,7 @@
 #include <algorithm>
 #include <cstdlib>
 #include <type_traits>
+#include <utility>
 
 #include "kquant_blocks.h"
 #include "ovfq_device.h"
@@ -770,23 +771,40 @@ __global__ __launch_bounds__(256) void kquant_mfma_small_kernel(const SArgs a) {
 // Grouped (MoE) Q4_K projections with few pairs per expert, on a persistent grid. A unit of work is (expert e,
 // matrix, 16-row weight tile, 16-pair chunk) and belongs to one wave: wave w of the launch takes units w,
 // w + (waves in the launch), ... (experts without pairs skipped) and walks each unit's super-blocks in ascending
-// order, one per step. A step's 16 weight rows (16 x 144 bytes) come into the wave's LDS ring slot by DMA two steps
-// ahead of use, crossing unit boundaries; its A operands (the chunk's pair rows, gathered from the Q8_K
-// activation) one step ahead in registers. The step runs the super-block's MFMAs and the reference's fp32 tail and
+// order, one per step. A step's 16 weight rows (16 x 144 bytes) and its activation scales come into the wave's LDS
+// ring slot by DMA, and its A operands (the chunk's pair rows, gathered from the Q8_K activation) into registers,
+// all issued two steps ahead of use and crossing unit boundaries. The step runs the super-block's MFMAs and the
+// reference's fp32 tail and
 // adds each block value to the lane's running sums: lane (g, r16) owns outputs (MFMA rows 4g + j, weight row r16),
 // so its sum is the reference's sequential sum over the row, with no exchange between waves. The unit's last step
 // stores biasO + sum.
-constexpr int kStreamDepth = 3;        // ring slots per wave: the weights of kStreamDepth - 1 steps in flight
-constexpr int kStreamSlot = 2304;      // 16 rows x 144 bytes: two 1 KiB DMA instructions and one of 256 bytes
+constexpr int kStreamW = 2304;         // a step's weights: 16 rows x 144 bytes, two 1 KiB DMAs and one of 256 bytes
+constexpr int kStreamSlot = kStreamW + 256;  // + the lanes' activation scales, one 4-byte DMA
 constexpr int kStreamMaxPairs = 1024;  // the pair -> activation row map is cached in LDS
 
+// Lane j of each row of 16 lanes, broadcast across the row (DPP row_newbcast: a VALU move, no LDS access).
+template <int J>
+__device__ __forceinline__ uint32_t row_bcast(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x150 + J, 0xf, 0xf, false);
+}
+
+// Calls f(slot 0), f(slot 1), ..., f(slot n - 1), f(slot 0), ... with each slot a compile-time constant, until one
+// call returns false.
+template <typename Fn, int... I>
+__device__ __forceinline__ void run_slots(Fn& f, std::integer_sequence<int, I...>) {
+    while ((f(std::integral_constant<int, I>{}) && ...)) {
+    }
+}
+
+// D = pipeline depth: D ring slots and D A-operand buffers per wave; step q's weights and A operands are issued
+// D - 1 steps before step q computes. Both share one slot index (q mod D), so every slot and buffer is named at
+// compile time in a loop unrolled D times.
+template <int D>
 __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int n_experts, int nmat, int pairs) {
+    static_assert(D >= 2 && 8 * (D - 1) <= 63, "the wait count below must fit the 6-bit vmcnt field");
     using F = Q4KMfma;
-    // The ring's slots are separate objects, each named by a compile-time index below, so the compiler's wait
-    // insertion sees which DMA a slot read depends on (one array would make every read wait for every DMA).
-    __shared__ __align__(16) uint8_t ring0[4][kStreamSlot];
-    __shared__ __align__(16) uint8_t ring1[4][kStreamSlot];
-    __shared__ __align__(16) uint8_t ring2[4][kStreamSlot];
+    // The ring is read with explicit LDS instructions after an explicit wait (below), so one array serves every slot.
+    __shared__ __align__(16) uint8_t ring[D][4][kStreamSlot];
     __shared__ int eoff[kMaxExperts + 1];
     __shared__ int prow[kStreamMaxPairs];
     const int tid = threadIdx.x, wave = wave_id(), lane = tid & 63;
@@ -815,7 +833,14 @@ __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int
     };
     // eoff is the same for every lane; reading it through readfirstlane lets the compiler keep every schedule field
     // in scalar registers (a value it must assume per-lane would turn each buffer access into a waterfall loop).
-    auto eoff_u = [&](int i) { return __builtin_amdgcn_readfirstlane(eoff[i]); };
+    // The read is an explicit instruction: the compiler's own LDS read would first wait for the ring's DMAs in
+    // flight (it cannot tell that they write other LDS), draining the pipeline at every unit change.
+    auto eoff_u = [&](int i) {
+        const uint32_t addr = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int*)(eoff + i);
+        int v;
+        asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr) : "memory");
+        return __builtin_amdgcn_readfirstlane(v);
+    };
     const uint8_t* wp = nullptr;  // the lead step's 16-row weight tile and the bytes to the end of its matrix
     uint32_t wbytes = 0;
     auto enter = [&](Step& c) {
@@ -861,14 +886,9 @@ __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int
         const uint32_t p = 128u + (uint32_t)lane / 4u;
         lane_off[2] = (p / 9u) * row_bytes + 16u * (p % 9u) + 4u * ((uint32_t)lane & 3u);
     }
-    auto slot = [&](auto j) -> uint8_t* {
-        if constexpr (decltype(j)::value == 0) return ring0[wave];
-        else if constexpr (decltype(j)::value == 1) return ring1[wave];
-        else return ring2[wave];
-    };
     // The lead step's weights go to ring slot j. Past the end the resource is empty: the DMA still issues (a fixed
     // instruction count keeps the waits below exact) and writes zeros.
-    auto issue_w = [&](const Step& c, auto j) {
+    auto issue_w = [&](const Step& c, int j) {
         // the descriptor from values marked uniform (else the compiler wraps each DMA in a waterfall loop)
         const uint64_t wpi = (uint64_t)(uintptr_t)wp;
         const uint64_t wpu = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(wpi >> 32)) << 32) |
@@ -876,35 +896,37 @@ __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int
         const uint32_t nb = __builtin_amdgcn_readfirstlane(c.t < T ? wbytes : 0u);
         const __amdgpu_buffer_rsrc_t wr = make_rsrc(reinterpret_cast<const void*>((uintptr_t)wpu), nb);
         const int soff = c.sb * kQ4KBytes;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (__attribute__((address_space(3))) void*)(slot(j)), 16,
+        uint8_t* sl = ring[j][wave];
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (__attribute__((address_space(3))) void*)sl, 16,
                                                  (int)lane_off[0], soff, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (__attribute__((address_space(3))) void*)(slot(j) + 1024), 16,
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (__attribute__((address_space(3))) void*)(sl + 1024), 16,
                                                  (int)lane_off[1], soff, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (__attribute__((address_space(3))) void*)(slot(j) + 2048), 4,
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (__attribute__((address_space(3))) void*)(sl + 2048), 4,
                                                  (int)lane_off[2], soff, 0, 0);
     };
     // A operands of a step: row r16 = pair my_pair of the chunk (an absent pair reads past the resource). The
     // lane's K piece splits into a lane part (g) and a compile-time part, which goes in the immediate offset.
+    // The lane's activation scale, that of pair 4 (r16 % 4) + g, goes to the ring slot by DMA (a scale in a
+    // register drew waits from the compiler that drained the pipeline); lane j of row g then holds the scale of
+    // result j (pair 4j + g), which the tail broadcasts across the row.
     const uint32_t a_lane = 16u * (4u * ((uint32_t)g >> 1) + ((uint32_t)g & 1u));
+    const int s_pair = 4 * (r16 & 3) + g;
     const __amdgpu_buffer_rsrc_t qr = make_rsrc(a.q, (uint32_t)a.act_rows * K);
     const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.s, (uint32_t)a.act_rows * (uint32_t)spr * 4u);
     struct AOp {
         u32x4 av[4];
-        uint32_t sv;
     };
-    auto load_a = [&](const Step& c, AOp& A) {
+    auto load_a = [&](const Step& c, AOp& A, int j) {
         uint32_t qb = 0x80000000u, sbase = 0x80000000u;
-        if (c.t < T && c.n0 + my_pair < c.cnt) {
-            const uint32_t arow = (uint32_t)prow[c.pbeg + c.n0 + my_pair];
-            qb = arow * K + a_lane;
-            sbase = arow * (uint32_t)spr * 4u;
-        }
+        if (c.t < T && c.n0 + my_pair < c.cnt) qb = (uint32_t)prow[c.pbeg + c.n0 + my_pair] * K + a_lane;
+        if (c.t < T && c.n0 + s_pair < c.cnt) sbase = (uint32_t)prow[c.pbeg + c.n0 + s_pair] * (uint32_t)spr * 4u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (__attribute__((address_space(3))) void*)(ring[j][wave] + kStreamW),
+                                                 4, (int)(sbase + (uint32_t)c.sb * 4u), 0, 0, 0);
         const uint32_t o = qb + (uint32_t)c.sb * kQK;
         A.av[0] = __builtin_amdgcn_raw_buffer_load_b128(qr, (int)o, 0, 0);
         A.av[1] = __builtin_amdgcn_raw_buffer_load_b128(qr, (int)(o + 128u), 0, 0);
         A.av[2] = __builtin_amdgcn_raw_buffer_load_b128(qr, (int)(o + 32u), 0, 0);
         A.av[3] = __builtin_amdgcn_raw_buffer_load_b128(qr, (int)(o + 160u), 0, 0);
-        A.sv = ld1(sr, sbase + (uint32_t)c.sb * 4u);
     };
 
     Step lead;  // the next step whose weights go out
@@ -913,42 +935,57 @@ __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int
         // this wave has no unit; the other waves of the workgroup run on independently
         return;
     }
-    // Priming issues W(0), A(0), W(1): from then on step q issues A(q + 1) and W(q + 2), and everything younger
-    // than A(q) is W(q + 1), A(q + 1), W(q + 2): eleven instructions.
-    static_assert(kStreamDepth == 3, "three ring slots: the wait count and the unrolled loop below");
-    using S0 = std::integral_constant<int, 0>;
-    using S1 = std::integral_constant<int, 1>;
-    using S2 = std::integral_constant<int, 2>;
-    Step D0 = lead, D1, D2;
-    issue_w(lead, S0{});
-    advance(lead);
-    AOp A0, A1, A2;
-    load_a(D0, A0);
-    D1 = lead;
-    issue_w(lead, S1{});
-    advance(lead);
+    // Issue order: the weights of a step (three DMA instructions), then its A operands (five loads); the first
+    // D - 1 steps are issued here, each later step q issues step q + D - 1 into the slot step q - 1 freed.
+    Step desc[D];
+    AOp A[D];
+#pragma unroll
+    for (int i = 0; i < D; i++) {
+        desc[i] = lead;  // defined from the start (an undefined scalar descriptor costs the compiler a wait)
+        A[i] = AOp{};
+    }
+#pragma unroll
+    for (int i = 0; i < D - 1; i++) {
+        desc[i] = lead;
+        issue_w(lead, i);
+        advance(lead);
+        load_a(desc[i], A[i], i);
+    }
 
     float run[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // sums of outputs (MFMA row 4g + j, weight row r16) so far
-    // Step q computes descriptor cur with ring slot q % 3 and A buffer q % 3, after loading the A operands of the
-    // next descriptor (nxt) and issuing the lead step's weights into the third slot, whose descriptor it records.
-    auto step = [&](const Step& cur, const Step& nxt, Step& rec, const AOp& acur, AOp& anxt, auto rd,
-                    auto wr_slot) -> bool {
-        load_a(nxt, anxt);
-        rec = lead;
-        issue_w(lead, wr_slot);
+    auto step = [&](auto sc) -> bool {
+        constexpr int s = decltype(sc)::value;         // this step's slot
+        constexpr int w = (s + D - 1) % D;             // the slot of the step issued now (freed by the last step)
+        const Step& cur = desc[s];
+        desc[w] = lead;
+        issue_w(lead, w);
         advance(lead);
-        asm volatile("s_waitcnt vmcnt(11)" ::: "memory");  // A(q) and, older, W(q) have landed
-        const uint8_t* rowp = slot(rd) + r16 * kQ4KBytes;
-        F::W w;
-        w.h = *reinterpret_cast<const u32x4*>(rowp);
-        w.q[0] = *reinterpret_cast<const u32x4*>(rowp + 16 + 16 * g);
-        w.q[1] = *reinterpret_cast<const u32x4*>(rowp + 16 + 64 + 16 * g);
+        load_a(desc[w], A[w], w);
+        // Step q's eight instructions (three weight DMAs, the scale DMA, four A loads) have landed: everything
+        // younger is the D - 1 later steps' eight each (a unit's output stores only add younger ones).
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(8 * (D - 1)) : "memory");
+        // The weights from the ring slot, read with explicit instructions after that wait.
+        const uint32_t rowa = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)(ring[s][wave]) +
+                              (uint32_t)r16 * kQ4KBytes;
+        const uint32_t sva = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)(ring[s][wave]) +
+                             (uint32_t)kStreamW + 4u * (uint32_t)lane;
+        F::W wv;
+        uint32_t sv;
+        asm volatile("ds_read_b128 %0, %4\n\t"
+                     "ds_read_b128 %1, %5 offset:16\n\t"
+                     "ds_read_b128 %2, %5 offset:80\n\t"
+                     "ds_read_b32 %3, %6\n\t"
+                     "s_waitcnt lgkmcnt(0)"
+                     : "=v"(wv.h), "=v"(wv.q[0]), "=v"(wv.q[1]), "=v"(sv)
+                     : "v"(rowa), "v"(rowa + 16u * (uint32_t)g), "v"(sva)
+                     : "memory");
+        const AOp& acur = A[s];
         // MFMAs of the super-block (as lohi_block_values), then the fp32 tail of the rows that hold pairs
         i32x4 op[4][F::kNumMfma];
-        F::template operands<0>(w, g, op[0]);
-        F::template operands<1>(w, g, op[1]);
-        F::template operands<2>(w, g, op[2]);
-        F::template operands<3>(w, g, op[3]);
+        F::template operands<0>(wv, g, op[0]);
+        F::template operands<1>(wv, g, op[1]);
+        F::template operands<2>(wv, g, op[2]);
+        F::template operands<3>(wv, g, op[3]);
         i32x4 acc[F::kNumMfma];
 #pragma unroll
         for (int k = 0; k < F::kNumMfma; k++) acc[k] = i32x4{0, 0, 0, 0};
@@ -958,11 +995,16 @@ __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int
 #pragma unroll
             for (int k = 0; k < F::kNumMfma; k++) acc[k] = mfma16(aop, op[t][k], acc[k]);
         }
-        const float d = F::d_of(w), dmin = F::dmin_of(w);
+        const float d = F::d_of(wv), dmin = F::dmin_of(wv);
         const int live = min(4, (cur.cnt - cur.n0 + 3) >> 2);  // results j < live hold pairs
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-            if (j < live) run[j] += F::tail(acc, j, d, dmin, as_float(__shfl(acur.sv, 4 * g + j, 64)));
+        auto tail = [&](auto jc) {
+            constexpr int j = decltype(jc)::value;
+            if (j < live) run[j] += F::tail(acc, j, d, dmin, as_float(row_bcast<j>(sv)));
+        };
+        tail(std::integral_constant<int, 0>{});
+        tail(std::integral_constant<int, 1>{});
+        tail(std::integral_constant<int, 2>{});
+        tail(std::integral_constant<int, 3>{});
         if (cur.sb == spr - 1) {
             const int o = cur.o0 + r16;
             const float* bias = cur.mat ? a.bias1 : a.bias0;
@@ -975,11 +1017,9 @@ __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int
                 run[j] = 0.0f;
             }
         }
-        return nxt.t < T;
+        return desc[(s + 1) % D].t < T;
     };
-    while (step(D0, D1, D2, A0, A1, S0{}, S2{}) && step(D1, D2, D0, A1, A2, S1{}, S0{}) &&
-           step(D2, D0, D1, A2, A0, S2{}, S1{})) {
-    }
+    run_slots(step, std::make_integer_sequence<int, D>{});
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the ring's last DMAs land before the wave ends
 }
 
@@ -1040,13 +1080,15 @@ hipError_t launch_mfma_small(int type, const GroupLaunch& L, hipStream_t st) {
         const long units = (long)L.experts * nmat * sa.tiles;
         int dev = 0, cus = 256;
         if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-        // workgroups per CU (measured on MI355X, config-5 MoE step: 3 / 4 / 5 / 6 -> 212 / 212 / 207 / 217 us)
+        // workgroups per CU (measured on MI355X, config-5 MoE step under the profiler: 4 / 5 -> 219 / 216 us)
         static const int per_cu = [] {
             const char* v = getenv("OVFQ_MOE_STREAM_WG");
             return v && *v ? atoi(v) : 5;
         }();
         const int grid = (int)std::min<long>((units + 3) / 4, (long)cus * per_cu);
-        hipLaunchKernelGGL(q4k_mfma_stream_kernel, dim3(grid), dim3(256), 0, st, sa, L.experts, nmat, pairs);
+        // Depth 3: measured equal to 4, 5 and 6 (each at the workgroups per CU its LDS and registers allow), so the
+        // smallest ring keeps the most workgroups resident.
+        hipLaunchKernelGGL(q4k_mfma_stream_kernel<3>, dim3(grid), dim3(256), 0, st, sa, L.experts, nmat, pairs);
         return hipGetLastError();
     }
     // super-blocks per wave batch (measured on MI355X: 2 beats 4 for every Llama/Mixtral shape)
