@@ -769,24 +769,20 @@ __global__ __launch_bounds__(256) void kquant_mfma_small_kernel(const SArgs a) {
 
 // ------------------------------------------------------------------------------------------ expert stream
 // Grouped (MoE) Q4_K projections with few pairs per expert, on a persistent grid. A unit of work is (expert e,
-// matrix, 16-row weight tile, 16-pair chunk) and belongs to one wave: wave w of the launch takes units w,
-// w + (waves in the launch), ... (experts without pairs skipped) and walks each unit's super-blocks in ascending
-// order, one per step. A step's 16 weight rows (16 x 144 bytes) and its activation scales come into the wave's LDS
-// ring slot by DMA, and its A operands (the chunk's pair rows, gathered from the Q8_K activation) into registers,
-// all issued two steps ahead of use and crossing unit boundaries. The step runs the super-block's MFMAs and the
-// reference's fp32 tail and
-// adds each block value to the lane's running sums: lane (g, r16) owns outputs (MFMA rows 4g + j, weight row r16),
-// so its sum is the reference's sequential sum over the row, with no exchange between waves. The unit's last step
-// stores biasO + sum.
-constexpr int kStreamW = 2304;         // a step's weights: 16 rows x 144 bytes, two 1 KiB DMAs and one of 256 bytes
-constexpr int kStreamSlot = kStreamW + 256;  // + the lanes' activation scales, one 4-byte DMA
+// matrix, 64-row weight group, 16-pair chunk) and belongs to one workgroup: workgroup b takes units b, b + (workgroups
+// in the launch), ... (experts without pairs skipped) and walks each unit's super-blocks in ascending order, one per
+// step, its four waves in step (wave w owns weight rows 16w .. 16w + 15 of the group). Per step each wave brings its
+// 16 weight rows (16 x 144 bytes) into its own LDS ring slot by DMA, and a quarter of the chunk's A operands (4 pairs
+// x 256 activation bytes) and scales into the workgroup's shared slot, so the four waves read the activation once
+// between them; all of it is issued two steps ahead of use and crosses unit boundaries. The step runs the
+// super-block's MFMAs and the reference's fp32 tail and adds each block value to the lane's running sums: lane
+// (g, r16) owns outputs (MFMA rows 4g + j, weight row r16), so its sum is the reference's sequential sum over the
+// row, with no exchange between waves. The unit's last step stores biasO + sum.
+constexpr int kStreamW = 2304;         // a wave's weights per step: 16 rows x 144 bytes, two 1 KiB DMAs and one of 256
+constexpr int kStreamA = 4096;         // the chunk's A operands per step: 16 pairs x 256 bytes, 1 KiB DMA per wave
+constexpr int kStreamS = 1024;         // the chunk's activation scales: 256 bytes per wave (4 used)
 constexpr int kStreamMaxPairs = 1024;  // the pair -> activation row map is cached in LDS
-
-// Lane j of each row of 16 lanes, broadcast across the row (DPP row_newbcast: a VALU move, no LDS access).
-template <int J>
-__device__ __forceinline__ uint32_t row_bcast(uint32_t v) {
-    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x150 + J, 0xf, 0xf, false);
-}
+constexpr int kStreamRows = 64;        // weight rows per unit (16 per wave)
 
 // Calls f(slot 0), f(slot 1), ..., f(slot n - 1), f(slot 0), ... with each slot a compile-time constant, until one
 // call returns false.
@@ -796,15 +792,15 @@ __device__ __forceinline__ void run_slots(Fn& f, std::integer_sequence<int, I...
     }
 }
 
-// D = pipeline depth: D ring slots and D A-operand buffers per wave; step q's weights and A operands are issued
-// D - 1 steps before step q computes. Both share one slot index (q mod D), so every slot and buffer is named at
-// compile time in a loop unrolled D times.
+// D = ring slots: steps q + 1 .. q + D - 1 are in flight while step q is computed.
 template <int D>
 __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int n_experts, int nmat, int pairs) {
-    static_assert(D >= 2 && 8 * (D - 1) <= 63, "the wait count below must fit the 6-bit vmcnt field");
+    static_assert(D >= 3 && 5 * (D - 2) + 3 <= 63, "the wait count below must fit the 6-bit vmcnt field");
     using F = Q4KMfma;
-    // The ring is read with explicit LDS instructions after an explicit wait (below), so one array serves every slot.
-    __shared__ __align__(16) uint8_t ring[D][4][kStreamSlot];
+    // The rings are read with explicit LDS instructions after explicit waits (below), so one array serves each.
+    __shared__ __align__(16) uint8_t wring[D][4][kStreamW];
+    __shared__ __align__(16) uint8_t aring[D][kStreamA];
+    __shared__ __align__(16) uint8_t sring[D][kStreamS];
     __shared__ int eoff[kMaxExperts + 1];
     __shared__ int prow[kStreamMaxPairs];
     const int tid = threadIdx.x, wave = wave_id(), lane = tid & 63;
@@ -815,21 +811,18 @@ __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int
     __syncthreads();
 
     const int spr = a.spr;
-    const int tiles = a.tiles, per_e = tiles * nmat, T = n_experts * per_e;
-    const int NW = (int)gridDim.x * 4;  // waves in the launch
+    const int groups = a.tiles, per_e = groups * nmat, T = n_experts * per_e;
+    const int NG = (int)gridDim.x;  // workgroups in the launch
     const uint32_t K = (uint32_t)spr * kQK;
     const uint32_t row_bytes = (uint32_t)spr * kQ4KBytes;
-    // MFMA row n of a chunk carries pair 4 (n % 4) + n / 4 of it: with up to 4 pairs they sit in rows 0, 4, 8,
-    // 12, the first of the four rows each lane's MFMA results cover, so the fp32 tail of the other three is skipped
-    // (8 pairs: two of four, ...). Lane (g, r16)'s result j is row 4g + j, i.e. pair 4j + g.
-    const int my_pair = 4 * (r16 & 3) + (r16 >> 2);  // pair (in the chunk) of A row r16
 
-    // The schedule: step (task t, pair chunk n0, super-block sb). A lead cursor walks it once; each step's fields
-    // are kept in a descriptor from the issue of its weights until it is computed.
+    // The schedule: step (unit t, pair chunk n0, super-block sb), the same in every wave of the workgroup. A lead
+    // cursor walks it once; each step's fields are kept in a descriptor from the issue of its loads until it is
+    // computed.
     struct Step {
         int t, n0, sb;  // t >= T: past the end
-        int pbeg, cnt;  // the task's expert: first pair and pair count
-        int mat, o0;    // matrix (gate / up) and first weight row
+        int pbeg, cnt;  // the unit's expert: first pair and pair count
+        int mat, o0;    // matrix (gate / up) and the wave's first weight row
     };
     // eoff is the same for every lane; reading it through readfirstlane lets the compiler keep every schedule field
     // in scalar registers (a value it must assume per-lane would turn each buffer access into a waterfall loop).
@@ -841,21 +834,21 @@ __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int
         asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr) : "memory");
         return __builtin_amdgcn_readfirstlane(v);
     };
-    const uint8_t* wp = nullptr;  // the lead step's 16-row weight tile and the bytes to the end of its matrix
+    const uint8_t* wp = nullptr;  // the lead step's 16-row weight tile (this wave's) and the bytes to its matrix end
     uint32_t wbytes = 0;
     auto enter = [&](Step& c) {
         const int e = c.t / per_e;
         const int r = c.t - e * per_e;
-        c.mat = r >= tiles ? 1 : 0;
-        c.o0 = (r - c.mat * tiles) * 16;
+        c.mat = r >= groups ? 1 : 0;
+        c.o0 = (r - c.mat * groups) * kStreamRows + 16 * wave;
         c.pbeg = eoff_u(e);
         c.cnt = eoff_u(e + 1) - c.pbeg;
         const uint64_t base = (uint64_t)c.o0 * row_bytes;
         wp = (c.mat ? a.w1[e] : a.w0[e]) + base;
         wbytes = rsrc_bytes((uint64_t)a.n_rows * row_bytes, base);
     };
-    auto seek = [&](Step& c, int t) {  // the first task from t on (stride NW) whose expert has pairs
-        for (; t < T; t += NW) {
+    auto seek = [&](Step& c, int t) {  // the first unit from t on (stride NG) whose expert has pairs
+        for (; t < T; t += NG) {
             const int e = t / per_e;
             if (eoff_u(e + 1) > eoff_u(e)) break;
         }
@@ -870,12 +863,12 @@ __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int
         c.sb = 0;
         c.n0 += 16;
         if (c.n0 < c.cnt) return;
-        seek(c, c.t + NW);
+        seek(c, c.t + NG);
     };
 
-    // DMA pieces of a step (16 rows x 9 pieces of 16 bytes): instruction i = 0, 1 moves pieces 64 i + lane (16
-    // bytes each), instruction 2 pieces 128 .. 143 as 4-byte words (lane L: word L % 4 of piece 128 + L / 4). The
-    // super-block's offset in the row goes in the scalar offset.
+    // Weight DMA pieces of a step (16 rows x 9 pieces of 16 bytes): instruction i = 0, 1 moves pieces 64 i + lane
+    // (16 bytes each), instruction 2 pieces 128 .. 143 as 4-byte words (lane L: word L % 4 of piece 128 + L / 4).
+    // The super-block's offset in the row goes in the scalar offset.
     uint32_t lane_off[3];
 #pragma unroll
     for (int i = 0; i < 2; i++) {
@@ -886,8 +879,8 @@ __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int
         const uint32_t p = 128u + (uint32_t)lane / 4u;
         lane_off[2] = (p / 9u) * row_bytes + 16u * (p % 9u) + 4u * ((uint32_t)lane & 3u);
     }
-    // The lead step's weights go to ring slot j. Past the end the resource is empty: the DMA still issues (a fixed
-    // instruction count keeps the waits below exact) and writes zeros.
+    // The lead step's weights go to this wave's ring slot j. Past the end the resource is empty: the DMA still issues
+    // (a fixed instruction count keeps the waits below exact) and writes zeros.
     auto issue_w = [&](const Step& c, int j) {
         // the descriptor from values marked uniform (else the compiler wraps each DMA in a waterfall loop)
         const uint64_t wpi = (uint64_t)(uintptr_t)wp;
@@ -896,7 +889,7 @@ __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int
         const uint32_t nb = __builtin_amdgcn_readfirstlane(c.t < T ? wbytes : 0u);
         const __amdgpu_buffer_rsrc_t wr = make_rsrc(reinterpret_cast<const void*>((uintptr_t)wpu), nb);
         const int soff = c.sb * kQ4KBytes;
-        uint8_t* sl = ring[j][wave];
+        uint8_t* sl = wring[j][wave];
         __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (__attribute__((address_space(3))) void*)sl, 16,
                                                  (int)lane_off[0], soff, 0, 0);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (__attribute__((address_space(3))) void*)(sl + 1024), 16,
@@ -904,82 +897,93 @@ __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int
         __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (__attribute__((address_space(3))) void*)(sl + 2048), 4,
                                                  (int)lane_off[2], soff, 0, 0);
     };
-    // A operands of a step: row r16 = pair my_pair of the chunk (an absent pair reads past the resource). The
-    // lane's K piece splits into a lane part (g) and a compile-time part, which goes in the immediate offset.
-    // The lane's activation scale, that of pair 4 (r16 % 4) + g, goes to the ring slot by DMA (a scale in a
-    // register drew waits from the compiler that drained the pipeline); lane j of row g then holds the scale of
-    // result j (pair 4j + g), which the tail broadcasts across the row.
-    const uint32_t a_lane = 16u * (4u * ((uint32_t)g >> 1) + ((uint32_t)g & 1u));
-    const int s_pair = 4 * (r16 & 3) + g;
+    // Shared A slot: pair p of the chunk (p < 16) at 1024 (p / 4) + 256 (p % 4), written by wave p / 4. The MFMA row
+    // of pair p is m(p) = 4 (p % 4) + p / 4 (pair p sits in MFMA row m(p)), and its 16-byte pieces are stored XORed
+    // with m(p) % 8, so the eight lanes of a read group (rows m = 0..7 or 8..15) hit different banks.
+    // Wave w's A DMA: lane L moves pair 4w + L / 16, physical piece L % 16 = logical piece (L % 16) ^ (m % 8).
+    const int a_pair = 4 * wave + (lane >> 4);                       // the pair this lane's A DMA moves
+    const uint32_t a_piece = (uint32_t)((lane & 15) ^ ((4 * (lane >> 4) + wave) & 7));
+    const int s_pair = 4 * (lane & 3) + wave;                        // lanes 0-3: the pair of this lane's scale DMA
     const __amdgpu_buffer_rsrc_t qr = make_rsrc(a.q, (uint32_t)a.act_rows * K);
     const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.s, (uint32_t)a.act_rows * (uint32_t)spr * 4u);
-    struct AOp {
-        u32x4 av[4];
+    auto issue_a = [&](const Step& c, int j) {
+        uint32_t qo = 0x80000000u, so = 0x80000000u;
+        if (c.t < T && c.n0 + a_pair < c.cnt)
+            qo = (uint32_t)prow[c.pbeg + c.n0 + a_pair] * K + (uint32_t)c.sb * kQK + 16u * a_piece;
+        if (c.t < T && lane < 4 && c.n0 + s_pair < c.cnt)
+            so = ((uint32_t)prow[c.pbeg + c.n0 + s_pair] * (uint32_t)spr + (uint32_t)c.sb) * 4u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(qr, (__attribute__((address_space(3))) void*)(aring[j] + 1024 * wave),
+                                                 16, (int)qo, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (__attribute__((address_space(3))) void*)(sring[j] + 256 * wave),
+                                                 4, (int)so, 0, 0, 0);
     };
-    auto load_a = [&](const Step& c, AOp& A, int j) {
-        uint32_t qb = 0x80000000u, sbase = 0x80000000u;
-        if (c.t < T && c.n0 + my_pair < c.cnt) qb = (uint32_t)prow[c.pbeg + c.n0 + my_pair] * K + a_lane;
-        if (c.t < T && c.n0 + s_pair < c.cnt) sbase = (uint32_t)prow[c.pbeg + c.n0 + s_pair] * (uint32_t)spr * 4u;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (__attribute__((address_space(3))) void*)(ring[j][wave] + kStreamW),
-                                                 4, (int)(sbase + (uint32_t)c.sb * 4u), 0, 0, 0);
-        const uint32_t o = qb + (uint32_t)c.sb * kQK;
-        A.av[0] = __builtin_amdgcn_raw_buffer_load_b128(qr, (int)o, 0, 0);
-        A.av[1] = __builtin_amdgcn_raw_buffer_load_b128(qr, (int)(o + 128u), 0, 0);
-        A.av[2] = __builtin_amdgcn_raw_buffer_load_b128(qr, (int)(o + 32u), 0, 0);
-        A.av[3] = __builtin_amdgcn_raw_buffer_load_b128(qr, (int)(o + 160u), 0, 0);
-    };
+    // Read side. MFMA t of lane (g, r16) takes logical piece 4 (g / 2) + g % 2 + {0, 8, 2, 10}[t] of pair p with
+    // m(p) = r16, i.e. p = 4 (r16 % 4) + r16 / 4, held at 1024 (r16 % 4) + 256 (r16 / 4).
+    uint32_t a_rd[4];
+    {
+        const uint32_t row = 1024u * (uint32_t)(r16 & 3) + 256u * (uint32_t)(r16 >> 2);
+        const uint32_t base = 4u * ((uint32_t)g >> 1) + ((uint32_t)g & 1u);
+        const uint32_t kt[4] = {0u, 8u, 2u, 10u};
+#pragma unroll
+        for (int t = 0; t < 4; t++) a_rd[t] = row + 16u * ((base + kt[t]) ^ ((uint32_t)r16 & 7u));
+    }
 
-    Step lead;  // the next step whose weights go out
-    seek(lead, (int)blockIdx.x * 4 + wave);
+    Step lead;  // the next step whose loads go out
+    seek(lead, (int)blockIdx.x);
     if (lead.t >= T) {
-        // this wave has no unit; the other waves of the workgroup run on independently
+        // no unit for this workgroup (the same in all its waves)
         return;
     }
-    // Issue order: the weights of a step (three DMA instructions), then its A operands (five loads); the first
-    // D - 1 steps are issued here, each later step q issues step q + D - 1 into the slot step q - 1 freed.
+    // Issue order: a step's weights, then its A operands and scales; the first D - 1 steps are issued here. Step q
+    // issues the weights of step q + D - 1 into this wave's slot that step q - 1 read, then (after its barrier, when
+    // every wave is past step q - 1) the A operands and scales of step q + D - 1 into the shared slot step q - 1
+    // read.
     Step desc[D];
-    AOp A[D];
 #pragma unroll
-    for (int i = 0; i < D; i++) {
-        desc[i] = lead;  // defined from the start (an undefined scalar descriptor costs the compiler a wait)
-        A[i] = AOp{};
-    }
+    for (int i = 0; i < D; i++) desc[i] = lead;  // defined from the start (undefined descriptors cost the compiler a wait)
 #pragma unroll
     for (int i = 0; i < D - 1; i++) {
         desc[i] = lead;
         issue_w(lead, i);
+        issue_a(lead, i);
         advance(lead);
-        load_a(desc[i], A[i], i);
     }
 
     float run[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // sums of outputs (MFMA row 4g + j, weight row r16) so far
     auto step = [&](auto sc) -> bool {
-        constexpr int s = decltype(sc)::value;         // this step's slot
-        constexpr int w = (s + D - 1) % D;             // the slot of the step issued now (freed by the last step)
+        constexpr int s = decltype(sc)::value;  // this step's slot
+        constexpr int w = (s + D - 1) % D;      // the slot of the step issued now (read by the last step)
         const Step& cur = desc[s];
         desc[w] = lead;
         issue_w(lead, w);
+        // This wave's loads of step q have landed: younger are the next D - 2 steps' five instructions each and the
+        // weights just issued, three (a unit's output stores only add younger ones). The barrier then makes the other
+        // waves' A operands and scales of step q visible, and frees slot w of the shared rings.
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(5 * (D - 2) + 3) : "memory");
+        __builtin_amdgcn_s_barrier();
+        issue_a(lead, w);
         advance(lead);
-        load_a(desc[w], A[w], w);
-        // Step q's eight instructions (three weight DMAs, the scale DMA, four A loads) have landed: everything
-        // younger is the D - 1 later steps' eight each (a unit's output stores only add younger ones).
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(8 * (D - 1)) : "memory");
-        // The weights from the ring slot, read with explicit instructions after that wait.
-        const uint32_t rowa = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)(ring[s][wave]) +
+        const uint32_t wrow = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)(wring[s][wave]) +
                               (uint32_t)r16 * kQ4KBytes;
-        const uint32_t sva = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)(ring[s][wave]) +
-                             (uint32_t)kStreamW + 4u * (uint32_t)lane;
+        const uint32_t abase = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)(aring[s]);
+        const uint32_t sadr = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)(sring[s]) + 256u * (uint32_t)g;
         F::W wv;
-        uint32_t sv;
-        asm volatile("ds_read_b128 %0, %4\n\t"
-                     "ds_read_b128 %1, %5 offset:16\n\t"
-                     "ds_read_b128 %2, %5 offset:80\n\t"
-                     "ds_read_b32 %3, %6\n\t"
+        u32x4 av[4];
+        f32x4 q8s;
+        asm volatile("ds_read_b128 %0, %8\n\t"
+                     "ds_read_b128 %1, %9 offset:16\n\t"
+                     "ds_read_b128 %2, %9 offset:80\n\t"
+                     "ds_read_b128 %3, %10\n\t"
+                     "ds_read_b128 %4, %11\n\t"
+                     "ds_read_b128 %5, %12\n\t"
+                     "ds_read_b128 %6, %13\n\t"
+                     "ds_read_b128 %7, %14\n\t"
                      "s_waitcnt lgkmcnt(0)"
-                     : "=v"(wv.h), "=v"(wv.q[0]), "=v"(wv.q[1]), "=v"(sv)
-                     : "v"(rowa), "v"(rowa + 16u * (uint32_t)g), "v"(sva)
+                     : "=v"(wv.h), "=v"(wv.q[0]), "=v"(wv.q[1]), "=v"(av[0]), "=v"(av[1]), "=v"(av[2]), "=v"(av[3]),
+                       "=v"(q8s)
+                     : "v"(wrow), "v"(wrow + 16u * (uint32_t)g), "v"(abase + a_rd[0]), "v"(abase + a_rd[1]),
+                       "v"(abase + a_rd[2]), "v"(abase + a_rd[3]), "v"(sadr)
                      : "memory");
-        const AOp& acur = A[s];
         // MFMAs of the super-block (as lohi_block_values), then the fp32 tail of the rows that hold pairs
         i32x4 op[4][F::kNumMfma];
         F::template operands<0>(wv, g, op[0]);
@@ -991,20 +995,15 @@ __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int
         for (int k = 0; k < F::kNumMfma; k++) acc[k] = i32x4{0, 0, 0, 0};
 #pragma unroll
         for (int t = 0; t < 4; t++) {
-            const i32x4 aop = i32x4{(int)acur.av[t].x, (int)acur.av[t].y, (int)acur.av[t].z, (int)acur.av[t].w};
+            const i32x4 aop = i32x4{(int)av[t].x, (int)av[t].y, (int)av[t].z, (int)av[t].w};
 #pragma unroll
             for (int k = 0; k < F::kNumMfma; k++) acc[k] = mfma16(aop, op[t][k], acc[k]);
         }
         const float d = F::d_of(wv), dmin = F::dmin_of(wv);
         const int live = min(4, (cur.cnt - cur.n0 + 3) >> 2);  // results j < live hold pairs
-        auto tail = [&](auto jc) {
-            constexpr int j = decltype(jc)::value;
-            if (j < live) run[j] += F::tail(acc, j, d, dmin, as_float(row_bcast<j>(sv)));
-        };
-        tail(std::integral_constant<int, 0>{});
-        tail(std::integral_constant<int, 1>{});
-        tail(std::integral_constant<int, 2>{});
-        tail(std::integral_constant<int, 3>{});
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (j < live) run[j] += F::tail(acc, j, d, dmin, q8s[j]);
         if (cur.sb == spr - 1) {
             const int o = cur.o0 + r16;
             const float* bias = cur.mat ? a.bias1 : a.bias0;
@@ -1020,7 +1019,7 @@ __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int
         return desc[(s + 1) % D].t < T;
     };
     run_slots(step, std::make_integer_sequence<int, D>{});
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the ring's last DMAs land before the wave ends
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the rings' last DMAs land before the wave ends
 }
 
 template <class F, int kBatch>
@@ -1076,18 +1075,17 @@ hipError_t launch_mfma_small(int type, const GroupLaunch& L, hipStream_t st) {
     const int pairs = L.expert_off ? L.pairs : L.rows;
     const bool dense_ok = (long)nmat * ((sa.n_rows + 15) / 16) >= stream_dense_tiles;
     if (stream && type == 12 && (L.expert_off || dense_ok) && pairs > 0 && pairs <= kStreamMaxPairs) {
-        sa.tiles = (sa.n_rows + 15) / 16;
+        sa.tiles = (sa.n_rows + kStreamRows - 1) / kStreamRows;  // 64-row groups
         const long units = (long)L.experts * nmat * sa.tiles;
         int dev = 0, cus = 256;
         if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-        // workgroups per CU (measured on MI355X, config-5 MoE step under the profiler: 4 / 5 -> 219 / 216 us)
+        // Three workgroups per CU fit the kernel's LDS. Measured on MI355X (config-5 MoE step): a 5-slot ring at two
+        // per CU leaves the down launch (512 units) unchanged, 64.4 vs 64.6 us, and makes gate/up 11 % slower.
         static const int per_cu = [] {
             const char* v = getenv("OVFQ_MOE_STREAM_WG");
-            return v && *v ? atoi(v) : 5;
+            return v && *v ? atoi(v) : 3;
         }();
-        const int grid = (int)std::min<long>((units + 3) / 4, (long)cus * per_cu);
-        // Depth 3: measured equal to 4, 5 and 6 (each at the workgroups per CU its LDS and registers allow), so the
-        // smallest ring keeps the most workgroups resident.
+        const int grid = (int)std::min<long>(units, (long)cus * per_cu);
         hipLaunchKernelGGL(q4k_mfma_stream_kernel<3>, dim3(grid), dim3(256), 0, st, sa, L.experts, nmat, pairs);
         return hipGetLastError();
     }
