@@ -780,8 +780,8 @@ __global__ __launch_bounds__(256) void kquant_mfma_small_kernel(const SArgs a) {
 // row, with no exchange between waves. The unit's last step stores biasO + sum.
 constexpr int kStreamW = 2304;         // a wave's weights per step: 16 rows x 144 bytes, two 1 KiB DMAs and one of 256
 constexpr int kStreamA = 4096;         // the chunk's A operands per step: 16 pairs x 256 bytes, 1 KiB DMA per wave
-constexpr int kStreamS = 1024;         // the chunk's activation scales: 256 bytes per wave (4 used)
-constexpr int kStreamMaxPairs = 1024;  // the pair -> activation row map is cached in LDS
+constexpr int kStreamS = 64;           // the chunk's activation scales: 4 per wave
+constexpr int kStreamMaxPairs = 1024;  // the pair -> activation row map is cached in LDS (dynamic, 4 bytes a pair)
 constexpr int kStreamRows = 64;        // weight rows per unit (16 per wave)
 
 // Calls f(slot 0), f(slot 1), ..., f(slot n - 1), f(slot 0), ... with each slot a compile-time constant, until one
@@ -802,7 +802,7 @@ __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int
     __shared__ __align__(16) uint8_t aring[D][kStreamA];
     __shared__ __align__(16) uint8_t sring[D][kStreamS];
     __shared__ int eoff[kMaxExperts + 1];
-    __shared__ int prow[kStreamMaxPairs];
+    extern __shared__ int prow[];  // pairs entries
     const int tid = threadIdx.x, wave = wave_id(), lane = tid & 63;
     const int g = lane >> 4, r16 = lane & 15;
     // without a pair list: one expert over activation rows 0 .. rows - 1 (a dense small batch)
@@ -834,38 +834,6 @@ __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int
         asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr) : "memory");
         return __builtin_amdgcn_readfirstlane(v);
     };
-    const uint8_t* wp = nullptr;  // the lead step's 16-row weight tile (this wave's) and the bytes to its matrix end
-    uint32_t wbytes = 0;
-    auto enter = [&](Step& c) {
-        const int e = c.t / per_e;
-        const int r = c.t - e * per_e;
-        c.mat = r >= groups ? 1 : 0;
-        c.o0 = (r - c.mat * groups) * kStreamRows + 16 * wave;
-        c.pbeg = eoff_u(e);
-        c.cnt = eoff_u(e + 1) - c.pbeg;
-        const uint64_t base = (uint64_t)c.o0 * row_bytes;
-        wp = (c.mat ? a.w1[e] : a.w0[e]) + base;
-        wbytes = rsrc_bytes((uint64_t)a.n_rows * row_bytes, base);
-    };
-    auto seek = [&](Step& c, int t) {  // the first unit from t on (stride NG) whose expert has pairs
-        for (; t < T; t += NG) {
-            const int e = t / per_e;
-            if (eoff_u(e + 1) > eoff_u(e)) break;
-        }
-        c.t = t;
-        c.n0 = 0;
-        c.sb = 0;
-        if (t < T) enter(c);
-    };
-    auto advance = [&](Step& c) {
-        if (c.t >= T) return;
-        if (++c.sb < spr) return;
-        c.sb = 0;
-        c.n0 += 16;
-        if (c.n0 < c.cnt) return;
-        seek(c, c.t + NG);
-    };
-
     // Weight DMA pieces of a step (16 rows x 9 pieces of 16 bytes): instruction i = 0, 1 moves pieces 64 i + lane
     // (16 bytes each), instruction 2 pieces 128 .. 143 as 4-byte words (lane L: word L % 4 of piece 128 + L / 4).
     // The super-block's offset in the row goes in the scalar offset.
@@ -879,24 +847,6 @@ __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int
         const uint32_t p = 128u + (uint32_t)lane / 4u;
         lane_off[2] = (p / 9u) * row_bytes + 16u * (p % 9u) + 4u * ((uint32_t)lane & 3u);
     }
-    // The lead step's weights go to this wave's ring slot j. Past the end the resource is empty: the DMA still issues
-    // (a fixed instruction count keeps the waits below exact) and writes zeros.
-    auto issue_w = [&](const Step& c, int j) {
-        // the descriptor from values marked uniform (else the compiler wraps each DMA in a waterfall loop)
-        const uint64_t wpi = (uint64_t)(uintptr_t)wp;
-        const uint64_t wpu = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(wpi >> 32)) << 32) |
-                             (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)wpi);
-        const uint32_t nb = __builtin_amdgcn_readfirstlane(c.t < T ? wbytes : 0u);
-        const __amdgpu_buffer_rsrc_t wr = make_rsrc(reinterpret_cast<const void*>((uintptr_t)wpu), nb);
-        const int soff = c.sb * kQ4KBytes;
-        uint8_t* sl = wring[j][wave];
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (__attribute__((address_space(3))) void*)sl, 16,
-                                                 (int)lane_off[0], soff, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (__attribute__((address_space(3))) void*)(sl + 1024), 16,
-                                                 (int)lane_off[1], soff, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (__attribute__((address_space(3))) void*)(sl + 2048), 4,
-                                                 (int)lane_off[2], soff, 0, 0);
-    };
     // Shared A slot: pair p of the chunk (p < 16) at 1024 (p / 4) + 256 (p % 4), written by wave p / 4. The MFMA row
     // of pair p is m(p) = 4 (p % 4) + p / 4 (pair p sits in MFMA row m(p)), and its 16-byte pieces are stored XORed
     // with m(p) % 8, so the eight lanes of a read group (rows m = 0..7 or 8..15) hit different banks.
@@ -906,16 +856,83 @@ __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int
     const int s_pair = 4 * (lane & 3) + wave;                        // lanes 0-3: the pair of this lane's scale DMA
     const __amdgpu_buffer_rsrc_t qr = make_rsrc(a.q, (uint32_t)a.act_rows * K);
     const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.s, (uint32_t)a.act_rows * (uint32_t)spr * 4u);
+    constexpr uint32_t kOut = 0x80000000u;  // an offset past every resource (the DMA then writes zeros)
+
+    // What the lead step's loads need, set when the lead enters a unit or a chunk (not per step): this wave's weight
+    // resource, and the lane's A and scale offsets at super-block 0.
+    __amdgpu_buffer_rsrc_t lead_w = make_rsrc(a.q, 0u);
+    uint32_t lead_q = kOut, lead_s = kOut;
+    auto prow_at = [&](int i) {  // an explicit read, like eoff_u's
+        const uint32_t addr = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int*)(prow + i);
+        int v;
+        asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr) : "memory");
+        return (uint32_t)v;
+    };
+    auto enter_chunk = [&](const Step& c) {
+        lead_q = c.n0 + a_pair < c.cnt ? prow_at(c.pbeg + c.n0 + a_pair) * K + 16u * a_piece : kOut;
+        lead_s = lane < 4 && c.n0 + s_pair < c.cnt ? prow_at(c.pbeg + c.n0 + s_pair) * (uint32_t)spr * 4u : kOut;
+    };
+    auto enter = [&](Step& c) {
+        const int e = c.t / per_e;
+        const int r = c.t - e * per_e;
+        c.mat = r >= groups ? 1 : 0;
+        c.o0 = (r - c.mat * groups) * kStreamRows + 16 * wave;
+        c.pbeg = eoff_u(e);
+        c.cnt = eoff_u(e + 1) - c.pbeg;
+        const uint64_t base = (uint64_t)c.o0 * row_bytes;
+        // the descriptor from values marked uniform (else the compiler wraps each DMA in a waterfall loop)
+        const uint64_t wpi = (uint64_t)(uintptr_t)((c.mat ? a.w1[e] : a.w0[e]) + base);
+        const uint64_t wpu = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(wpi >> 32)) << 32) |
+                             (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)wpi);
+        const uint32_t nb = __builtin_amdgcn_readfirstlane(rsrc_bytes((uint64_t)a.n_rows * row_bytes, base));
+        lead_w = make_rsrc(reinterpret_cast<const void*>((uintptr_t)wpu), nb);
+        enter_chunk(c);
+    };
+    auto seek = [&](Step& c, int t) {  // the first unit from t on (stride NG) whose expert has pairs
+        for (; t < T; t += NG) {
+            const int e = t / per_e;
+            if (eoff_u(e + 1) > eoff_u(e)) break;
+        }
+        c.t = t;
+        c.n0 = 0;
+        c.sb = 0;
+        if (t < T) {
+            enter(c);
+        } else {  // past the end: the loads still issue (a fixed count keeps the waits below exact) and write zeros
+            lead_w = make_rsrc(a.q, 0u);
+            lead_q = lead_s = kOut;
+        }
+    };
+    auto advance = [&](Step& c) {
+        if (c.t >= T) return;
+        if (++c.sb < spr) return;
+        c.sb = 0;
+        c.n0 += 16;
+        if (c.n0 < c.cnt) {
+            enter_chunk(c);
+            return;
+        }
+        seek(c, c.t + NG);
+    };
+
+    // The lead step's weights go to this wave's ring slot j, its A operands and scales to the shared slot j.
+    auto issue_w = [&](const Step& c, int j) {
+        const int soff = c.sb * kQ4KBytes;
+        uint8_t* sl = wring[j][wave];
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(lead_w, (__attribute__((address_space(3))) void*)sl, 16,
+                                                 (int)lane_off[0], soff, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(lead_w, (__attribute__((address_space(3))) void*)(sl + 1024), 16,
+                                                 (int)lane_off[1], soff, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(lead_w, (__attribute__((address_space(3))) void*)(sl + 2048), 4,
+                                                 (int)lane_off[2], soff, 0, 0);
+    };
     auto issue_a = [&](const Step& c, int j) {
-        uint32_t qo = 0x80000000u, so = 0x80000000u;
-        if (c.t < T && c.n0 + a_pair < c.cnt)
-            qo = (uint32_t)prow[c.pbeg + c.n0 + a_pair] * K + (uint32_t)c.sb * kQK + 16u * a_piece;
-        if (c.t < T && lane < 4 && c.n0 + s_pair < c.cnt)
-            so = ((uint32_t)prow[c.pbeg + c.n0 + s_pair] * (uint32_t)spr + (uint32_t)c.sb) * 4u;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(qr, (__attribute__((address_space(3))) void*)(aring[j] + 1024 * wave),
-                                                 16, (int)qo, 0, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (__attribute__((address_space(3))) void*)(sring[j] + 256 * wave),
-                                                 4, (int)so, 0, 0, 0);
+                                                 16, (int)(lead_q + (uint32_t)c.sb * kQK), 0, 0, 0);
+        // lanes 0-3 only: the DMA writes only active lanes, so four scales per wave fill 16 bytes
+        if (lane < 4)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (__attribute__((address_space(3))) void*)(sring[j] + 16 * wave),
+                                                     4, (int)(lead_s + (uint32_t)c.sb * 4u), 0, 0, 0);
     };
     // Read side. MFMA t of lane (g, r16) takes logical piece 4 (g / 2) + g % 2 + {0, 8, 2, 10}[t] of pair p with
     // m(p) = r16, i.e. p = 4 (r16 % 4) + r16 / 4, held at 1024 (r16 % 4) + 256 (r16 / 4).
@@ -966,7 +983,7 @@ __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int
         const uint32_t wrow = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)(wring[s][wave]) +
                               (uint32_t)r16 * kQ4KBytes;
         const uint32_t abase = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)(aring[s]);
-        const uint32_t sadr = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)(sring[s]) + 256u * (uint32_t)g;
+        const uint32_t sadr = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)(sring[s]) + 16u * (uint32_t)g;
         F::W wv;
         u32x4 av[4];
         f32x4 q8s;
@@ -1040,6 +1057,17 @@ static hipError_t launch_small(SArgs& sa, int nmat, int experts, hipStream_t st)
     return hipGetLastError();
 }
 
+// Static LDS of the expert-stream kernel (its dynamic part is the pair map, 4 bytes a pair).
+static size_t stream_lds_bytes() {
+    static const size_t bytes = [] {
+        hipFuncAttributes fa{};
+        return hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(q4k_mfma_stream_kernel<3>)) == hipSuccess
+                   ? fa.sharedSizeBytes
+                   : (size_t)(160 * 1024);
+    }();
+    return bytes;
+}
+
 bool mfma_small_supported(int type, int in) { return (type == 12 || type == 14) && in % kQK == 0 && in / kQK <= 64; }
 
 hipError_t launch_mfma_small(int type, const GroupLaunch& L, hipStream_t st) {
@@ -1079,14 +1107,17 @@ hipError_t launch_mfma_small(int type, const GroupLaunch& L, hipStream_t st) {
         const long units = (long)L.experts * nmat * sa.tiles;
         int dev = 0, cus = 256;
         if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-        // Three workgroups per CU fit the kernel's LDS. Measured on MI355X (config-5 MoE step): a 5-slot ring at two
-        // per CU leaves the down launch (512 units) unchanged, 64.4 vs 64.6 us, and makes gate/up 11 % slower.
-        static const int per_cu = [] {
+        // Workgroups per CU: as many as the kernel's LDS allows (four up to 140 pairs, else three). Measured on MI355X
+        // (config-5 MoE step): a 5-slot ring at two per CU leaves the down launch (512 units) unchanged, 64.4 vs
+        // 64.6 us, and makes gate/up 11 % slower.
+        static const int per_cu_env = [] {
             const char* v = getenv("OVFQ_MOE_STREAM_WG");
-            return v && *v ? atoi(v) : 3;
+            return v && *v ? atoi(v) : 0;
         }();
+        const size_t dyn = (size_t)pairs * sizeof(int);
+        const int per_cu = per_cu_env ? per_cu_env : (stream_lds_bytes() + dyn <= 160 * 1024 / 4 ? 4 : 3);
         const int grid = (int)std::min<long>(units, (long)cus * per_cu);
-        hipLaunchKernelGGL(q4k_mfma_stream_kernel<3>, dim3(grid), dim3(256), 0, st, sa, L.experts, nmat, pairs);
+        hipLaunchKernelGGL(q4k_mfma_stream_kernel<3>, dim3(grid), dim3(256), dyn, st, sa, L.experts, nmat, pairs);
         return hipGetLastError();
     }
     // super-blocks per wave batch (measured on MI355X: 2 beats 4 for every Llama/Mixtral shape)
