@@ -239,7 +239,10 @@ bool use_tiled_mfma(const ovfq_ctx* c, int type, const ovfq::ProjJob* jobs, int 
 // multi-row / previous kernel): 2 rows 14336x4096 Q4_K 10.8 / 13.7, Q6_K 4096x14336 16.6 / 19.5; 4 rows 13.0 /
 // 14.9; 8 rows 17.8 / 16.3. A fused q/k/v launch (three weights, which the small-M kernel runs one by one) is
 // 7.0 / 19.1 at 3 rows and 10.1 / 20.0 at 8. Automatic: up to 4 rows, and up to 8 for three or more weights.
-bool use_gemv_rows(const ovfq_ctx* c, int type, int in, int rows, int count) {
+// A gate/up-shaped Q4_K pair (`pair_out` output rows each) tall enough for the expert-stream kernel takes that kernel
+// from 3 rows (MI355X, us, multi-row / stream with its Q8_K launch, 2x14336x4096: 2 rows 17.2 / 20.7, 3 rows
+// 20.1 / 19.4, 4 rows 22.9 / 19.6).
+bool use_gemv_rows(const ovfq_ctx* c, int type, int in, int rows, int count, int pair_out = 0) {
     if ((type != OVFQ_TYPE_Q4_K && type != OVFQ_TYPE_Q6_K) || !ovfq::gemv_rows_supported(in, rows)) return false;
     // Decode rows of 16384 < K <= 32768, past the one-row kernel (which is faster wherever it runs: MI355X, us, one-row
     // / multi-row kernel at M = 1: 4096x4096 Q4_K 4.8 / 5.5, 4096x14336 Q6_K 14.0 / 14.3). At K = 28672 it
@@ -247,15 +250,18 @@ bool use_gemv_rows(const ovfq_ctx* c, int type, int in, int rows, int count) {
     if (rows == 1) return gemv_enabled() && !ovfq::gemv_supported(in);
     if (c->batched_kernel == OVFQ_BATCHED_ROWS) return true;
     if (c->batched_kernel != OVFQ_BATCHED_AUTO) return false;
+    if (count == 2 && pair_out > 0 && rows >= 3 && small_mfma_enabled(rows) &&
+        ovfq::stream_pair_preferred(type, in, pair_out))
+        return false;
     return rows <= 4 || count >= 3;
 }
 
 // Whether the projection launch quantises its fp32 input itself instead of a separate Q8_K / Q8_0 launch: one row on
 // a decode kernel (K <= 8192), or up to 64 super-blocks of rows on the multi-row decode kernel.
-bool quantize_in_launch(const ovfq_ctx* c, int type, int in, int rows, int count) {
+bool quantize_in_launch(const ovfq_ctx* c, int type, int in, int rows, int count, int pair_out = 0) {
     if (type == OVFQ_TYPE_Q8_0) return rows == 1 && gemv_enabled() && ovfq::q8_0_gemv_quantize_inside(in);
     if (rows == 1 && ovfq::gemv_supported(in)) return gemv_enabled() && ovfq::gemv_quantize_inside(in);
-    return use_gemv_rows(c, type, in, rows, count) && ovfq::gemv_rows_quantize_inside(in, rows);
+    return use_gemv_rows(c, type, in, rows, count, pair_out) && ovfq::gemv_rows_quantize_inside(in, rows);
 }
 
 // One launch for `count` weights sharing an activation: either the fp32 activation x (quantised inside the
@@ -273,7 +279,8 @@ int launch_projection(ovfq_ctx* c, const ovfq_weight* const* ws, int count, cons
     }
     const int type = ws[0]->type;
     const int in = ws[0]->in;
-    if (x && rows > 1 && !use_gemv_rows(c, type, in, rows, count))
+    const int pair_out = count == 2 && ws[0]->out == ws[1]->out ? ws[0]->out : 0;
+    if (x && rows > 1 && !use_gemv_rows(c, type, in, rows, count, pair_out))
         return fail(OVFQ_ERR_SIZE, "in-launch quantisation of %d rows needs the multi-row decode kernel", rows);
     // Every kernel below reads either the fp32 input (decode kernels that quantise it) or the quantised activation.
     if (!x && (!act.q || !act.s)) return fail(OVFQ_ERR_NULL, "projection launch without a quantised activation");
@@ -310,7 +317,7 @@ int launch_projection(ovfq_ctx* c, const ovfq_weight* const* ws, int count, cons
             HIP_TRY(ovfq::launch_project_q8_0(jobs, count, in, rows, act, c->stream));
     } else if (rows == 1 && gemv_enabled() && ovfq::gemv_supported(in)) {
         HIP_TRY(ovfq::launch_gemv_kquant(type, jobs, count, in, x, act, c->stream));
-    } else if (use_gemv_rows(c, type, in, rows, count)) {
+    } else if (use_gemv_rows(c, type, in, rows, count, pair_out)) {
         HIP_TRY(ovfq::launch_gemv_rows_kquant(type, jobs, count, in, rows, x, act, c->stream));
     } else if (use_tiled_mfma(c, type, jobs, count, in, rows)) {
         HIP_TRY(ovfq::launch_project_mfma(type, jobs, count, in, rows, act, c->stream));
@@ -827,7 +834,8 @@ static int project_impl(ovfq_ctx* ctx, int count, const ovfq_weight* const* ws, 
             bd[i] = biases ? biases[i] : nullptr;
         }
     }
-    if (quantize_in_launch(ctx, ws[0]->type, in, rows, count)) {
+    if (quantize_in_launch(ctx, ws[0]->type, in, rows, count,
+                           count == 2 && ws[0]->out == ws[1]->out ? ws[0]->out : 0)) {
         // Decode: the Q8_K quantisation happens inside the projection launch.
         if ((rc = launch_projection(ctx, ws, count, bd, yd, rows, ovfq::ActQ{nullptr, nullptr, nullptr}, xd)))
             return rc;
@@ -1347,7 +1355,7 @@ static int ffn_impl(ovfq_ctx* ctx, const ovfq_weight* gate, const ovfq_weight* u
     // gate/up (one launch; for one or a few short rows the Q8_K quantisation runs inside it)
     const ovfq_weight* gu[2] = {gate, up};
     float* gu_out[2] = {g, u};
-    if (quantize_in_launch(ctx, gate->type, dmodel, rows, 2)) {
+    if (quantize_in_launch(ctx, gate->type, dmodel, rows, 2, gate->out == up->out ? gate->out : 0)) {
         if ((rc = launch_projection(ctx, gu, 2, nullptr, gu_out, rows, ovfq::ActQ{nullptr, nullptr, nullptr}, xd)))
             return rc;
     } else {

@@ -1070,6 +1070,29 @@ static size_t stream_lds_bytes() {
 
 bool mfma_small_supported(int type, int in) { return (type == 12 || type == 14) && in % kQK == 0 && in / kQK <= 64; }
 
+static bool stream_enabled() {
+    static const int stream = [] {
+        const char* v = getenv("OVFQ_MOE_STREAM");
+        return v && *v ? atoi(v) : 1;
+    }();
+    return stream != 0;
+}
+
+// A dense small batch takes the stream kernel only with many 16-row tiles: a few units leave most of the chip idle
+// (MI355X, us, stream / super-block-parallel kernel: 14336x4096 at 16 rows 18.9 / 20.2, 32 rows 29.9 / 34.8;
+// 4096x4096 at 16 rows 17.9 / 9.4; 4096x14336 at 16 rows 44.7 / 19.0).
+static bool stream_dense_ok(int nmat, int n_rows) {
+    static const int min_tiles = [] {
+        const char* v = getenv("OVFQ_SMALL_STREAM_MIN_TILES");
+        return v && *v ? atoi(v) : 768;
+    }();
+    return (long)nmat * ((n_rows + 15) / 16) >= min_tiles;
+}
+
+bool stream_pair_preferred(int type, int in, int n_rows) {
+    return stream_enabled() && type == 12 && mfma_small_supported(type, in) && stream_dense_ok(2, n_rows);
+}
+
 hipError_t launch_mfma_small(int type, const GroupLaunch& L, hipStream_t st) {
     SArgs sa{};
     for (int i = 0; i < L.experts; i++) {
@@ -1089,20 +1112,9 @@ hipError_t launch_mfma_small(int type, const GroupLaunch& L, hipStream_t st) {
     sa.q = L.act.q;
     sa.s = L.act.s;
     const int nmat = L.w1 ? 2 : 1;
-    static const int stream = [] {
-        const char* v = getenv("OVFQ_MOE_STREAM");
-        return v && *v ? atoi(v) : 1;
-    }();
-    // A dense small batch takes the stream kernel only with many 16-row tiles: one wave per tile leaves most of
-    // the chip idle below that (MI355X, us, stream / super-block-parallel kernel: 14336x4096 at 16 rows 18.9 / 20.2,
-    // 32 rows 29.9 / 34.8; 4096x4096 at 16 rows 17.9 / 9.4; 4096x14336 at 16 rows 44.7 / 19.0).
-    static const int stream_dense_tiles = [] {
-        const char* v = getenv("OVFQ_SMALL_STREAM_MIN_TILES");
-        return v && *v ? atoi(v) : 768;
-    }();
     const int pairs = L.expert_off ? L.pairs : L.rows;
-    const bool dense_ok = (long)nmat * ((sa.n_rows + 15) / 16) >= stream_dense_tiles;
-    if (stream && type == 12 && (L.expert_off || dense_ok) && pairs > 0 && pairs <= kStreamMaxPairs) {
+    if (stream_enabled() && type == 12 && (L.expert_off || stream_dense_ok(nmat, sa.n_rows)) && pairs > 0 &&
+        pairs <= kStreamMaxPairs) {
         sa.tiles = (sa.n_rows + kStreamRows - 1) / kStreamRows;  // 64-row groups
         const long units = (long)L.experts * nmat * sa.tiles;
         int dev = 0, cus = 256;

@@ -76,6 +76,9 @@ struct GroupLaunch {
 };
 // On MFMA with super-block-parallel waves (mfma.hip), 16 activation rows per tile.
 bool mfma_small_supported(int type, int in);
+// Whether a gate/up-shaped pair of Q4_K weights (n_rows outputs each, `in` inputs) runs on the expert-stream kernel
+// when it takes the small-M path.
+bool stream_pair_preferred(int type, int in, int n_rows);
 hipError_t launch_mfma_small(int type, const GroupLaunch& launch, hipStream_t st);
 // MFMA-ready copy of a Q4_K / Q6_K weight: its size, and the kernel that writes it from the GGUF blocks.
 size_t mfma_prepared_bytes(int in, int out);

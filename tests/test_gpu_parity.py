@@ -509,6 +509,25 @@ def test_stream_kernel_dense_bit_exact(orc, batched, rows, k, n):
                          "stream up")
 
 
+@pytest.mark.parametrize("rows", [2, 3, 4, 5])
+def test_gate_up_pair_rows_boundary_bit_exact(orc, ctx, rows):
+    """A gate/up-shaped Q4_K pair tall enough for the expert-stream kernel (6144 rows each: 768 16-row tiles) under
+    the automatic choice: 2 rows on the multi-row decode kernel, from 3 rows on the stream kernel; each output
+    bit-exact against the oracle, both through the fp32 entry point and the prequantised one."""
+    case("gate/up pair boundary", rows)
+    n, k = 6144, 256
+    rng = np.random.default_rng(600 + rows)
+    bg, bu = _kq_blocks(rng, "q4k", n, k), _kq_blocks(rng, "q4k", n, k)
+    wg, wu = ov.Q4KWeight(bg, k, n), ov.Q4KWeight(bu, k, n)
+    x = normal(rng, (rows, k))
+    g = torch.empty(rows * n, device=DEV)
+    u = torch.empty(rows * n, device=DEV)
+    ctx.project_multi_dev([wg, wu], t(x), [g, u], rows=rows)
+    torch.cuda.synchronize()
+    assert_bit_exact(g.cpu().numpy().reshape(rows, n), orc.q4k_project_batched(x, rows, bg, k, n, None), "pair gate")
+    assert_bit_exact(u.cpu().numpy().reshape(rows, n), orc.q4k_project_batched(x, rows, bu, k, n, None), "pair up")
+
+
 def test_moe_ffn_skewed_routing(orc):
     """Few pairs in all (the expert-stream kernel) but one expert with 21 of them (two 16-pair chunks of its units),
     one with a single pair, one with none: against the oracle at the FFN tolerance."""
