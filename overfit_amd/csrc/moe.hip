@@ -112,8 +112,9 @@ __global__ __launch_bounds__(64) void moe_topk_kernel(const float* __restrict__ 
 // routing table is staged in LDS when it fits (rows * k ints <= 48 KB).
 // With `tiles`, it also lists the experts' pair ranges in tiles of `nt` rows, expert-major: entry t = expert | (tile
 // index within the expert << 8), with the list's length at *tile_count.
-// Workgroup 0 does all of the above; workgroups 1.. quantise the tokens' activation x to Q8_K (one wave per
-// 256-element block, the standalone quantiser's arithmetic), which the plan does not depend on: one launch for both.
+// Workgroup 0 does all of the above (up to 64 entries in one wave, without barriers); workgroups 1.. quantise the
+// tokens' activation x to Q8_K (one wave per 256-element block, the standalone quantiser's arithmetic), which the
+// plan does not depend on: one launch for both.
 __global__ __launch_bounds__(256) void moe_plan_kernel(const int* __restrict__ idx_g, int rows, int k, int n_experts,
                                                        int* __restrict__ expert_off, int* __restrict__ pair_row,
                                                        int* __restrict__ pair_of, int staged, int nt,
@@ -124,6 +125,43 @@ __global__ __launch_bounds__(256) void moe_plan_kernel(const int* __restrict__ i
     if (blockIdx.x > 0) {
         const int64_t blk = (int64_t)(blockIdx.x - 1) * 4 + wave_id();
         if (blk < n_blocks) q8k_quantize_block(x, blk, xq, xs, xb);
+        return;
+    }
+    if (rows * k <= 64) {
+        // Up to 64 (token, slot) entries: one wave does the whole plan, lane i taking entry i (token i / k, slot
+        // i % k), with no barrier. Per expert a ballot of its claiming lanes gives the count and each lane's rank
+        // (entries of lower tokens come first, and a token claims an expert at most once), so the positions are the
+        // ones the general path below computes.
+        if (wave_id() != 0) return;
+        const int lane = threadIdx.x & 63;
+        const uint64_t below = (1ull << lane) - 1ull;
+        const bool valid = lane < rows * k;
+        const int ex = valid ? idx_g[lane] : -1;
+        const int slot = valid ? lane % k : 0;
+        bool claim = valid && ex >= 0 && ex < n_experts;
+        for (int d = 1; d < k; d++) {  // an earlier slot of the same token with the same expert claims it instead
+            const int prev = __shfl(ex, lane - d < 0 ? 0 : lane - d, 64);
+            if (slot >= d && prev == ex) claim = false;
+        }
+        int pos = -1, off = 0, tb = 0;
+        for (int e = 0; e < n_experts; e++) {
+            const uint64_t m = __ballot(claim && ex == e);
+            if (claim && ex == e) pos = off + __popcll(m & below);
+            if (lane == 0) expert_off[e] = off;
+            const int c = __popcll(m);
+            if (tiles) {
+                const int nt_e = (c + nt - 1) / nt;
+                for (int i = lane; i < nt_e; i += 64) tiles[tb + i] = e | (i << 8);
+                tb += nt_e;
+            }
+            off += c;
+        }
+        if (lane == 0) {
+            expert_off[n_experts] = off;
+            if (tiles) *tile_count = tb;
+        }
+        if (valid) pair_of[lane] = pos;
+        if (pos >= 0) pair_row[pos] = lane / k;
         return;
     }
     extern __shared__ int sidx[];
