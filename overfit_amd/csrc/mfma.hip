@@ -834,18 +834,14 @@ __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int
         asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr) : "memory");
         return __builtin_amdgcn_readfirstlane(v);
     };
-    // Weight DMA pieces of a step (16 rows x 9 pieces of 16 bytes): instruction i = 0, 1 moves pieces 64 i + lane
-    // (16 bytes each), instruction 2 pieces 128 .. 143 as 4-byte words (lane L: word L % 4 of piece 128 + L / 4).
-    // The super-block's offset in the row goes in the scalar offset.
+    // Weight DMA pieces of a step (16 rows x 9 pieces of 16 bytes): instruction i = 0, 1, 2 moves pieces 64 i + lane
+    // (16 bytes each; instruction 2 on lanes 0-15 only, pieces 128 .. 143). The super-block's offset in the row goes
+    // in the scalar offset.
     uint32_t lane_off[3];
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const uint32_t p = 64u * i + (uint32_t)lane;
+    for (int i = 0; i < 3; i++) {
+        const uint32_t p = 64u * i + (uint32_t)(i == 2 ? (lane & 15) : lane);
         lane_off[i] = (p / 9u) * row_bytes + 16u * (p % 9u);
-    }
-    {
-        const uint32_t p = 128u + (uint32_t)lane / 4u;
-        lane_off[2] = (p / 9u) * row_bytes + 16u * (p % 9u) + 4u * ((uint32_t)lane & 3u);
     }
     // Shared A slot: pair p of the chunk (p < 16) at 1024 (p / 4) + 256 (p % 4), written by wave p / 4. The MFMA row
     // of pair p is m(p) = 4 (p % 4) + p / 4 (pair p sits in MFMA row m(p)), and its 16-byte pieces are stored XORed
@@ -923,8 +919,10 @@ __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int
                                                  (int)lane_off[0], soff, 0, 0);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(lead_w, (__attribute__((address_space(3))) void*)(sl + 1024), 16,
                                                  (int)lane_off[1], soff, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(lead_w, (__attribute__((address_space(3))) void*)(sl + 2048), 4,
-                                                 (int)lane_off[2], soff, 0, 0);
+        // lanes 0-15 only: the DMA writes only active lanes (16 pieces, 256 bytes)
+        if (lane < 16)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(lead_w, (__attribute__((address_space(3))) void*)(sl + 2048), 16,
+                                                     (int)lane_off[2], soff, 0, 0);
     };
     auto issue_a = [&](const Step& c, int j) {
         __builtin_amdgcn_raw_ptr_buffer_load_lds(qr, (__attribute__((address_space(3))) void*)(aring[j] + 1024 * wave),
