@@ -4,9 +4,10 @@
 //   1. MoeRouter.SelectTopK per token (RT/MoeRouter.cs:40-128)                       -> moe_topk_kernel
 //   2. group the (token, top-k slot) pairs by expert, tokens ascending, and quantise
 //      the tokens' activation to Q8_K in the same launch                            -> moe_plan_kernel
-//   3. per expert: gate/up = batched projections of its tokens                   (mfma.hip, grid.y = expert)
+//   3. per expert: gate/up = batched projections of its tokens, all experts in one launch (mfma.hip: the
+//      expert-stream kernel for Q4_K with few pairs, else the small-M or tiled MFMA kernel)
 //   4. SiLU(gate) * up, quantised to Q8_K for the down projection                    -> gate_up_q8k_kernel
-//   5. per expert: down projection of its pairs                                  (mfma.hip)
+//   5. per expert: down projection of its pairs, one launch                      (mfma.hip, as step 3)
 //   6. y[token] = sum over top-k slots, in slot order, of weight * expert output     -> moe_combine_kernel
 // Pairs are numbered expert-major (expert 0's tokens first, ascending), which is the order the reference
 // gathers rows in; pair_of[token * k + slot] maps a slot back to its pair.
