@@ -306,6 +306,19 @@ OVFQ_API int ovfq_moe_ffn_dev(ovfq_ctx* ctx, int n_experts, const ovfq_weight* c
                               int rows, int top_k, const int* expert_indices, const float* expert_weights,
                               float* y);
 
+/* MoeFeedForwardBlock.DecodeBatched (RT/MoeFeedForwardBlock.cs:140-241) from the router logits on: the routing
+ * of ovfq_moe_select_topk (router_logits [rows][n_experts], top_k <= n_experts, normalize as there), written to
+ * expert_indices / expert_weights [rows][top_k], then ovfq_moe_ffn with it. Outputs equal those two calls'; for up
+ * to 64 (token, slot) entries the routing runs inside the grouping launch (one launch fewer). */
+OVFQ_API int ovfq_moe_ffn_routed(ovfq_ctx* ctx, int n_experts, const ovfq_weight* const* gate,
+                                 const ovfq_weight* const* up, const ovfq_weight* const* down, const float* x,
+                                 int rows, const float* router_logits, int top_k, int normalize,
+                                 int* expert_indices, float* expert_weights, float* y);
+OVFQ_API int ovfq_moe_ffn_routed_dev(ovfq_ctx* ctx, int n_experts, const ovfq_weight* const* gate,
+                                     const ovfq_weight* const* up, const ovfq_weight* const* down, const float* x,
+                                     int rows, const float* router_logits, int top_k, int normalize,
+                                     int* expert_indices, float* expert_weights, float* y);
+
 /* ---------------------------------------------------------------------------------- weight quantisation */
 
 /* GgmlQuant.QuantizeQ4_K (LD/GgmlQuant.cs:132-161): output-major f32 [out][in] (in % 256 == 0) -> Q4_K

@@ -7,7 +7,7 @@ from . import _lib
 from .errors import (OverfitArgumentError, OverfitArgumentNullError, OverfitArgumentOutOfRangeError,
                      OverfitHipError, OverfitUnsupportedTypeError)
 from .kernels import (BatchedQuantProjection, FeedForwardActivation, MoeRouter, Q4KDotKernel, Q6KDotKernel,
-                      Q8DotKernel, ffn_gated, ffn_swiglu, moe_ffn, project, project_gate_up, project_heads_q8_0,
+                      Q8DotKernel, ffn_gated, ffn_swiglu, moe_ffn, moe_ffn_routed, project, project_gate_up, project_heads_q8_0,
                       quantize_weight)
 from .runtime import Context, default_context
 from .weights import DecodeWeight, Q4KWeight, Q6KWeight, Q8Weight, load_gguf_experts, load_gguf_tensor
@@ -20,6 +20,6 @@ __all__ = [
     "BatchedQuantProjection", "Context", "DecodeWeight", "FeedForwardActivation", "MoeRouter", "OverfitArgumentError",
     "OverfitArgumentNullError", "OverfitArgumentOutOfRangeError", "OverfitHipError", "OverfitUnsupportedTypeError",
     "Q4KDotKernel", "Q4KWeight", "Q6KDotKernel", "Q6KWeight", "Q8DotKernel", "Q8Weight", "TYPE_Q4_K", "TYPE_Q6_K",
-    "TYPE_Q8_0", "default_context", "ffn_gated", "ffn_swiglu", "load_gguf_experts", "load_gguf_tensor", "moe_ffn", "project",
+    "TYPE_Q8_0", "default_context", "ffn_gated", "ffn_swiglu", "load_gguf_experts", "load_gguf_tensor", "moe_ffn", "moe_ffn_routed", "project",
     "project_gate_up", "project_heads_q8_0", "quantize_weight",
 ]

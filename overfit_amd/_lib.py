@@ -67,6 +67,8 @@ SIGNATURES = {
     "ovfq_moe_select_topk_dev": (ci, [vp, vp, ci, ci, ci, ci, vp, vp]),
     "ovfq_moe_ffn": (ci, [vp, ci, PP, PP, PP, vp, ci, ci, vp, vp, vp]),
     "ovfq_moe_ffn_dev": (ci, [vp, ci, PP, PP, PP, vp, ci, ci, vp, vp, vp]),
+    "ovfq_moe_ffn_routed": (ci, [vp, ci, PP, PP, PP, vp, ci, vp, ci, ci, vp, vp, vp]),
+    "ovfq_moe_ffn_routed_dev": (ci, [vp, ci, PP, PP, PP, vp, ci, vp, ci, ci, vp, vp, vp]),
     "ovfq_project_gate_up_dev": (ci, [vp, vp, vp, vp, vp, vp]),
     "ovfq_project_multi_dev": (ci, [vp, ci, PP, vp, ci, PP, PP]),
     "ovfq_project_heads_q8_0": (ci, [vp, ci, PP, vp, ci, vp, vp]),

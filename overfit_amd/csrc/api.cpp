@@ -1153,12 +1153,15 @@ int ovfq_moe_select_topk_dev(ovfq_ctx* ctx, const float* logits, int rows, int n
     return topk_impl(ctx, logits, rows, n_experts, top_k, normalize, expert_indices, expert_weights, false);
 }
 
+// With `logits` (router logits [rows][E]) the routing is computed here (MoeRouter.SelectTopK) and written to idx / w
+// ([rows][k], outputs); without, idx / w are the caller's routing (inputs).
 static int moe_impl(ovfq_ctx* ctx, int E, const ovfq_weight* const* gate, const ovfq_weight* const* up,
                     const ovfq_weight* const* down, const float* x, int rows, int k, const int* idx, const float* w,
-                    float* y, bool host) {
+                    float* y, bool host, const float* logits = nullptr, int normalize = 0) {
     if (!ctx) return fail(OVFQ_ERR_NULL, "ctx is NULL");
     if (!gate || !up || !down) return fail(OVFQ_ERR_NULL, "expert weight arrays are NULL");
     if (!x || !idx || !w || !y) return fail(OVFQ_ERR_NULL, "x / expert_indices / expert_weights / y is NULL");
+    const bool route = logits != nullptr;
     if (E < 1 || E > OVFQ_MAX_EXPERTS) return fail(OVFQ_ERR_RANGE, "n_experts (%d) must be in [1, %d]", E, OVFQ_MAX_EXPERTS);
     int rc;
     if ((rc = check_rows(rows))) return rc;
@@ -1179,11 +1182,12 @@ static int moe_impl(ovfq_ctx* ctx, int E, const ovfq_weight* const* gate, const 
             down[e]->in != dff || down[e]->out != dmodel)
             return fail(OVFQ_ERR_SIZE, "expert %d shapes differ (gate/up [d_ff][d_model], down [d_model][d_ff])", e);
     }
-    if (!host && (rc_align(x) || rc_align(idx) || rc_align(w) || rc_align(y)))
+    if (!host && (rc_align(x) || rc_align(idx) || rc_align(w) || rc_align(y) || (route && rc_align(logits))))
         return fail(OVFQ_ERR_SIZE, "device pointers must be 4-byte aligned");
     // token rows and (token, slot) pair rows of the activation, gate/up and expert-output planes
     if ((rc = check_plane(rows, dmodel, "activation")) || (rc = check_plane((int64_t)rows * k, dff, "gate/up output")) ||
-        (rc = check_plane((int64_t)rows * k, dmodel, "expert output")))
+        (rc = check_plane((int64_t)rows * k, dmodel, "expert output")) ||
+        (route && (rc = check_plane(rows, E, "router logits"))))
         return rc;
     const size_t P = (size_t)rows * k;
     std::lock_guard<std::mutex> lk(ctx->mu);
@@ -1203,7 +1207,7 @@ static int moe_impl(ovfq_ctx* ctx, int E, const ovfq_weight* const* gate, const 
                              (ctx->batched_kernel == OVFQ_BATCHED_AUTO && P >= (size_t)grouped_min * E);
     const int max_tiles = (int)((P + ovfq::kGroupedTileRows - 1) / ovfq::kGroupedTileRows) + E;
     auto carve = [&](Carver& c, int** off, int** prow, int** pof, float** g, float** u, int8_t** iq, float** is,
-                     int16_t** ib, float** out, float** hx, int** hidx, float** hw, float** hy) {
+                     int16_t** ib, float** out, float** hx, int** hidx, float** hw, float** hy, float** hl) {
         *off = c.take<int>((size_t)(E + 2 + max_tiles) * 4);  // expert_off[E + 1], tile count, tile list
         *prow = c.take<int>(P * 4);
         *pof = c.take<int>(P * 4);
@@ -1218,25 +1222,32 @@ static int moe_impl(ovfq_ctx* ctx, int E, const ovfq_weight* const* gate, const 
             *hidx = c.take<int>(P * 4);
             *hw = c.take<float>(P * 4);
             *hy = c.take<float>((size_t)rows * dmodel * 4);
+            if (route) *hl = c.take<float>((size_t)rows * E * 4);
         }
     };
     int *off, *prow, *pof, *hidx = nullptr;
-    float *g, *u, *is, *out, *hx = nullptr, *hw = nullptr, *hy = nullptr;
+    float *g, *u, *is, *out, *hx = nullptr, *hw = nullptr, *hy = nullptr, *hl = nullptr;
     int8_t* iq;
     int16_t* ib;
     Carver sizing{nullptr};
-    carve(sizing, &off, &prow, &pof, &g, &u, &iq, &is, &ib, &out, &hx, &hidx, &hw, &hy);
+    carve(sizing, &off, &prow, &pof, &g, &u, &iq, &is, &ib, &out, &hx, &hidx, &hw, &hy, &hl);
     if ((rc = ensure(ctx, ctx->moe, sizing.used))) return rc;
     Carver c{static_cast<char*>(ctx->moe.p)};
-    carve(c, &off, &prow, &pof, &g, &u, &iq, &is, &ib, &out, &hx, &hidx, &hw, &hy);
+    carve(c, &off, &prow, &pof, &g, &u, &iq, &is, &ib, &out, &hx, &hidx, &hw, &hy, &hl);
     const float* xd = x;
-    const int* idxd = idx;
-    const float* wd = w;
+    const float* ld = logits;
+    int* idxd = const_cast<int*>(idx);  // written only when routing here (then the caller's output)
+    float* wd = const_cast<float*>(w);
     float* yd = y;
     if (host) {
         HIP_TRY(hipMemcpyAsync(hx, x, (size_t)rows * dmodel * 4, hipMemcpyHostToDevice, ctx->stream));
-        HIP_TRY(hipMemcpyAsync(hidx, idx, P * 4, hipMemcpyHostToDevice, ctx->stream));
-        HIP_TRY(hipMemcpyAsync(hw, w, P * 4, hipMemcpyHostToDevice, ctx->stream));
+        if (route) {
+            HIP_TRY(hipMemcpyAsync(hl, logits, (size_t)rows * E * 4, hipMemcpyHostToDevice, ctx->stream));
+            ld = hl;
+        } else {
+            HIP_TRY(hipMemcpyAsync(hidx, idx, P * 4, hipMemcpyHostToDevice, ctx->stream));
+            HIP_TRY(hipMemcpyAsync(hw, w, P * 4, hipMemcpyHostToDevice, ctx->stream));
+        }
         xd = hx;
         idxd = hidx;
         wd = hw;
@@ -1250,10 +1261,16 @@ static int moe_impl(ovfq_ctx* ctx, int E, const ovfq_weight* const* gate, const 
     const ovfq::ActQ act{(const int8_t*)ctx->act_q.p, (const float*)ctx->act_s.p, (const int16_t*)ctx->act_b.p};
     int* tile_count = off + E + 1;
     int* tiles = off + E + 2;
-    HIP_TRY(ovfq::launch_moe_plan(idxd, rows, k, E, off, prow, pof, ovfq::kGroupedTileRows,
-                                  grouped_big ? tiles : nullptr, tile_count, xd, (int64_t)(n_x / OVFQ_QK),
-                                  (int8_t*)ctx->act_q.p, (float*)ctx->act_s.p, (int16_t*)ctx->act_b.p,
-                                  ctx->stream));
+    if (route)
+        HIP_TRY(ovfq::launch_moe_route_plan(ld, rows, k, E, normalize, idxd, wd, off, prow, pof,
+                                            ovfq::kGroupedTileRows, grouped_big ? tiles : nullptr, tile_count, xd,
+                                            (int64_t)(n_x / OVFQ_QK), (int8_t*)ctx->act_q.p, (float*)ctx->act_s.p,
+                                            (int16_t*)ctx->act_b.p, ctx->stream));
+    else
+        HIP_TRY(ovfq::launch_moe_plan(idxd, rows, k, E, off, prow, pof, ovfq::kGroupedTileRows,
+                                      grouped_big ? tiles : nullptr, tile_count, xd, (int64_t)(n_x / OVFQ_QK),
+                                      (int8_t*)ctx->act_q.p, (float*)ctx->act_s.p, (int16_t*)ctx->act_b.p,
+                                      ctx->stream));
     const uint8_t* gw[OVFQ_MAX_EXPERTS];
     const uint8_t* uw[OVFQ_MAX_EXPERTS];
     const uint8_t* dw[OVFQ_MAX_EXPERTS];
@@ -1298,6 +1315,10 @@ static int moe_impl(ovfq_ctx* ctx, int E, const ovfq_weight* const* gate, const 
     HIP_TRY(ovfq::launch_moe_combine(out, pof, wd, rows, k, dmodel, yd, ctx->stream));
     if (host) {
         HIP_TRY(hipMemcpyAsync(y, yd, (size_t)rows * dmodel * 4, hipMemcpyDeviceToHost, ctx->stream));
+        if (route) {
+            HIP_TRY(hipMemcpyAsync(const_cast<int*>(idx), idxd, P * 4, hipMemcpyDeviceToHost, ctx->stream));
+            HIP_TRY(hipMemcpyAsync(const_cast<float*>(w), wd, P * 4, hipMemcpyDeviceToHost, ctx->stream));
+        }
         HIP_TRY(hipStreamSynchronize(ctx->stream));
     }
     return ok();
@@ -1406,6 +1427,23 @@ int ovfq_moe_ffn_dev(ovfq_ctx* ctx, int n_experts, const ovfq_weight* const* gat
                      const ovfq_weight* const* down, const float* x, int rows, int top_k, const int* expert_indices,
                      const float* expert_weights, float* y) {
     return moe_impl(ctx, n_experts, gate, up, down, x, rows, top_k, expert_indices, expert_weights, y, false);
+}
+
+int ovfq_moe_ffn_routed(ovfq_ctx* ctx, int n_experts, const ovfq_weight* const* gate, const ovfq_weight* const* up,
+                        const ovfq_weight* const* down, const float* x, int rows, const float* router_logits,
+                        int top_k, int normalize, int* expert_indices, float* expert_weights, float* y) {
+    if (!router_logits) return fail(OVFQ_ERR_NULL, "router_logits is NULL");
+    return moe_impl(ctx, n_experts, gate, up, down, x, rows, top_k, expert_indices, expert_weights, y, true,
+                    router_logits, normalize);
+}
+
+int ovfq_moe_ffn_routed_dev(ovfq_ctx* ctx, int n_experts, const ovfq_weight* const* gate,
+                            const ovfq_weight* const* up, const ovfq_weight* const* down, const float* x, int rows,
+                            const float* router_logits, int top_k, int normalize, int* expert_indices,
+                            float* expert_weights, float* y) {
+    if (!router_logits) return fail(OVFQ_ERR_NULL, "router_logits is NULL");
+    return moe_impl(ctx, n_experts, gate, up, down, x, rows, top_k, expert_indices, expert_weights, y, false,
+                    router_logits, normalize);
 }
 
 // ---------------------------------------------------------------------------------------- weight encoders

@@ -27,20 +27,10 @@ namespace ovfq {
 // at run time would sit in scratch memory). One insertion is the reference's loop written as a selection per
 // entry: with pos0 = min(filled, k - 1), the entries j in (p, pos0] take entry j - 1 and entry p takes the new
 // logit, where p is where the reference's `while (pos > 0 && w[pos - 1] < l) pos--` stops (RT/MoeRouter.cs:70-91).
+// Token n's selection from its logits l[0 .. n_experts): indices and weights of its top k (k <= KM) in idx / wv.
 template <int KM>
-__global__ __launch_bounds__(64) void moe_topk_kernel(const float* __restrict__ logits, int rows, int n_experts,
-                                                      int k, int stride, int normalize, int* __restrict__ idx_out,
-                                                      float* __restrict__ w_out) {
-    __shared__ float sl[64 * kMaxExperts];
-    const int row0 = blockIdx.x * 64;
-    const int nrow = min(64, rows - row0);
-    for (int i = threadIdx.x; i < nrow * n_experts; i += 64) sl[i] = logits[(size_t)row0 * n_experts + i];
-    __syncthreads();
-    const int n = row0 + threadIdx.x;
-    if (n >= rows) return;
-    const float* l = sl + threadIdx.x * n_experts;
-    int idx[KM];
-    float wv[KM];
+__device__ __forceinline__ void topk_select(const float* l, int n_experts, int k, int normalize, int (&idx)[KM],
+                                            float (&wv)[KM]) {
 #pragma unroll
     for (int i = 0; i < KM; i++) {
         idx[i] = -1;
@@ -94,6 +84,22 @@ __global__ __launch_bounds__(64) void moe_topk_kernel(const float* __restrict__ 
 #pragma unroll
         for (int i = 0; i < KM; i++) wv[i] = expf(wv[i] - mx) * inv;
     }
+}
+
+template <int KM>
+__global__ __launch_bounds__(64) void moe_topk_kernel(const float* __restrict__ logits, int rows, int n_experts,
+                                                      int k, int stride, int normalize, int* __restrict__ idx_out,
+                                                      float* __restrict__ w_out) {
+    __shared__ float sl[64 * kMaxExperts];
+    const int row0 = blockIdx.x * 64;
+    const int nrow = min(64, rows - row0);
+    for (int i = threadIdx.x; i < nrow * n_experts; i += 64) sl[i] = logits[(size_t)row0 * n_experts + i];
+    __syncthreads();
+    const int n = row0 + threadIdx.x;
+    if (n >= rows) return;
+    int idx[KM];
+    float wv[KM];
+    topk_select<KM>(sl + threadIdx.x * n_experts, n_experts, k, normalize, idx, wv);
 #pragma unroll
     for (int i = 0; i < KM; i++) {
         if (i < k) {
@@ -104,6 +110,43 @@ __global__ __launch_bounds__(64) void moe_topk_kernel(const float* __restrict__ 
 }
 
 // ------------------------------------------------------------------------------------------ grouping
+// The grouping plan of up to 64 (token, slot) entries in one wave: lane i holds entry i's expert `ex` (token i / k,
+// slot i % k; -1 past the entries). Per expert a ballot of its claiming lanes gives the count and each lane's rank
+// (entries of lower tokens come first, and a token claims an expert at most once), so the positions are the ones
+// the general path of moe_plan_kernel computes.
+__device__ __forceinline__ void plan_one_wave(int ex, int rows, int k, int n_experts, int* __restrict__ expert_off,
+                                              int* __restrict__ pair_row, int* __restrict__ pair_of, int nt,
+                                              int* __restrict__ tiles, int* __restrict__ tile_count) {
+    const int lane = threadIdx.x & 63;
+    const uint64_t below = (1ull << lane) - 1ull;
+    const bool valid = lane < rows * k;
+    const int slot = valid ? lane % k : 0;
+    bool claim = valid && ex >= 0 && ex < n_experts;
+    for (int d = 1; d < k; d++) {  // an earlier slot of the same token with the same expert claims it instead
+        const int prev = __shfl(ex, lane - d < 0 ? 0 : lane - d, 64);
+        if (slot >= d && prev == ex) claim = false;
+    }
+    int pos = -1, off = 0, tb = 0;
+    for (int e = 0; e < n_experts; e++) {
+        const uint64_t m = __ballot(claim && ex == e);
+        if (claim && ex == e) pos = off + __popcll(m & below);
+        if (lane == 0) expert_off[e] = off;
+        const int c = __popcll(m);
+        if (tiles) {
+            const int nt_e = (c + nt - 1) / nt;
+            for (int i = lane; i < nt_e; i += 64) tiles[tb + i] = e | (i << 8);
+            tb += nt_e;
+        }
+        off += c;
+    }
+    if (lane == 0) {
+        expert_off[n_experts] = off;
+        if (tiles) *tile_count = tb;
+    }
+    if (valid) pair_of[lane] = pos;
+    if (pos >= 0) pair_row[pos] = lane / k;
+}
+
 // One workgroup. Expert e's pairs are the tokens n (ascending) with a slot j such that idx[n][j] == e (the first
 // such slot: RT/MoeFeedForwardBlock.cs:191-204). A slot whose expert is out of range, or repeats an earlier slot's
 // expert, belongs to no pair (pair_of = -1) and contributes nothing to the combine.
@@ -129,40 +172,11 @@ __global__ __launch_bounds__(256) void moe_plan_kernel(const int* __restrict__ i
         return;
     }
     if (rows * k <= 64) {
-        // Up to 64 (token, slot) entries: one wave does the whole plan, lane i taking entry i (token i / k, slot
-        // i % k), with no barrier. Per expert a ballot of its claiming lanes gives the count and each lane's rank
-        // (entries of lower tokens come first, and a token claims an expert at most once), so the positions are the
-        // ones the general path below computes.
+        // Up to 64 (token, slot) entries: one wave does the whole plan, without barriers.
         if (wave_id() != 0) return;
         const int lane = threadIdx.x & 63;
-        const uint64_t below = (1ull << lane) - 1ull;
-        const bool valid = lane < rows * k;
-        const int ex = valid ? idx_g[lane] : -1;
-        const int slot = valid ? lane % k : 0;
-        bool claim = valid && ex >= 0 && ex < n_experts;
-        for (int d = 1; d < k; d++) {  // an earlier slot of the same token with the same expert claims it instead
-            const int prev = __shfl(ex, lane - d < 0 ? 0 : lane - d, 64);
-            if (slot >= d && prev == ex) claim = false;
-        }
-        int pos = -1, off = 0, tb = 0;
-        for (int e = 0; e < n_experts; e++) {
-            const uint64_t m = __ballot(claim && ex == e);
-            if (claim && ex == e) pos = off + __popcll(m & below);
-            if (lane == 0) expert_off[e] = off;
-            const int c = __popcll(m);
-            if (tiles) {
-                const int nt_e = (c + nt - 1) / nt;
-                for (int i = lane; i < nt_e; i += 64) tiles[tb + i] = e | (i << 8);
-                tb += nt_e;
-            }
-            off += c;
-        }
-        if (lane == 0) {
-            expert_off[n_experts] = off;
-            if (tiles) *tile_count = tb;
-        }
-        if (valid) pair_of[lane] = pos;
-        if (pos >= 0) pair_row[pos] = lane / k;
+        plan_one_wave(lane < rows * k ? idx_g[lane] : -1, rows, k, n_experts, expert_off, pair_row, pair_of, nt, tiles,
+                      tile_count);
         return;
     }
     extern __shared__ int sidx[];
@@ -238,6 +252,53 @@ __global__ __launch_bounds__(256) void moe_plan_kernel(const int* __restrict__ i
         if (tid < n_experts) run[tid] += wcnt[0][tid] + wcnt[1][tid] + wcnt[2][tid] + wcnt[3][tid];
         __syncthreads();
     }
+}
+
+// Router + grouping plan in one launch (MoeFeedForwardBlock.DecodeBatched's SelectTopK and grouping, RT/
+// MoeFeedForwardBlock.cs:140-204): for up to 64 tokens and 64 (token, slot) entries, wave 0 of workgroup 0 selects
+// each token's top k (lane n = token n, topk_select as in moe_topk_kernel), writes the indices and weights
+// [rows][k], hands entry i's expert to lane i by lane shuffles and runs plan_one_wave; workgroups 1.. quantise x to
+// Q8_K as in moe_plan_kernel.
+template <int KM>
+__global__ __launch_bounds__(256) void moe_route_plan_kernel(const float* __restrict__ logits, int rows, int k,
+                                                             int n_experts, int normalize, int* __restrict__ idx_out,
+                                                             float* __restrict__ w_out, int* __restrict__ expert_off,
+                                                             int* __restrict__ pair_row, int* __restrict__ pair_of,
+                                                             int nt, int* __restrict__ tiles,
+                                                             int* __restrict__ tile_count, const float* __restrict__ x,
+                                                             int64_t n_blocks, int8_t* __restrict__ xq,
+                                                             float* __restrict__ xs, int16_t* __restrict__ xb) {
+    if (blockIdx.x > 0) {
+        const int64_t blk = (int64_t)(blockIdx.x - 1) * 4 + wave_id();
+        if (blk < n_blocks) q8k_quantize_block(x, blk, xq, xs, xb);
+        return;
+    }
+    if (wave_id() != 0) return;
+    const int lane = threadIdx.x & 63;
+    int idx[KM];
+    float wv[KM];
+#pragma unroll
+    for (int i = 0; i < KM; i++) idx[i] = -1;
+    if (lane < rows) {
+        topk_select<KM>(logits + (size_t)lane * n_experts, n_experts, k, normalize, idx, wv);
+#pragma unroll
+        for (int i = 0; i < KM; i++) {
+            if (i < k) {
+                idx_out[lane * k + i] = idx[i];
+                w_out[lane * k + i] = wv[i];
+            }
+        }
+    }
+    // entry i = (token i / k, slot i % k): its expert from lane i / k's list
+    const int src = lane < rows * k ? lane / k : 0, slot = lane < rows * k ? lane % k : 0;
+    int ex = -1;
+#pragma unroll
+    for (int i = 0; i < KM; i++) {
+        const int v = __shfl(idx[i], src, 64);
+        if (i == slot) ex = v;
+    }
+    plan_one_wave(lane < rows * k ? ex : -1, rows, k, n_experts, expert_off, pair_row, pair_of, nt, tiles,
+                  tile_count);
 }
 
 // ------------------------------------------------------------------------------------------ gate * up
@@ -320,6 +381,37 @@ hipError_t launch_moe_topk(const float* logits, int rows, int n_experts, int k, 
     else
         hipLaunchKernelGGL(moe_topk_kernel<kMaxExperts>, grid, block, 0, st, logits, rows, n_experts, k, stride, normalize,
                            idx, w);
+    return hipGetLastError();
+}
+
+bool moe_route_plan_fused(int rows, int k) { return rows * k <= 64 && k <= kMaxExperts; }
+
+hipError_t launch_moe_route_plan(const float* logits, int rows, int k, int n_experts, int normalize, int* idx,
+                                 float* w, int* expert_off, int* pair_row, int* pair_of, int nt, int* tiles,
+                                 int* tile_count, const float* x, int64_t n_blocks, int8_t* xq, float* xs, int16_t* xb,
+                                 hipStream_t st) {
+    if (!moe_route_plan_fused(rows, k)) {
+        hipError_t e = launch_moe_topk(logits, rows, n_experts, k, k, normalize, idx, w, st);
+        if (e != hipSuccess) return e;
+        return launch_moe_plan(idx, rows, k, n_experts, expert_off, pair_row, pair_of, nt, tiles, tile_count, x,
+                               n_blocks, xq, xs, xb, st);
+    }
+    const int64_t grid = 1 + (n_blocks + 3) / 4;
+#define OVFQ_ROUTE_PLAN(KM)                                                                                           \
+    hipLaunchKernelGGL(moe_route_plan_kernel<KM>, dim3((unsigned)grid), dim3(256), 0, st, logits, rows, k, n_experts, \
+                       normalize, idx, w, expert_off, pair_row, pair_of, nt, tiles, tile_count, x, n_blocks, xq, xs,  \
+                       xb)
+    if (k <= 2)
+        OVFQ_ROUTE_PLAN(2);
+    else if (k <= 4)
+        OVFQ_ROUTE_PLAN(4);
+    else if (k <= 8)
+        OVFQ_ROUTE_PLAN(8);
+    else if (k <= 16)
+        OVFQ_ROUTE_PLAN(16);
+    else
+        OVFQ_ROUTE_PLAN(kMaxExperts);
+#undef OVFQ_ROUTE_PLAN
     return hipGetLastError();
 }
 

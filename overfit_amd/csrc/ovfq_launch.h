@@ -93,6 +93,13 @@ hipError_t launch_moe_topk(const float* logits, int rows, int n_experts, int k, 
 hipError_t launch_moe_plan(const int* idx, int rows, int k, int n_experts, int* expert_off, int* pair_row,
                            int* pair_of, int nt, int* tiles, int* tile_count, const float* x, int64_t n_blocks,
                            int8_t* xq, float* xs, int16_t* xb, hipStream_t st);
+// Router top-k (writing idx / w [rows][k]) and the plan above from router logits [rows][n_experts] (k <=
+// n_experts): one launch when moe_route_plan_fused(rows, k), else launch_moe_topk then launch_moe_plan.
+bool moe_route_plan_fused(int rows, int k);
+hipError_t launch_moe_route_plan(const float* logits, int rows, int k, int n_experts, int normalize, int* idx,
+                                 float* w, int* expert_off, int* pair_row, int* pair_of, int nt, int* tiles,
+                                 int* tile_count, const float* x, int64_t n_blocks, int8_t* xq, float* xs, int16_t* xb,
+                                 hipStream_t st);
 // The batched int8-MFMA kernel over expert groups: tile list entry t covers rows [64 i, 64 i + 64) of expert e's
 // pairs; gate/up pairs (w1 set) share the launch. Activation rows are gathered through pair_row (NULL: pair p reads
 // row p); outputs are pair-major.

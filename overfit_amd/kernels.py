@@ -443,6 +443,41 @@ def moe_ffn(gate_experts, up_experts, down_experts, x, rows, top_k, expert_indic
     return out
 
 
+def moe_ffn_routed(gate_experts, up_experts, down_experts, x, rows, router_logits, top_k, normalize=True,
+                   expert_indices=None, expert_weights=None, out=None):
+    """MoeFeedForwardBlock.DecodeBatched from the router logits on (RT/MoeFeedForwardBlock.cs:140-241): the
+    routing of MoeRouter.SelectTopK (RT/MoeRouter.cs:40-128) and the routed FFN (ovfq_moe_ffn_routed[_dev]).
+    Returns (out, expert_indices, expert_weights); the routing arrays [rows][top_k] are allocated if not given."""
+    E = len(gate_experts)
+    if not (len(up_experts) == len(down_experts) == E):
+        raise OverfitArgumentError("gate/up/down expert lists differ in length")
+    inp = as_buf(x, np.float32, "x")
+    d_model = gate_experts[0].InputSize
+
+    def alloc(n, dtype):  # on the input's side: a device tensor beside a device input, else a numpy array
+        if inp.device:
+            import torch
+
+            return torch.empty(n, dtype={np.int32: torch.int32, np.float32: torch.float32}[dtype],
+                               device=inp.obj.device)
+        return np.zeros(n, dtype)
+
+    out = alloc(rows * d_model, np.float32) if out is None else out
+    expert_indices = alloc(rows * top_k, np.int32) if expert_indices is None else expert_indices
+    expert_weights = alloc(rows * top_k, np.float32) if expert_weights is None else expert_weights
+    o = as_buf(out, np.float32, "out")
+    lg = as_buf(router_logits, np.float32, "router_logits")
+    ix = as_buf(expert_indices, np.int32, "expert_indices")
+    wt = as_buf(expert_weights, np.float32, "expert_weights")
+    same_side(inp, o, lg, ix, wt)
+    ctx = gate_experts[0].context
+    arr = lambda ws: (ctypes.c_void_p * E)(*[w.handle.value for w in ws])
+    fn = ctx.lib.ovfq_moe_ffn_routed_dev if inp.device else ctx.lib.ovfq_moe_ffn_routed
+    raise_for_status(fn(ctx.handle, E, arr(gate_experts), arr(up_experts), arr(down_experts), inp.ptr, rows, lg.ptr,
+                        top_k, 1 if normalize else 0, ix.ptr, wt.ptr, o.ptr), ctx.lib)
+    return out, expert_indices, expert_weights
+
+
 def project_heads_q8_0(head_weights, x, rows=1, bias=None, out=None):
     """The attention output projection with per-head Q8_0 Wo (ovfq_project_heads_q8_0[_dev]): for each of `rows`
     rows of x [rows][n_heads * head_dim], out = bias (or zero) plus, heads ascending, each head's

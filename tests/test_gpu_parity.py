@@ -696,6 +696,66 @@ def test_moe_ffn_matches_oracle(orc, gfmt, dfmt):
     _moe_check(ov.moe_ffn(gw, uw, dw, x, rows, k, idx2, w), ref2, f"{gfmt}/{dfmt} sparse routing")
 
 
+@pytest.mark.parametrize("rows,E,k,normalize", [(16, 8, 2, True), (30, 8, 1, False), (4, 16, 4, True),
+                                                 (40, 8, 2, True), (64, 4, 1, True)])
+def test_moe_ffn_routed_equals_two_calls(orc, rows, E, k, normalize):
+    """ovfq_moe_ffn_routed[_dev] (routing inside the grouping launch up to 64 (token, slot) entries, else the
+    router launch first) gives the indices, weights and output of ovfq_moe_select_topk + ovfq_moe_ffn bit for bit,
+    on the device and from host buffers; the routing itself against the oracle's SelectTopK."""
+    case("moe routed", rows, E, k, normalize)
+    rng = np.random.default_rng(1000 + rows * E + k)
+    dm, dff = 256, 512
+    gb = [orc.quantize_q4k(normal(rng, (dff, dm), 0.05)) for _ in range(E)]
+    ub = [orc.quantize_q4k(normal(rng, (dff, dm), 0.05)) for _ in range(E)]
+    db = [orc.quantize_q4k(normal(rng, (dm, dff), 0.05)) for _ in range(E)]
+    gw = [ov.Q4KWeight(b, dm, dff) for b in gb]
+    uw = [ov.Q4KWeight(b, dm, dff) for b in ub]
+    dw = [ov.Q4KWeight(b, dff, dm) for b in db]
+    x = normal(rng, (rows, dm))
+    logits = rng.random((rows, E)).astype(np.float32)
+    logits[1, :] = 0.25  # all tied: the lowest indices win
+    ctx = ov.default_context()
+    i2 = torch.empty(rows * k, dtype=torch.int32, device=DEV)
+    w2 = torch.empty(rows * k, device=DEV)
+    assert ctx.lib.ovfq_moe_select_topk_dev(ctx.handle, ctypes.c_void_p(t(logits).data_ptr()), rows, E, k,
+                                            1 if normalize else 0, ctypes.c_void_p(i2.data_ptr()),
+                                            ctypes.c_void_p(w2.data_ptr())) == 0
+    y2 = ov.moe_ffn(gw, uw, dw, t(x), rows, k, i2, w2)
+    y1, i1, w1 = ov.moe_ffn_routed(gw, uw, dw, t(x), rows, t(logits), k, normalize)
+    torch.cuda.synchronize()
+    assert torch.equal(i1, i2), "indices differ from ovfq_moe_select_topk"
+    assert torch.equal(w1.view(torch.int32), w2.view(torch.int32)), "weights differ from ovfq_moe_select_topk"
+    assert torch.equal(y1.view(torch.int32), y2.view(torch.int32)), "output differs from the two-call path"
+    ref_idx = np.stack([orc.moe_select_topk(logits[n], k, normalize)[0] for n in range(rows)])
+    assert np.array_equal(i1.cpu().numpy().reshape(rows, k), ref_idx)
+    yh, ih, wh = ov.moe_ffn_routed(gw, uw, dw, x, rows, logits, k, normalize)
+    assert np.array_equal(np.asarray(yh).view(np.int32), y1.cpu().numpy().view(np.int32))
+    assert np.array_equal(np.asarray(ih), i1.cpu().numpy())
+    assert np.array_equal(np.asarray(wh).view(np.int32), w1.cpu().numpy().view(np.int32))
+
+
+def test_moe_ffn_routed_rejects_bad_arguments():
+    """NULL router logits, and top_k above n_experts, are refused before any work."""
+    case("moe routed arguments")
+    ctx = ov.default_context()
+    rng = np.random.default_rng(7)
+    E, dm, dff = 2, 256, 256
+    ws = [[ov.Q4KWeight(random_q4k_blocks(rng, n * (kk // 256)).reshape(n, -1), kk, n) for _ in range(E)]
+          for n, kk in ((dff, dm), (dff, dm), (dm, dff))]
+    arr = lambda w: (ctypes.c_void_p * E)(*[v.handle.value for v in w])
+    x = np.zeros(dm, np.float32)
+    y = np.zeros(dm, np.float32)
+    lg = np.zeros(E, np.float32)
+    ix = np.zeros(4, np.int32)
+    wt = np.zeros(4, np.float32)
+    P = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    f = ctx.lib.ovfq_moe_ffn_routed
+    assert f(ctx.handle, E, arr(ws[0]), arr(ws[1]), arr(ws[2]), P(x), 1, None, 1, 1, P(ix), P(wt),
+             P(y)) == _lib.OVFQ_ERR_NULL
+    assert f(ctx.handle, E, arr(ws[0]), arr(ws[1]), arr(ws[2]), P(x), 1, P(lg), 3, 1, P(ix), P(wt),
+             P(y)) == _lib.OVFQ_ERR_RANGE
+
+
 def test_moe_ffn_many_tokens(orc):
     """A prefill-sized MoE batch: 300 tokens (more than one 256-token grouping chunk), top-3 of 8 experts, with a
     repeated expert in one token's slots, an out-of-range expert id and an expert no token chose."""
