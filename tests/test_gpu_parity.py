@@ -697,7 +697,8 @@ def test_moe_ffn_matches_oracle(orc, gfmt, dfmt):
 
 
 @pytest.mark.parametrize("rows,E,k,normalize", [(16, 8, 2, True), (30, 8, 1, False), (4, 16, 4, True),
-                                                 (40, 8, 2, True), (64, 4, 1, True)])
+                                                 (40, 8, 2, True), (64, 4, 1, True), (3, 32, 16, False),
+                                                 (1, 64, 20, True)])
 def test_moe_ffn_routed_equals_two_calls(orc, rows, E, k, normalize):
     """ovfq_moe_ffn_routed[_dev] (routing inside the grouping launch up to 64 (token, slot) entries, else the
     router launch first) gives the indices, weights and output of ovfq_moe_select_topk + ovfq_moe_ffn bit for bit,
@@ -713,7 +714,7 @@ def test_moe_ffn_routed_equals_two_calls(orc, rows, E, k, normalize):
     dw = [ov.Q4KWeight(b, dff, dm) for b in db]
     x = normal(rng, (rows, dm))
     logits = rng.random((rows, E)).astype(np.float32)
-    logits[1, :] = 0.25  # all tied: the lowest indices win
+    logits[min(1, rows - 1), :] = 0.25  # all tied: the lowest indices win
     ctx = ov.default_context()
     i2 = torch.empty(rows * k, dtype=torch.int32, device=DEV)
     w2 = torch.empty(rows * k, device=DEV)
