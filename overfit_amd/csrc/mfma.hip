@@ -845,10 +845,11 @@ __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int
     }
     // Shared A slot: pair p of the chunk (p < 16) at 1024 (p / 4) + 256 (p % 4), written by wave p / 4. The MFMA row
     // of pair p is m(p) = 4 (p % 4) + p / 4 (pair p sits in MFMA row m(p)), and its 16-byte pieces are stored XORed
-    // with m(p) % 8, so the eight lanes of a read group (rows m = 0..7 or 8..15) hit different banks.
-    // Wave w's A DMA: lane L moves pair 4w + L / 16, physical piece L % 16 = logical piece (L % 16) ^ (m % 8).
+    // with m(p), so the 16 lanes of a read group (one lane group, rows m = 0..15: the slots are 256-byte aligned)
+    // hit 16 different 16-byte bank groups.
+    // Wave w's A DMA: lane L moves pair 4w + L / 16, physical piece L % 16 = logical piece (L % 16) ^ m.
     const int a_pair = 4 * wave + (lane >> 4);                       // the pair this lane's A DMA moves
-    const uint32_t a_piece = (uint32_t)((lane & 15) ^ ((4 * (lane >> 4) + wave) & 7));
+    const uint32_t a_piece = (uint32_t)((lane & 15) ^ (4 * (lane >> 4) + wave));
     const int s_pair = 4 * (lane & 3) + wave;                        // lanes 0-3: the pair of this lane's scale DMA
     const __amdgpu_buffer_rsrc_t qr = make_rsrc(a.q, (uint32_t)a.act_rows * K);
     const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.s, (uint32_t)a.act_rows * (uint32_t)spr * 4u);
@@ -940,7 +941,7 @@ __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int
         const uint32_t base = 4u * ((uint32_t)g >> 1) + ((uint32_t)g & 1u);
         const uint32_t kt[4] = {0u, 8u, 2u, 10u};
 #pragma unroll
-        for (int t = 0; t < 4; t++) a_rd[t] = row + 16u * ((base + kt[t]) ^ ((uint32_t)r16 & 7u));
+        for (int t = 0; t < 4; t++) a_rd[t] = row + 16u * ((base + kt[t]) ^ (uint32_t)r16);
     }
 
     Step lead;  // the next step whose loads go out

@@ -18,6 +18,8 @@
 
 namespace ovfq {
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 // ------------------------------------------------------------------------------------------ router
 // One thread per token: insertion of each logit into a descending top-k list (ties keep the lower index), then
 // softmax over the k kept logits (normalize) or the full softmax evaluated at them. The workgroup's 64 logit rows
@@ -274,13 +276,31 @@ __global__ __launch_bounds__(256) void moe_route_plan_kernel(const float* __rest
         return;
     }
     if (wave_id() != 0) return;
+    __shared__ float sl[64 * kMaxExperts];
     const int lane = threadIdx.x & 63;
+    // The logits (rows * n_experts <= 4096) go to LDS in batches of eight coalesced loads per lane, so the scan
+    // below does not wait for memory once per expert.
+    const int total = rows * n_experts;
+    for (int u0 = 0; u0 < total; u0 += 8 * 64) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int i = u0 + u * 64 + lane;
+            v[u] = i < total ? logits[i] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int i = u0 + u * 64 + lane;
+            if (i < total) sl[i] = v[u];
+        }
+    }
+    wave_sync();
     int idx[KM];
     float wv[KM];
 #pragma unroll
     for (int i = 0; i < KM; i++) idx[i] = -1;
     if (lane < rows) {
-        topk_select<KM>(logits + (size_t)lane * n_experts, n_experts, k, normalize, idx, wv);
+        topk_select<KM>(sl + lane * n_experts, n_experts, k, normalize, idx, wv);
 #pragma unroll
         for (int i = 0; i < KM; i++) {
             if (i < k) {
@@ -314,12 +334,14 @@ __global__ __launch_bounds__(256) void gate_up_q8k_kernel(const float* __restric
                                                          float* __restrict__ s, int16_t* __restrict__ bs) {
     const int64_t blk = (int64_t)blockIdx.x * 4 + wave_id();
     if (blk >= (int64_t)max_pairs * spr) return;
-    const int pairs = expert_off ? expert_off[n_experts] : max_pairs;
-    if (blk / spr >= pairs) return;
     const int lane = threadIdx.x & 63;
+    // The block's loads go out before the pair count arrives (both buffers hold max_pairs rows); a block past the
+    // count stores nothing.
     const __amdgpu_buffer_rsrc_t gr = make_rsrc(gate + blk * kQK, kQK * 4);
     const __amdgpu_buffer_rsrc_t ur = make_rsrc(up + blk * kQK, kQK * 4);
     const u32x4 gv = ld4(gr, lane * 16), uv = ld4(ur, lane * 16);
+    const int pairs = expert_off ? expert_off[n_experts] : max_pairs;
+    const bool live = blk / spr < pairs;
     const float g[4] = {as_float(gv.x), as_float(gv.y), as_float(gv.z), as_float(gv.w)};
     const float u[4] = {as_float(uv.x), as_float(uv.y), as_float(uv.z), as_float(uv.w)};
     float v[4];
@@ -337,6 +359,7 @@ __global__ __launch_bounds__(256) void gate_up_q8k_kernel(const float* __restric
         v[i] = act * u[i];
     }
     const Q8KLane r = q8k_quantize_wave(v[0], v[1], v[2], v[3]);
+    if (!live) return;
     reinterpret_cast<uint32_t*>(q + blk * kQK)[lane] = r.packed;
     if ((lane & 3) == 0) bs[blk * 16 + (lane >> 2)] = (int16_t)r.group_sum;
     if (lane == 0) s[blk] = r.scale;
@@ -344,7 +367,10 @@ __global__ __launch_bounds__(256) void gate_up_q8k_kernel(const float* __restric
 
 // ------------------------------------------------------------------------------------------ combine
 // y[n][d] = 0; for each slot j in order: y[n][d] += w[n][j] * out[pair_of[n][j]][d] (RT/MoeFeedForwardBlock.cs:
-// 225-239). Each thread owns four consecutive d of one token.
+// 225-239). Each thread owns four consecutive d of one token (dmodel % 4 == 0). Slots go four at a time: their
+// pair numbers and weights, then their four output rows, are each loaded together before any is used, so a token's
+// k slots cost ceil(k / 4) dependent memory round trips rather than 2k. A slot without a pair (pair_of < 0) reads
+// pair 0 (out holds at least one row) and adds nothing.
 __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ out, const int* __restrict__ pair_of,
                                                           const float* __restrict__ w, int rows, int k, int dmodel,
                                                           float* __restrict__ y) {
@@ -352,15 +378,27 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
     if (i >= (int64_t)rows * dmodel) return;
     const int n = (int)(i / dmodel), d = (int)(i % dmodel);
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int j = 0; j < k; j++) {
-        const int p = pair_of[n * k + j];
-        if (p < 0) continue;
-        const float wj = w[n * k + j];
-        const float* src = out + (size_t)p * dmodel + d;
+    for (int j0 = 0; j0 < k; j0 += 4) {
+        int p[4];
+        float wj[4];
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const float prod = wj * src[c];
-            acc[c] = acc[c] + prod;
+        for (int u = 0; u < 4; u++) {
+            const int j = j0 + u;
+            p[u] = j < k ? pair_of[n * k + j] : -1;
+            wj[u] = j < k ? w[n * k + j] : 0.0f;
+        }
+        f32x4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            v[u] = *reinterpret_cast<const f32x4*>(out + (size_t)(p[u] < 0 ? 0 : p[u]) * dmodel + d);
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            if (p[u] < 0) continue;
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const float prod = wj[u] * v[u][c];
+                acc[c] = acc[c] + prod;
+            }
         }
     }
 #pragma unroll
