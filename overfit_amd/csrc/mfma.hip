@@ -775,7 +775,8 @@ __global__ __launch_bounds__(256) void kquant_mfma_small_kernel(const SArgs a) {
 // 16 weight rows (16 x 144 bytes) into its own LDS ring slot by DMA, and a quarter of the chunk's A operands (4 pairs
 // x 256 activation bytes) and scales into the workgroup's shared slot, so the four waves read the activation once
 // between them; all of it is issued two steps ahead of use and crosses unit boundaries. The step runs the
-// super-block's MFMAs and the reference's fp32 tail and adds each block value to the lane's running sums: lane
+// super-block's MFMAs on raw nibbles (Q4KRaw) and the reference's fp32 tail for the results that hold pairs, and adds
+// each block value to the lane's running sums: lane
 // (g, r16) owns outputs (MFMA rows 4g + j, weight row r16), so its sum is the reference's sequential sum over the
 // row, with no exchange between waves. The unit's last step stores biasO + sum.
 constexpr int kStreamW = 2304;         // a wave's weights per step: 16 rows x 144 bytes, two 1 KiB DMAs and one of 256
@@ -792,11 +793,65 @@ __device__ __forceinline__ void run_slots(Fn& f, std::integer_sequence<int, I...
     }
 }
 
+// A Q4_K super-block of the expert-stream kernel on raw nibbles. Per sub-block s (32 elements) one
+// v_mfma_i32_16x16x32_i8 of the activation bytes and the weight nibbles gives acc_s = sum nib * q8; the 6-bit scales
+// are applied to the results that hold pairs, mainAcc = sum_s sc_s * acc_s (24-bit multiply-adds, exact: |acc_s| <=
+// 32 * 15 * 127). minAcc = sum_s m_s * (sum of the sub-block's q8) comes from four v_mfma_i32_16x16x64_i8 over the
+// sub-block pairs (s, s + 4): the A operand is the two sub-blocks' activation bytes side by side, as read from LDS,
+// and the B operand m_s in the first eight bytes of each lane group, m_{s+4} in the last eight. These are the
+// integers of Q4KMfma's split-scale form (fewer operand instructions, one fewer MFMA), so the fp32 tail gives the same
+// block value. Lane (g, r16) holds: h = the block's d, dmin and 12 scale bytes; q01 / q23 = qs[32 c + 8 g .. + 7]
+// for c = 0, 1 / 2, 3 (low nibbles: sub-block 2c, high: 2c + 1; qs byte b holds elements 64 (b / 32) + b % 32 and
+// +32); av[t] = its pair's activation bytes 32 s + 8 g .. + 7 of sub-blocks s = t and t + 4; q8s[j] = the q8 scale of
+// result j's pair. Both operands of every MFMA hold the same element in the same byte.
+struct Q4KRaw {
+    __device__ __forceinline__ static i32x4 mfma32(uint32_t a0, uint32_t a1, uint32_t b0, uint32_t b1) {
+        const long av = (long)(((uint64_t)a1 << 32) | a0), bv = (long)(((uint64_t)b1 << 32) | b0);
+        return __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv, i32x4{0, 0, 0, 0}, 0, 0, 0);
+    }
+    __device__ __forceinline__ static void accumulate(const u32x4& h, const u32x4& q01, const u32x4& q23,
+                                                      const u32x4 (&av)[4], const f32x4& q8s, int live,
+                                                      float (&run)[4]) {
+        const uint32_t qw[8] = {q01.x, q01.y, q01.z, q01.w, q23.x, q23.y, q23.z, q23.w};
+        i32x4 acc[8];
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            const int c = s >> 1, sh = 4 * (s & 1);
+            const uint32_t b0 = (qw[2 * c] >> sh) & 0x0f0f0f0fu, b1 = (qw[2 * c + 1] >> sh) & 0x0f0f0f0fu;
+            acc[s] = s < 4 ? mfma32(av[s & 3].x, av[s & 3].y, b0, b1) : mfma32(av[s & 3].z, av[s & 3].w, b0, b1);
+        }
+        // the eight 6-bit scales and mins, one byte each (LD/GgmlDequant.cs:64-79 unpacking)
+        const uint32_t sc_lo = h.y & 0x3f3f3f3fu, m_lo = h.z & 0x3f3f3f3fu;
+        const uint32_t sc_hi = (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u);
+        const uint32_t m_hi = ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u);
+        i32x4 mn = i32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const int ml = (int)__builtin_amdgcn_perm(0u, m_lo, 0x01010101u * t);  // m_t in all four bytes
+            const int mh = (int)__builtin_amdgcn_perm(0u, m_hi, 0x01010101u * t);  // m_{t+4}
+            mn = mfma16(i32x4{(int)av[t].x, (int)av[t].y, (int)av[t].z, (int)av[t].w}, i32x4{ml, ml, mh, mh}, mn);
+        }
+        int sc[8];
+#pragma unroll
+        for (int s = 0; s < 8; s++) sc[s] = (int)(((s < 4 ? sc_lo : sc_hi) >> (8 * (s & 3))) & 0xffu);
+        const float d = half_lo(h.x), dmin = half_hi(h.x);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            if (j < live) {
+                int main_acc = __mul24(sc[0], acc[0][j]);
+#pragma unroll
+                for (int s = 1; s < 8; s++) main_acc += __mul24(sc[s], acc[s][j]);
+                // q8Scale * (d * mainAcc - dmin * minAcc)   (RT/Q4KDotKernel.cs:944)
+                run[j] += q8s[j] * (d * (float)main_acc - dmin * (float)mn[j]);
+            }
+        }
+    }
+};
+
 // D = ring slots: steps q + 1 .. q + D - 1 are in flight while step q is computed.
 template <int D>
 __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int n_experts, int nmat, int pairs) {
     static_assert(D >= 3 && 5 * (D - 2) + 3 <= 63, "the wait count below must fit the 6-bit vmcnt field");
-    using F = Q4KMfma;
     // The rings are read with explicit LDS instructions after explicit waits (below), so one array serves each.
     __shared__ __align__(16) uint8_t wring[D][4][kStreamW];
     __shared__ __align__(16) uint8_t aring[D][kStreamA];
@@ -845,11 +900,11 @@ __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int
     }
     // Shared A slot: pair p of the chunk (p < 16) at 1024 (p / 4) + 256 (p % 4), written by wave p / 4. The MFMA row
     // of pair p is m(p) = 4 (p % 4) + p / 4 (pair p sits in MFMA row m(p)), and its 16-byte pieces are stored XORed
-    // with m(p), so the 16 lanes of a read group (one lane group, rows m = 0..15: the slots are 256-byte aligned)
-    // hit 16 different 16-byte bank groups.
-    // Wave w's A DMA: lane L moves pair 4w + L / 16, physical piece L % 16 = logical piece (L % 16) ^ m.
+    // with m(p) % 8: rows m and m + 8 then share banks (a two-way conflict on the reads), but logical pieces i and
+    // i + 8 stay 128 bytes apart in every row, so one ds_read2_b64 fetches a sub-block pair (s, s + 4).
+    // Wave w's A DMA: lane L moves pair 4w + L / 16, physical piece L % 16 = logical piece (L % 16) ^ (m % 8).
     const int a_pair = 4 * wave + (lane >> 4);                       // the pair this lane's A DMA moves
-    const uint32_t a_piece = (uint32_t)((lane & 15) ^ (4 * (lane >> 4) + wave));
+    const uint32_t a_piece = (uint32_t)((lane & 15) ^ ((4 * (lane >> 4) + wave) & 7));
     const int s_pair = 4 * (lane & 3) + wave;                        // lanes 0-3: the pair of this lane's scale DMA
     const __amdgpu_buffer_rsrc_t qr = make_rsrc(a.q, (uint32_t)a.act_rows * K);
     const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.s, (uint32_t)a.act_rows * (uint32_t)spr * 4u);
@@ -933,15 +988,15 @@ __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int
             __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (__attribute__((address_space(3))) void*)(sring[j] + 16 * wave),
                                                      4, (int)(lead_s + (uint32_t)c.sb * 4u), 0, 0, 0);
     };
-    // Read side. MFMA t of lane (g, r16) takes logical piece 4 (g / 2) + g % 2 + {0, 8, 2, 10}[t] of pair p with
-    // m(p) = r16, i.e. p = 4 (r16 % 4) + r16 / 4, held at 1024 (r16 % 4) + 256 (r16 / 4).
+    // Read side (Q4KRaw): lane (g, r16) takes activation bytes 32 s + 8 g .. + 7 of sub-block s = 0..7 of pair p with
+    // m(p) = r16, i.e. p = 4 (r16 % 4) + r16 / 4, held at 1024 (r16 % 4) + 256 (r16 / 4): half g % 2 of logical piece
+    // 2 s + g / 2, and for sub-block s + 4 the same half 128 bytes further.
     uint32_t a_rd[4];
     {
         const uint32_t row = 1024u * (uint32_t)(r16 & 3) + 256u * (uint32_t)(r16 >> 2);
-        const uint32_t base = 4u * ((uint32_t)g >> 1) + ((uint32_t)g & 1u);
-        const uint32_t kt[4] = {0u, 8u, 2u, 10u};
 #pragma unroll
-        for (int t = 0; t < 4; t++) a_rd[t] = row + 16u * ((base + kt[t]) ^ (uint32_t)r16);
+        for (int t = 0; t < 4; t++)
+            a_rd[t] = row + 16u * ((2u * t + ((uint32_t)g >> 1)) ^ ((uint32_t)r16 & 7u)) + 8u * ((uint32_t)g & 1u);
     }
 
     Step lead;  // the next step whose loads go out
@@ -983,43 +1038,23 @@ __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int
                               (uint32_t)r16 * kQ4KBytes;
         const uint32_t abase = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)(aring[s]);
         const uint32_t sadr = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)(sring[s]) + 16u * (uint32_t)g;
-        F::W wv;
-        u32x4 av[4];
+        u32x4 h, q01, q23, av[4];
         f32x4 q8s;
         asm volatile("ds_read_b128 %0, %8\n\t"
-                     "ds_read_b128 %1, %9 offset:16\n\t"
-                     "ds_read_b128 %2, %9 offset:80\n\t"
-                     "ds_read_b128 %3, %10\n\t"
-                     "ds_read_b128 %4, %11\n\t"
-                     "ds_read_b128 %5, %12\n\t"
-                     "ds_read_b128 %6, %13\n\t"
+                     "ds_read2_b64 %1, %9 offset1:4\n\t"
+                     "ds_read2_b64 %2, %9 offset0:8 offset1:12\n\t"
+                     "ds_read2_b64 %3, %10 offset1:16\n\t"
+                     "ds_read2_b64 %4, %11 offset1:16\n\t"
+                     "ds_read2_b64 %5, %12 offset1:16\n\t"
+                     "ds_read2_b64 %6, %13 offset1:16\n\t"
                      "ds_read_b128 %7, %14\n\t"
                      "s_waitcnt lgkmcnt(0)"
-                     : "=v"(wv.h), "=v"(wv.q[0]), "=v"(wv.q[1]), "=v"(av[0]), "=v"(av[1]), "=v"(av[2]), "=v"(av[3]),
-                       "=v"(q8s)
-                     : "v"(wrow), "v"(wrow + 16u * (uint32_t)g), "v"(abase + a_rd[0]), "v"(abase + a_rd[1]),
+                     : "=v"(h), "=v"(q01), "=v"(q23), "=v"(av[0]), "=v"(av[1]), "=v"(av[2]), "=v"(av[3]), "=v"(q8s)
+                     : "v"(wrow), "v"(wrow + 16u + 8u * (uint32_t)g), "v"(abase + a_rd[0]), "v"(abase + a_rd[1]),
                        "v"(abase + a_rd[2]), "v"(abase + a_rd[3]), "v"(sadr)
                      : "memory");
-        // MFMAs of the super-block (as lohi_block_values), then the fp32 tail of the rows that hold pairs
-        i32x4 op[4][F::kNumMfma];
-        F::template operands<0>(wv, g, op[0]);
-        F::template operands<1>(wv, g, op[1]);
-        F::template operands<2>(wv, g, op[2]);
-        F::template operands<3>(wv, g, op[3]);
-        i32x4 acc[F::kNumMfma];
-#pragma unroll
-        for (int k = 0; k < F::kNumMfma; k++) acc[k] = i32x4{0, 0, 0, 0};
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-            const i32x4 aop = i32x4{(int)av[t].x, (int)av[t].y, (int)av[t].z, (int)av[t].w};
-#pragma unroll
-            for (int k = 0; k < F::kNumMfma; k++) acc[k] = mfma16(aop, op[t][k], acc[k]);
-        }
-        const float d = F::d_of(wv), dmin = F::dmin_of(wv);
         const int live = min(4, (cur.cnt - cur.n0 + 3) >> 2);  // results j < live hold pairs
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-            if (j < live) run[j] += F::tail(acc, j, d, dmin, q8s[j]);
+        Q4KRaw::accumulate(h, q01, q23, av, q8s, live, run);
         if (cur.sb == spr - 1) {
             const int o = cur.o0 + r16;
             const float* bias = cur.mat ? a.bias1 : a.bias0;
