@@ -475,8 +475,9 @@ def main():
         torch.cuda.empty_cache()
         roof = lambda t: {"bound": "mfma", "achieved": round(t, 1), "peak": INT8_PEAK_TOPS,  # noqa: E731
                           "unit": "TOPS", "frac": round(t / INT8_PEAK_TOPS, 4),
-                          "note": "useful int8 ops 2*M*N*K; the exact kernel issues 3 (Q4_K) / 2 (Q6_K) MFMAs "
-                                  "per 64-wide K chunk (lo/hi operand split + min term)"}
+                          "note": "useful int8 ops 2*M*N*K; the exact kernel issues 2 int8 MFMAs per 64-wide K "
+                                  "chunk (lo/hi operand split), plus for Q4_K one fp16 16x16x16 MFMA per super-block "
+                                  "and 16-row tile for the min term"}
         return {"what": "benchmark config 3: Llama-3-8B layer projections at M=%d (prefill) on int8 MFMA" % m,
                 "us_per_layer": round(us, 2), "tokens_per_s": round(m / (us * 1e-6), 1),
                 "useful_TOPS": round(tops, 1), "roofline": roof(tops),

@@ -200,9 +200,9 @@ OVFQ_API int ovfq_project_noalloc_dev(ovfq_ctx* ctx, const ovfq_weight* w, const
  * ovfq_quantize_q8k writes. For Q8_0 weights pass the Q8_0 activation scales in `scales` and NULL bsums.
  * Precondition, as in the reference: bsums[g] is the sum of the 16 quants of group g (QuantizeActivationQ8K's
  * definition, RT/Q4KDotKernel.cs:122-135), which every quantiser here writes. The decode kernels (1 to 8 rows)
- * read the bsums plane as the reference's Dot does; the MFMA kernels that take larger batches form the same
- * sums from the quants themselves. Bsums that are not those sums therefore give results that depend on the
- * row count. */
+ * read the bsums plane as the reference's Dot does, and so does the tiled Q4_K MFMA kernel of large batches (as
+ * fp16, exact for every group sum: |bsums| <= 2032); the other MFMA kernels form the same sums from the quants
+ * themselves. Bsums that are not those sums therefore give results that depend on the row count. */
 OVFQ_API int ovfq_project_prequantized(ovfq_ctx* ctx, const ovfq_weight* w, const int8_t* quants,
                                        const float* scales, const int16_t* bsums, int rows, const float* bias,
                                        float* y);

@@ -7,12 +7,14 @@
 //  Q4_K  mainAcc = sum_e (sc*nib)_e * q8_e. sc*nib <= 945 does not fit int8, so the scale is split as
 //        sc = 8*sc_hi + sc_lo (both in [0,7]); the operands sc_lo*nib and sc_hi*nib are <= 105, two MFMAs give
 //        sum lo*q8 and sum hi*q8, mainAcc = acc_lo + (acc_hi << 3).
-//        minAcc = sum_s m_s * (bsums[2s] + bsums[2s+1]) = sum_e m_{s(e)} * q8_e: a third MFMA whose weight operand
-//        is the sub-block min broadcast over its 32 elements.
+//        minAcc = sum_s m_s * (bsums[2s] + bsums[2s+1]) = sum_e m_{s(e)} * q8_e: in the small-M kernel a third MFMA
+//        whose weight operand is the sub-block min broadcast over its 32 elements; in the tiled kernel one
+//        v_mfma_f32_16x16x16_f16 per 16-row sub-tile over the 16 bsums of each row (|bsums| <= 2032 and m <= 63
+//        are exact in fp16, every partial sum is an integer below 2^24, so the fp32 result is minAcc exactly).
 //  Q6_K  unsignedTerm - 32*bsumTerm = sum_e sc_{s(e)} * (q_e - 32) * q8_e. W = sc*(q-32) lies in [-4064, 4096]
 //        (sc = -128 is a legal scale), split as 128*hi + lo (lo in [0,127], hi in [-32,32]); two MFMAs.
-// Both regroupings use the Q8_K definition bsums[j] = sum of quants 16j..16j+15 (the quantiser's output), so the
-// bsums plane itself is not read. The fp32 tail of each super-block — q8Scale * (d*mainAcc - dmin*minAcc) and
+// The regroupings use the Q8_K definition bsums[j] = sum of quants 16j..16j+15 (the quantiser's output); only the
+// tiled Q4_K kernel reads the bsums plane. The fp32 tail of each super-block — q8Scale * (d*mainAcc - dmin*minAcc) and
 // d*q8Scale*mainAcc (RT/Q4KDotKernel.cs:944, RT/Q6KDotKernel.cs:114-115) — is evaluated per (n, o) in the
 // reference's operation order and accumulated over super-blocks in ascending order from +0, then biasO + sum.
 //
@@ -39,6 +41,8 @@ namespace ovfq {
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 struct MJob {
     const uint8_t* w;
@@ -73,6 +77,7 @@ struct MArgs {
     int spr;      // K / 256
     const int8_t* q;
     const float* s;
+    const int16_t* b;  // Q8_K bsums (Q4_K: the min term's activation operand)
     MGroup grp;
 };
 
@@ -292,6 +297,12 @@ __global__ __launch_bounds__(256, 2) void kquant_mfma_kernel(const MArgs a) {
     constexpr int kDma = NT / 16;  // 1 KiB (4-row) activation DMA chunks per wave per super-block
     __shared__ __align__(16) uint8_t act[2][NT * 256];
     __shared__ __align__(16) float act_s[2][NT];
+    // Q4_K: the min term is one v_mfma_f32_16x16x16_f16 per 16-row sub-tile and super-block, minAcc = sum over the 16
+    // groups k of m_{k/2} * bsums[k], from the activation's bsums (int16 in LDS, [row][16], converted to fp16 as
+    // read) and the sub-block mins: every product and partial sum is an integer below 2^24 (|bsums| <= 16 * 127,
+    // m <= 63), so the fp32 result is minAcc exactly, in place of the third int8 MFMA per 64-element chunk.
+    constexpr bool kMinF16 = F::kNumMfma == 3;
+    __shared__ __align__(16) int16_t act_b[2][kMinF16 ? NT * 16 : 8];
 
     const int wave = wave_id();
     const int lane = threadIdx.x & 63;
@@ -363,7 +374,14 @@ __global__ __launch_bounds__(256, 2) void kquant_mfma_kernel(const MArgs a) {
             return r;
         }
     };
-
+    // Q4_K bsums, 32 bytes a tile row, by LDS DMA with the quants: waves w < NT / 32 move rows 32w .. 32w + 31, lane L
+    // half L % 2 of row 32w + L / 2.
+    const __amdgpu_buffer_rsrc_t br =
+        make_rsrc(a.b + (kMinF16 ? a0 * spr * 16 : 0),
+                  kMinF16 ? rsrc_bytes((uint64_t)a.m_rows * spr * 32, a0 * spr * 32) : 0u);
+    const uint32_t b_src =
+        kMinF16 && wave < NT / 32 ? act_row(32u * wave + ((uint32_t)lane >> 1)) * (uint32_t)spr * 32u + 16u * (lane & 1)
+                                  : 0u;
     // DMA chunk c = wave * kDma + i covers LDS bytes [1024c, 1024c + 1024): lane L writes physical slot L % 16 of
     // row 4c + L / 16, which holds logical slot (L % 16) ^ (row % 16).
     uint32_t dma_src[kDma];
@@ -384,6 +402,10 @@ __global__ __launch_bounds__(256, 2) void kquant_mfma_kernel(const MArgs a) {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 sr, (__attribute__((address_space(3))) void*)&act_s[buf][wave * 64], 4,
                 (int)(s_src + (uint32_t)sb * 4u), 0, 0, 0);
+        if (kMinF16 && wave < NT / 32)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                br, (__attribute__((address_space(3))) void*)&act_b[buf][512 * wave], 16,
+                (int)(b_src + (uint32_t)sb * 32u), 0, 0, 0);
     };
     // A-operand byte offset of logical slot 4t + g in row r16 of a sub-tile: ((4t + g) ^ r16) = 4t ^ (g ^ r16).
     uint32_t a_off[4];
@@ -396,11 +418,37 @@ __global__ __launch_bounds__(256, 2) void kquant_mfma_kernel(const MArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; i++) out[s][i] = 0.0f;
 
-    // MFMAs and fp32 tail of one super-block from the weight operands `op` and the block's d / dmin
-    auto mma_tail = [&](int buf, const i32x4 (&op)[4][F::kNumMfma], float d, float dmin) {
+    // MFMAs and fp32 tail of one super-block from the weight operands `op` and the block's d / dmin; Q4_K: mb = the
+    // min MFMA's B operand (m_{2g}, m_{2g}, m_{2g+1}, m_{2g+1} in fp16: lane group g holds groups 4g .. 4g + 3).
+    auto mma_tail = [&](int buf, const i32x4 (&op)[4][F::kNumMfma], float d, float dmin, u32x2 mb) {
         const uint8_t* tile = act[buf];
 #pragma unroll
         for (int s = 0; s < kSub; s++) {
+            if constexpr (kMinF16) {
+                i32x4 acc[2] = {i32x4{0, 0, 0, 0}, i32x4{0, 0, 0, 0}};
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    const u32x4 av = *reinterpret_cast<const u32x4*>(tile + s * 4096 + a_off[t]);
+                    const i32x4 aop = i32x4{(int)av.x, (int)av.y, (int)av.z, (int)av.w};
+                    acc[0] = mfma16(aop, op[t][0], acc[0]);
+                    acc[1] = mfma16(aop, op[t][1], acc[1]);
+                }
+                // the row's bsums 4g .. 4g + 3 as fp16 (exact: |b| <= 2048)
+                const s16x4 bi = *reinterpret_cast<const s16x4*>(&act_b[buf][(s * 16 + r16) * 16 + 4 * g]);
+                const f16x4 bq = f16x4{(_Float16)bi.x, (_Float16)bi.y, (_Float16)bi.z, (_Float16)bi.w};
+                const f32x4 mn = __builtin_amdgcn_mfma_f32_16x16x16f16(bq,
+                                                                        __builtin_bit_cast(f16x4, mb),
+                                                                        f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                const f32x4 q8s = *reinterpret_cast<const f32x4*>(&act_s[buf][s * 16 + 4 * g]);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int main_acc = acc[0][i] + (acc[1][i] << 3);
+                    // q8Scale * (d * mainAcc - dmin * minAcc)   (RT/Q4KDotKernel.cs:944)
+                    out[s][i] += q8s[i] * (d * (float)main_acc - dmin * mn[i]);
+                }
+                __builtin_amdgcn_sched_barrier(0);  // sub-tiles one after another: fewer live accumulators
+                continue;
+            }
             i32x4 acc[F::kNumMfma];
 #pragma unroll
             for (int k = 0; k < F::kNumMfma; k++) acc[k] = i32x4{0, 0, 0, 0};
@@ -424,7 +472,18 @@ __global__ __launch_bounds__(256, 2) void kquant_mfma_kernel(const MArgs a) {
             F::template operands<1>(w, g, op[1]);
             F::template operands<2>(w, g, op[2]);
             F::template operands<3>(w, g, op[3]);
-            mma_tail(buf, op, F::d_of(w), F::dmin_of(w));
+            u32x2 mb = u32x2{0u, 0u};
+            if constexpr (kMinF16) {
+                // the eight 6-bit mins, one byte each (LD/GgmlDequant.cs:64-79 unpacking); lane group g takes
+                // sub-blocks 2g and 2g + 1
+                const uint32_t m_lo = w.h.z & 0x3f3f3f3fu;
+                const uint32_t m_hi = ((w.h.w >> 4) & 0x0f0f0f0fu) | ((w.h.z >> 2) & 0x30303030u);
+                const uint32_t mg = (g < 2 ? m_lo : m_hi) >> (16 * (g & 1));
+                const uint32_t m0 = __builtin_bit_cast(uint16_t, (_Float16)(mg & 0xffu));
+                const uint32_t m1 = __builtin_bit_cast(uint16_t, (_Float16)((mg >> 8) & 0xffu));
+                mb = u32x2{m0 * 0x00010001u, m1 * 0x00010001u};
+            }
+            mma_tail(buf, op, F::d_of(w), F::dmin_of(w), mb);
         };
         typename F::W wcur = F::load(wr, woff, g);
         stage(0, 0);
@@ -478,7 +537,7 @@ __global__ __launch_bounds__(256, 2) void kquant_mfma_kernel(const MArgs a) {
                     op[t][2] = i32x4{mm, mm, mm, mm};
                 }
             }
-            mma_tail(buf, op, half_lo(p.hdr.y), F::kNumMfma == 3 ? half_hi(p.hdr.y) : 0.0f);
+            mma_tail(buf, op, half_lo(p.hdr.y), F::kNumMfma == 3 ? half_hi(p.hdr.y) : 0.0f, u32x2{0u, 0u});
         };
         PreW pcur = load_pre(0);
         stage(0, 0);
@@ -531,6 +590,8 @@ hipError_t launch_mfma_grouped(int type, const GroupLaunch& L, const int* tiles,
     ma.spr = L.in / kQK;
     ma.q = L.act.q;
     ma.s = L.act.s;
+    ma.b = L.act.b;
+    if (type == 12 && !ma.b) return hipErrorInvalidValue;  // the Q4_K kernel reads the bsums
     for (int e = 0; e < L.experts; e++) {
         ma.grp.w0[e] = L.w0[e];
         ma.grp.w1[e] = L.w1 ? L.w1[e] : nullptr;
@@ -602,6 +663,8 @@ hipError_t launch_project_mfma(int type, const ProjJob* jobs, int njobs, int in,
     ma.spr = in / kQK;
     ma.q = act.q;
     ma.s = act.s;
+    ma.b = act.b;
+    if (type == 12 && !ma.b) return hipErrorInvalidValue;  // the Q4_K kernel reads the bsums
     const int nt = mfma_tile_rows(rows);
     if (type == 12)
         return nt == 128 ? launch_mfma<Q4KMfma, 128>(ma, pre, st) : launch_mfma<Q4KMfma, 64>(ma, pre, st);
