@@ -422,33 +422,47 @@ __global__ __launch_bounds__(256, 2) void kquant_mfma_kernel(const MArgs a) {
     // min MFMA's B operand (m_{2g}, m_{2g}, m_{2g+1}, m_{2g+1} in fp16: lane group g holds groups 4g .. 4g + 3).
     auto mma_tail = [&](int buf, const i32x4 (&op)[4][F::kNumMfma], float d, float dmin, u32x2 mb) {
         const uint8_t* tile = act[buf];
+        if constexpr (kMinF16) {
+            // Sub-tile s's MFMAs, then sub-tile s - 1's tail (its results are ready by then), one stage after another:
+            // two sub-tiles' accumulators live, not all four (left to itself the compiler overlaps every sub-tile and
+            // needs 132-146 VGPRs, three waves per SIMD). The same staging measured slower for Q6_K.
+            i32x4 pacc[2];
+            f32x4 pmn;
+#pragma unroll
+            for (int s = 0; s <= kSub; s++) {
+                i32x4 acc[2] = {i32x4{0, 0, 0, 0}, i32x4{0, 0, 0, 0}};
+                f32x4 mn = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                if (s < kSub) {
+#pragma unroll
+                    for (int t = 0; t < 4; t++) {
+                        const u32x4 av = *reinterpret_cast<const u32x4*>(tile + s * 4096 + a_off[t]);
+                        const i32x4 aop = i32x4{(int)av.x, (int)av.y, (int)av.z, (int)av.w};
+                        acc[0] = mfma16(aop, op[t][0], acc[0]);
+                        acc[1] = mfma16(aop, op[t][1], acc[1]);
+                    }
+                    // the row's bsums 4g .. 4g + 3 as fp16 (exact: |b| <= 2048)
+                    const s16x4 bi = *reinterpret_cast<const s16x4*>(&act_b[buf][(s * 16 + r16) * 16 + 4 * g]);
+                    const f16x4 bq = f16x4{(_Float16)bi.x, (_Float16)bi.y, (_Float16)bi.z, (_Float16)bi.w};
+                    mn = __builtin_amdgcn_mfma_f32_16x16x16f16(bq, __builtin_bit_cast(f16x4, mb), mn, 0, 0, 0);
+                }
+                if (s > 0) {
+                    const f32x4 q8s = *reinterpret_cast<const f32x4*>(&act_s[buf][(s - 1) * 16 + 4 * g]);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int main_acc = pacc[0][i] + (pacc[1][i] << 3);
+                        // q8Scale * (d * mainAcc - dmin * minAcc)   (RT/Q4KDotKernel.cs:944)
+                        out[s - 1][i] += q8s[i] * (d * (float)main_acc - dmin * pmn[i]);
+                    }
+                }
+                pacc[0] = acc[0];
+                pacc[1] = acc[1];
+                pmn = mn;
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            return;
+        }
 #pragma unroll
         for (int s = 0; s < kSub; s++) {
-            if constexpr (kMinF16) {
-                i32x4 acc[2] = {i32x4{0, 0, 0, 0}, i32x4{0, 0, 0, 0}};
-#pragma unroll
-                for (int t = 0; t < 4; t++) {
-                    const u32x4 av = *reinterpret_cast<const u32x4*>(tile + s * 4096 + a_off[t]);
-                    const i32x4 aop = i32x4{(int)av.x, (int)av.y, (int)av.z, (int)av.w};
-                    acc[0] = mfma16(aop, op[t][0], acc[0]);
-                    acc[1] = mfma16(aop, op[t][1], acc[1]);
-                }
-                // the row's bsums 4g .. 4g + 3 as fp16 (exact: |b| <= 2048)
-                const s16x4 bi = *reinterpret_cast<const s16x4*>(&act_b[buf][(s * 16 + r16) * 16 + 4 * g]);
-                const f16x4 bq = f16x4{(_Float16)bi.x, (_Float16)bi.y, (_Float16)bi.z, (_Float16)bi.w};
-                const f32x4 mn = __builtin_amdgcn_mfma_f32_16x16x16f16(bq,
-                                                                        __builtin_bit_cast(f16x4, mb),
-                                                                        f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-                const f32x4 q8s = *reinterpret_cast<const f32x4*>(&act_s[buf][s * 16 + 4 * g]);
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int main_acc = acc[0][i] + (acc[1][i] << 3);
-                    // q8Scale * (d * mainAcc - dmin * minAcc)   (RT/Q4KDotKernel.cs:944)
-                    out[s][i] += q8s[i] * (d * (float)main_acc - dmin * mn[i]);
-                }
-                __builtin_amdgcn_sched_barrier(0);  // sub-tiles one after another: fewer live accumulators
-                continue;
-            }
             i32x4 acc[F::kNumMfma];
 #pragma unroll
             for (int k = 0; k < F::kNumMfma; k++) acc[k] = i32x4{0, 0, 0, 0};
