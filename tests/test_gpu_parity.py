@@ -319,6 +319,32 @@ def test_multi_projection_rows_bit_exact(orc, ctx, batched, rows, kernel):
         assert_bit_exact(y.cpu().numpy().reshape(rows, -1), ref, f"multi prequantized rows={rows} job {i}")
 
 
+@pytest.mark.parametrize("rows,kernel", [(4, "auto"), (40, "tiled")])
+def test_prequantized_bsums_read_as_reference(orc, ctx, batched, rows, kernel):
+    """The decode kernel (up to 8 rows) and the tiled Q4_K MFMA kernel take the min term from the caller's bsums, as
+    the reference's Dot does (RT/Q4KDotKernel.cs:249-253): with bsums that are not the group sums (every group
+    shifted, within the fp16-exact range |b| <= 2048), both match the oracle's prequantised batched projection
+    bit for bit."""
+    case("prequantized bsums", rows, kernel)
+    batched(kernel)
+    rng = np.random.default_rng(700 + rows)
+    k, n = 1024, 128
+    blocks = _kq_blocks(rng, "q4k", n, k)
+    w = ov.Q4KWeight(blocks, k, n)
+    x = normal(rng, (rows, k))
+    q, s, b = orc.quantize_q8k(x)
+    b = (b.astype(np.int32) + rng.integers(-9, 10, b.shape)).clip(-2048, 2048).astype(np.int16)
+    ref = np.zeros((rows, n), np.float32)
+    L = orc.lib()
+    rc = L.orc_q4k_project_batched_prequantized(rows, orc.P(np.ascontiguousarray(blocks, np.uint8)), k, n, None,
+                                                 orc.P(ref), orc.P(q), orc.P(s), orc.P(b))
+    assert rc == 0
+    y = torch.empty(rows * n, device=DEV)
+    ctx.project_prequantized_dev(w, t(q), t(s), t(b), y, rows=rows)
+    torch.cuda.synchronize()
+    assert_bit_exact(y.cpu().numpy().reshape(rows, n), ref, f"prequantized shifted bsums rows={rows} {kernel}")
+
+
 @pytest.mark.parametrize("rows,kernel", [(1, "auto"), (5, "auto"), (5, "tiled"), (70, "auto")])
 def test_q8_0_multi_projection_rows_bit_exact(orc, ctx, batched, rows, kernel):
     """Fused Q8_0 q/k/v-style call over `rows` activation rows (the decode kernel up to 8 rows with rows x K <= 32768,
@@ -930,6 +956,9 @@ def test_kquant_prefill_range_extremes(orc, batched, kernel, rows, k, fmt):
     rng = np.random.default_rng(5)
     x = np.sign(normal(rng, (rows, k))).astype(np.float32)  # every quant +-127
     x[1::2] = normal(rng, (rows // 2, k))
+    x[0] = 1.0                 # every group sum +2032 (the tiled Q4_K kernel's fp16 bsums at their largest)
+    x[-1, : k // 2] = -1.0     # and -2032
+    x[-1, k // 2:] = 1.0
     w = (ov.Q4KWeight if fmt == "q4k" else ov.Q6KWeight)(blocks, k, n)
     ref = (orc.q4k_project_batched if fmt == "q4k" else orc.q6k_project_batched)(x, rows, blocks, k, n)
     assert_bit_exact(ov.project(w, x, None, rows=rows).reshape(rows, n), ref, f"{fmt} extremes")
