@@ -23,9 +23,9 @@
 // the lane's own weight row, built in registers straight from the GGUF bytes), so the 4 results a lane holds,
 // D[4*(lane/16) + i][lane % 16], all belong to its own weight row: d, dmin and the bias stay lane-local. In both
 // operands byte j of lane-group g = lane / 16 carries K index 16*g + j of a 64-element chunk.
-// Per super-block the workgroup stages NT rows x 256 quants (+ scales) in LDS (double-buffered; 272-byte row stride
-// keeps the 16 lanes reading one K slice on distinct banks) while the next super-block's weights and activation
-// are in flight. Workgroups are numbered XCD-aware: the workgroups of one weight tile run consecutively on the
+// Per super-block the workgroup stages NT rows x 256 quants (+ scales, and for Q4_K the rows' bsums) in LDS by DMA
+// (double-buffered; 256-byte rows whose 16-byte slots are XOR-swizzled by row, so the 16 lanes reading one K slice
+// hit distinct banks) while the next super-block's weights and activation are in flight. Workgroups are numbered XCD-aware: the workgroups of one weight tile run consecutively on the
 // same XCD (blockIdx % 8), so its bytes come from HBM once and from that XCD's L2 for the other activation tiles.
 #include <algorithm>
 #include <cstdlib>
