@@ -604,6 +604,45 @@ def test_moe_select_topk_matches_oracle(orc, normalize):
         assert np.array_equal(li[n * 5:n * 5 + 3], ri) and np.all(li[n * 5 + 3:(n + 1) * 5] == 99)
 
 
+@pytest.mark.parametrize("normalize", [True, False])
+def test_moe_select_topk_non_finite_logits(orc, normalize):
+    """Router logits with +inf, -inf and NaN entries (and a row of all -inf): the selection follows the reference's
+    comparisons (RT/MoeRouter.cs:66-91, where a NaN never compares greater or less-or-equal), on the standalone top-k
+    launch and inside the routed MoE launch, against the oracle; weights NaN where the reference's are."""
+    case("moe topk non-finite", normalize)
+    rng = np.random.default_rng(90 + normalize)
+    rows, E, k = 6, 8, 3
+    logits = rng.random((rows, E)).astype(np.float32)
+    logits[0, 4] = np.inf
+    logits[1, 2] = -np.inf
+    logits[2, 5] = np.nan
+    logits[3, 0] = np.nan
+    logits[3, 7] = np.inf
+    logits[4, :] = -np.inf
+    logits[5, 1] = np.nan
+    logits[5, 6] = -np.inf
+    idx = torch.zeros(rows * k, dtype=torch.int32, device=DEV)
+    w = torch.zeros(rows * k, dtype=torch.float32, device=DEV)
+    assert ov.MoeRouter.SelectTopK(t(logits), k, idx, w, normalize, rows=rows) == k
+    torch.cuda.synchronize()
+    gi, gw = idx.cpu().numpy().reshape(rows, k), w.cpu().numpy().reshape(rows, k)
+    for n in range(rows):
+        ri, rw = orc.moe_select_topk(logits[n], k, normalize)
+        assert np.array_equal(gi[n], ri), (n, gi[n], ri)
+        np.testing.assert_allclose(gw[n], rw, rtol=4e-7, atol=0, equal_nan=True)
+    # the same selection inside the routed launch (routing fused into the grouping launch at rows * k <= 64)
+    dm, dff = 256, 256
+    gb = [orc.quantize_q4k(normal(rng, (dff, dm), 0.05)) for _ in range(E)]
+    db = [orc.quantize_q4k(normal(rng, (dm, dff), 0.05)) for _ in range(E)]
+    gws = [ov.Q4KWeight(b, dm, dff) for b in gb]
+    dws = [ov.Q4KWeight(b, dff, dm) for b in db]
+    x = normal(rng, (rows, dm))
+    _, ri, rw = ov.moe_ffn_routed(gws, gws, dws, t(x), rows, t(logits), k, normalize)
+    torch.cuda.synchronize()
+    assert np.array_equal(ri.cpu().numpy().reshape(rows, k), gi)
+    assert np.array_equal(rw.cpu().numpy().view(np.int32), w.cpu().numpy().view(np.int32))
+
+
 def _moe_check(y, ref, what):
     y = np.asarray(y, np.float32).reshape(ref.shape)
     rel, cos = north_star(y, ref)
