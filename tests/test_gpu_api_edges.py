@@ -179,3 +179,38 @@ def test_graph_replay_after_scratch_growth(orc):
     import gc
     gc.collect()
     ctx.close()
+
+
+def test_reset_stream_and_swiglu_dev(orc):
+    """ovfq_ffn_swiglu_dev equals ovfq_ffn_gated_dev with OVFQ_FFN_SWIGLU bit for bit, on a stream bound with
+    ovfq_ctx_set_stream and again after ovfq_ctx_reset_stream returns the context to its own stream (whose work
+    ovfq_ctx_synchronize then waits for)."""
+    case("reset stream + swiglu dev")
+    rng = np.random.default_rng(71)
+    dm, dff, rows = 256, 512, 3
+    ctx = ov.Context(0)
+    gate = ov.Q4KWeight(random_q4k_blocks(rng, dff * dm // 256).reshape(dff, -1), dm, dff, ctx=ctx)
+    up = ov.Q4KWeight(random_q4k_blocks(rng, dff * dm // 256).reshape(dff, -1), dm, dff, ctx=ctx)
+    down = ov.Q6KWeight(random_q6k_blocks(rng, dm * dff // 256).reshape(dm, -1), dff, dm, ctx=ctx)
+    x = t(normal(rng, (rows, dm)))
+    lib = ctx.lib
+    ys = [torch.empty(rows * dm, device=DEV) for _ in range(3)]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        ctx.set_stream(side.cuda_stream)
+        assert lib.ovfq_ffn_swiglu_dev(ctx.handle, gate.handle, up.handle, down.handle, vp(x), rows, vp(ys[0])) == 0
+        assert lib.ovfq_ffn_gated_dev(ctx.handle, gate.handle, up.handle, down.handle, vp(x), rows,
+                                      _lib.OVFQ_FFN_SWIGLU, vp(ys[1])) == 0
+        side.synchronize()
+    assert lib.ovfq_ctx_reset_stream(ctx.handle) == 0
+    torch.cuda.synchronize()
+    assert lib.ovfq_ffn_swiglu_dev(ctx.handle, gate.handle, up.handle, down.handle, vp(x), rows, vp(ys[2])) == 0
+    assert lib.ovfq_ctx_synchronize(ctx.handle) == 0
+    a, b, c = (y.cpu().numpy().view(np.uint32) for y in ys)
+    assert np.array_equal(a, b), "swiglu_dev differs from gated_dev(SWIGLU)"
+    assert np.array_equal(a, c), "result on the context's own stream differs"
+    del gate, up, down
+    import gc
+    gc.collect()
+    ctx.close()
