@@ -1206,11 +1206,13 @@ static int moe_impl(ovfq_ctx* ctx, int E, const ovfq_weight* const* gate, const 
     const bool grouped_big = !small_ok || ctx->batched_kernel == OVFQ_BATCHED_TILED ||
                              (ctx->batched_kernel == OVFQ_BATCHED_AUTO && P >= (size_t)grouped_min * E);
     const int max_tiles = (int)((P + ovfq::kGroupedTileRows - 1) / ovfq::kGroupedTileRows) + E;
-    auto carve = [&](Carver& c, int** off, int** prow, int** pof, float** g, float** u, int8_t** iq, float** is,
-                     int16_t** ib, float** out, float** hx, int** hidx, float** hw, float** hy, float** hl) {
+    auto carve = [&](Carver& c, int** off, int** prow, int** pof, float** pw, float** g, float** u, int8_t** iq,
+                     float** is, int16_t** ib, float** out, float** hx, int** hidx, float** hw, float** hy,
+                     float** hl) {
         *off = c.take<int>((size_t)(E + 2 + max_tiles) * 4);  // expert_off[E + 1], tile count, tile list
         *prow = c.take<int>(P * 4);
         *pof = c.take<int>(P * 4);
+        *pw = c.take<float>(P * 4);
         *g = c.take<float>(P * dff * 4);
         *u = c.take<float>(P * dff * 4);
         *iq = c.take<int8_t>(P * dff);
@@ -1226,14 +1228,14 @@ static int moe_impl(ovfq_ctx* ctx, int E, const ovfq_weight* const* gate, const 
         }
     };
     int *off, *prow, *pof, *hidx = nullptr;
-    float *g, *u, *is, *out, *hx = nullptr, *hw = nullptr, *hy = nullptr, *hl = nullptr;
+    float *pw, *g, *u, *is, *out, *hx = nullptr, *hw = nullptr, *hy = nullptr, *hl = nullptr;
     int8_t* iq;
     int16_t* ib;
     Carver sizing{nullptr};
-    carve(sizing, &off, &prow, &pof, &g, &u, &iq, &is, &ib, &out, &hx, &hidx, &hw, &hy, &hl);
+    carve(sizing, &off, &prow, &pof, &pw, &g, &u, &iq, &is, &ib, &out, &hx, &hidx, &hw, &hy, &hl);
     if ((rc = ensure(ctx, ctx->moe, sizing.used))) return rc;
     Carver c{static_cast<char*>(ctx->moe.p)};
-    carve(c, &off, &prow, &pof, &g, &u, &iq, &is, &ib, &out, &hx, &hidx, &hw, &hy, &hl);
+    carve(c, &off, &prow, &pof, &pw, &g, &u, &iq, &is, &ib, &out, &hx, &hidx, &hw, &hy, &hl);
     const float* xd = x;
     const float* ld = logits;
     int* idxd = const_cast<int*>(idx);  // written only when routing here (then the caller's output)
@@ -1296,7 +1298,6 @@ static int moe_impl(ovfq_ctx* ctx, int E, const ovfq_weight* const* gate, const 
         HIP_TRY(ovfq::launch_mfma_grouped(gt, L, tiles, tile_count, max_tiles, ctx->stream));
     else
         HIP_TRY(ovfq::launch_mfma_small(gt, L, ctx->stream));
-    HIP_TRY(ovfq::launch_gate_up_q8k(g, u, off, E, (int)P, dff, false, iq, is, ib, ctx->stream));
     ovfq::GroupLaunch D{};
     D.w0 = dw;
     D.y0 = out;
@@ -1308,11 +1309,22 @@ static int moe_impl(ovfq_ctx* ctx, int E, const ovfq_weight* const* gate, const 
     D.pair_row = nullptr;  // the intermediate is already pair-major
     D.act = ovfq::ActQ{iq, is, ib};
     D.pairs = (int)P;
+    // With top-1 / top-2 and the down projection on the expert-stream kernel, the combine is folded into it: each
+    // token output gets at most two float-atomic adds onto zero, whose sum does not depend on their order, so it is
+    // the combine kernel's (0 + w0 o0) + w1 o1 exactly. The zeroing and the per-pair weights go in the gate * up launch.
+    ovfq::MoeFold fold{};
+    if (k <= 2 && !grouped_big && ovfq::mfma_small_streams(dt, D)) {
+        fold = ovfq::MoeFold{yd, (int64_t)rows * dmodel, pof, wd, (int)P, pw};
+        D.comb = yd;
+        D.comb_tok = prow;
+        D.comb_w = pw;
+    }
+    HIP_TRY(ovfq::launch_gate_up_q8k(g, u, off, E, (int)P, dff, false, iq, is, ib, ctx->stream, fold));
     if (grouped_big)
         HIP_TRY(ovfq::launch_mfma_grouped(dt, D, tiles, tile_count, max_tiles, ctx->stream));
     else
         HIP_TRY(ovfq::launch_mfma_small(dt, D, ctx->stream));
-    HIP_TRY(ovfq::launch_moe_combine(out, pof, wd, rows, k, dmodel, yd, ctx->stream));
+    if (!D.comb) HIP_TRY(ovfq::launch_moe_combine(out, pof, wd, rows, k, dmodel, yd, ctx->stream));
     if (host) {
         HIP_TRY(hipMemcpyAsync(y, yd, (size_t)rows * dmodel * 4, hipMemcpyDeviceToHost, ctx->stream));
         if (route) {

@@ -736,6 +736,9 @@ struct SArgs {
     const int* pair_row;
     const int8_t* q;
     const float* s;
+    float* comb;            // expert-stream kernel: add comb_w[pair] * value to comb[comb_tok[pair]] (GroupLaunch)
+    const int* comb_tok;
+    const float* comb_w;
 };
 
 template <class F, int kBatch, bool kPipe>
@@ -934,12 +937,19 @@ __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int
     __shared__ __align__(16) uint8_t aring[D][kStreamA];
     __shared__ __align__(16) uint8_t sring[D][kStreamS];
     __shared__ int eoff[kMaxExperts + 1];
-    extern __shared__ int prow[];  // pairs entries
+    extern __shared__ int prow[];  // pairs entries; with comb, then the pairs' tokens and combine weights
+    int* ctok = prow + pairs;
+    float* cw = reinterpret_cast<float*>(prow + 2 * pairs);
     const int tid = threadIdx.x, wave = wave_id(), lane = tid & 63;
     const int g = lane >> 4, r16 = lane & 15;
     // without a pair list: one expert over activation rows 0 .. rows - 1 (a dense small batch)
     for (int i = tid; i <= n_experts; i += 256) eoff[i] = a.expert_off ? a.expert_off[i] : (i == 0 ? 0 : a.rows);
     for (int i = tid; i < pairs; i += 256) prow[i] = a.pair_row ? a.pair_row[i] : i;
+    if (a.comb)
+        for (int i = tid; i < pairs; i += 256) {
+            ctok[i] = a.comb_tok[i];
+            cw[i] = a.comb_w[i];
+        }
     __syncthreads();
 
     const int spr = a.spr;
@@ -1139,8 +1149,26 @@ __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const int pr = cur.n0 + 4 * j + g;
-                if (j < live && pr < cur.cnt && o < a.n_rows)
-                    y[(size_t)(cur.pbeg + pr) * a.n_rows + o] = bias ? bias[o] + run[j] : run[j];
+                if (j < live && pr < cur.cnt && o < a.n_rows) {
+                    const float v = bias ? bias[o] + run[j] : run[j];
+                    const int p = cur.pbeg + pr;
+                    if (a.comb) {
+                        // explicit LDS reads, like prow_at's (a compiler read would wait for the rings' DMAs)
+                        const uint32_t ta = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int*)(ctok + p);
+                        const uint32_t wa = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)(cw + p);
+                        int tok;
+                        float wt;
+                        asm volatile("ds_read_b32 %0, %2\n\tds_read_b32 %1, %3\n\ts_waitcnt lgkmcnt(0)"
+                                     : "=v"(tok), "=v"(wt)
+                                     : "v"(ta), "v"(wa)
+                                     : "memory");
+                        const float prod = wt * v;
+                        __hip_atomic_fetch_add(a.comb + (size_t)tok * a.n_rows + o, prod, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+                    } else {
+                        y[(size_t)p * a.n_rows + o] = v;
+                    }
+                }
                 run[j] = 0.0f;
             }
         }
@@ -1204,6 +1232,13 @@ bool stream_pair_preferred(int type, int in, int n_rows) {
     return stream_enabled() && type == 12 && mfma_small_supported(type, in) && stream_dense_ok(2, n_rows);
 }
 
+bool mfma_small_streams(int type, const GroupLaunch& L) {
+    const int nmat = L.w1 ? 2 : 1;
+    const int pairs = L.expert_off ? L.pairs : L.rows;
+    return stream_enabled() && type == 12 && (L.expert_off || stream_dense_ok(nmat, L.n_rows)) && pairs > 0 &&
+           pairs <= kStreamMaxPairs;
+}
+
 hipError_t launch_mfma_small(int type, const GroupLaunch& L, hipStream_t st) {
     SArgs sa{};
     for (int i = 0; i < L.experts; i++) {
@@ -1222,10 +1257,14 @@ hipError_t launch_mfma_small(int type, const GroupLaunch& L, hipStream_t st) {
     sa.pair_row = L.pair_row;
     sa.q = L.act.q;
     sa.s = L.act.s;
+    sa.comb = L.comb;
+    sa.comb_tok = L.comb_tok;
+    sa.comb_w = L.comb_w;
     const int nmat = L.w1 ? 2 : 1;
     const int pairs = L.expert_off ? L.pairs : L.rows;
-    if (stream_enabled() && type == 12 && (L.expert_off || stream_dense_ok(nmat, sa.n_rows)) && pairs > 0 &&
-        pairs <= kStreamMaxPairs) {
+    const bool streams = mfma_small_streams(type, L);
+    if (L.comb && (!streams || nmat != 1 || !L.expert_off || !L.comb_tok || !L.comb_w)) return hipErrorInvalidValue;
+    if (streams) {
         sa.tiles = (sa.n_rows + kStreamRows - 1) / kStreamRows;  // 64-row groups
         const long units = (long)L.experts * nmat * sa.tiles;
         int dev = 0, cus = 256;
@@ -1237,7 +1276,7 @@ hipError_t launch_mfma_small(int type, const GroupLaunch& L, hipStream_t st) {
             const char* v = getenv("OVFQ_MOE_STREAM_WG");
             return v && *v ? atoi(v) : 0;
         }();
-        const size_t dyn = (size_t)pairs * sizeof(int);
+        const size_t dyn = (size_t)pairs * sizeof(int) * (L.comb ? 3 : 1);
         const int per_cu = per_cu_env ? per_cu_env : (stream_lds_bytes() + dyn <= 160 * 1024 / 4 ? 4 : 3);
         const int grid = (int)std::min<long>(units, (long)cus * per_cu);
         hipLaunchKernelGGL(q4k_mfma_stream_kernel<3>, dim3(grid), dim3(256), dyn, st, sa, L.experts, nmat, pairs);

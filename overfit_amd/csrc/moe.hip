@@ -11,6 +11,7 @@
 //   6. y[token] = sum over top-k slots, in slot order, of weight * expert output     -> moe_combine_kernel
 // Pairs are numbered expert-major (expert 0's tokens first, ascending), which is the order the reference
 // gathers rows in; pair_of[token * k + slot] maps a slot back to its pair.
+#include <algorithm>
 #include <cmath>
 
 #include "ovfq_device.h"
@@ -327,11 +328,22 @@ __global__ __launch_bounds__(256) void moe_route_plan_kernel(const float* __rest
 // projection's BatchedQuantProjection.Dispatch applies to its input (RT/Q4KDotKernel.cs:71-136). act is SiLU,
 // g * sigmoid(g) (ApplySiLU :464-472), or with GELU the tanh approximation 0.5 g (1 + tanh(sqrt(2/pi) (g + 0.044715
 // g^3))) in ApplyGeLU's operation order (:498-517). Pairs at or past expert_off[n_experts] are skipped.
+// The launch also does the MoeFold work (zeroing the step's output, the per-pair combine weights), one element per
+// thread of the grid, which covers both.
 template <bool GELU>
 __global__ __launch_bounds__(256) void gate_up_q8k_kernel(const float* __restrict__ gate, const float* __restrict__ up,
                                                          const int* __restrict__ expert_off, int n_experts,
                                                          int max_pairs, int spr, int8_t* __restrict__ q,
-                                                         float* __restrict__ s, int16_t* __restrict__ bs) {
+                                                         float* __restrict__ s, int16_t* __restrict__ bs,
+                                                         const MoeFold fold) {
+    {
+        const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+        for (int64_t j = i * 4; j < fold.y_len && j < i * 4 + 4; j++) fold.y[j] = 0.0f;
+        if (i < fold.slots) {
+            const int p = fold.pair_of[i];
+            if (p >= 0) fold.pw[p] = fold.w[i];
+        }
+    }
     const int64_t blk = (int64_t)blockIdx.x * 4 + wave_id();
     if (blk >= (int64_t)max_pairs * spr) return;
     const int lane = threadIdx.x & 63;
@@ -466,16 +478,18 @@ hipError_t launch_moe_plan(const int* idx, int rows, int k, int n_experts, int* 
 }
 
 hipError_t launch_gate_up_q8k(const float* gate, const float* up, const int* expert_off, int n_experts, int max_pairs,
-                              int dff, bool gelu, int8_t* q, float* s, int16_t* b, hipStream_t st) {
+                              int dff, bool gelu, int8_t* q, float* s, int16_t* b, hipStream_t st,
+                              const MoeFold& fold) {
     const int spr = dff / kQK;
     const int64_t waves = (int64_t)max_pairs * spr;
-    const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
+    const int64_t fold_threads = std::max<int64_t>((fold.y_len + 3) / 4, fold.slots);
+    const dim3 grid((unsigned)std::max((waves + 3) / 4, (fold_threads + 255) / 256)), block(256);
     if (gelu)
         hipLaunchKernelGGL(gate_up_q8k_kernel<true>, grid, block, 0, st, gate, up, expert_off, n_experts, max_pairs, spr,
-                           q, s, b);
+                           q, s, b, fold);
     else
         hipLaunchKernelGGL(gate_up_q8k_kernel<false>, grid, block, 0, st, gate, up, expert_off, n_experts, max_pairs,
-                           spr, q, s, b);
+                           spr, q, s, b, fold);
     return hipGetLastError();
 }
 

@@ -73,12 +73,20 @@ struct GroupLaunch {
     const int* pair_row;
     ActQ act;
     int pairs = 0;  // grouped launches: the pair count bound (rows x top_k), sizing the pair -> row map
+    // Grouped single-matrix launches that take the expert-stream kernel only (mfma_small_streams): instead of
+    // storing y0[pair][o], add comb_w[pair] * value to comb[comb_tok[pair]][o] with a float atomic (comb zeroed
+    // beforehand). Exact when at most two pairs add to one output: (0 + a) + b == (0 + b) + a in fp32.
+    float* comb = nullptr;
+    const int* comb_tok = nullptr;
+    const float* comb_w = nullptr;
 };
 // On MFMA with super-block-parallel waves (mfma.hip), 16 activation rows per tile.
 bool mfma_small_supported(int type, int in);
 // Whether a gate/up-shaped pair of Q4_K weights (n_rows outputs each, `in` inputs) runs on the expert-stream kernel
 // when it takes the small-M path.
 bool stream_pair_preferred(int type, int in, int n_rows);
+// Whether launch_mfma_small runs this launch on the expert-stream kernel (the one that supports comb).
+bool mfma_small_streams(int type, const GroupLaunch& launch);
 hipError_t launch_mfma_small(int type, const GroupLaunch& launch, hipStream_t st);
 // MFMA-ready copy of a Q4_K / Q6_K weight: its size, and the kernel that writes it from the GGUF blocks.
 size_t mfma_prepared_bytes(int in, int out);
@@ -106,9 +114,20 @@ hipError_t launch_moe_route_plan(const float* logits, int rows, int k, int n_exp
 hipError_t launch_mfma_grouped(int type, const GroupLaunch& launch, const int* tiles, const int* tile_count,
                                int max_tiles, hipStream_t st);
 constexpr int kGroupedTileRows = 64;
+// Work for a MoE step whose down projection adds into its output (GroupLaunch::comb), done in the launch before it:
+// y[0 .. y_len) = 0, and pw[pair_of[i]] = w[i] for the slots i < slots that hold a pair (pair_of[i] >= 0).
+struct MoeFold {
+    float* y = nullptr;
+    int64_t y_len = 0;
+    const int* pair_of = nullptr;
+    const float* w = nullptr;
+    int slots = 0;
+    float* pw = nullptr;
+};
 // act(gate) * up (act: SiLU, or GELU with the tanh approximation), quantised to Q8_K for the down projection.
 hipError_t launch_gate_up_q8k(const float* gate, const float* up, const int* expert_off, int n_experts, int max_pairs,
-                              int dff, bool gelu, int8_t* q, float* s, int16_t* b, hipStream_t st);
+                              int dff, bool gelu, int8_t* q, float* s, int16_t* b, hipStream_t st,
+                              const MoeFold& fold = MoeFold{});
 hipError_t launch_moe_combine(const float* out, const int* pair_of, const float* w, int rows, int k, int dmodel,
                               float* y, hipStream_t st);
 
