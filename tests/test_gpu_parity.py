@@ -761,6 +761,43 @@ def test_moe_ffn_matches_oracle(orc, gfmt, dfmt):
     _moe_check(ov.moe_ffn(gw, uw, dw, x, rows, k, idx2, w), ref2, f"{gfmt}/{dfmt} sparse routing")
 
 
+@pytest.mark.parametrize("k", [1, 2])
+def test_moe_ffn_top2_combine_bit_exact(orc, k):
+    """Top-1 / top-2 with Q4_K experts on few pairs: the down launch adds weight * expert output into y with float
+    atomics instead of a combine launch. y must equal, bit for bit, the reference's in-order combine
+    (0 + w0 o0) + w1 o1 (RT/MoeFeedForwardBlock.cs:225-239) of each expert's output, taken here from the one-token
+    SwiGLU FFN on the same expert (the same projections and SiLU launch, bit-identical per pair), with an unclaimed
+    slot and a repeated index adding nothing, y first filled with NaN (every element written), and a second call
+    with fewer tokens into the same buffer (no stale sums)."""
+    case("moe top-k combine fold", k)
+    rng = np.random.default_rng(400 + k)
+    E, dm, dff, rows = 8, 256, 512, 16
+    gw, uw, dw = ([ov.Q4KWeight(orc.quantize_q4k(normal(rng, shp, 0.05)), shp[1], shp[0]) for _ in range(E)]
+                  for shp in ((dff, dm), (dff, dm), (dm, dff)))
+    x = normal(rng, (rows, dm))
+    idx = np.stack([rng.choice(E, k, replace=False) for _ in range(rows)]).astype(np.int32)
+    w = (rng.random((rows, k)) - 0.3).astype(np.float32)  # signed weights
+    idx[3, 0] = E + 1  # unclaimed slot
+    if k == 2:
+        idx[5] = [4, 4]  # the repeat contributes nothing
+    y = torch.full((rows * dm,), float("nan"), device=DEV)
+    for n in (rows, 5):
+        out = ov.moe_ffn(gw, uw, dw, t(x[:n]), n, k, t(idx[:n]), t(w[:n]), out=y[: n * dm])
+        torch.cuda.synchronize()
+        got = out.cpu().numpy().reshape(n, dm)
+        want = np.zeros((n, dm), np.float32)
+        for tok in range(n):
+            seen = set()
+            for j in range(k):
+                e = int(idx[tok, j])
+                if e < 0 or e >= E or e in seen:
+                    continue
+                seen.add(e)
+                o = ov.ffn_swiglu(gw[e], uw[e], dw[e], t(x[tok:tok + 1]), 1).cpu().numpy()
+                want[tok] = want[tok] + np.float32(w[tok, j]) * o
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"top-{k}, {n} tokens: combine differs"
+
+
 @pytest.mark.parametrize("rows,E,k,normalize", [(16, 8, 2, True), (30, 8, 1, False), (4, 16, 4, True),
                                                  (40, 8, 2, True), (64, 4, 1, True), (3, 32, 16, False),
                                                  (1, 64, 20, True)])
