@@ -1269,15 +1269,17 @@ hipError_t launch_mfma_small(int type, const GroupLaunch& L, hipStream_t st) {
         const long units = (long)L.experts * nmat * sa.tiles;
         int dev = 0, cus = 256;
         if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-        // Workgroups per CU: as many as the kernel's LDS allows (four up to 140 pairs, else three). Measured on MI355X
-        // (config-5 MoE step): a 5-slot ring at two per CU leaves the down launch (512 units) unchanged, 64.4 vs
-        // 64.6 us, and makes gate/up 11 % slower.
+        // Workgroups per CU: three (two if the pair map's LDS does not fit three). Measured on MI355X (config-5 MoE
+        // step, whose gate/up launch has 3584 units): three per CU, 179.6 us mean of five alternating runs against
+        // 181.3 us at four (LDS would allow four up to 140 pairs); 896 or 640 workgroups were slower, 188-190 us. A
+        // 5-slot ring at two per CU leaves the down launch (512 units) unchanged, 64.4 vs 64.6 us, and makes gate/up
+        // 11 % slower.
         static const int per_cu_env = [] {
             const char* v = getenv("OVFQ_MOE_STREAM_WG");
             return v && *v ? atoi(v) : 0;
         }();
         const size_t dyn = (size_t)pairs * sizeof(int) * (L.comb ? 3 : 1);
-        const int per_cu = per_cu_env ? per_cu_env : (stream_lds_bytes() + dyn <= 160 * 1024 / 4 ? 4 : 3);
+        const int per_cu = per_cu_env ? per_cu_env : (stream_lds_bytes() + dyn <= 160 * 1024 / 3 ? 3 : 2);
         const int grid = (int)std::min<long>(units, (long)cus * per_cu);
         hipLaunchKernelGGL(q4k_mfma_stream_kernel<3>, dim3(grid), dim3(256), dyn, st, sa, L.experts, nmat, pairs);
         return hipGetLastError();
