@@ -1271,7 +1271,8 @@ hipError_t launch_mfma_small(int type, const GroupLaunch& L, hipStream_t st) {
         if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
         // Workgroups per CU: three (two if the pair map's LDS does not fit three). Measured on MI355X (config-5 MoE
         // step, whose gate/up launch has 3584 units): three per CU, 179.6 us mean of five alternating runs against
-        // 181.3 us at four (LDS would allow four up to 140 pairs); 896 or 640 workgroups were slower, 188-190 us. A
+        // 181.3 us at four (LDS would allow four up to 140 pairs); two per CU 184.9-186.1 against 180.6-183.9 us, and 896
+        // or 640 workgroups 188-190 us, were slower. A
         // 5-slot ring at two per CU leaves the down launch (512 units) unchanged, 64.4 vs 64.6 us, and makes gate/up
         // 11 % slower.
         static const int per_cu_env = [] {
