@@ -761,17 +761,18 @@ def test_moe_ffn_matches_oracle(orc, gfmt, dfmt):
     _moe_check(ov.moe_ffn(gw, uw, dw, x, rows, k, idx2, w), ref2, f"{gfmt}/{dfmt} sparse routing")
 
 
-@pytest.mark.parametrize("k", [1, 2])
-def test_moe_ffn_top2_combine_bit_exact(orc, k):
+@pytest.mark.parametrize("rows,E,k", [(16, 8, 1), (16, 8, 2), (300, 64, 2)])
+def test_moe_ffn_top2_combine_bit_exact(orc, rows, E, k):
     """Top-1 / top-2 with Q4_K experts on few pairs: the down launch adds weight * expert output into y with float
     atomics instead of a combine launch. y must equal, bit for bit, the reference's in-order combine
     (0 + w0 o0) + w1 o1 (RT/MoeFeedForwardBlock.cs:225-239) of each expert's output, taken here from the one-token
     SwiGLU FFN on the same expert (the same projections and SiLU launch, bit-identical per pair), with an unclaimed
     slot and a repeated index adding nothing, y first filled with NaN (every element written), and a second call
-    with fewer tokens into the same buffer (no stale sums)."""
-    case("moe top-k combine fold", k)
-    rng = np.random.default_rng(400 + k)
-    E, dm, dff, rows = 8, 256, 512, 16
+    with fewer tokens into the same buffer (no stale sums). 300 tokens over 64 experts: 600 pairs in the stream
+    kernel's pair map, one expert with more than 40 pairs (several 16-pair chunks)."""
+    case("moe top-k combine fold", rows, E, k)
+    rng = np.random.default_rng(400 + rows + k)
+    dm, dff = 256, 512
     gw, uw, dw = ([ov.Q4KWeight(orc.quantize_q4k(normal(rng, shp, 0.05)), shp[1], shp[0]) for _ in range(E)]
                   for shp in ((dff, dm), (dff, dm), (dm, dff)))
     x = normal(rng, (rows, dm))
@@ -780,7 +781,11 @@ def test_moe_ffn_top2_combine_bit_exact(orc, k):
     idx[3, 0] = E + 1  # unclaimed slot
     if k == 2:
         idx[5] = [4, 4]  # the repeat contributes nothing
+    if rows > 64:
+        idx[64:110, 1] = 5  # expert 5: over 40 pairs
+        idx[64:110, 0] = np.where(idx[64:110, 0] == 5, 6, idx[64:110, 0])
     y = torch.full((rows * dm,), float("nan"), device=DEV)
+    expert_out = {}
     for n in (rows, 5):
         out = ov.moe_ffn(gw, uw, dw, t(x[:n]), n, k, t(idx[:n]), t(w[:n]), out=y[: n * dm])
         torch.cuda.synchronize()
@@ -793,7 +798,9 @@ def test_moe_ffn_top2_combine_bit_exact(orc, k):
                 if e < 0 or e >= E or e in seen:
                     continue
                 seen.add(e)
-                o = ov.ffn_swiglu(gw[e], uw[e], dw[e], t(x[tok:tok + 1]), 1).cpu().numpy()
+                if (tok, e) not in expert_out:
+                    expert_out[tok, e] = ov.ffn_swiglu(gw[e], uw[e], dw[e], t(x[tok:tok + 1]), 1).cpu().numpy()
+                o = expert_out[tok, e]
                 want[tok] = want[tok] + np.float32(w[tok, j]) * o
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"top-{k}, {n} tokens: combine differs"
 
