@@ -298,7 +298,7 @@ OVFQ_API int ovfq_moe_select_topk_dev(ovfq_ctx* ctx, const float* logits, int ro
  * bit-identical to the reference's; SiLU uses expf (the reference's TensorPrimitives.Sigmoid is itself only
  * specified to a few ULP), so y matches to the projection tolerance. An index outside [0, n_experts), or a
  * repeated index in a token's slots, contributes nothing. n_experts <= OVFQ_MAX_EXPERTS. With top_k <= 2 and
- * Q4_K down experts on few pairs, the down projection adds each weighted expert output into y with a float atomic
+ * few pairs per expert, the down projection adds each weighted expert output into y with a float atomic
  * (at most two adds onto zero per element, so the sum is the in-order one); the _dev variants' y must therefore
  * be ordinary device memory (hipMalloc, torch), not host-mapped memory. */
 OVFQ_API int ovfq_moe_ffn(ovfq_ctx* ctx, int n_experts, const ovfq_weight* const* gate,

@@ -1309,11 +1309,12 @@ static int moe_impl(ovfq_ctx* ctx, int E, const ovfq_weight* const* gate, const 
     D.pair_row = nullptr;  // the intermediate is already pair-major
     D.act = ovfq::ActQ{iq, is, ib};
     D.pairs = (int)P;
-    // With top-1 / top-2 and the down projection on the expert-stream kernel, the combine is folded into it: each
-    // token output gets at most two float-atomic adds onto zero, whose sum does not depend on their order, so it is
-    // the combine kernel's (0 + w0 o0) + w1 o1 exactly. The zeroing and the per-pair weights go in the gate * up launch.
+    // With top-1 / top-2 and the down projection on the small-M path (the expert-stream or small-M kernel), the
+    // combine is folded into it: each token output gets at most two float-atomic adds onto zero, whose sum does not
+    // depend on their order, so it is the combine kernel's (0 + w0 o0) + w1 o1 exactly. The zeroing and the per-pair
+    // weights go in the gate * up launch.
     ovfq::MoeFold fold{};
-    if (k <= 2 && !grouped_big && ovfq::mfma_small_streams(dt, D)) {
+    if (k <= 2 && !grouped_big) {
         fold = ovfq::MoeFold{yd, (int64_t)rows * dmodel, pof, wd, (int)P, pw};
         D.comb = yd;
         D.comb_tok = prow;

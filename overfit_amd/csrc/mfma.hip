@@ -736,7 +736,7 @@ struct SArgs {
     const int* pair_row;
     const int8_t* q;
     const float* s;
-    float* comb;            // expert-stream kernel: add comb_w[pair] * value to comb[comb_tok[pair]] (GroupLaunch)
+    float* comb;            // if set: add comb_w[pair] * value to comb[comb_tok[pair]] (GroupLaunch)
     const int* comb_tok;
     const float* comb_w;
 };
@@ -839,8 +839,16 @@ __global__ __launch_bounds__(256) void kquant_mfma_small_kernel(const SArgs a) {
             for (int sb = 0; sb < spr; sb++) sum += vals[sb * 256 + threadIdx.x];
             if (n0 + n < cnt && o0 + o < a.n_rows) {
                 const float* bias = mat ? a.bias1 : a.bias0;
-                float* y = mat ? a.y1 : a.y0;
-                y[(size_t)(pbeg + n0 + n) * a.n_rows + o0 + o] = bias ? bias[o0 + o] + sum : sum;
+                const float v = bias ? bias[o0 + o] + sum : sum;
+                const int p = pbeg + n0 + n;
+                if (a.comb) {
+                    const float prod = a.comb_w[p] * v;
+                    __hip_atomic_fetch_add(a.comb + (size_t)a.comb_tok[p] * a.n_rows + o0 + o, prod, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+                } else {
+                    float* y = mat ? a.y1 : a.y0;
+                    y[(size_t)p * a.n_rows + o0 + o] = v;
+                }
             }
         }
         __syncthreads();  // the next row tile overwrites vals
@@ -1232,7 +1240,8 @@ bool stream_pair_preferred(int type, int in, int n_rows) {
     return stream_enabled() && type == 12 && mfma_small_supported(type, in) && stream_dense_ok(2, n_rows);
 }
 
-bool mfma_small_streams(int type, const GroupLaunch& L) {
+// Whether launch_mfma_small runs this launch on the expert-stream kernel.
+static bool mfma_small_streams(int type, const GroupLaunch& L) {
     const int nmat = L.w1 ? 2 : 1;
     const int pairs = L.expert_off ? L.pairs : L.rows;
     return stream_enabled() && type == 12 && (L.expert_off || stream_dense_ok(nmat, L.n_rows)) && pairs > 0 &&
@@ -1262,9 +1271,8 @@ hipError_t launch_mfma_small(int type, const GroupLaunch& L, hipStream_t st) {
     sa.comb_w = L.comb_w;
     const int nmat = L.w1 ? 2 : 1;
     const int pairs = L.expert_off ? L.pairs : L.rows;
-    const bool streams = mfma_small_streams(type, L);
-    if (L.comb && (!streams || nmat != 1 || !L.expert_off || !L.comb_tok || !L.comb_w)) return hipErrorInvalidValue;
-    if (streams) {
+    if (L.comb && (nmat != 1 || !L.expert_off || !L.comb_tok || !L.comb_w)) return hipErrorInvalidValue;
+    if (mfma_small_streams(type, L)) {
         sa.tiles = (sa.n_rows + kStreamRows - 1) / kStreamRows;  // 64-row groups
         const long units = (long)L.experts * nmat * sa.tiles;
         int dev = 0, cus = 256;

@@ -73,9 +73,9 @@ struct GroupLaunch {
     const int* pair_row;
     ActQ act;
     int pairs = 0;  // grouped launches: the pair count bound (rows x top_k), sizing the pair -> row map
-    // Grouped single-matrix launches that take the expert-stream kernel only (mfma_small_streams): instead of
-    // storing y0[pair][o], add comb_w[pair] * value to comb[comb_tok[pair]][o] with a float atomic (comb zeroed
-    // beforehand). Exact when at most two pairs add to one output: (0 + a) + b == (0 + b) + a in fp32.
+    // Grouped single-matrix launch_mfma_small launches only: instead of storing y0[pair][o], add
+    // comb_w[pair] * value to comb[comb_tok[pair]][o] with a float atomic (comb zeroed beforehand). Exact when at
+    // most two pairs add to one output: (0 + a) + b == (0 + b) + a in fp32.
     float* comb = nullptr;
     const int* comb_tok = nullptr;
     const float* comb_w = nullptr;
@@ -85,8 +85,6 @@ bool mfma_small_supported(int type, int in);
 // Whether a gate/up-shaped pair of Q4_K weights (n_rows outputs each, `in` inputs) runs on the expert-stream kernel
 // when it takes the small-M path.
 bool stream_pair_preferred(int type, int in, int n_rows);
-// Whether launch_mfma_small runs this launch on the expert-stream kernel (the one that supports comb).
-bool mfma_small_streams(int type, const GroupLaunch& launch);
 hipError_t launch_mfma_small(int type, const GroupLaunch& launch, hipStream_t st);
 // MFMA-ready copy of a Q4_K / Q6_K weight: its size, and the kernel that writes it from the GGUF blocks.
 size_t mfma_prepared_bytes(int in, int out);

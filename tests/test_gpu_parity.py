@@ -761,20 +761,25 @@ def test_moe_ffn_matches_oracle(orc, gfmt, dfmt):
     _moe_check(ov.moe_ffn(gw, uw, dw, x, rows, k, idx2, w), ref2, f"{gfmt}/{dfmt} sparse routing")
 
 
-@pytest.mark.parametrize("rows,E,k", [(16, 8, 1), (16, 8, 2), (300, 64, 2)])
-def test_moe_ffn_top2_combine_bit_exact(orc, rows, E, k):
-    """Top-1 / top-2 with Q4_K experts on few pairs: the down launch adds weight * expert output into y with float
-    atomics instead of a combine launch. y must equal, bit for bit, the reference's in-order combine
+@pytest.mark.parametrize("rows,E,k,dfmt", [(16, 8, 1, "q4k"), (16, 8, 2, "q4k"), (300, 64, 2, "q4k"),
+                                            (16, 8, 2, "q6k"), (40, 8, 1, "q6k")])
+def test_moe_ffn_top2_combine_bit_exact(orc, rows, E, k, dfmt):
+    """Top-1 / top-2 with few pairs per expert: the down launch (the expert-stream kernel for Q4_K, the small-M
+    kernel for Q6_K) adds weight * expert output into y with float atomics instead of a combine launch. y must equal, bit for bit, the reference's in-order combine
     (0 + w0 o0) + w1 o1 (RT/MoeFeedForwardBlock.cs:225-239) of each expert's output, taken here from the one-token
     SwiGLU FFN on the same expert (the same projections and SiLU launch, bit-identical per pair), with an unclaimed
     slot and a repeated index adding nothing, y first filled with NaN (every element written), and a second call
     with fewer tokens into the same buffer (no stale sums). 300 tokens over 64 experts: 600 pairs in the stream
     kernel's pair map, one expert with more than 40 pairs (several 16-pair chunks)."""
-    case("moe top-k combine fold", rows, E, k)
+    case("moe top-k combine fold", rows, E, k, dfmt)
     rng = np.random.default_rng(400 + rows + k)
     dm, dff = 256, 512
-    gw, uw, dw = ([ov.Q4KWeight(orc.quantize_q4k(normal(rng, shp, 0.05)), shp[1], shp[0]) for _ in range(E)]
-                  for shp in ((dff, dm), (dff, dm), (dm, dff)))
+    gw, uw = ([ov.Q4KWeight(orc.quantize_q4k(normal(rng, shp, 0.05)), shp[1], shp[0]) for _ in range(E)]
+              for shp in ((dff, dm), (dff, dm)))
+    if dfmt == "q6k":
+        dw = [ov.Q6KWeight(orc.quantize_q6k(normal(rng, (dm, dff), 0.05)), dff, dm) for _ in range(E)]
+    else:
+        dw = [ov.Q4KWeight(orc.quantize_q4k(normal(rng, (dm, dff), 0.05)), dff, dm) for _ in range(E)]
     x = normal(rng, (rows, dm))
     idx = np.stack([rng.choice(E, k, replace=False) for _ in range(rows)]).astype(np.int32)
     w = (rng.random((rows, k)) - 0.3).astype(np.float32)  # signed weights
