@@ -141,7 +141,9 @@ def test_q8_0_weight_quantize_rows(orc):
 
 # ------------------------------------------------------------------------------------------------ projections
 
-KQ_SHAPES = [(256, 1), (256, 7), (512, 96), (1024, 33), (4096, 129), (4096, 1024), (14336, 65), (3072, 4099)]
+# Rows of 7, 21, 24 and 56 super-blocks: 16-block decode chunks that do not fill the row (the last one partial).
+KQ_SHAPES = [(256, 1), (256, 7), (512, 96), (1024, 33), (4096, 129), (4096, 1024), (14336, 65), (3072, 4099),
+             (1792, 5), (5376, 9), (6144, 31)]
 
 
 def _kq_blocks(rng, fmt, n, k):
@@ -1149,6 +1151,33 @@ def test_gate_up_and_multi_projection(orc, ctx):
     assert_bit_exact(ys[0].cpu().numpy(), rg, "multi gate")
     assert_bit_exact(ys[1].cpu().numpy(), ru, "multi up")
     assert_bit_exact(ys[2].cpu().numpy(), orc.q4k_project(x, v, k, n2, bias_v), "multi v")
+
+
+@pytest.mark.parametrize("fmt", ["q4k", "q6k"])
+def test_partial_chunk_decode_multi_and_prequantized(orc, ctx, fmt):
+    """Decode kernel on rows of 21 super-blocks (a partial last 16-block chunk): a fused three-job launch with odd row
+    counts and one bias, and the prequantised entry point, against the oracle's sequential per-row sums."""
+    case("decode 21-block rows multi/prequantized", fmt)
+    rng = np.random.default_rng(2121)
+    k = 5376
+    ns = [33, 7, 130]
+    blocks = [_kq_blocks(rng, fmt, n, k) for n in ns]
+    W = ov.Q4KWeight if fmt == "q4k" else ov.Q6KWeight
+    ws = [W(b, k, n) for b, n in zip(blocks, ns)]
+    proj = orc.q4k_project if fmt == "q4k" else orc.q6k_project
+    x = normal(rng, k)
+    bias = normal(rng, ns[2])
+    refs = [proj(x, blocks[0], k, ns[0]), proj(x, blocks[1], k, ns[1]), proj(x, blocks[2], k, ns[2], bias)]
+    ys = [torch.empty(n, device=DEV) for n in ns]
+    ctx.project_multi_dev(ws, t(x), ys, [None, None, t(bias)])
+    torch.cuda.synchronize()
+    for i in range(3):
+        assert_bit_exact(ys[i].cpu().numpy(), refs[i], f"{fmt} multi job {i}")
+    q, s, b = orc.quantize_q8k(x)
+    y = torch.empty(ns[2], device=DEV)
+    ctx.project_prequantized_dev(ws[2], t(q.ravel()), t(s.ravel()), t(b.ravel()), y, bias=t(bias))
+    torch.cuda.synchronize()
+    assert_bit_exact(y.cpu().numpy(), refs[2], f"{fmt} prequantized")
 
 
 def test_reference_mirror_api_host_and_device(orc):
