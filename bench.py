@@ -665,15 +665,17 @@ def main():
     gu_avg = replay_us(g_gu, 4 * len(copies), 16)
     gu_bytes = 2 * weight_bytes(14336, 4096, "q4k") + 4 * 4096 + 4 * 2 * 14336
     achieved = gu_bytes / (gu_avg * 1e-6) / 1e9
-    traffic = None
+    traffic = traffic_commit = None
     tfile = os.path.join(ROOT, "profiles", "traffic_q4k_gate_up_gemv.json")
     if os.path.exists(tfile):
-        traffic = json.load(open(tfile)).get("bytes_per_launch")
+        tinfo = json.load(open(tfile))
+        traffic, traffic_commit = tinfo.get("bytes_per_launch"), tinfo.get("commit")
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                 "traffic_source": "not measured in this run: the committed profiles/traffic_q4k_gate_up_gemv.json "
                                   "(two rocprofv3 --pmc passes, FETCH_SIZE and WRITE_SIZE, calibrated by a 64 MiB "
-                                  "device copy)" if traffic is not None else None,
+                                  "device copy; kernel source of commit %s)" % traffic_commit
+                                  if traffic is not None else None,
                 "kernel": "kquant_gemv_kernel<Q4K,2,true> (Q8_K quantise + fused gate+up GEMV, 2x14336x4096)",
                 "avg_us": round(gu_avg, 3), "algorithmic_bytes": gu_bytes,
                 "timing": "HIP graph replay of 4x%d launches over %d weight copies, /launch" % (len(copies), len(copies))}
