@@ -530,42 +530,62 @@ def main():
 
     def host_token_line(layers, head, reps=5):
         """Config 4 end to end through the host-pointer entry points, as the C# drop-in issues them per layer:
-        ovfq_project for q, k and v, ovfq_project for o, ovfq_project_gate_up, ovfq_project for down, then the LM
-        head — each call synchronous, its fp32 input copied up from pageable host memory and its output copied back
-        (6 calls per layer, 193 per token). Timed on the host clock around whole tokens; the call arguments are
-        prepared ctypes objects, so Python adds about a microsecond per call. Attention, RMSNorm and RoPE (host-side
-        by the benchmark's definition) are not run."""
+        ovfq_project_multi for q/k/v (one quantised hidden row, RT/CachedMultiHeadAttention.cs:196-207), ovfq_project
+        for o and ovfq_ffn_swiglu for gate/up -> SiLU*up -> down (RT/CachedFeedForwardBlock.cs:261-318), then the LM
+        head: 97 calls per token, each synchronous, its fp32 input copied up from pageable host memory through the
+        context's page-locked staging and its outputs copied back. Beside it, the same projections as six separate
+        calls per layer (q, k, v, o, gate/up, down; 193 calls). Timed on the host clock around whole tokens; the call
+        arguments are prepared ctypes objects, so Python adds about a microsecond per call. Attention, RMSNorm and
+        RoPE (host-side by the benchmark's definition) are not run."""
         import ctypes
 
         lib = ctx.lib
         hx = {k: np.random.default_rng(k).standard_normal(k).astype(np.float32) for k in (4096, 14336)}
         outs = {n: np.zeros(n, np.float32) for n in (4096, 1024, 14336, 128256)}
+        qkv = [np.zeros(n, np.float32) for n in (4096, 1024, 1024)]
         up_out = np.zeros(14336, np.float32)
         P = lambda a: ctypes.c_void_p(a.ctypes.data)  # noqa: E731
-        calls = []
+        x4, x14 = P(hx[4096]), P(hx[14336])
+        fused, separate = [], []
+        keep = []
         for ws in layers:
-            x4, x14 = P(hx[4096]), P(hx[14336])
+            W = (ctypes.c_void_p * 3)(ws["q"].handle.value, ws["k"].handle.value, ws["v"].handle.value)
+            Y = (ctypes.c_void_p * 3)(*[a.ctypes.data for a in qkv])
+            keep += [W, Y]
+            fused.append((lib.ovfq_project_multi, (ctx.handle, 3, W, x4, 1, None, Y)))
+            fused.append((lib.ovfq_project, (ctx.handle, ws["o"].handle, x4, 1, None, P(outs[4096]))))
+            fused.append((lib.ovfq_ffn_swiglu, (ctx.handle, ws["gate"].handle, ws["up"].handle, ws["down"].handle, x4,
+                                                1, P(outs[4096]))))
             for name, n in (("q", 4096), ("k", 1024), ("v", 1024), ("o", 4096)):
-                calls.append((lib.ovfq_project, (ctx.handle, ws[name].handle, x4, 1, None, P(outs[n]))))
-            calls.append((lib.ovfq_project_gate_up, (ctx.handle, ws["gate"].handle, ws["up"].handle, x4,
-                                                     P(outs[14336]), P(up_out))))
-            calls.append((lib.ovfq_project, (ctx.handle, ws["down"].handle, x14, 1, None, P(outs[4096]))))
-        calls.append((lib.ovfq_project, (ctx.handle, head.handle, P(hx[4096]), 1, None, P(outs[128256]))))
+                separate.append((lib.ovfq_project, (ctx.handle, ws[name].handle, x4, 1, None, P(outs[n]))))
+            separate.append((lib.ovfq_project_gate_up, (ctx.handle, ws["gate"].handle, ws["up"].handle, x4,
+                                                        P(outs[14336]), P(up_out))))
+            separate.append((lib.ovfq_project, (ctx.handle, ws["down"].handle, x14, 1, None, P(outs[4096]))))
+        head_call = (lib.ovfq_project, (ctx.handle, head.handle, x4, 1, None, P(outs[128256])))
+        fused.append(head_call)
+        separate.append(head_call)
 
-        def token():
-            for fn, args in calls:
-                if fn(*args):
-                    raise RuntimeError(lib.ovfq_last_error())
+        def best_token_us(calls):
+            def token():
+                for fn, a in calls:
+                    if fn(*a):
+                        raise RuntimeError(lib.ovfq_last_error())
 
-        token()
-        best = float("inf")
-        for _ in range(reps):
-            t0 = time.perf_counter()
             token()
-            best = min(best, time.perf_counter() - t0)
-        return {"what": "the same token through the synchronous host-pointer entry points (input up, output down per "
-                        "call, %d calls)" % len(calls),
-                "us": round(best * 1e6, 1), "proj_tok_s": round(1.0 / best, 1),
+            best = float("inf")
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                token()
+                best = min(best, time.perf_counter() - t0)
+            return best * 1e6
+
+        us = best_token_us(fused)
+        us_sep = best_token_us(separate)
+        return {"what": "the same token through the synchronous host-pointer entry points, input up and outputs down "
+                        "per call through page-locked staging: q/k/v in one ovfq_project_multi, o, the fused SwiGLU "
+                        "FFN, the LM head (%d calls)" % len(fused),
+                "us": round(us, 1), "proj_tok_s": round(1e6 / us, 1),
+                "separate_calls": {"calls": len(separate), "us": round(us_sep, 1), "proj_tok_s": round(1e6 / us_sep, 1)},
                 "timing": "host clock, best of %d tokens" % reps}
 
     def moe_line(n_sets=2, tokens=16, top_k=2, n_experts=8, keep_host=False):

@@ -20,13 +20,15 @@
  *    per-context lock and run in order on the context's stream (the reference calls Project concurrently from
  *    its head-parallel workers, RT/CachedMultiHeadAttention.cs:280, :876-907).
  *  - Lifetime: a weight belongs to the context it was created on, and that context must outlive it
- *    (ovfq_ctx_destroy returns OVFQ_ERR_SIZE, destroying nothing, while any of its weights is alive).
+ *    (ovfq_ctx_destroy returns OVFQ_ERR_STATE, destroying nothing, while any of its weights is alive; the
+ *    reference's counterpart of that state error is InvalidOperationException).
  *  - Sizes: every activation and output plane (rows x its width) stays below 2^31 elements, the length limit
  *    of the reference's Span<T> scratch and outputs; larger calls return OVFQ_ERR_SIZE.
  *  - Scratch and HIP graphs: the context grows its device scratch on demand (activation quantisation, FFN and
- *    MoE intermediates, host staging) and never frees a superseded buffer before ovfq_ctx_destroy, so a graph
- *    captured from _dev calls stays valid after later, larger calls on the same context. Work captured into a
- *    graph and work issued eagerly on the same context share that scratch: they must not run concurrently.
+ *    MoE intermediates, host staging) and never frees a superseded buffer before ovfq_ctx_destroy (or
+ *    ovfq_ctx_release_retired), so a graph captured from _dev calls stays valid after later, larger calls on the
+ *    same context. Work captured into a graph and work issued eagerly on the same context share that scratch:
+ *    they must not run concurrently.
  */
 #ifndef OVFQ_H
 #define OVFQ_H
@@ -46,6 +48,7 @@ extern "C" {
 #define OVFQ_ERR_SIZE (-2)  /* a size or shape is inconsistent            */
 #define OVFQ_ERR_RANGE (-3) /* a count is zero/negative or an index is out of range */
 #define OVFQ_ERR_TYPE (-4)  /* unsupported weight type for this entry point */
+#define OVFQ_ERR_STATE (-5) /* the object's state forbids the call (a context that still owns weights) */
 #define OVFQ_ERR_HIP (-10)  /* the HIP runtime reported an error          */
 
 /* Weight formats (numbered as ggml's type ids). */
@@ -75,6 +78,14 @@ OVFQ_API int ovfq_ctx_set_stream(ovfq_ctx* ctx, void* stream);
 /* Returns the context to its own stream. */
 OVFQ_API int ovfq_ctx_reset_stream(ovfq_ctx* ctx);
 OVFQ_API int ovfq_ctx_synchronize(ovfq_ctx* ctx);
+/* Frees the scratch buffers that later, larger calls have superseded (kept until now so that HIP graphs captured
+ * from earlier _dev calls stay valid). Waits for the context's stream first. Only for callers that hold no graph
+ * captured from this context's calls, or have destroyed every such graph: replaying one afterwards reads freed
+ * memory. New; the reference has no device scratch. */
+OVFQ_API int ovfq_ctx_release_retired(ovfq_ctx* ctx);
+/* Device scratch the context holds: `live` bytes in use by its growable buffers, `retired` bytes of superseded
+ * buffers kept for captured graphs (either pointer may be NULL). New; for serving code that watches memory. */
+OVFQ_API int ovfq_ctx_scratch_bytes(ovfq_ctx* ctx, size_t* live, size_t* retired);
 /* Kernel choice for batched K-quant work of 2 or more activation rows (projections, fused q/k/v and gate/up
  * launches, the SwiGLU FFN, routed expert groups). OVFQ_BATCHED_AUTO (the default) picks by shape;
  * OVFQ_BATCHED_SMALL forces the super-block-parallel small-M MFMA kernel wherever it takes the shape (3 or more
@@ -218,10 +229,16 @@ OVFQ_API int ovfq_project_gate_up(ovfq_ctx* ctx, const ovfq_weight* gate, const 
 OVFQ_API int ovfq_project_gate_up_dev(ovfq_ctx* ctx, const ovfq_weight* gate, const ovfq_weight* up,
                                       const float* x, float* gate_out, float* up_out);
 
-/* Several projections of the SAME activation in one launch (the generalisation of gate/up that the
- * attention block's shared quantised hidden row needs, RT/CachedMultiHeadAttention.cs:196-207): weights[i]
- * share input_size and type; x is rows x input_size; ys[i] receives rows x output_size_i; biases may be NULL or
- * hold NULL entries. At most 4 weights. Prefill (rows >= 2) uses it for the fused q/k/v and gate/up GEMMs. */
+/* Several projections of the SAME activation in one launch: the attention block quantises its hidden row once
+ * (QuantizeActivationQ8K) and runs the q, k and v projections against it with ProjectPreQuantized
+ * (RT/CachedMultiHeadAttention.cs:196-207, RT/Q4KDotKernel.cs:445-476); gate/up is the two-weight case
+ * (ProjectGateUpParallel, RT/Q4KDotKernel.cs:563-645). weights[i] share input_size and type; x is rows x input_size;
+ * ys[i] receives rows x output_size_i; biases may be NULL or hold NULL entries. At most 4 weights. Host pointers,
+ * synchronous (one upload of x, one launch, the outputs downloaded together). Prefill (rows >= 2) uses it for the
+ * fused q/k/v and gate/up GEMMs. */
+OVFQ_API int ovfq_project_multi(ovfq_ctx* ctx, int count, const ovfq_weight* const* weights, const float* x,
+                                int rows, const float* const* biases, float* const* ys);
+/* As ovfq_project_multi, with device pointers (enqueued on the context's stream). */
 OVFQ_API int ovfq_project_multi_dev(ovfq_ctx* ctx, int count, const ovfq_weight* const* weights,
                                     const float* x, int rows, const float* const* biases, float* const* ys);
 
@@ -299,8 +316,8 @@ OVFQ_API int ovfq_moe_select_topk_dev(ovfq_ctx* ctx, const float* logits, int ro
  * specified to a few ULP), so y matches to the projection tolerance. An index outside [0, n_experts), or a
  * repeated index in a token's slots, contributes nothing. n_experts <= OVFQ_MAX_EXPERTS. With top_k <= 2 and
  * few pairs per expert, the down projection adds each weighted expert output into y with a float atomic
- * (at most two adds onto zero per element, so the sum is the in-order one); the _dev variants' y must therefore
- * be ordinary device memory (hipMalloc, torch), not host-mapped memory. */
+ * (at most two adds onto zero per element, so the sum is the in-order one) when y is ordinary device memory
+ * (hipMalloc, torch); a _dev caller's y in host-mapped memory gets the separate combine launch instead. */
 OVFQ_API int ovfq_moe_ffn(ovfq_ctx* ctx, int n_experts, const ovfq_weight* const* gate,
                           const ovfq_weight* const* up, const ovfq_weight* const* down, const float* x, int rows,
                           int top_k, const int* expert_indices, const float* expert_weights, float* y);

@@ -5,10 +5,10 @@ Q4_K / Q6_K / Q8_0 block-dequantize-and-dot projections as hand-written HIP kern
 """
 from . import _lib
 from .errors import (OverfitArgumentError, OverfitArgumentNullError, OverfitArgumentOutOfRangeError,
-                     OverfitHipError, OverfitUnsupportedTypeError)
+                     OverfitHipError, OverfitInvalidOperationError, OverfitUnsupportedTypeError)
 from .kernels import (BatchedQuantProjection, FeedForwardActivation, MoeRouter, Q4KDotKernel, Q6KDotKernel,
                       Q8DotKernel, ffn_gated, ffn_swiglu, moe_ffn, moe_ffn_routed, project, project_gate_up, project_heads_q8_0,
-                      quantize_weight)
+                      project_multi, quantize_weight)
 from .runtime import Context, default_context
 from .weights import DecodeWeight, Q4KWeight, Q6KWeight, Q8Weight, load_gguf_experts, load_gguf_tensor
 
@@ -18,8 +18,9 @@ TYPE_Q6_K = _lib.TYPE_Q6_K
 
 __all__ = [
     "BatchedQuantProjection", "Context", "DecodeWeight", "FeedForwardActivation", "MoeRouter", "OverfitArgumentError",
-    "OverfitArgumentNullError", "OverfitArgumentOutOfRangeError", "OverfitHipError", "OverfitUnsupportedTypeError",
+    "OverfitArgumentNullError", "OverfitArgumentOutOfRangeError", "OverfitHipError", "OverfitInvalidOperationError",
+    "OverfitUnsupportedTypeError",
     "Q4KDotKernel", "Q4KWeight", "Q6KDotKernel", "Q6KWeight", "Q8DotKernel", "Q8Weight", "TYPE_Q4_K", "TYPE_Q6_K",
     "TYPE_Q8_0", "default_context", "ffn_gated", "ffn_swiglu", "load_gguf_experts", "load_gguf_tensor", "moe_ffn", "moe_ffn_routed", "project",
-    "project_gate_up", "project_heads_q8_0", "quantize_weight",
+    "project_gate_up", "project_heads_q8_0", "project_multi", "quantize_weight",
 ]

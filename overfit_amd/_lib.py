@@ -14,6 +14,7 @@ OVFQ_ERR_NULL = -1
 OVFQ_ERR_SIZE = -2
 OVFQ_ERR_RANGE = -3
 OVFQ_ERR_TYPE = -4
+OVFQ_ERR_STATE = -5
 OVFQ_ERR_HIP = -10
 OVFQ_FFN_SWIGLU = 3
 OVFQ_FFN_GEGLU = 4
@@ -34,6 +35,8 @@ SIGNATURES = {
     "ovfq_ctx_set_stream": (ci, [vp, vp]),
     "ovfq_ctx_reset_stream": (ci, [vp]),
     "ovfq_ctx_synchronize": (ci, [vp]),
+    "ovfq_ctx_release_retired": (ci, [vp]),
+    "ovfq_ctx_scratch_bytes": (ci, [vp, ctypes.POINTER(sz), ctypes.POINTER(sz)]),
     "ovfq_ctx_set_batched_kernel": (ci, [vp, ci]),
     "ovfq_last_error": (ctypes.c_char_p, []),
     "ovfq_version": (ctypes.c_char_p, []),
@@ -70,6 +73,7 @@ SIGNATURES = {
     "ovfq_moe_ffn_routed": (ci, [vp, ci, PP, PP, PP, vp, ci, vp, ci, ci, vp, vp, vp]),
     "ovfq_moe_ffn_routed_dev": (ci, [vp, ci, PP, PP, PP, vp, ci, vp, ci, ci, vp, vp, vp]),
     "ovfq_project_gate_up_dev": (ci, [vp, vp, vp, vp, vp, vp]),
+    "ovfq_project_multi": (ci, [vp, ci, PP, vp, ci, PP, PP]),
     "ovfq_project_multi_dev": (ci, [vp, ci, PP, vp, ci, PP, PP]),
     "ovfq_project_heads_q8_0": (ci, [vp, ci, PP, vp, ci, vp, vp]),
     "ovfq_project_heads_q8_0_dev": (ci, [vp, ci, PP, vp, ci, vp, vp]),

@@ -59,9 +59,12 @@ struct ovfq_ctx {
     DevBuf act_q, act_s, act_b, x_stage, y_stage, y2_stage, bias_stage;
     // Routed-MoE scratch (plan, gate/up/intermediate/expert outputs, host staging), carved from one buffer.
     DevBuf moe;
+    // Page-locked host arenas of the host-pointer entry points (hipHostMalloc): inputs go up, outputs come down.
+    DevBuf h_up, h_down;
     // Scratch buffers replaced by larger ones. A HIP graph captured from _dev calls keeps the addresses it
     // was recorded with, so a superseded buffer stays allocated until the context is destroyed.
     std::vector<void*> retired;
+    size_t retired_bytes = 0;
     // Live weights created on this context (ovfq_ctx_destroy refuses while any remain).
     int live_weights = 0;
 };
@@ -97,11 +100,89 @@ int ensure(ovfq_ctx* c, DevBuf& b, size_t bytes) {
     cap = (cap + 255) & ~size_t(255);
     void* p = nullptr;
     HIP_TRY(hipMalloc(&p, cap));
-    if (b.p) c->retired.push_back(b.p);
+    if (b.p) {
+        c->retired.push_back(b.p);
+        c->retired_bytes += b.cap;
+    }
     b.p = p;
     b.cap = cap;
     return OVFQ_OK;
 }
+
+// Replaces the page-locked arena `b` by one of at least `bytes` (doubling). The caller has made sure that no queued
+// copy still reads or writes the old arena.
+int host_grow(DevBuf& b, size_t bytes) {
+    size_t cap = bytes < 65536 ? 65536 : bytes;
+    if (cap < 2 * b.cap) cap = 2 * b.cap;
+    cap = (cap + 4095) & ~size_t(4095);
+    void* p = nullptr;
+    HIP_TRY(hipHostMalloc(&p, cap, hipHostMallocDefault));
+    if (b.p) (void)hipHostFree(b.p);
+    b.p = p;
+    b.cap = cap;
+    return OVFQ_OK;
+}
+
+// The staging of one host-pointer call (made under the context lock). The caller's buffers are ordinary pageable
+// memory; copying them through the context's page-locked arenas lets the DMA engines move them directly, where the
+// runtime's pageable path stages every copy through buffers of its own and blocks the host on each. up() copies an
+// input into the up arena and enqueues its upload; down() enqueues an output's download into the down arena;
+// finish() waits for the stream and copies the outputs to the caller. An arena too small for a call is grown after a
+// wait (and then fits the next call of that size).
+struct HostIO {
+    static constexpr int kMaxOuts = 8;
+    struct Out {
+        void* dst;
+        size_t off, n;
+    };
+    ovfq_ctx* c;
+    size_t up_off = 0, down_off = 0;
+    Out outs[kMaxOuts];
+    int n_outs = 0;
+
+    explicit HostIO(ovfq_ctx* ctx) : c(ctx) {}
+
+    static size_t round(size_t n) { return (n + 255) & ~size_t(255); }
+
+    int up(void* dev_dst, const void* src, size_t n) {
+        if (up_off + n > c->h_up.cap) {
+            HIP_TRY(hipStreamSynchronize(c->stream));  // uploads already queued read the old arena
+            int rc = host_grow(c->h_up, up_off + n);
+            if (rc) return rc;
+            up_off = 0;
+        }
+        char* p = static_cast<char*>(c->h_up.p) + up_off;
+        memcpy(p, src, n);
+        HIP_TRY(hipMemcpyAsync(dev_dst, p, n, hipMemcpyHostToDevice, c->stream));
+        up_off += round(n);
+        return OVFQ_OK;
+    }
+
+    int down(void* dst, const void* dev_src, size_t n) {
+        if (down_off + n > c->h_down.cap || n_outs == kMaxOuts) {
+            const size_t need = down_off + n;
+            int rc = flush();
+            if (rc) return rc;
+            if (n > c->h_down.cap && (rc = host_grow(c->h_down, need))) return rc;
+        }
+        HIP_TRY(hipMemcpyAsync(static_cast<char*>(c->h_down.p) + down_off, dev_src, n, hipMemcpyDeviceToHost,
+                               c->stream));
+        outs[n_outs++] = Out{dst, down_off, n};
+        down_off += round(n);
+        return OVFQ_OK;
+    }
+
+    // Waits for the stream and hands the downloaded outputs to the caller.
+    int flush() {
+        HIP_TRY(hipStreamSynchronize(c->stream));
+        for (int i = 0; i < n_outs; i++) memcpy(outs[i].dst, static_cast<char*>(c->h_down.p) + outs[i].off, outs[i].n);
+        n_outs = 0;
+        down_off = 0;
+        return OVFQ_OK;
+    }
+
+    int finish() { return flush(); }
+};
 
 static_assert(ovfq::kNoAllocMaxElems == OVFQ_NOALLOC_MAX_ELEMS, "header and library disagree on the fixed scratch");
 static_assert(ovfq::kHeadsMax == OVFQ_MAX_HEADS, "header and library disagree on the head count");
@@ -423,7 +504,7 @@ int ovfq_ctx_destroy(ovfq_ctx* c) {
         std::lock_guard<std::mutex> lk(c->mu);
         // A weight locks its context when destroyed, so the context must outlive every weight made on it.
         if (c->live_weights > 0)
-            return fail(OVFQ_ERR_SIZE, "context still owns %d weight(s): destroy them first", c->live_weights);
+            return fail(OVFQ_ERR_STATE, "context still owns %d weight(s): destroy them first", c->live_weights);
         (void)hipSetDevice(c->device);
         (void)hipStreamSynchronize(c->stream);
         DevBuf* bufs[] = {&c->act_q,   &c->act_s,   &c->act_b,      &c->x_stage,
@@ -431,6 +512,8 @@ int ovfq_ctx_destroy(ovfq_ctx* c) {
         for (DevBuf* b : bufs)
             if (b->p) (void)hipFree(b->p);
         for (void* p : c->retired) (void)hipFree(p);
+        if (c->h_up.p) (void)hipHostFree(c->h_up.p);
+        if (c->h_down.p) (void)hipHostFree(c->h_down.p);
         if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
     }
     delete c;
@@ -452,6 +535,35 @@ int ovfq_ctx_reset_stream(ovfq_ctx* c) {
     HIP_TRY(hipSetDevice(c->device));
     HIP_TRY(hipStreamSynchronize(c->stream));
     c->stream = c->own_stream;
+    return ok();
+}
+
+int ovfq_ctx_release_retired(ovfq_ctx* c) {
+    if (!c) return fail(OVFQ_ERR_NULL, "ctx is NULL");
+    std::lock_guard<std::mutex> lk(c->mu);
+    HIP_TRY(hipSetDevice(c->device));
+    // queued work may still read a superseded buffer
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    hipError_t first = hipSuccess;
+    for (void* p : c->retired) {
+        hipError_t e = hipFree(p);
+        if (first == hipSuccess) first = e;
+    }
+    c->retired.clear();
+    c->retired_bytes = 0;
+    if (first != hipSuccess) return fail(OVFQ_ERR_HIP, "hipFree failed: %s", hipGetErrorString(first));
+    return ok();
+}
+
+int ovfq_ctx_scratch_bytes(ovfq_ctx* c, size_t* live, size_t* retired) {
+    if (!c) return fail(OVFQ_ERR_NULL, "ctx is NULL");
+    std::lock_guard<std::mutex> lk(c->mu);
+    const DevBuf* bufs[] = {&c->act_q, &c->act_s, &c->act_b, &c->x_stage, &c->y_stage, &c->y2_stage, &c->bias_stage,
+                            &c->moe};
+    size_t n = 0;
+    for (const DevBuf* b : bufs) n += b->cap;
+    if (live) *live = n;
+    if (retired) *retired = c->retired_bytes;
     return ok();
 }
 
@@ -702,8 +814,8 @@ static int decode_row_impl(ovfq_ctx* ctx, const ovfq_weight* w, int row, float* 
     }
     HIP_TRY(ovfq::launch_decode_row(w->type, w->blocks, w->scales, w->in, row, d, ctx->stream));
     if (host) {
-        HIP_TRY(hipMemcpyAsync(dst, d, (size_t)w->in * 4, hipMemcpyDeviceToHost, ctx->stream));
-        HIP_TRY(hipStreamSynchronize(ctx->stream));
+        HostIO io(ctx);
+        if ((rc = io.down(dst, d, (size_t)w->in * 4)) || (rc = io.finish())) return rc;
     }
     return ok();
 }
@@ -740,12 +852,13 @@ static int quantize_impl(ovfq_ctx* ctx, bool k_quant, const float* x, int rows, 
     int8_t* qd = q;
     float* sd = s;
     int16_t* bd = b;
+    HostIO io(ctx);
     if (host) {
         if ((rc = ensure(ctx, ctx->x_stage, n * 4))) return rc;
         if ((rc = ensure(ctx, ctx->y_stage, n))) return rc;
         if ((rc = ensure(ctx, ctx->y2_stage, n / blk * 4))) return rc;
         if (k_quant && (rc = ensure(ctx, ctx->bias_stage, n / 16 * 2))) return rc;
-        HIP_TRY(hipMemcpyAsync(ctx->x_stage.p, x, n * 4, hipMemcpyHostToDevice, ctx->stream));
+        if ((rc = io.up(ctx->x_stage.p, x, n * 4))) return rc;
         xd = (const float*)ctx->x_stage.p;
         qd = (int8_t*)ctx->y_stage.p;
         sd = (float*)ctx->y2_stage.p;
@@ -757,10 +870,9 @@ static int quantize_impl(ovfq_ctx* ctx, bool k_quant, const float* x, int rows, 
         HIP_TRY(ovfq::launch_quantize_q8_0(xd, (int64_t)(n / OVFQ_Q8_BLOCK), qd, sd, ctx->stream));
     }
     if (host) {
-        HIP_TRY(hipMemcpyAsync(q, qd, n, hipMemcpyDeviceToHost, ctx->stream));
-        HIP_TRY(hipMemcpyAsync(s, sd, n / blk * 4, hipMemcpyDeviceToHost, ctx->stream));
-        if (k_quant) HIP_TRY(hipMemcpyAsync(b, bd, n / 16 * 2, hipMemcpyDeviceToHost, ctx->stream));
-        HIP_TRY(hipStreamSynchronize(ctx->stream));
+        if ((rc = io.down(q, qd, n)) || (rc = io.down(s, sd, n / blk * 4)) ||
+            (k_quant && (rc = io.down(b, bd, n / 16 * 2))) || (rc = io.finish()))
+            return rc;
     }
     return ok();
 }
@@ -806,6 +918,7 @@ static int project_impl(ovfq_ctx* ctx, int count, const ovfq_weight* const* ws, 
     const float* bd[ovfq::kMaxJobs] = {nullptr, nullptr, nullptr, nullptr};
     float* yd[ovfq::kMaxJobs];
     size_t y_off[ovfq::kMaxJobs];
+    HostIO io(ctx);
     if (host) {
         size_t ytotal = 0, btotal = 0;
         for (int i = 0; i < count; i++) {
@@ -816,14 +929,14 @@ static int project_impl(ovfq_ctx* ctx, int count, const ovfq_weight* const* ws, 
         if ((rc = ensure(ctx, ctx->x_stage, (size_t)rows * in * 4))) return rc;
         if ((rc = ensure(ctx, ctx->y_stage, ytotal * 4))) return rc;
         if (btotal && (rc = ensure(ctx, ctx->bias_stage, btotal * 4))) return rc;
-        HIP_TRY(hipMemcpyAsync(ctx->x_stage.p, x, (size_t)rows * in * 4, hipMemcpyHostToDevice, ctx->stream));
+        if ((rc = io.up(ctx->x_stage.p, x, (size_t)rows * in * 4))) return rc;
         xd = (const float*)ctx->x_stage.p;
         size_t boff = 0;
         for (int i = 0; i < count; i++) {
             yd[i] = (float*)ctx->y_stage.p + y_off[i];
             if (biases && biases[i]) {
                 float* bdst = (float*)ctx->bias_stage.p + boff;
-                HIP_TRY(hipMemcpyAsync(bdst, biases[i], (size_t)ws[i]->out * 4, hipMemcpyHostToDevice, ctx->stream));
+                if ((rc = io.up(bdst, biases[i], (size_t)ws[i]->out * 4))) return rc;
                 bd[i] = bdst;
                 boff += ws[i]->out;
             }
@@ -845,10 +958,9 @@ static int project_impl(ovfq_ctx* ctx, int count, const ovfq_weight* const* ws, 
         if ((rc = launch_projection(ctx, ws, count, bd, yd, rows, act))) return rc;
     }
     if (host) {
-        for (int i = 0; i < count; i++) {
-            HIP_TRY(hipMemcpyAsync(ys[i], yd[i], (size_t)rows * ws[i]->out * 4, hipMemcpyDeviceToHost, ctx->stream));
-        }
-        HIP_TRY(hipStreamSynchronize(ctx->stream));
+        for (int i = 0; i < count; i++)
+            if ((rc = io.down(ys[i], yd[i], (size_t)rows * ws[i]->out * 4))) return rc;
+        if ((rc = io.finish())) return rc;
     }
     return ok();
 }
@@ -935,6 +1047,11 @@ int ovfq_project_gate_up_dev(ovfq_ctx* ctx, const ovfq_weight* gate, const ovfq_
     return project_impl(ctx, 2, ws, x, 1, nullptr, ys, false);
 }
 
+int ovfq_project_multi(ovfq_ctx* ctx, int count, const ovfq_weight* const* weights, const float* x, int rows,
+                       const float* const* biases, float* const* ys) {
+    return project_impl(ctx, count, weights, x, rows, biases, ys, true);
+}
+
 int ovfq_project_multi_dev(ovfq_ctx* ctx, int count, const ovfq_weight* const* weights, const float* x, int rows,
                            const float* const* biases, float* const* ys) {
     return project_impl(ctx, count, weights, x, rows, biases, ys, false);
@@ -961,17 +1078,18 @@ static int prequant_impl(ovfq_ctx* ctx, const ovfq_weight* w, const int8_t* q, c
     ovfq::ActQ act{q, s, b};
     const float* bd = bias;
     float* yd = y;
+    HostIO io(ctx);
     if (host) {
         if ((rc = ensure(ctx, ctx->act_q, n))) return rc;
         if ((rc = ensure(ctx, ctx->act_s, n / blk * 4))) return rc;
         if (kq && (rc = ensure(ctx, ctx->act_b, n / 16 * 2))) return rc;
         if ((rc = ensure(ctx, ctx->y_stage, (size_t)rows * w->out * 4))) return rc;
         if (bias && (rc = ensure(ctx, ctx->bias_stage, (size_t)w->out * 4))) return rc;
-        HIP_TRY(hipMemcpyAsync(ctx->act_q.p, q, n, hipMemcpyHostToDevice, ctx->stream));
-        HIP_TRY(hipMemcpyAsync(ctx->act_s.p, s, n / blk * 4, hipMemcpyHostToDevice, ctx->stream));
-        if (kq) HIP_TRY(hipMemcpyAsync(ctx->act_b.p, b, n / 16 * 2, hipMemcpyHostToDevice, ctx->stream));
+        if ((rc = io.up(ctx->act_q.p, q, n)) || (rc = io.up(ctx->act_s.p, s, n / blk * 4)) ||
+            (kq && (rc = io.up(ctx->act_b.p, b, n / 16 * 2))))
+            return rc;
         if (bias) {
-            HIP_TRY(hipMemcpyAsync(ctx->bias_stage.p, bias, (size_t)w->out * 4, hipMemcpyHostToDevice, ctx->stream));
+            if ((rc = io.up(ctx->bias_stage.p, bias, (size_t)w->out * 4))) return rc;
             bd = (const float*)ctx->bias_stage.p;
         }
         act = ovfq::ActQ{(const int8_t*)ctx->act_q.p, (const float*)ctx->act_s.p,
@@ -982,10 +1100,7 @@ static int prequant_impl(ovfq_ctx* ctx, const ovfq_weight* w, const int8_t* q, c
     const float* bs[1] = {bd};
     float* ys[1] = {yd};
     if ((rc = launch_projection(ctx, ws, 1, bs, ys, rows, act))) return rc;
-    if (host) {
-        HIP_TRY(hipMemcpyAsync(y, yd, (size_t)rows * w->out * 4, hipMemcpyDeviceToHost, ctx->stream));
-        HIP_TRY(hipStreamSynchronize(ctx->stream));
-    }
+    if (host && ((rc = io.down(y, yd, (size_t)rows * w->out * 4)) || (rc = io.finish()))) return rc;
     return ok();
 }
 
@@ -1059,12 +1174,13 @@ static int heads_impl(ovfq_ctx* ctx, int H, const ovfq_weight* const* wo, const 
     const float* xd = x;
     const float* bd = bias;
     float* yd = y;
+    HostIO io(ctx);
     if (host) {
         if ((rc = ensure(ctx, ctx->x_stage, (size_t)rows * K * 4)) || (rc = ensure(ctx, ctx->y_stage, (size_t)rows * dm * 4)))
             return rc;
         if (bias && (rc = ensure(ctx, ctx->bias_stage, (size_t)dm * 4))) return rc;
-        HIP_TRY(hipMemcpyAsync(ctx->x_stage.p, x, (size_t)rows * K * 4, hipMemcpyHostToDevice, ctx->stream));
-        if (bias) HIP_TRY(hipMemcpyAsync(ctx->bias_stage.p, bias, (size_t)dm * 4, hipMemcpyHostToDevice, ctx->stream));
+        if ((rc = io.up(ctx->x_stage.p, x, (size_t)rows * K * 4))) return rc;
+        if (bias && (rc = io.up(ctx->bias_stage.p, bias, (size_t)dm * 4))) return rc;
         xd = (const float*)ctx->x_stage.p;
         bd = bias ? (const float*)ctx->bias_stage.p : nullptr;
         yd = (float*)ctx->y_stage.p;
@@ -1087,10 +1203,7 @@ static int heads_impl(ovfq_ctx* ctx, int H, const ovfq_weight* const* wo, const 
         HIP_TRY(ovfq::launch_q8_0_heads(wq, ws, H, hd, dm, n, bd, inside ? xd + (size_t)r0 * K : nullptr, a,
                                         yd + (size_t)r0 * dm, ctx->stream));
     }
-    if (host) {
-        HIP_TRY(hipMemcpyAsync(y, yd, (size_t)rows * dm * 4, hipMemcpyDeviceToHost, ctx->stream));
-        HIP_TRY(hipStreamSynchronize(ctx->stream));
-    }
+    if (host && ((rc = io.down(y, yd, (size_t)rows * dm * 4)) || (rc = io.finish()))) return rc;
     return ok();
 }
 
@@ -1132,14 +1245,11 @@ static int topk_impl(ovfq_ctx* ctx, const float* logits, int rows, int n_experts
     float* dl = reinterpret_cast<float*>(base);
     int* di = reinterpret_cast<int*>(base + ((lb + 255) & ~size_t(255)));
     float* dw = reinterpret_cast<float*>(base + ((lb + 255) & ~size_t(255)) + ((ob + 255) & ~size_t(255)));
-    HIP_TRY(hipMemcpyAsync(dl, logits, lb, hipMemcpyHostToDevice, ctx->stream));
+    HostIO io(ctx);
     // slots past min(top_k, n_experts) keep the caller's values
-    HIP_TRY(hipMemcpyAsync(di, idx, ob, hipMemcpyHostToDevice, ctx->stream));
-    HIP_TRY(hipMemcpyAsync(dw, w, ob, hipMemcpyHostToDevice, ctx->stream));
+    if ((rc = io.up(dl, logits, lb)) || (rc = io.up(di, idx, ob)) || (rc = io.up(dw, w, ob))) return rc;
     HIP_TRY(ovfq::launch_moe_topk(dl, rows, n_experts, k, top_k, normalize, di, dw, ctx->stream));
-    HIP_TRY(hipMemcpyAsync(idx, di, ob, hipMemcpyDeviceToHost, ctx->stream));
-    HIP_TRY(hipMemcpyAsync(w, dw, ob, hipMemcpyDeviceToHost, ctx->stream));
-    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    if ((rc = io.down(idx, di, ob)) || (rc = io.down(w, dw, ob)) || (rc = io.finish())) return rc;
     return ok();
 }
 
@@ -1241,14 +1351,14 @@ static int moe_impl(ovfq_ctx* ctx, int E, const ovfq_weight* const* gate, const 
     int* idxd = const_cast<int*>(idx);  // written only when routing here (then the caller's output)
     float* wd = const_cast<float*>(w);
     float* yd = y;
+    HostIO io(ctx);
     if (host) {
-        HIP_TRY(hipMemcpyAsync(hx, x, (size_t)rows * dmodel * 4, hipMemcpyHostToDevice, ctx->stream));
+        if ((rc = io.up(hx, x, (size_t)rows * dmodel * 4))) return rc;
         if (route) {
-            HIP_TRY(hipMemcpyAsync(hl, logits, (size_t)rows * E * 4, hipMemcpyHostToDevice, ctx->stream));
+            if ((rc = io.up(hl, logits, (size_t)rows * E * 4))) return rc;
             ld = hl;
         } else {
-            HIP_TRY(hipMemcpyAsync(hidx, idx, P * 4, hipMemcpyHostToDevice, ctx->stream));
-            HIP_TRY(hipMemcpyAsync(hw, w, P * 4, hipMemcpyHostToDevice, ctx->stream));
+            if ((rc = io.up(hidx, idx, P * 4)) || (rc = io.up(hw, w, P * 4))) return rc;
         }
         xd = hx;
         idxd = hidx;
@@ -1313,8 +1423,18 @@ static int moe_impl(ovfq_ctx* ctx, int E, const ovfq_weight* const* gate, const 
     // combine is folded into it: each token output gets at most two float-atomic adds onto zero, whose sum does not
     // depend on their order, so it is the combine kernel's (0 + w0 o0) + w1 o1 exactly. The zeroing and the per-pair
     // weights go in the gate * up launch.
+    // Float atomics on the output need ordinary device memory: a _dev caller's y that is host-mapped (or not known to
+    // HIP) keeps the separate combine launch. The host entry points write into the context's own device staging.
+    bool y_device = host;
+    if (!host) {
+        hipPointerAttribute_t attr{};
+        if (hipPointerGetAttributes(&attr, y) == hipSuccess)
+            y_device = attr.type == hipMemoryTypeDevice;
+        else
+            (void)hipGetLastError();  // an unregistered host pointer: clear the sticky error
+    }
     ovfq::MoeFold fold{};
-    if (k <= 2 && !grouped_big) {
+    if (k <= 2 && !grouped_big && y_device) {
         fold = ovfq::MoeFold{yd, (int64_t)rows * dmodel, pof, wd, (int)P, pw};
         D.comb = yd;
         D.comb_tok = prow;
@@ -1327,12 +1447,11 @@ static int moe_impl(ovfq_ctx* ctx, int E, const ovfq_weight* const* gate, const 
         HIP_TRY(ovfq::launch_mfma_small(dt, D, ctx->stream));
     if (!D.comb) HIP_TRY(ovfq::launch_moe_combine(out, pof, wd, rows, k, dmodel, yd, ctx->stream));
     if (host) {
-        HIP_TRY(hipMemcpyAsync(y, yd, (size_t)rows * dmodel * 4, hipMemcpyDeviceToHost, ctx->stream));
-        if (route) {
-            HIP_TRY(hipMemcpyAsync(const_cast<int*>(idx), idxd, P * 4, hipMemcpyDeviceToHost, ctx->stream));
-            HIP_TRY(hipMemcpyAsync(const_cast<float*>(w), wd, P * 4, hipMemcpyDeviceToHost, ctx->stream));
-        }
-        HIP_TRY(hipStreamSynchronize(ctx->stream));
+        if ((rc = io.down(y, yd, (size_t)rows * dmodel * 4))) return rc;
+        if (route && ((rc = io.down(const_cast<int*>(idx), idxd, P * 4)) ||
+                      (rc = io.down(const_cast<float*>(w), wd, P * 4))))
+            return rc;
+        if ((rc = io.finish())) return rc;
     }
     return ok();
 }
@@ -1381,8 +1500,9 @@ static int ffn_impl(ovfq_ctx* ctx, const ovfq_weight* gate, const ovfq_weight* u
     carve(c, &g, &u, &iq, &is, &ib, &hx, &hy);
     const float* xd = x;
     float* yd = y;
+    HostIO io(ctx);
     if (host) {
-        HIP_TRY(hipMemcpyAsync(hx, x, R * dmodel * 4, hipMemcpyHostToDevice, ctx->stream));
+        if ((rc = io.up(hx, x, R * dmodel * 4))) return rc;
         xd = hx;
         yd = hy;
     }
@@ -1403,10 +1523,7 @@ static int ffn_impl(ovfq_ctx* ctx, const ovfq_weight* gate, const ovfq_weight* u
     const ovfq_weight* dw[1] = {down};
     float* dy[1] = {yd};
     if ((rc = launch_projection(ctx, dw, 1, nullptr, dy, rows, ovfq::ActQ{iq, is, ib}))) return rc;
-    if (host) {
-        HIP_TRY(hipMemcpyAsync(y, yd, R * dmodel * 4, hipMemcpyDeviceToHost, ctx->stream));
-        HIP_TRY(hipStreamSynchronize(ctx->stream));
-    }
+    if (host && ((rc = io.down(y, yd, R * dmodel * 4)) || (rc = io.finish()))) return rc;
     return ok();
 }
 

@@ -164,7 +164,6 @@ constexpr int kHeadsMaxDim = 256;       // head_dim
 constexpr int kHeadsMaxRows = 8;        // activation rows per launch
 constexpr int kHeadsMaxIn = 32768;      // rows * n_heads * head_dim staged in LDS
 constexpr int kHeadsMaxRowHeads = 256;  // rows * n_heads head values kept in LDS
-constexpr int kHeadsQuantMaxIn = 8192;  // in-launch quantisation (every workgroup quantises the whole input)
 constexpr size_t kHeadsMaxLds = 65536;
 bool q8_0_heads_supported(int n_heads, int head_dim, int rows);
 bool q8_0_heads_quantize_inside(int n_heads, int head_dim, int rows);

@@ -22,6 +22,10 @@ class OverfitUnsupportedTypeError(OverfitArgumentError):
     """A weight type the entry point does not accept."""
 
 
+class OverfitInvalidOperationError(RuntimeError):
+    """InvalidOperationException: the object's state forbids the call (a context that still owns weights)."""
+
+
 class OverfitHipError(RuntimeError):
     """The HIP runtime reported an error."""
 
@@ -38,4 +42,6 @@ def raise_for_status(rc: int, lib) -> None:
         raise OverfitArgumentOutOfRangeError(msg)
     if rc == -4:
         raise OverfitUnsupportedTypeError(msg)
+    if rc == -5:
+        raise OverfitInvalidOperationError(msg)
     raise OverfitHipError(f"status {rc}: {msg}")

@@ -528,6 +528,35 @@ def project(weight, x, bias=None, rows=1, out=None):
     return out
 
 
+def project_multi(weights, x, rows=1, biases=None, outs=None):
+    """Several projections of one activation in one launch (ovfq_project_multi[_dev]): the attention block's q/k/v
+    against its once-quantised hidden rows (RT/CachedMultiHeadAttention.cs:196-207). Returns the outputs, each
+    rows x OutputSize (allocated on the input's side when `outs` is None)."""
+    n = len(weights)
+    if n == 0:
+        raise OverfitArgumentError("weights is empty")
+    inp = as_buf(x, np.float32, "x")
+    if outs is None:
+        if inp.device:
+            import torch
+
+            outs = [torch.empty(rows * w.OutputSize, dtype=torch.float32, device=inp.obj.device) for w in weights]
+        else:
+            outs = [np.zeros(rows * w.OutputSize, np.float32) for w in weights]
+    if len(outs) != n or (biases is not None and len(biases) != n):
+        raise OverfitArgumentError("weights, outs and biases must have the same length")
+    ob = [as_buf(o, np.float32, "out") for o in outs]
+    bb = [None] * n if biases is None else [as_buf(b, np.float32, "bias", allow_none=True) for b in biases]
+    same_side(inp, *ob, *bb)
+    ctx = weights[0].context
+    W = (ctypes.c_void_p * n)(*[w.handle.value for w in weights])
+    Y = (ctypes.c_void_p * n)(*[o.ptr for o in ob])
+    B = (ctypes.c_void_p * n)(*[None if is_empty(b) else b.ptr for b in bb])
+    fn = ctx.lib.ovfq_project_multi_dev if inp.device else ctx.lib.ovfq_project_multi
+    raise_for_status(fn(ctx.handle, n, W, inp.ptr, rows, B, Y), ctx.lib)
+    return outs
+
+
 def project_gate_up(gate, up, x, gate_out=None, up_out=None):
     """Convenience: fused gate/up (ovfq_project_gate_up[_dev]) with the library's own scratch."""
     inp = as_buf(x, np.float32, "x")

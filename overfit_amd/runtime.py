@@ -100,6 +100,17 @@ class Context:
     def synchronize(self):
         self.check(self.lib.ovfq_ctx_synchronize(self.handle))
 
+    def release_retired(self):
+        """Frees scratch buffers that later, larger calls superseded (kept so that captured HIP graphs stay valid).
+        Only when no graph captured from this context's calls will be replayed again."""
+        self.check(self.lib.ovfq_ctx_release_retired(self.handle))
+
+    def scratch_bytes(self):
+        """(live, retired): device scratch bytes in the context's growable buffers and in superseded ones."""
+        live, retired = ctypes.c_size_t(), ctypes.c_size_t()
+        self.check(self.lib.ovfq_ctx_scratch_bytes(self.handle, ctypes.byref(live), ctypes.byref(retired)))
+        return live.value, retired.value
+
     BATCHED_KERNELS = {"auto": 0, "small": 1, "tiled": 2, "rows": 3}
 
     def set_batched_kernel(self, kind: str):

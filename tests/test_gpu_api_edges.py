@@ -42,7 +42,7 @@ def test_context_outlives_its_weights(orc):
     blocks = random_q4k_blocks(rng, 4).reshape(2, -1)
     w = ov.Q4KWeight(blocks, 512, 2, ctx=ctx)
     rc = ctx.lib.ovfq_ctx_destroy(ctx.handle)
-    assert rc == _lib.OVFQ_ERR_SIZE and b"destroy them first" in ctx.lib.ovfq_last_error()
+    assert rc == _lib.OVFQ_ERR_STATE and b"destroy them first" in ctx.lib.ovfq_last_error()
     x = normal(rng, 512)
     y = ov.project(w, x)  # the context is still usable
     assert np.array_equal(y.view(np.uint32), orc.q4k_project(x, blocks, 512, 2).view(np.uint32))
@@ -175,10 +175,53 @@ def test_graph_replay_after_scratch_growth(orc):
         for y, e in zip(ys, eager):
             assert np.array_equal(y.cpu().numpy().view(np.uint32), e.view(np.uint32)), f"replay {rep}"
     del g
+    # With the graph gone the superseded scratch can be given back: device memory is freed, and the context's
+    # calls stay exact on the buffers it keeps.
+    torch.cuda.synchronize()
+    live0, retired0 = ctx.scratch_bytes()
+    assert retired0 > 0 and live0 > 0
+    free0 = torch.cuda.mem_get_info()[0]
+    ctx.release_retired()
+    free1 = torch.cuda.mem_get_info()[0]
+    assert ctx.scratch_bytes() == (live0, 0), "release_retired left superseded scratch"
+    assert free1 >= free0  # the runtime may keep small freed blocks in its own pool
+    ctx.release_retired()  # nothing left to free
+    rows = big_rows // 3
+    ctx.project_dev(wd, t(xb[:rows]), yb, rows=rows)
+    ref = orc.q6k_project_batched(xb[:rows], rows, bd, k2, n, None)
+    assert np.array_equal(yb[: rows * n].cpu().numpy().view(np.uint32), ref.reshape(-1).view(np.uint32))
     del wq, wd
     import gc
     gc.collect()
     ctx.close()
+
+
+def test_moe_ffn_dev_into_host_mapped_output(orc):
+    """ovfq_moe_ffn_dev with top-2 routing folds the combine into float atomics on y only when y is device
+    memory; a y in pinned (host-mapped) memory takes the combine launch. Both give the same bits."""
+    case("moe dev host-mapped y")
+    rng = np.random.default_rng(33)
+    E, dm, dff, rows, k = 4, 256, 512, 6, 2
+    ctx = ov.default_context()
+    mk = lambda n, kk: ov.Q4KWeight(random_q4k_blocks(rng, n * kk // 256).reshape(n, -1), kk, n)
+    gate = [mk(dff, dm) for _ in range(E)]
+    up = [mk(dff, dm) for _ in range(E)]
+    down = [mk(dm, dff) for _ in range(E)]
+    x = t(normal(rng, (rows, dm)))
+    idx = t(np.stack([rng.permutation(E)[:k] for _ in range(rows)]).astype(np.int32))
+    wts = t(rng.random((rows, k)).astype(np.float32))
+    y_dev = torch.full((rows * dm,), float("nan"), device=DEV)
+    y_host = torch.full((rows * dm,), float("nan")).pin_memory()
+    arr = lambda ws: (ctypes.c_void_p * E)(*[w.handle.value for w in ws])
+    for y in (y_dev, y_host):
+        rc = ctx.lib.ovfq_moe_ffn_dev(ctx.handle, E, arr(gate), arr(up), arr(down), vp(x), rows, k, vp(idx), vp(wts),
+                                      ctypes.c_void_p(y.data_ptr()))
+        assert rc == 0, ctx.lib.ovfq_last_error()
+    torch.cuda.synchronize()
+    a = y_dev.cpu().numpy().view(np.uint32)
+    b = y_host.numpy().view(np.uint32)
+    assert np.array_equal(a, b), "host-mapped output differs from the device output"
+    assert not np.isnan(y_host.numpy()).any()
 
 
 def test_reset_stream_and_swiglu_dev(orc):

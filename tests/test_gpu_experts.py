@@ -123,7 +123,7 @@ def test_experts_moe_ffn_and_lifetime(orc):
     assert np.array_equal(np.asarray(ov.project(keep, xv), np.float32).view(np.uint32),
                           orc.q4k_project(xv, g_ref[2], dm, dff).view(np.uint32))
     rc = ctx.lib.ovfq_ctx_destroy(ctx.handle)
-    assert rc == _lib.OVFQ_ERR_SIZE and b"destroy them first" in ctx.lib.ovfq_last_error()
+    assert rc == _lib.OVFQ_ERR_STATE and b"destroy them first" in ctx.lib.ovfq_last_error()
     del gw, uw, dw, keep
     gc.collect()
     ctx.close()

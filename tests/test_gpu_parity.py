@@ -1153,6 +1153,33 @@ def test_gate_up_and_multi_projection(orc, ctx):
     assert_bit_exact(ys[2].cpu().numpy(), orc.q4k_project(x, v, k, n2, bias_v), "multi v")
 
 
+@pytest.mark.parametrize("fmt,rows", [("q4k", 1), ("q4k", 5), ("q6k", 1), ("q6k", 40), ("q8_0", 1), ("q8_0", 9)])
+def test_project_multi_host_pointers(orc, ctx, fmt, rows):
+    """ovfq_project_multi (host pointers, synchronous; the attention block's q/k/v against one quantised hidden row,
+    RT/CachedMultiHeadAttention.cs:196-207) equals the oracle's separate projections bit for bit, through the
+    context's page-locked staging; a second call with fewer rows reuses it."""
+    case("project_multi host", fmt, rows)
+    rng = np.random.default_rng(4242 + rows)
+    k = 4096 if fmt != "q6k" else 2048
+    ns = [512, 128, 128]
+    if fmt == "q8_0":
+        planes = [orc.q8_quantize_rows(normal(rng, (n, k), 0.05)) for n in ns]
+        ws = [ov.Q8Weight(q, s_, k, n) for (q, s_), n in zip(planes, ns)]
+        ref = lambda i, x, r, b: orc.q8_project_batched(x, r, planes[i][0], planes[i][1], k, ns[i], b)
+    else:
+        blocks = [_kq_blocks(rng, fmt, n, k) for n in ns]
+        W = ov.Q4KWeight if fmt == "q4k" else ov.Q6KWeight
+        ws = [W(b, k, n) for b, n in zip(blocks, ns)]
+        pb = orc.q4k_project_batched if fmt == "q4k" else orc.q6k_project_batched
+        ref = lambda i, x, r, b: pb(x, r, blocks[i], k, ns[i], b)
+    bias = normal(rng, ns[1])
+    for r in (rows, max(1, rows // 2)):
+        x = normal(rng, (r, k))
+        outs = ov.project_multi(ws, x, rows=r, biases=[None, bias, None])
+        for i in range(3):
+            assert_bit_exact(outs[i], ref(i, x, r, bias if i == 1 else None).reshape(-1), f"{fmt} job {i} rows {r}")
+
+
 @pytest.mark.parametrize("fmt", ["q4k", "q6k"])
 def test_partial_chunk_decode_multi_and_prequantized(orc, ctx, fmt):
     """Decode kernel on rows of 21 super-blocks (a partial last 16-block chunk): a fused three-job launch with odd row

@@ -93,3 +93,35 @@ def test_noalloc_refuses_past_the_fixed_scratch(orc):
     y = torch.zeros(rows * n, device=DEV)
     assert _call(lib, ctx, lib.ovfq_project_noalloc_dev, w, x, rows, None, y) == _lib.OVFQ_ERR_SIZE
     assert b"fixed scratch" in lib.ovfq_last_error()
+
+
+def test_noalloc_allocates_no_device_memory(orc):
+    """On a fresh context that has never grown its scratch, calls of ovfq_project_noalloc_dev up to the fixed
+    scratch's full size leave the device's free memory unchanged (every tensor is allocated beforehand; the first,
+    small call loads the kernels). A path that fell back to the context's growable scratch would allocate at least
+    the 2 MiB quant plane here."""
+    ctx = ov.Context(0)
+    lib = ctx.lib
+    rng = np.random.default_rng(8)
+    k, n, rows = 4096, 256, (1 << 21) // 4096
+    blocks = random_q4k_blocks(rng, n * k // 256).reshape(n, -1)
+    w = ov.Q4KWeight(blocks, k, n, ctx=ctx)
+    x_small, x_big = t(normal(rng, (40, k))), t(normal(rng, (rows, k)))
+    y_small = torch.empty(40 * n, device=DEV)
+    y_big = torch.empty(rows * n, device=DEV)
+    case("noalloc fresh context", rows)
+    assert ctx.scratch_bytes() == (0, 0)
+    assert _call(lib, ctx, lib.ovfq_project_noalloc_dev, w, x_small, 40, None, y_small) == 0, lib.ovfq_last_error()
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    assert _call(lib, ctx, lib.ovfq_project_noalloc_dev, w, x_big, rows, None, y_big) == 0, lib.ovfq_last_error()
+    torch.cuda.synchronize()
+    free1 = torch.cuda.mem_get_info()[0]
+    assert free1 == free0, f"device free memory changed by {free0 - free1} bytes"
+    assert ctx.scratch_bytes() == (0, 0), "the allocation-free entry point grew the context's scratch"
+    ref = orc.q4k_project_batched(x_big.cpu().numpy(), rows, blocks, k, n, None).reshape(-1)
+    assert np.array_equal(y_big.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+    del w
+    import gc
+    gc.collect()
+    ctx.close()
