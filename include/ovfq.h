@@ -55,6 +55,9 @@ extern "C" {
 #define OVFQ_TYPE_Q8_0 8
 #define OVFQ_TYPE_Q4_K 12
 #define OVFQ_TYPE_Q6_K 14
+/* GGUF-only source types: ovfq_weight_create_gguf / _experts_gguf turn them into resident Q8_0 weights. */
+#define OVFQ_TYPE_Q5_0 6
+#define OVFQ_TYPE_Q5_K 13
 
 /* Block geometry. */
 #define OVFQ_QK 256          /* elements per K-quant super-block (RT/Q4KWeight.cs:26) */
@@ -125,20 +128,25 @@ OVFQ_API int ovfq_weight_create_from_device(ovfq_ctx* ctx, int type, const void*
 /* A tensor exactly as stored in a GGUF file (a slice of the memory-mapped file): Q4_K / Q6_K super-blocks are
  * uploaded verbatim (GgufReader.LoadTensorQ4_KRaw / Q6_KRaw, LD/GgufReader.cs:276-344); Q8_0's 34-byte blocks (fp16 d +
  * 32 int8, GgufReader.LoadTensorQ8_0Raw, LD/GgufReader.cs:198-266) are de-interleaved on the device into the
- * resident int8 quant plane and f32 scale plane (d widened exactly). `nbytes` must cover output_size rows. */
+ * resident int8 quant plane and f32 scale plane (d widened exactly). Q5_0 (22-byte blocks of 32) and Q5_K (176-byte
+ * super-blocks) tensors become resident Q8_0 weights as the reference's loader makes them (LD/GgufLlamaLoader.cs:
+ * 665-680 and its F32 fallback for per-layer tensors): every block decoded exactly as GgmlDequant.DecodeQ5_0Block /
+ * DecodeQ5_KBlock (LD/GgmlDequant.cs:222-320), then requantised with Q8Weight.QuantizeRows (RT/Q8Weight.cs:115-175),
+ * both on the device; ovfq_weight_info then reports OVFQ_TYPE_Q8_0. `nbytes` must cover output_size rows. */
 OVFQ_API int ovfq_weight_create_gguf(ovfq_ctx* ctx, int type, const void* gguf_bytes, size_t nbytes, int input_size,
                                      int output_size, ovfq_weight** out);
 /* As ovfq_weight_create_gguf, from device memory. */
 OVFQ_API int ovfq_weight_create_gguf_dev(ovfq_ctx* ctx, int type, const void* gguf_bytes, size_t nbytes,
                                          int input_size, int output_size, ovfq_weight** out);
-/* Replaces GgufLlamaLoader.LoadExperts (LD/GgufLlamaLoader.cs:600-690) for Q4_K / Q6_K / Q8_0: a 3-D expert tensor
+/* Replaces GgufLlamaLoader.LoadExperts (LD/GgufLlamaLoader.cs:600-690) for Q4_K / Q5_0 / Q5_K / Q6_K / Q8_0: a 3-D
+ * expert tensor
  * (ffn_gate_exps / ffn_up_exps / ffn_down_exps) as stored in a GGUF file, dims [ne0 = input_size, ne1 = output_size,
  * ne2 = n_experts] with the expert axis slowest, -> n_experts weights written to out[0 .. n_experts). Each expert is
- * the contiguous slice e of the tensor: K-quant bytes verbatim, Q8_0 blocks de-interleaved per expert. All experts
+ * the contiguous slice e of the tensor: Q4_K / Q6_K bytes verbatim, Q8_0 blocks de-interleaved per expert, Q5_0 / Q5_K
+ * decoded and requantised to Q8_0 per expert (as ovfq_weight_create_gguf does; LD/GgufLlamaLoader.cs:665-680). All experts
  * share one device allocation (each slice 256-byte aligned), freed when the last of them is destroyed; each is
  * destroyed with ovfq_weight_destroy like any weight. `nbytes` must cover n_experts slices. 1 <= n_experts <=
- * OVFQ_MAX_EXPERT_SLICES. The reference's Q5_0 / Q5_K re-quantisation to Q8_0 is not in this library
- * (OVFQ_ERR_TYPE). */
+ * OVFQ_MAX_EXPERT_SLICES. */
 #define OVFQ_MAX_EXPERT_SLICES 4096
 OVFQ_API int ovfq_weight_create_experts_gguf(ovfq_ctx* ctx, int type, const void* gguf_bytes, size_t nbytes,
                                              int input_size, int output_size, int n_experts, ovfq_weight** out);

@@ -27,6 +27,9 @@ _SIGS = {
     "orc_unpack_q4k_scales_mins": (None, [c_u8p, c_u8p, c_u8p]),
     "orc_pack_q4k_scales_mins": (None, [c_u8p, c_u8p, c_u8p]),
     "orc_decode_q4k_block": (None, [c_u8p, c_f32p]),
+    "orc_decode_q5_0_block": (None, [c_u8p, c_f32p]),
+    "orc_decode_q5k_block": (None, [c_u8p, c_f32p]),
+    "orc_q5_requantize_q8_0": (c_int, [c_int, c_u8p, c_int, c_int, c_i8p, c_f32p]),
     "orc_decode_q6k_block": (None, [c_u8p, c_f32p]),
     "orc_q4k_decode_row": (c_int, [c_u8p, c_int, c_int, c_int, c_f32p]),
     "orc_q6k_decode_row": (c_int, [c_u8p, c_int, c_int, c_int, c_f32p]),
@@ -167,6 +170,29 @@ def decode_q4k_block(block):
     dst = np.zeros(256, np.float32)
     lib().orc_decode_q4k_block(P(b), P(dst))
     return dst
+
+
+def decode_q5_0_block(block):
+    b = np.ascontiguousarray(block, dtype=np.uint8)
+    dst = np.zeros(32, np.float32)
+    lib().orc_decode_q5_0_block(P(b), P(dst))
+    return dst
+
+
+def decode_q5k_block(block):
+    b = np.ascontiguousarray(block, dtype=np.uint8)
+    dst = np.zeros(256, np.float32)
+    lib().orc_decode_q5k_block(P(b), P(dst))
+    return dst
+
+
+def q5_requantize_q8_0(type_id, data, rows, k):
+    """Q5_0 / Q5_K rows -> the loader's resident Q8_0 planes (decode to F32, Q8Weight.QuantizeRows)."""
+    d = np.ascontiguousarray(data, np.uint8).ravel()
+    q = np.zeros((rows, k), np.int8)
+    s = np.zeros((rows, k // 32), np.float32)
+    _check(lib().orc_q5_requantize_q8_0(type_id, P(d), rows, k, P(q), P(s)))
+    return q, s
 
 
 def decode_q6k_block(block):

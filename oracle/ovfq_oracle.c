@@ -130,6 +130,49 @@ void orc_decode_q4k_block(const uint8_t* b, float* dst) {
     }
 }
 
+void orc_decode_q5_0_block(const uint8_t* b, float* dst) {
+    /* LD/GgmlDequant.cs:222-248: d fp16 @0, qh u32 LE @2 (the 5th bit of each quant), qs @6; element j takes the low
+     * nibble of qs[j] and qh bit j, element j + 16 the high nibble and bit j + 16; dst = (q - 16) * d. */
+    float d = orc_half_to_float(rd_u16(b));
+    uint32_t qh = (uint32_t)b[2] | ((uint32_t)b[3] << 8) | ((uint32_t)b[4] << 16) | ((uint32_t)b[5] << 24);
+    const uint8_t* qs = b + 6;
+    for (int j = 0; j < 16; j++) {
+        int xh0 = (int)((qh >> j) << 4) & 0x10;
+        int xh1 = (int)(qh >> (j + 12)) & 0x10;
+        int x0 = ((qs[j] & 0x0f) | xh0) - 16;
+        int x1 = ((qs[j] >> 4) | xh1) - 16;
+        dst[j] = (float)x0 * d;
+        dst[j + 16] = (float)x1 * d;
+    }
+}
+
+void orc_decode_q5k_block(const uint8_t* b, float* dst) {
+    /* LD/GgmlDequant.cs:262-320: the Q4_K layout (d, dmin, 12 packed scale/min bytes) with 32 bytes of 5th bits
+     * (qh @16) before the 128 nibble bytes (qs @48); group g's low nibbles take qh bit 2g, its high nibbles bit
+     * 2g + 1. */
+    float d = orc_half_to_float(rd_u16(b));
+    float dmin = orc_half_to_float(rd_u16(b + 2));
+    uint8_t sc[8], m[8];
+    orc_unpack_q4k_scales_mins(b + 4, sc, m);
+    const uint8_t* qh = b + 16;
+    const uint8_t* qs = b + 48;
+    for (int g = 0; g < 4; g++) {
+        float scale1 = d * (float)sc[2 * g];
+        float min1 = dmin * (float)m[2 * g];
+        float scale2 = d * (float)sc[2 * g + 1];
+        float min2 = dmin * (float)m[2 * g + 1];
+        int u1 = 1 << (2 * g), u2 = 2 << (2 * g);
+        for (int l = 0; l < 32; l++) {
+            int hi = (qh[l] & u1) ? 16 : 0;
+            dst[64 * g + l] = scale1 * (float)((qs[32 * g + l] & 0x0f) + hi) - min1;
+        }
+        for (int l = 0; l < 32; l++) {
+            int hi = (qh[l] & u2) ? 16 : 0;
+            dst[64 * g + 32 + l] = scale2 * (float)((qs[32 * g + l] >> 4) + hi) - min2;
+        }
+    }
+}
+
 void orc_decode_q6k_block(const uint8_t* b, float* dst) {
     /* LD/GgmlDequant.cs:143-209 */
     const uint8_t* ql = b;
@@ -820,6 +863,32 @@ int orc_q8_quantize_rows(const float* rm, int rows, int len, int8_t* quants, flo
 }
 
 /* ---------------------------------------------------------------- MoE router */
+
+int orc_q5_requantize_q8_0(int type, const uint8_t* src, int rows, int len, int8_t* quants, float* scales) {
+    /* A Q5_0 (ggml type 6) or Q5_K (13) tensor of `rows` rows of `len` elements -> the resident Q8_0 planes, as the
+     * loader makes them: every block decoded to F32 (GgufReader.LoadQ5RegionAsF32, LD/GgufReader.cs:677-732, and the
+     * F32 fallback, LD/GgufLlamaLoader.cs:665-680), then Q8Weight.QuantizeRows (RT/Q8Weight.cs:115-175). */
+    if (!src || !quants || !scales) return ORC_ERR_NULL;
+    if (rows <= 0 || len <= 0) return ORC_ERR_RANGE;
+    const int blk = type == 6 ? 32 : type == 13 ? 256 : 0;
+    if (!blk) return ORC_ERR_SIZE;
+    if (len % blk) return ORC_ERR_SIZE;
+    const int bb = type == 6 ? 22 : 176;
+    float* row = (float*)malloc(sizeof(float) * (size_t)len);
+    if (!row) return ORC_ERR_NULL;
+    for (int r = 0; r < rows; r++) {
+        const uint8_t* rb = src + (size_t)r * (len / blk) * bb;
+        for (int b = 0; b < len / blk; b++) {
+            if (type == 6)
+                orc_decode_q5_0_block(rb + (size_t)b * bb, row + (size_t)b * blk);
+            else
+                orc_decode_q5k_block(rb + (size_t)b * bb, row + (size_t)b * blk);
+        }
+        orc_q8_quantize_rows(row, 1, len, quants + (size_t)r * len, scales + (size_t)r * (len / ORC_Q8_BLOCK));
+    }
+    free(row);
+    return ORC_OK;
+}
 
 int orc_q8_0_deinterleave(const uint8_t* gguf, long n_blocks, int8_t* quants, float* scales) {
     /* LD/GgufReader.cs:250-260: scale = (float)Half(bits), quants copied */

@@ -43,6 +43,11 @@ void orc_pack_q4k_scales_mins(const uint8_t* sc8, const uint8_t* m8, uint8_t* pa
 
 /* a19: LD/GgmlDequant.cs:95-141 and :143-209 */
 void orc_decode_q4k_block(const uint8_t* block144, float* dst256);
+/* GgmlDequant.DecodeQ5_0Block / DecodeQ5_KBlock (LD/GgmlDequant.cs:222-320). */
+void orc_decode_q5_0_block(const uint8_t* block22, float* dst32);
+void orc_decode_q5k_block(const uint8_t* block176, float* dst256);
+/* Q5_0 (type 6) / Q5_K (type 13) rows -> resident Q8_0 planes (decode to F32, then Q8Weight.QuantizeRows). */
+int orc_q5_requantize_q8_0(int type, const uint8_t* src, int rows, int len, int8_t* quants, float* scales);
 void orc_decode_q6k_block(const uint8_t* block210, float* dst256);
 /* a15: RT/Q4KWeight.cs:121-138, RT/Q6KWeight.cs DecodeRow, RT/Q8Weight.cs:81-106 */
 int orc_q4k_decode_row(const uint8_t* blocks, int input_size, int output_size, int row, float* dst);

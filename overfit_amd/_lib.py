@@ -22,6 +22,8 @@ OVFQ_FFN_GEGLU = 4
 TYPE_Q8_0 = 8
 TYPE_Q4_K = 12
 TYPE_Q6_K = 14
+TYPE_Q5_0 = 6
+TYPE_Q5_K = 13
 
 vp = ctypes.c_void_p
 ci = ctypes.c_int

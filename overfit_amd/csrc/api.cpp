@@ -597,26 +597,49 @@ int ovfq_weight_create_from_device(ovfq_ctx* ctx, int type, const void* blocks, 
                          hipMemcpyDeviceToDevice);
 }
 
+// GGUF tensor types whose resident form is the Q8_0 planes: Q8_0 itself (de-interleaved) and the 5-bit types, which
+// the reference's loader decodes to F32 and requantises to Q8_0 (LD/GgufLlamaLoader.cs:665-680).
+bool gguf_as_q8(int type) { return type == OVFQ_TYPE_Q8_0 || type == OVFQ_TYPE_Q5_0 || type == OVFQ_TYPE_Q5_K; }
+
+// Source bytes per 32 weights of such a tensor: 34 for Q8_0 (fp16 d + 32 int8); 22 for Q5_0 (a block) and for Q5_K
+// (176 bytes per 256).
+size_t gguf_bytes_per_32(int type) { return type == OVFQ_TYPE_Q8_0 ? 34 : 22; }
+
+// Shape checks of a GGUF tensor that becomes Q8_0 planes: the resident Q8_0 weight's, and whole Q5_K super-blocks.
+int check_gguf_q8_shape(int type, int in, int out) {
+    int rc = check_weight_shape(OVFQ_TYPE_Q8_0, in, out);
+    if (rc) return rc;
+    if (type == OVFQ_TYPE_Q5_K && in % OVFQ_QK)
+        return fail(OVFQ_ERR_SIZE, "Q5_K inputSize (%d) must be a multiple of 256", in);
+    return OVFQ_OK;
+}
+
+hipError_t launch_gguf_to_q8(int type, const void* src, int64_t n_blocks, int8_t* q, float* s, hipStream_t st) {
+    if (type == OVFQ_TYPE_Q8_0) return ovfq::launch_q8_0_deinterleave(src, n_blocks, q, s, st);
+    return ovfq::launch_q5_to_q8_0(src, type == OVFQ_TYPE_Q5_K, n_blocks, q, s, st);
+}
+
 static int weight_create_gguf(ovfq_ctx* ctx, int type, const void* src, size_t nbytes, int in, int out,
                               ovfq_weight** res, bool host) {
-    if (type != OVFQ_TYPE_Q8_0)
+    if (!gguf_as_q8(type))
         return weight_create(ctx, type, src, nbytes, nullptr, in, out, res,
                              host ? hipMemcpyHostToDevice : hipMemcpyDeviceToDevice);
     if (!ctx) return fail(OVFQ_ERR_NULL, "ctx is NULL");
     if (!src) return fail(OVFQ_ERR_NULL, "gguf_bytes is NULL");
     if (!res) return fail(OVFQ_ERR_NULL, "out is NULL");
-    int rc = check_weight_shape(type, in, out);
+    int rc = check_gguf_q8_shape(type, in, out);
     if (rc) return rc;
     const int64_t n_blocks = (int64_t)out * (in / OVFQ_Q8_BLOCK);
-    const size_t gguf_len = (size_t)n_blocks * 34;
+    const size_t gguf_len = (size_t)n_blocks * gguf_bytes_per_32(type);
     if (nbytes < gguf_len)
-        return fail(OVFQ_ERR_SIZE, "Q8_0 region (%zu B) is smaller than the expected %zu B", nbytes, gguf_len);
-    if (!host && !aligned(src, 2)) return fail(OVFQ_ERR_SIZE, "device gguf_bytes must be 2-byte aligned");
+        return fail(OVFQ_ERR_SIZE, "GGUF region (%zu B) is smaller than the expected %zu B", nbytes, gguf_len);
+    if (!host && type == OVFQ_TYPE_Q8_0 && !aligned(src, 2))
+        return fail(OVFQ_ERR_SIZE, "device gguf_bytes must be 2-byte aligned");
     std::lock_guard<std::mutex> lk(ctx->mu);
     HIP_TRY(hipSetDevice(ctx->device));
     ovfq_weight* w = new ovfq_weight();
     w->ctx = ctx;
-    w->type = type;
+    w->type = OVFQ_TYPE_Q8_0;
     w->in = in;
     w->out = out;
     void* staged = nullptr;
@@ -629,14 +652,14 @@ static int weight_create_gguf(ovfq_ctx* ctx, int type, const void* src, size_t n
         dsrc = staged;
     }
     if (e == hipSuccess)
-        e = ovfq::launch_q8_0_deinterleave(dsrc, n_blocks, static_cast<int8_t*>(w->blocks), w->scales, ctx->stream);
+        e = launch_gguf_to_q8(type, dsrc, n_blocks, static_cast<int8_t*>(w->blocks), w->scales, ctx->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     if (staged) (void)hipFree(staged);
     if (e != hipSuccess) {
         if (w->blocks) (void)hipFree(w->blocks);
         if (w->scales) (void)hipFree(w->scales);
         delete w;
-        return fail(OVFQ_ERR_HIP, "Q8_0 GGUF upload failed: %s", hipGetErrorString(e));
+        return fail(OVFQ_ERR_HIP, "GGUF upload to Q8_0 failed: %s", hipGetErrorString(e));
     }
     w->nbytes = (size_t)n_blocks * (OVFQ_Q8_BLOCK + sizeof(float));
     ctx->live_weights++;
@@ -664,17 +687,19 @@ static int experts_gguf_impl(ovfq_ctx* ctx, int type, const void* src, size_t nb
     if (!ctx) return fail(OVFQ_ERR_NULL, "ctx is NULL");
     if (!src) return fail(OVFQ_ERR_NULL, "gguf_bytes is NULL");
     if (!res) return fail(OVFQ_ERR_NULL, "out is NULL");
-    int rc = check_weight_shape(type, in, out);
+    const bool q8 = gguf_as_q8(type);
+    int rc = q8 ? check_gguf_q8_shape(type, in, out) : check_weight_shape(type, in, out);
     if (rc) return rc;
     if (n_experts <= 0 || n_experts > OVFQ_MAX_EXPERT_SLICES)
         return fail(OVFQ_ERR_RANGE, "n_experts (%d) must be in [1, %d]", n_experts, OVFQ_MAX_EXPERT_SLICES);
-    const bool q8 = type == OVFQ_TYPE_Q8_0;
     const int64_t blocks_per_expert = (int64_t)out * (in / OVFQ_Q8_BLOCK);
-    const size_t src_expert = q8 ? (size_t)blocks_per_expert * 34 : block_bytes_per_row(type, in) * (size_t)out;
+    const size_t src_expert =
+        q8 ? (size_t)blocks_per_expert * gguf_bytes_per_32(type) : block_bytes_per_row(type, in) * (size_t)out;
     if (nbytes / (size_t)n_experts < src_expert)
         return fail(OVFQ_ERR_SIZE, "expert tensor region (%zu B) is smaller than the expected %d x %zu B", nbytes,
                     n_experts, src_expert);
-    if (!host && q8 && !aligned(src, 2)) return fail(OVFQ_ERR_SIZE, "device gguf_bytes must be 2-byte aligned");
+    if (!host && type == OVFQ_TYPE_Q8_0 && !aligned(src, 2))
+        return fail(OVFQ_ERR_SIZE, "device gguf_bytes must be 2-byte aligned");
     auto pad = [](size_t b) { return (b + 255) & ~size_t(255); };
     const size_t q_bytes = q8 ? (size_t)out * in : src_expert;
     const size_t s_bytes = q8 ? (size_t)blocks_per_expert * sizeof(float) : 0;
@@ -699,10 +724,9 @@ static int experts_gguf_impl(ovfq_ctx* ctx, int type, const void* src, size_t nb
         }
         float* scales = reinterpret_cast<float*>(base + E * q_stride);
         for (size_t x = 0; x < E && e == hipSuccess; x++)
-            e = ovfq::launch_q8_0_deinterleave(dsrc + x * src_expert, blocks_per_expert,
-                                               reinterpret_cast<int8_t*>(base + x * q_stride),
-                                               reinterpret_cast<float*>(reinterpret_cast<char*>(scales) + x * s_stride),
-                                               ctx->stream);
+            e = launch_gguf_to_q8(type, dsrc + x * src_expert, blocks_per_expert,
+                                  reinterpret_cast<int8_t*>(base + x * q_stride),
+                                  reinterpret_cast<float*>(reinterpret_cast<char*>(scales) + x * s_stride), ctx->stream);
     }
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     if (staged) (void)hipFree(staged);
@@ -716,7 +740,7 @@ static int experts_gguf_impl(ovfq_ctx* ctx, int type, const void* src, size_t nb
     for (size_t x = 0; x < E; x++) {
         ovfq_weight* w = new ovfq_weight();
         w->ctx = ctx;
-        w->type = type;
+        w->type = q8 ? OVFQ_TYPE_Q8_0 : type;
         w->in = in;
         w->out = out;
         w->blocks = base + x * q_stride;

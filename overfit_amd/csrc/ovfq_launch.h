@@ -173,6 +173,9 @@ hipError_t launch_q8_0_heads(const int8_t* const* wq, const float* const* ws, in
 
 // GGUF Q8_0 (34-byte blocks) -> int8 quant plane + f32 scale plane.
 hipError_t launch_q8_0_deinterleave(const void* gguf, int64_t n_blocks, int8_t* q, float* s, hipStream_t st);
+// GGUF Q5_0 (22-byte blocks of 32) or Q5_K (176-byte super-blocks) -> resident Q8_0 planes: decoded and requantised
+// in registers; n_blocks counts 32-element blocks.
+hipError_t launch_q5_to_q8_0(const void* gguf, bool q5k, int64_t n_blocks, int8_t* q, float* s, hipStream_t st);
 hipError_t launch_encode_q4k(const float* w, int64_t n_blocks, uint8_t* dst, hipStream_t st);
 hipError_t launch_encode_q6k(const float* w, int64_t n_blocks, uint8_t* dst, hipStream_t st);
 

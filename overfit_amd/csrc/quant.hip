@@ -244,6 +244,82 @@ __global__ __launch_bounds__(256) void q8_0_deinterleave_kernel(const uint16_t* 
     for (int i = 0; i < 8; i++) q[blk * 8 + i] = (uint32_t)b[1 + 2 * i] | ((uint32_t)b[2 + 2 * i] << 16);
 }
 
+// ------------------------------------------------------------------------------------------ GGUF Q5_0 / Q5_K upload
+// The loader keeps 5-bit tensors as Q8_0 (LD/GgufLlamaLoader.cs:665-680 for experts, the F32 fallback of the
+// per-layer tensors): every block decoded to F32 as GgmlDequant.DecodeQ5_0Block / DecodeQ5_KBlock do
+// (LD/GgmlDequant.cs:222-320), then requantised with Q8Weight.QuantizeRows (RT/Q8Weight.cs:115-175). Here both
+// happen in registers: eight lanes per 32-element Q8_0 block, four elements per lane, the block's absmax by three
+// lane exchanges. Rows are whole numbers of blocks, so the flat 32-element block index of the tensor is also the
+// block index of the resident planes. Source blocks are 2-byte aligned (22 bytes) or 16-byte aligned (176 bytes);
+// they are read byte by byte (load time only).
+__global__ __launch_bounds__(256) void q5_to_q8_0_kernel(const uint8_t* __restrict__ src, int kquant, int64_t n_blocks,
+                                                         int8_t* __restrict__ q, float* __restrict__ s) {
+    const int64_t wblk = ((int64_t)blockIdx.x * 4 + wave_id()) * 8;
+    if (wblk >= n_blocks) return;
+    const int lane = threadIdx.x & 63;
+    const int64_t blk = wblk + (lane >> 3);
+    const int sub = lane & 7;
+    const bool live = blk < n_blocks;
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (live && !kquant) {
+        // Q5_0: d fp16 @0, qh @2 (bit i = the 5th bit of element i), qs @6 (element i < 16: low nibble of qs[i],
+        // element i >= 16: high nibble of qs[i - 16]); value (q - 16) * d.
+        const uint8_t* b = src + blk * 22;
+        const float d = half_bits_to_float((uint16_t)(b[0] | (b[1] << 8)));
+        const uint32_t qh = (uint32_t)b[2] | ((uint32_t)b[3] << 8) | ((uint32_t)b[4] << 16) | ((uint32_t)b[5] << 24);
+        for (int k = 0; k < 4; k++) {
+            const int i = 4 * sub + k;
+            const int packed = b[6 + (i & 15)];
+            const int nib = i < 16 ? (packed & 0x0f) : (packed >> 4);
+            const int x = (nib | (int)(((qh >> i) & 1u) << 4)) - 16;
+            v[k] = (float)x * d;
+        }
+    } else if (live) {
+        // Q5_K: the Q4_K header (d, dmin, 12 packed scale/min bytes), qh @16, qs @48. Sub-block j = 2g + h of the
+        // super-block takes the low (h = 0) or high (h = 1) nibbles of qs[32g ..] and qh bit 2g + h of qh[l].
+        const uint8_t* b = src + (blk >> 3) * 176;
+        const int j = (int)(blk & 7), g = j >> 1, h = j & 1;
+        const float d = half_bits_to_float((uint16_t)(b[0] | (b[1] << 8)));
+        const float dmin = half_bits_to_float((uint16_t)(b[2] | (b[3] << 8)));
+        const uint8_t* pk = b + 4;
+        int sc, m;
+        if (j < 4) {
+            sc = pk[j] & 63;
+            m = pk[j + 4] & 63;
+        } else {
+            sc = (pk[j + 4] & 0x0f) | ((pk[j - 4] >> 6) << 4);
+            m = (pk[j + 4] >> 4) | ((pk[j] >> 6) << 4);
+        }
+        const float scale = d * (float)sc;
+        const float mn = dmin * (float)m;
+        for (int k = 0; k < 4; k++) {
+            const int l = 4 * sub + k;
+            const int packed = b[48 + 32 * g + l];
+            const int nib = h ? (packed >> 4) : (packed & 0x0f);
+            const int hi = ((b[16 + l] >> (2 * g + h)) & 1) ? 16 : 0;
+            v[k] = scale * (float)(nib + hi) - mn;
+        }
+    }
+    u32x4 raw;
+    raw.x = __builtin_bit_cast(uint32_t, v[0]);
+    raw.y = __builtin_bit_cast(uint32_t, v[1]);
+    raw.z = __builtin_bit_cast(uint32_t, v[2]);
+    raw.w = __builtin_bit_cast(uint32_t, v[3]);
+    const Q80Lane r = q8_0_quantize_lane(raw);  // every lane of the block takes part in the exchanges
+    if (live) {
+        reinterpret_cast<uint32_t*>(q + blk * 32)[sub] = r.packed;
+        if (sub == 0) s[blk] = r.scale;
+    }
+}
+
+hipError_t launch_q5_to_q8_0(const void* gguf, bool q5k, int64_t n_blocks, int8_t* q, float* s, hipStream_t st) {
+    if (n_blocks <= 0) return hipSuccess;
+    const int64_t grid = (n_blocks * 8 + 255) / 256;
+    hipLaunchKernelGGL(q5_to_q8_0_kernel, dim3((unsigned)grid), dim3(256), 0, st, static_cast<const uint8_t*>(gguf),
+                       q5k ? 1 : 0, n_blocks, q, s);
+    return hipGetLastError();
+}
+
 hipError_t launch_quantize_q8k(const float* x, int64_t n_blocks, int8_t* q, float* s, int16_t* b, hipStream_t st) {
     if (n_blocks <= 0) return hipSuccess;
     const int64_t grid = (n_blocks + 3) / 4;

@@ -140,11 +140,17 @@ class Q8Weight(_ResidentWeight):
         self._upload(q, q.size, s, input_size, output_size, ctx)
 
 
+# GGUF tensor type -> the resident weight class it becomes (the 5-bit types are kept as Q8_0).
+_GGUF_CLASS = {_lib.TYPE_Q4_K: Q4KWeight, _lib.TYPE_Q6_K: Q6KWeight, _lib.TYPE_Q8_0: Q8Weight,
+               _lib.TYPE_Q5_0: Q8Weight, _lib.TYPE_Q5_K: Q8Weight}
+
+
 def load_gguf_tensor(type_id, data, input_size: int, output_size: int, ctx=None):
     """A quantized tensor exactly as a GGUF file stores it -> the matching resident weight (GgufReader's
     LoadTensorQ4_KRaw / LoadTensorQ6_KRaw / LoadTensorQ8_0Raw, LD/GgufReader.cs:198-344): Q4_K/Q6_K bytes verbatim,
-    Q8_0's 34-byte blocks de-interleaved on the device into the int8 + f32 planes."""
-    cls = {_lib.TYPE_Q4_K: Q4KWeight, _lib.TYPE_Q6_K: Q6KWeight, _lib.TYPE_Q8_0: Q8Weight}.get(type_id)
+    Q8_0's 34-byte blocks de-interleaved on the device into the int8 + f32 planes, Q5_0 / Q5_K decoded and requantised
+    to a Q8_0 weight on the device (the loader's path for 5-bit tensors, LD/GgufLlamaLoader.cs:665-680)."""
+    cls = _GGUF_CLASS.get(type_id)
     if cls is None:
         raise OverfitUnsupportedTypeError(f"type {type_id}")
     buf = as_buf(data, np.uint8, "data")
@@ -163,8 +169,9 @@ def load_gguf_tensor(type_id, data, input_size: int, output_size: int, ctx=None)
 def load_gguf_experts(type_id, data, input_size: int, output_size: int, n_experts: int, ctx=None):
     """GgufLlamaLoader.LoadExperts (LD/GgufLlamaLoader.cs:600-690): a 3-D GGUF expert tensor [input_size,
     output_size, n_experts] (expert axis slowest) -> one resident weight per expert, the experts sharing one device
-    allocation (freed with the last of them). Q4_K/Q6_K slices verbatim, Q8_0 de-interleaved per expert."""
-    cls = {_lib.TYPE_Q4_K: Q4KWeight, _lib.TYPE_Q6_K: Q6KWeight, _lib.TYPE_Q8_0: Q8Weight}.get(type_id)
+    allocation (freed with the last of them). Q4_K/Q6_K slices verbatim, Q8_0 de-interleaved per expert, Q5_0 / Q5_K
+    requantised to Q8_0 per expert."""
+    cls = _GGUF_CLASS.get(type_id)
     if cls is None:
         raise OverfitUnsupportedTypeError(f"type {type_id}")
     buf = as_buf(data, np.uint8, "data")

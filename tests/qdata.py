@@ -62,3 +62,17 @@ Q8_0_KATS = [
     ([2.0], np.array([-128, -1, 0, 1, 127] + [i - 16 for i in range(5, 32)], np.int8)),
     ([0.5, 1.0, 0.125], np.array([b * 10 + i - 5 for b in range(3) for i in range(32)], np.int8)),
 ]
+
+
+def random_q5_blocks(rng, type_id, n_rows, k):
+    """GGUF Q5_0 (type 6: 22-byte blocks of 32) or Q5_K (type 13: 176-byte super-blocks) rows: random bytes with
+    sane fp16 scales (d, and dmin for Q5_K), as a [n_rows][bytes per row] uint8 array."""
+    bb, blk = (22, 32) if type_id == 6 else (176, 256)
+    b = rng.integers(0, 256, size=(n_rows, k // blk, bb), dtype=np.uint8)
+    nb = n_rows * (k // blk)
+    b[..., 0:2] = np.frombuffer(rng.uniform(0.001, 0.05, nb).astype(np.float16).tobytes(), np.uint8).reshape(
+        n_rows, k // blk, 2)
+    if type_id == 13:
+        b[..., 2:4] = np.frombuffer(rng.uniform(0.001, 0.03, nb).astype(np.float16).tobytes(), np.uint8).reshape(
+            n_rows, k // blk, 2)
+    return b.reshape(n_rows, -1)

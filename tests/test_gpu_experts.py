@@ -13,7 +13,8 @@ import sys
 import numpy as np
 import pytest
 
-from qdata import normal, q8_0_gguf_blocks, random_q4k_blocks, random_q6k_blocks, set_subnormal_scales
+from qdata import (normal, q8_0_gguf_blocks, random_q4k_blocks, random_q5_blocks, random_q6k_blocks,
+                   set_subnormal_scales)
 
 pytestmark = pytest.mark.gpu
 
@@ -45,6 +46,11 @@ def _expert_tensor(orc, rng, fmt, E, k, n):
             b = set_subnormal_scales(random_q6k_blocks(rng, n * (k // 256)), q6=True).reshape(n, -1)
             slices.append(b.ravel())
             ref.append(b)
+        elif fmt in ("q5_0", "q5_k"):
+            tid = TYPE[fmt]
+            b = random_q5_blocks(rng, tid, n, k)
+            slices.append(b.ravel())
+            ref.append(orc.q5_requantize_q8_0(tid, b, n, k))
         else:
             q = rng.integers(-128, 128, size=(n * k // 32, 32), dtype=np.int8)
             s = rng.uniform(1e-4, 2e-2, size=n * k // 32).astype(np.float16).astype(np.float32)
@@ -62,11 +68,12 @@ def _project_ref(orc, fmt, r, x, k, n):
     return orc.q8_project_batched(x, 1, r[0], r[1], k, n).ravel()
 
 
-TYPE = {"q4k": 12, "q6k": 14, "q8_0": 8}
+TYPE = {"q4k": 12, "q6k": 14, "q8_0": 8, "q5_0": 6, "q5_k": 13}
 
 
 @pytest.mark.parametrize("fmt,E,k,n", [("q4k", 4, 512, 96), ("q6k", 5, 768, 33), ("q8_0", 3, 96, 40),
-                                       ("q6k", 2, 256, 7), ("q4k", 1, 256, 1)])
+                                       ("q6k", 2, 256, 7), ("q4k", 1, 256, 1), ("q5_0", 3, 96, 40),
+                                       ("q5_0", 2, 4096, 65), ("q5_k", 4, 512, 33), ("q5_k", 1, 256, 1)])
 @pytest.mark.parametrize("on_device", [False, True])
 def test_experts_slice_bit_exact(orc, fmt, E, k, n, on_device):
     """Each sliced expert projects exactly like the oracle on its slice (Q6_K rows of 3 super-blocks: 630-byte
@@ -84,7 +91,11 @@ def test_experts_slice_bit_exact(orc, fmt, E, k, n, on_device):
         assert bad == 0, f"expert {e}: {bad}/{n} outputs differ"
     row = np.zeros(k, np.float32)
     ws[-1].DecodeRow(n - 1, row)
-    if fmt == "q8_0":
+    if fmt in ("q8_0", "q5_0", "q5_k"):
+        info = ctypes.c_int()
+        assert ws[-1].context.lib.ovfq_weight_info(ws[-1].handle, ctypes.byref(info), None, None, None, None) == 0
+        assert info.value == 8, "a 5-bit GGUF tensor is resident as Q8_0"
+    if fmt in ("q8_0", "q5_0", "q5_k"):
         q, s = ref[-1]
         expect = q.reshape(n, k)[n - 1].astype(np.float32) * np.repeat(s.reshape(n, -1)[n - 1], 32)
     else:

@@ -11,7 +11,8 @@ import sys
 import numpy as np
 import pytest
 
-from qdata import Q8_0_KATS, normal, q8_0_gguf_blocks, random_q4k_blocks, random_q6k_blocks, set_subnormal_scales
+from qdata import (Q8_0_KATS, normal, q8_0_gguf_blocks, random_q4k_blocks, random_q5_blocks, random_q6k_blocks,
+                   set_subnormal_scales)
 
 pytestmark = pytest.mark.gpu
 
@@ -438,6 +439,31 @@ def test_gguf_upload_q8_0_q4k_q6k(orc, on_device):
                                 k, n)
         ref = (orc.q4k_project if fmt == "q4k" else orc.q6k_project)(x, b, k, n)
         assert_bit_exact(ov.project(w, x), ref, f"gguf {fmt}")
+
+
+@pytest.mark.parametrize("type_id,k,n", [(6, 4096, 1024), (6, 96, 7), (13, 4096, 300), (13, 14336, 33), (13, 256, 1)])
+@pytest.mark.parametrize("on_device", [False, True])
+def test_gguf_upload_q5_requantised_to_q8_0(orc, type_id, k, n, on_device):
+    """Q5_0 / Q5_K tensors (a Q4_K_M file's attn_v or ffn_down) become resident Q8_0 weights on the device: the
+    planes equal the oracle's decode-then-QuantizeRows bit for bit (LD/GgufLlamaLoader.cs:665-680), and the weight
+    projects (one row and a batch) and decodes its rows like the oracle's Q8Weight."""
+    case("gguf upload q5", type_id, k, n, on_device)
+    rng = np.random.default_rng(type_id * 7 + k + n + on_device)
+    data = random_q5_blocks(rng, type_id, n, k)
+    rq, rs = orc.q5_requantize_q8_0(type_id, data, n, k)
+    w = ov.load_gguf_tensor(type_id, t(data.ravel()) if on_device else data.ravel(), k, n)
+    typ, nbytes, dptr = ctypes.c_int(), ctypes.c_size_t(), ctypes.c_void_p()
+    lib = w.context.lib
+    assert lib.ovfq_weight_info(w.handle, ctypes.byref(typ), None, None, ctypes.byref(nbytes), ctypes.byref(dptr)) == 0
+    assert typ.value == ov.TYPE_Q8_0 and nbytes.value == n * k + n * (k // 32) * 4
+    for rows in (1, 9):
+        x = normal(rng, (rows, k))
+        assert_bit_exact(ov.project(w, x, rows=rows), orc.q8_project_batched(x, rows, rq, rs, k, n).ravel(),
+                         f"projection rows {rows}")
+    dec = np.zeros(k, np.float32)
+    for r in sorted({0, n // 2, n - 1}):  # Q8Weight.DecodeRow: quant x scale, so the planes themselves
+        w.DecodeRow(r, dec)
+        assert np.array_equal(dec.view(np.uint32), (rq[r].astype(np.float32) * np.repeat(rs[r], 32)).view(np.uint32))
 
 
 # ------------------------------------------------------------------------------------------------ small batch

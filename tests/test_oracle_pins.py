@@ -129,6 +129,125 @@ def test_decode_q4k_kat_scale_and_min_per_sub_block(orc):
         assert np.all(dst[64 * p + 32:64 * p + 64] == hi)
 
 
+def _q5_0_block(d, qh, qs_fill):
+    b = np.zeros(22, np.uint8)
+    b[0:2] = np.frombuffer(np.float16(d).tobytes(), np.uint8)
+    b[2:6] = np.frombuffer(np.uint32(qh).tobytes(), np.uint8)
+    b[6:] = qs_fill
+    return b
+
+
+def test_decode_q5_0_kats(orc):
+    # TL/Loading/GgmlDequantTests.cs:330-380: zero quants give the -16 bias; low nibble -> element j, high -> j + 16;
+    # qh bit k -> element k.
+    assert np.all(orc.decode_q5_0_block(_q5_0_block(1.0, 0, 0x00)) == -16.0)
+    dst = orc.decode_q5_0_block(_q5_0_block(2.0, 0, 0x21))
+    assert np.all(dst[:16] == -30.0) and np.all(dst[16:] == -28.0)
+    for k in (0, 16, 31):
+        dst = orc.decode_q5_0_block(_q5_0_block(1.0, 1 << k, 0x00))
+        assert dst[k] == 0.0 and np.all(np.delete(dst, k) == -16.0)
+
+
+def test_decode_q5_0_every_bit_owns_one_element(orc):
+    # Brute force over all 32 qh bits and all 32 nibbles (d = 1, so every value is the integer q - 16): each bit
+    # moves exactly the element the block format gives it, by its weight (16 for qh, 1..8 for a nibble bit).
+    base = orc.decode_q5_0_block(_q5_0_block(1.0, 0, 0x00))
+    for k in range(32):
+        diff = orc.decode_q5_0_block(_q5_0_block(1.0, 1 << k, 0x00)) - base
+        assert np.flatnonzero(diff).tolist() == [k] and diff[k] == 16.0
+    for j in range(16):
+        for bit in range(8):
+            b = _q5_0_block(1.0, 0, 0x00)
+            b[6 + j] = 1 << bit
+            diff = orc.decode_q5_0_block(b) - base
+            elem = j if bit < 4 else j + 16
+            assert np.flatnonzero(diff).tolist() == [elem] and diff[elem] == float(1 << (bit % 4))
+
+
+def test_decode_q5_0_scale_is_exact_multiplication(orc):
+    # Random blocks: every element is (q - 16) * d with q the 5-bit code (exact products, so float64 agrees).
+    rng = np.random.default_rng(50)
+    for _ in range(200):
+        b = rng.integers(0, 256, 22, dtype=np.uint8)
+        b[0:2] = np.frombuffer(np.float16(rng.uniform(-0.05, 0.05)).tobytes(), np.uint8)
+        d = np.float64(np.frombuffer(b[0:2].tobytes(), np.float16)[0])
+        qh = int(np.frombuffer(b[2:6].tobytes(), np.uint32)[0])
+        q = np.array([((int(b[6 + (i % 16)]) >> (4 * (i // 16))) & 15) | (((qh >> i) & 1) << 4) for i in range(32)])
+        assert np.array_equal(orc.decode_q5_0_block(b).astype(np.float64), (q - 16) * d)
+
+
+def _q5k_block(d, dmin, packed, qh_fill, qs_fill):
+    b = np.zeros(176, np.uint8)
+    b[0:2] = np.frombuffer(np.float16(d).tobytes(), np.uint8)
+    b[2:4] = np.frombuffer(np.float16(dmin).tobytes(), np.uint8)
+    b[4:16] = packed
+    b[16:48] = qh_fill
+    b[48:] = qs_fill
+    return b
+
+
+def test_decode_q5k_kats(orc):
+    # TL/Loading/GgmlDequantTests.cs:392-436: scales 1, mins 0, nibbles 0x21 -> 1 / 2 per 32-element half; every qh
+    # bit set adds 16 -> 17 / 18.
+    packed = np.zeros(12, np.uint8)
+    packed[:4] = 1
+    packed[8:12] = 1
+    for qh, lo, hi in ((0x00, 1.0, 2.0), (0xFF, 17.0, 18.0)):
+        dst = orc.decode_q5k_block(_q5k_block(1.0, 0.0, packed, qh, 0x21))
+        for g in range(4):
+            assert np.all(dst[64 * g:64 * g + 32] == lo) and np.all(dst[64 * g + 32:64 * g + 64] == hi)
+
+
+def test_decode_q5k_without_fifth_bits_is_the_q4k_decode(orc):
+    # With qh = 0 a Q5_K block is the Q4_K block with the same d, dmin, packed scales/mins and nibbles (the formats
+    # share the element map and the float operations), so it decodes bit-identically to the pinned Q4_K decoder.
+    rng = np.random.default_rng(51)
+    for b4 in random_q4k_blocks(rng, 300):
+        b5 = np.zeros(176, np.uint8)
+        b5[:16] = b4[:16]
+        b5[48:] = b4[16:]
+        assert np.array_equal(orc.decode_q5k_block(b5).view(np.uint32), orc.decode_q4k_block(b4).view(np.uint32))
+
+
+def test_decode_q5k_every_fifth_bit_owns_one_element(orc):
+    # d = 1, dmin = 0, all scales 1: qh byte l bit b lifts exactly element 64 (b // 2) + 32 (b % 2) + l by 16.
+    packed = np.zeros(12, np.uint8)
+    packed[:4] = 1
+    packed[8:12] = 1
+    base = orc.decode_q5k_block(_q5k_block(1.0, 0.0, packed, 0x00, 0x00))
+    for l in range(32):
+        for bit in range(8):
+            b = _q5k_block(1.0, 0.0, packed, 0x00, 0x00)
+            b[16 + l] = 1 << bit
+            diff = orc.decode_q5k_block(b) - base
+            elem = 64 * (bit // 2) + 32 * (bit % 2) + l
+            assert np.flatnonzero(diff).tolist() == [elem] and diff[elem] == 16.0
+
+
+@pytest.mark.parametrize("type_id,k", [(6, 96), (6, 4096), (13, 256), (13, 1024)])
+def test_q5_requantize_is_decode_then_quantize_rows(orc, type_id, k):
+    # The loader's Q5 -> Q8_0 path: the resident planes are Q8Weight.QuantizeRows of the decoded F32 rows; their
+    # dequantised values stay within half a Q8_0 step of the decoded weights (ties of a 5-bit grid against the
+    # 127-step grid reach exactly half a step, so the bound allows the float error of scale and 1 / scale).
+    rng = np.random.default_rng(type_id * 1000 + k)
+    rows = 7
+    bb, blk = (22, 32) if type_id == 6 else (176, 256)
+    data = rng.integers(0, 256, (rows, k // blk, bb), dtype=np.uint8)
+    data[..., 0:2] = np.frombuffer(rng.uniform(0.001, 0.05, rows * (k // blk)).astype(np.float16).tobytes(),
+                                   np.uint8).reshape(rows, k // blk, 2)
+    if type_id == 13:
+        data[..., 2:4] = np.frombuffer(rng.uniform(0.001, 0.03, rows * (k // blk)).astype(np.float16).tobytes(),
+                                       np.uint8).reshape(rows, k // blk, 2)
+    dec = orc.decode_q5_0_block if type_id == 6 else orc.decode_q5k_block
+    f32 = np.stack([np.concatenate([dec(data[r, b]) for b in range(k // blk)]) for r in range(rows)])
+    q, s = orc.q5_requantize_q8_0(type_id, data, rows, k)
+    q_ref, s_ref = orc.q8_quantize_rows(f32)
+    assert np.array_equal(q, q_ref) and np.array_equal(s.view(np.uint32), s_ref.view(np.uint32))
+    back = q.astype(np.float64).reshape(rows, -1, 32) * s.astype(np.float64)[..., None]
+    step = s.astype(np.float64)[..., None]
+    assert np.all(np.abs(back - f32.reshape(rows, -1, 32)) <= 0.5 * step * (1 + 1e-5))
+
+
 def _q6k_block(d, scales, ql=None, ql_fill=0, qh_fill=0):
     b = np.zeros(210, np.uint8)
     b[:128] = ql_fill if ql is None else ql
