@@ -409,7 +409,26 @@ def main():
                                                      bands[h * d_model:(h + 1) * d_model])
                                      for h in range(n_heads)]) for hs in sets[:4]])
         us_sep = replay_us(g, 4, 8)
-        del g, sets
+        del g
+        # Prefill rows (RT/CachedMultiHeadAttention.cs:689-710): the int8-MFMA kernel (automatic from 9 rows) beside
+        # the decode kernel's launches of 8 rows each (forced), graph-replayed over 2 weight copies.
+        prefill = {}
+        for m in (9, 16, 32, 64, 512):
+            xm = torch.randn(m * n_heads * head_dim, generator=gen5, device=dev)
+            ym = torch.empty(m * d_model, device=dev)
+            calls = [(lambda hs=hs: ov.project_heads_q8_0(hs, xm, rows=m, out=ym)) for hs in sets[:2]] * 2
+            g = capture(calls)
+            us_m = replay_us(g, 4, 8)
+            del g
+            ctx.set_batched_kernel("rows")
+            g = capture(calls)
+            ctx.set_batched_kernel("auto")
+            us_8 = replay_us(g, 4, 4)
+            del g, xm, ym
+            ops = 2.0 * m * d_model * n_heads * head_dim
+            prefill["m%d" % m] = {"us": round(us_m, 2), "per8_launches_us": round(us_8, 2),
+                                  "useful_TOPS": round(ops / (us_m * 1e-6) / 1e12, 1)}
+        del sets
         torch.cuda.empty_cache()
         wb = n_heads * (d_model * head_dim + 4 * d_model * head_dim // 32)
         nbytes = wb + 4 * n_heads * head_dim + 4 * d_model
@@ -418,7 +437,11 @@ def main():
                 "GB_s": round(nbytes / (us * 1e-6) / 1e9, 1),
                 "pct_peak": round(100 * nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 2),
                 "separate_launches_us": round(us_sep, 2),
-                "timing": "HIP graph replay over %d weight copies, per call (separate: 32 launches, 4 copies)" % n_copies}
+                "prefill": prefill,
+                "prefill_what": "the same o-projection over m prefill rows: Q8_0 quantise + the int8-MFMA per-head "
+                                "kernel (us) against the decode kernel in launches of 8 rows (per8_launches_us)",
+                "timing": "HIP graph replay over %d weight copies, per call (separate: 32 launches, 4 copies; "
+                          "prefill: 2 copies)" % n_copies}
 
     def rows_layer(m):
         """fp32 inputs / outputs for the layer's four projection launches at m rows, and the step over one copy:

@@ -268,8 +268,10 @@ OVFQ_API int ovfq_project_multi_prequantized_dev(ovfq_ctx* ctx, int count, const
  * x [rows][n_heads * head_dim] (head h's attention output at columns h * head_dim ..):
  *   y[n] = bias (or zero), then for h = 0, 1, ..., n_heads - 1:  y[n] += Q8DotKernel.Project(x[n][h], wo[h]) (no bias)
  * — the per-head projections of RT/CachedSingleHeadAttention.cs:323-337 and the ascending head reduction of
- * RT/CachedMultiHeadAttention.cs:185-194, :292-297 (prefill rows: :600-614, :703-711), bit-identical, in one launch
- * for up to 8 rows (more rows take one launch per 8). Replaces the n_heads separate projections plus the host sum. */
+ * RT/CachedMultiHeadAttention.cs:185-194, :292-297 (prefill rows: :600-614, :689-711), bit-identical. Up to 8 rows run
+ * in one decode launch, up to 31 in launches of 8; batches of 32 rows or more (prefill) quantise the rows once and run
+ * on int8 MFMA, each head's Wo streamed once per 64 rows (ovfq_ctx_set_batched_kernel: OVFQ_BATCHED_TILED forces that
+ * kernel, SMALL / ROWS the decode launches). Replaces the n_heads separate projections plus the host sum. */
 OVFQ_API int ovfq_project_heads_q8_0(ovfq_ctx* ctx, int n_heads, const ovfq_weight* const* wo, const float* x,
                                      int rows, const float* bias, float* y);
 OVFQ_API int ovfq_project_heads_q8_0_dev(ovfq_ctx* ctx, int n_heads, const ovfq_weight* const* wo, const float* x,

@@ -1188,11 +1188,22 @@ static int heads_impl(ovfq_ctx* ctx, int H, const ovfq_weight* const* wo, const 
     if (!host && ((rc = check_dev_align(x, "input")) || (rc = check_dev_align(y, "output")) ||
                   (rc = check_dev_align(bias, "bias"))))
         return rc;
-    // rows per launch: as many as the LDS copy of the activation and the head values allow (up to 8)
+    // Batches from 32 rows: the int8-MFMA kernel streams each head's Wo once per 16-64 activation rows; fewer rows take
+    // the decode kernel, one launch per 8 rows. MI355X, Llama-3-8B Wo (32 x 4096x128), graph replay, us, MFMA / per-8
+    // launches: 9 rows 36.9 / 19.5, 16 rows 37.6 / 28.7, 32 rows 46.4 / 47.7, 64 rows 64.7 / 89.2, 512 rows 73.3 /
+    // 628.8. OVFQ_HEADS_MFMA_MIN_ROWS sets the switch (measurements).
+    static const int heads_mfma_min = [] {
+        const char* v = getenv("OVFQ_HEADS_MFMA_MIN_ROWS");
+        return v && *v ? atoi(v) : 32;
+    }();
+    bool mfma = rows >= heads_mfma_min && ovfq::q8_0_heads_mfma_supported(H, hd, rows);
+    if (ctx->batched_kernel == OVFQ_BATCHED_TILED) mfma = ovfq::q8_0_heads_mfma_supported(H, hd, rows);
+    else if (ctx->batched_kernel != OVFQ_BATCHED_AUTO) mfma = false;
+    // rows per decode launch: as many as the LDS copy of the activation and the head values allow (up to 8)
     int R = 0;
-    for (int r = rows < ovfq::kHeadsMaxRows ? rows : ovfq::kHeadsMaxRows; r >= 1 && !R; r--)
+    for (int r = rows < ovfq::kHeadsMaxRows ? rows : ovfq::kHeadsMaxRows; r >= 1 && !R && !mfma; r--)
         if (ovfq::q8_0_heads_supported(H, hd, r)) R = r;
-    if (!R) return fail(OVFQ_ERR_SIZE, "n_heads x head_dim (%d) too large for one launch", K);
+    if (!R && !mfma) return fail(OVFQ_ERR_SIZE, "n_heads x head_dim (%d) too large for one launch", K);
     std::lock_guard<std::mutex> lk(ctx->mu);
     HIP_TRY(hipSetDevice(ctx->device));
     const float* xd = x;
@@ -1215,9 +1226,15 @@ static int heads_impl(ovfq_ctx* ctx, int H, const ovfq_weight* const* wo, const 
         wq[h] = static_cast<const int8_t*>(wo[h]->blocks);
         ws[h] = wo[h]->scales;
     }
+    ovfq::ActQ act{nullptr, nullptr, nullptr};
+    if (mfma) {
+        if ((rc = quantize_into_scratch(ctx, OVFQ_TYPE_Q8_0, xd, rows, K, &act))) return rc;
+        HIP_TRY(ovfq::launch_q8_0_heads_mfma(wq, ws, H, hd, dm, rows, bd, act, yd, ctx->stream));
+        if (host && ((rc = io.down(y, yd, (size_t)rows * dm * 4)) || (rc = io.finish()))) return rc;
+        return ok();
+    }
     // One launch per R rows; the Q8_0 quantisation of the heads' inputs runs inside it when the rows are short, else
     // once for all rows beforehand.
-    ovfq::ActQ act{nullptr, nullptr, nullptr};
     const bool inside = ovfq::q8_0_heads_quantize_inside(H, hd, R);
     if (!inside && (rc = quantize_into_scratch(ctx, OVFQ_TYPE_Q8_0, xd, rows, K, &act))) return rc;
     for (int r0 = 0; r0 < rows; r0 += R) {

@@ -170,6 +170,11 @@ bool q8_0_heads_quantize_inside(int n_heads, int head_dim, int rows);
 size_t q8_0_heads_lds_bytes(int n_heads, int head_dim, int rows);
 hipError_t launch_q8_0_heads(const int8_t* const* wq, const float* const* ws, int n_heads, int head_dim, int d_model,
                              int rows, const float* bias, const float* x, ActQ act, float* y, hipStream_t st);
+// The same projection for batches on int8 MFMA (project.hip): 64 outputs x 16-64 activation rows per workgroup, the
+// contraction walked head by head; act is the Q8_0 activation [rows][n_heads * head_dim].
+bool q8_0_heads_mfma_supported(int n_heads, int head_dim, int rows);
+hipError_t launch_q8_0_heads_mfma(const int8_t* const* wq, const float* const* ws, int n_heads, int head_dim,
+                                  int d_model, int rows, const float* bias, ActQ act, float* y, hipStream_t st);
 
 // GGUF Q8_0 (34-byte blocks) -> int8 quant plane + f32 scale plane.
 hipError_t launch_q8_0_deinterleave(const void* gguf, int64_t n_blocks, int8_t* q, float* s, hipStream_t st);

@@ -703,6 +703,196 @@ __global__ __launch_bounds__(256, 2) void q8_0_mfma_kernel(const Q8MArgs a) {
     }
 }
 
+// ------------------------------------------------------------------------------------------ per-head Q8_0 Wo on MFMA
+// The attention output projection of prefill rows with per-head Q8_0 Wo (RT/CachedMultiHeadAttention.cs:600-614,
+// :689-710: BatchedQuantProjection.Dispatch of each head's attention rows through its own Wo_h [d_model][head_dim],
+// then TensorPrimitives.Add into the output, heads ascending, the output starting as the attention bias or zero). The
+// kernel above with the contraction walked head by head: a group of up to four blocks never crosses a head, so its
+// weight rows come from one head's planes (a wave-uniform resource per group); each head's blocks are summed from +0
+// in block order (the head's Q8 Dot), and at the head's last group that value is added to the running output, which
+// starts as bias-or-zero. Every (row, output) therefore gets ((bias + head 0) + head 1) + ... bit for bit.
+struct Q8HMArgs {
+    const int8_t* wq[kHeadsMax];
+    const float* ws[kHeadsMax];
+    const float* bias;
+    float* y;
+    int n_out;     // d_model
+    int n_heads;
+    int head_dim;
+    int rows;
+    const int8_t* q;  // Q8_0 activation [rows][n_heads * head_dim]
+    const float* s;
+};
+
+template <int T, int kW>
+__global__ __launch_bounds__(256, 2) void q8_0_heads_mfma_kernel(const Q8HMArgs a) {
+    static_assert(kW == 4 || T == 1, "a one-wave workgroup stages one 16-row tile");
+    __shared__ __align__(16) uint8_t la[2][16 * T * kQ8Row];
+    __shared__ __align__(16) float lxs[2][16 * T * 4];
+    __shared__ __align__(16) uint8_t lw[kW][2][16 * kQ8Row];
+    const int tid = (int)threadIdx.x;
+    const int wave = wave_id();
+    const int lane = tid & 63;
+    const int g = lane >> 4, c16 = lane & 15;
+    const int o0 = (int)blockIdx.x * 16 * kW + wave * 16;
+    const int m0 = (int)blockIdx.y * 16 * T;
+    const uint32_t hd = (uint32_t)a.head_dim, nbh = hd / 32;
+    const uint32_t K = (uint32_t)a.n_heads * hd, nb = K / 32;
+    const int gph = (int)(nbh + 3) / 4;  // groups per head
+    const int G = a.n_heads * gph;
+    const uint32_t wrows = (uint32_t)max(0, min(16, a.n_out - o0)), arows = (uint32_t)min(16 * T, a.rows - m0);
+    const uint64_t obase = o0 < a.n_out ? (uint64_t)o0 : 0;
+    const __amdgpu_buffer_rsrc_t qr = make_rsrc(a.q + (uint64_t)m0 * K, arows * K);
+    const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.s + (uint64_t)m0 * nb, arows * nb * 4);
+    const int ar = tid >> 2, aj = tid & 3, wrow = lane >> 2, wj = lane & 3;
+    const bool astage = tid < 64 * T;
+    struct Stage {
+        u32x4 a0, a1, w0, w1;
+        uint32_t xs;
+    };
+    auto head_of = [&](int gi) { return gph == 1 ? gi : gi / gph; };
+    auto fetch = [&](int gi, Stage& st) {  // blocks past the head's last: other bytes or zeros, unused
+        const int h = head_of(gi);
+        const uint32_t lb0 = (uint32_t)(gi - h * gph) * 4;
+        const uint32_t b0 = (uint32_t)h * nbh + lb0;  // the group's first block of the activation row
+        if (astage) {
+            const uint32_t ao = (uint32_t)ar * K + (b0 + aj) * 32;
+            st.a0 = ld4(qr, ao);
+            st.a1 = ld4(qr, ao + 16);
+            st.xs = ld1(sr, ((uint32_t)ar * nb + b0 + aj) * 4);
+        }
+        const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.wq[h] + obase * hd, wrows * hd);
+        const uint32_t wo = (uint32_t)wrow * hd + (lb0 + wj) * 32;
+        st.w0 = ld4(wr, wo);
+        st.w1 = ld4(wr, wo + 16);
+    };
+    auto stage = [&](int buf, const Stage& st) {
+        if (astage) {
+            q8_stage_block(la[buf], ar, aj, st.a0, st.a1);
+            lxs[buf][ar * 4 + aj] = as_float(st.xs);
+        }
+        q8_stage_block(lw[wave][buf], wrow, wj, st.w0, st.w1);
+    };
+    const int o = o0 + c16;
+    const float start = (a.bias && o < a.n_out) ? a.bias[o] : 0.0f;  // the output starts as bias or zero
+    float tot[T][4], hacc[T][4];
+#pragma unroll
+    for (int t = 0; t < T; t++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            tot[t][i] = start;
+            hacc[t][i] = 0.0f;
+        }
+    Stage sa, sb;
+    fetch(0, sa);
+    stage(0, sa);
+    if (1 < G) fetch(1, sb);
+    __syncthreads();
+    int buf = 0;
+    int gi = 0;
+    auto group = [&](auto full_tag, Stage& next, Stage& after) -> bool {
+        constexpr bool kFull = decltype(full_tag)::value;
+        if (gi + 2 < G) fetch(gi + 2, after);
+        const int h = head_of(gi);
+        const uint32_t lb0 = (uint32_t)(gi - h * gph) * 4;
+        const uint32_t nblk = min(4u, nbh - lb0);
+        const __amdgpu_buffer_rsrc_t wsr = make_rsrc(a.ws[h] + obase * nbh, wrows * nbh * 4);
+        const u32x4 wsv = ld4(wsr, ((uint32_t)c16 * nbh + lb0) * 4);
+        const uint8_t* wp = lw[wave][buf] + c16 * kQ8Row + 32 * g;
+        const u32x4 wlo = *reinterpret_cast<const u32x4*>(wp), whi = *reinterpret_cast<const u32x4*>(wp + 16);
+        const uint32_t bw[8] = {wlo.x, wlo.y, wlo.z, wlo.w, whi.x, whi.y, whi.z, whi.w};
+#pragma unroll
+        for (int t = 0; t < T; t++) {
+            const uint8_t* ap = la[buf] + (16 * t + c16) * kQ8Row + 32 * g;
+            const u32x4 alo = *reinterpret_cast<const u32x4*>(ap), ahi = *reinterpret_cast<const u32x4*>(ap + 16);
+            const uint32_t aw[8] = {alo.x, alo.y, alo.z, alo.w, ahi.x, ahi.y, ahi.z, ahi.w};
+            u32x4 xv[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) xv[i] = *reinterpret_cast<const u32x4*>(&lxs[buf][(16 * t + 4 * g + i) * 4]);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                if (kFull || (uint32_t)j < nblk) {  // wave-uniform
+                    const long aop = (long)(((uint64_t)aw[2 * j + 1] << 32) | aw[2 * j]);
+                    const long bop = (long)(((uint64_t)bw[2 * j + 1] << 32) | bw[2 * j]);
+                    const i32x4m d = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, i32x4m{0, 0, 0, 0}, 0, 0, 0);
+                    const uint32_t wsw = j == 0 ? wsv.x : j == 1 ? wsv.y : j == 2 ? wsv.z : wsv.w;
+                    const float wsc = as_float(wsw);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const uint32_t xw = j == 0 ? xv[i].x : j == 1 ? xv[i].y : j == 2 ? xv[i].z : xv[i].w;
+                        hacc[t][i] += (wsc * as_float(xw)) * (float)d[i];
+                    }
+                }
+            }
+        }
+        if (lb0 + 4 >= nbh) {  // the head's last group: output += head value
+#pragma unroll
+            for (int t = 0; t < T; t++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    tot[t][i] = tot[t][i] + hacc[t][i];
+                    hacc[t][i] = 0.0f;
+                }
+        }
+        if (gi + 1 < G) stage(buf ^ 1, next);
+        __syncthreads();
+        buf ^= 1;
+        gi += 1;
+        return gi < G;
+    };
+    auto step = [&](Stage& next, Stage& after) -> bool {
+        const int h = head_of(gi);
+        const uint32_t lb0 = (uint32_t)(gi - h * gph) * 4;
+        return nbh - lb0 >= 4 ? group(std::true_type{}, next, after) : group(std::false_type{}, next, after);
+    };
+    for (;;) {
+        if (!step(sb, sa)) break;
+        if (!step(sa, sb)) break;
+    }
+    if (o < a.n_out) {
+#pragma unroll
+        for (int t = 0; t < T; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int m = m0 + 16 * t + 4 * g + i;
+                if (m < a.rows) a.y[(size_t)m * a.n_out + o] = tot[t][i];
+            }
+    }
+}
+
+bool q8_0_heads_mfma_supported(int n_heads, int head_dim, int rows) {
+    const uint64_t K = (uint64_t)n_heads * head_dim;
+    return n_heads >= 1 && n_heads <= kHeadsMax && head_dim >= 32 && head_dim % 32 == 0 && rows >= 1 &&
+           K * 64 < (1ull << 31) && K * (uint64_t)rows < (1ull << 31);
+}
+
+hipError_t launch_q8_0_heads_mfma(const int8_t* const* wq, const float* const* ws, int n_heads, int head_dim,
+                                  int d_model, int rows, const float* bias, ActQ act, float* y, hipStream_t st) {
+    if (!q8_0_heads_mfma_supported(n_heads, head_dim, rows) || !act.q || !act.s) return hipErrorInvalidValue;
+    Q8HMArgs ha{};
+    for (int h = 0; h < n_heads; h++) {
+        ha.wq[h] = wq[h];
+        ha.ws[h] = ws[h];
+    }
+    ha.bias = bias;
+    ha.y = y;
+    ha.n_out = d_model;
+    ha.n_heads = n_heads;
+    ha.head_dim = head_dim;
+    ha.rows = rows;
+    ha.q = act.q;
+    ha.s = act.s;
+    const int T = rows <= 16 ? 1 : rows <= 32 ? 2 : 4;
+    const dim3 grid4((d_model + 63) / 64, (rows + 16 * T - 1) / (16 * T));
+    if (T == 1)
+        hipLaunchKernelGGL((q8_0_heads_mfma_kernel<1, 1>), dim3((d_model + 15) / 16, 1), dim3(64), 0, st, ha);
+    else if (T == 2)
+        hipLaunchKernelGGL((q8_0_heads_mfma_kernel<2, 4>), grid4, dim3(256), 0, st, ha);
+    else
+        hipLaunchKernelGGL((q8_0_heads_mfma_kernel<4, 4>), grid4, dim3(256), 0, st, ha);
+    return hipGetLastError();
+}
+
 bool q8_0_mfma_supported(int in, int rows) {
     // 32-bit resource offsets: 64 activation rows and 16 weight rows of K bytes, and the whole activation
     return in % 32 == 0 && (uint64_t)in * 64 < (1ull << 31) && (uint64_t)in * (uint64_t)rows < (1ull << 31);

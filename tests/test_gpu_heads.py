@@ -1,5 +1,8 @@
 """The per-head Q8_0 attention output projection (ovfq_project_heads_q8_0[_dev]) against the oracle.
 
+Up to 31 rows run on the decode kernel (one launch per 8 rows); from 32 rows the int8-MFMA kernel walks the
+contraction head by head (prefill rows, RT/CachedMultiHeadAttention.cs:689-710). Both are covered, also forced.
+
 The reference's default Llama decode o-path: Wo requantised per head to Q8_0 (LD/GgufLlamaLoader.cs:977-995), each
 head's Q8DotKernel.Project of its head_dim slice, and output = bias (or zero) + the head outputs in ascending head
 order (RT/CachedMultiHeadAttention.cs:185-194, :292-297; prefill rows :600-614, :703-711). Bit-exact everywhere:
@@ -81,6 +84,50 @@ def test_heads_bit_exact(orc, H, hd, dm, rows):
         torch.cuda.synchronize()
         ref = orc.q8_project_heads(x, rows, qs, ss, hd, dm, b)
         _check(y.cpu().numpy(), ref, f"bias={b is not None}")
+
+
+@pytest.mark.parametrize("H,hd,dm,rows", [
+    (32, 128, 4096, 512),  # Llama-3-8B prefill: 512 rows, 64-row MFMA tiles
+    (32, 128, 4096, 32),   # the first automatic MFMA row count: 32-row tiles
+    (32, 128, 1000, 33),   # 64-row tiles with a partial last tile, partial output tile
+    (8, 64, 200, 40),      # two blocks per head: every group partial
+    (6, 96, 72, 37),       # three blocks per head
+    (4, 256, 136, 70),     # eight blocks per head: two groups per head
+    (3, 160, 24, 100),     # five blocks per head: a full group and a partial one
+    (1, 32, 16, 64),       # one head of one block
+])
+def test_heads_batched_mfma_bit_exact(orc, H, hd, dm, rows):
+    case("heads mfma", H, hd, dm, rows)
+    rng = np.random.default_rng(H * 11 + hd + dm + rows)
+    qs, ss, ws = _heads(orc, rng, H, hd, dm)
+    x = normal(rng, (rows, H * hd))
+    x[rows - 1, -32:] = 0.0  # an all-zero block
+    bias = normal(rng, dm)
+    for b in (None, bias):
+        y = ov.project_heads_q8_0(ws, t(x), rows=rows, bias=None if b is None else t(b))
+        torch.cuda.synchronize()
+        ref = orc.q8_project_heads(x, rows, qs, ss, hd, dm, b)
+        _check(y.cpu().numpy(), ref, f"bias={b is not None}")
+
+
+@pytest.mark.parametrize("kernel,rows", [("tiled", 2), ("tiled", 9), ("tiled", 17), ("rows", 20), ("small", 40)])
+def test_heads_forced_kernel_bit_exact(orc, kernel, rows):
+    """OVFQ_BATCHED_TILED forces the MFMA kernel down to small batches, the other choices the decode kernel's
+    per-8-row launches for any batch; both stay exact."""
+    case("heads forced", kernel, rows)
+    ctx = ov.default_context()
+    rng = np.random.default_rng(rows + len(kernel))
+    H, hd, dm = 32, 128, 512
+    qs, ss, ws = _heads(orc, rng, H, hd, dm)
+    x = normal(rng, (rows, H * hd))
+    bias = normal(rng, dm)
+    ctx.set_batched_kernel(kernel)
+    try:
+        y = ov.project_heads_q8_0(ws, t(x), rows=rows, bias=t(bias))
+        torch.cuda.synchronize()
+    finally:
+        ctx.set_batched_kernel("auto")
+    _check(y.cpu().numpy(), orc.q8_project_heads(x, rows, qs, ss, hd, dm, bias), kernel)
 
 
 def test_heads_host_entry_and_raw_planes(orc):
