@@ -22,6 +22,8 @@
 
 namespace ovfq {
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 struct GJob {
     const uint8_t* w;
     const float* bias;
@@ -42,6 +44,31 @@ struct GArgs {
 };
 
 constexpr int kGemvMaxSpr = 64;  // K <= 16384: the whole Q8_K activation fits in LDS (<= 23 KB)
+// Per output row, the 16 block values of an item are written to LDS (one 80-byte row: 16-byte aligned, so the lane
+// that sums them reads the row with four 16-byte loads).
+constexpr int kRedStride = 20;
+
+// acc + the item's nq block values of LDS row `row`, in ascending block order (from registers: four 16-byte reads).
+__device__ __forceinline__ float ordered_item_sum(float acc, const float* row, int nq) {
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const f32x4 x = reinterpret_cast<const f32x4*>(row)[i];
+        v[4 * i] = x.x;
+        v[4 * i + 1] = x.y;
+        v[4 * i + 2] = x.z;
+        v[4 * i + 3] = x.w;
+    }
+    if (nq == 16) {  // wave-uniform: every chunk but a row's short last one
+#pragma unroll
+        for (int qq = 0; qq < 16; qq++) acc += v[qq];
+    } else {
+#pragma unroll
+        for (int qq = 0; qq < 16; qq++)
+            if (qq < nq) acc += v[qq];
+    }
+    return acc;
+}
 
 // Activation prologue: each wave takes four super-blocks at a time, one per 16-lane DPP row; lane l of a row
 // owns elements [16l, 16l+16) of its block, i.e. bsum group l, and writes one 16-byte LDS chunk.
@@ -130,7 +157,7 @@ __global__ __launch_bounds__(256) void kquant_gemv_kernel(const GArgs a) {
     const int stride = gridDim.x * 4;
     const int total = a.total_groups;
     const uint32_t row_bytes = (uint32_t)spr * F::kBytes;
-    float* rw = red + wave * R * 17;
+    float* rw = red + wave * R * kRedStride;
 
     // One work item = (row group g, 16-block chunk c): the weights of R rows plus, on a row group's last chunk,
     // the bias of those rows.
@@ -220,13 +247,10 @@ __global__ __launch_bounds__(256) void kquant_gemv_kernel(const GArgs a) {
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const float v = F::dot(cur.w[r], av, t);
-            if (t == 0 && live) rw[r * 17 + q] = v;
+            if (t == 0 && live) rw[r * kRedStride + q] = v;
         }
         wave_sync();
-        if (lane < R) {
-            const int nq = min(16, spr - c * 16);
-            for (int qq = 0; qq < nq; qq++) acc += rw[lane * 17 + qq];
-        }
+        if (lane < R) acc = ordered_item_sum(acc, rw + lane * kRedStride, min(16, spr - c * 16));
         wave_sync();
         if (c == nchunks - 1) {
             if (lane < R && cj.row0 + lane < cj.n_rows) {
@@ -277,7 +301,7 @@ hipError_t launch_gemv(GArgs& ga, const ProjJob* jobs, int njobs, hipStream_t st
     int wgs = (groups + 3) / 4;
     const int cap = cu_count() * wg_per_cu;
     if (wgs > cap) wgs = cap;
-    const size_t lds = (size_t)((ga.spr * (kLdsSlot + 36) + 15) & ~15) + 4 * R * 17 * sizeof(float);
+    const size_t lds = (size_t)((ga.spr * (kLdsSlot + 36) + 15) & ~15) + 4 * R * kRedStride * sizeof(float);
     if (njobs > 1)
         hipLaunchKernelGGL((kquant_gemv_kernel<F, R, true>), dim3(wgs), dim3(256), lds, st, ga);
     else
@@ -325,7 +349,7 @@ __global__ __launch_bounds__(256) void kquant_gemv_rows_kernel(const RArgs a) {
     const int stride = gridDim.x * 4;
     const int total = a.total_groups;
     const uint32_t row_bytes = (uint32_t)spr * F::kBytes;
-    float* rw = red + wave * (R * kRowsMax * 17);
+    float* rw = red + wave * (R * kRowsMax * kRedStride);
 
     struct Item {
         typename F::W w[R];
@@ -468,14 +492,11 @@ __global__ __launch_bounds__(256) void kquant_gemv_rows_kernel(const RArgs a) {
 #pragma unroll
             for (int r = 0; r < R; r++) {
                 const float v = F::dot_p(pw[r], av);
-                if (t == 0 && live) rw[(m * R + r) * 17 + q] = v;
+                if (t == 0 && live) rw[(m * R + r) * kRedStride + q] = v;
             }
         }
         wave_sync();
-        if (lane < rows * R) {
-            const int nq = min(16, spr - c * 16);
-            for (int qq = 0; qq < nq; qq++) acc += rw[lane * 17 + qq];
-        }
+        if (lane < rows * R) acc = ordered_item_sum(acc, rw + lane * kRedStride, min(16, spr - c * 16));
         wave_sync();
         if (c == nchunks - 1) {
             const Cur jb = locate(g);
@@ -524,7 +545,7 @@ hipError_t launch_gemv_rows(RArgs& ra, const ProjJob* jobs, int njobs, hipStream
     const int cap = cu_count() * wg_per_cu;
     if (wgs > cap) wgs = cap;
     const int slots = ra.rows * ra.spr;
-    const size_t lds = (size_t)((slots * (kLdsSlot + 36) + 15) & ~15) + 4 * R * kRowsMax * 17 * sizeof(float);
+    const size_t lds = (size_t)((slots * (kLdsSlot + 36) + 15) & ~15) + 4 * R * kRowsMax * kRedStride * sizeof(float);
     hipLaunchKernelGGL((kquant_gemv_rows_kernel<F, R>), dim3(wgs), dim3(256), lds, st, ra);
     return hipGetLastError();
 }
