@@ -80,7 +80,8 @@ struct Q4K {
             dlo = sdot4(qw[k] & 0x0f0f0f0fu, aw[k], dlo);
             dhi = sdot4((qw[k] >> 4) & 0x0f0f0f0fu, aw[8 + k], dhi);
         }
-        int main_acc = (int)(sc01 & 0xffu) * dlo + (int)(sc01 >> 8) * dhi;
+        // |dlo|, |dhi| <= 32 * 15 * 127 and sc <= 63: full-rate 24-bit multiplies are exact
+        int main_acc = __mul24((int)(sc01 & 0xffu), dlo) + __mul24((int)(sc01 >> 8), dhi);
         int min_acc = sdot2_k(a.bs.x, (int)(m01 & 0xffu), 0);
         min_acc = sdot2_k(a.bs.y, (int)(m01 >> 8), min_acc);
         main_acc = quad_sum(main_acc);
@@ -121,7 +122,7 @@ struct Q4K {
             dlo = sdot4(p.lo[k], aw[k], dlo);
             dhi = sdot4(p.hi[k], aw[8 + k], dhi);
         }
-        int main_acc = (int)(p.sc01 & 0xffu) * dlo + (int)(p.sc01 >> 8) * dhi;
+        int main_acc = __mul24((int)(p.sc01 & 0xffu), dlo) + __mul24((int)(p.sc01 >> 8), dhi);
         int min_acc = sdot2_k(a.bs.x, (int)(p.m01 & 0xffu), 0);
         min_acc = sdot2_k(a.bs.y, (int)(p.m01 >> 8), min_acc);
         main_acc = quad_sum(main_acc);
@@ -223,8 +224,10 @@ struct Q6K {
         const int b2 = __builtin_amdgcn_sbfe((int)a.bs.y, hs, 16);
         const int b3 = __builtin_amdgcn_sbfe((int)a.bs.z, hs, 16);
         const int b4 = __builtin_amdgcn_sbfe((int)a.bs.w, hs, 16);
-        // unsignedDot - 32 * bsumTerm, exact in int32 (|.| < 2^28).
-        int part = s1 * (d1 - 32 * b1) + s2 * (d2 - 32 * b2) + s3 * (d3 - 32 * b3) + s4 * (d4 - 32 * b4);
+        // unsignedDot - 32 * bsumTerm, exact in int32 (|.| < 2^28). Each factor fits 24 bits (|s| <= 128; |d - 32 b|
+        // <= 16 * 63 * 127 + 32 * 2032 < 2^18), so the products are full-rate 24-bit multiplies.
+        int part = __mul24(s1, d1 - 32 * b1) + __mul24(s2, d2 - 32 * b2) + __mul24(s3, d3 - 32 * b3) +
+                   __mul24(s4, d4 - 32 * b4);
         part = quad_sum(part);
         const float d = half_lo(w.d);
         // d * q8Scale * mainAcc
@@ -272,7 +275,8 @@ struct Q6K {
         const int b2 = __builtin_amdgcn_sbfe((int)a.bs.y, hs, 16);
         const int b3 = __builtin_amdgcn_sbfe((int)a.bs.z, hs, 16);
         const int b4 = __builtin_amdgcn_sbfe((int)a.bs.w, hs, 16);
-        int part = p.s[0] * (d1 - 32 * b1) + p.s[1] * (d2 - 32 * b2) + p.s[2] * (d3 - 32 * b3) + p.s[3] * (d4 - 32 * b4);
+        int part = __mul24(p.s[0], d1 - 32 * b1) + __mul24(p.s[1], d2 - 32 * b2) + __mul24(p.s[2], d3 - 32 * b3) +
+                   __mul24(p.s[3], d4 - 32 * b4);
         part = quad_sum(part);
         const float d = half_lo(p.d);
         return d * a.s * (float)part;
