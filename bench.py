@@ -234,9 +234,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--copies", type=int, default=4, help="layer copies rotated to defeat the 256 MB cache")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--profile", choices=["layer", "prefill", "moe", "small", "q8", "heads", "config1"], default=None,
+    ap.add_argument("--profile", choices=["layer", "prefill", "moe", "moe_q6k", "small", "q8", "heads", "config1"],
+                    default=None,
                     help="for rocprof runs: only the timed decode-layer loop, the config-3 prefill line, the "
-                         "config-5 MoE line, the small-batch layer line, the Q8_0 line, the per-head Q8_0 Wo line "
+                         "config-5 MoE line (Q4_K or Q6_K down experts), the small-batch layer line, the Q8_0 line, the per-head Q8_0 Wo line "
                          "or the config-1 Q4_K 4096x4096 GEMV line")
     ap.add_argument("--pmc", action="store_true",
                     help="for rocprofv3 --pmc runs: 16 gate/up launches, then 16 plain 64 MiB device copies "
@@ -611,7 +612,7 @@ def main():
                 "separate_calls": {"calls": len(separate), "us": round(us_sep, 1), "proj_tok_s": round(1e6 / us_sep, 1)},
                 "timing": "host clock, best of %d tokens" % reps}
 
-    def moe_line(n_sets=2, tokens=16, top_k=2, n_experts=8, keep_host=False):
+    def moe_line(n_sets=2, tokens=16, top_k=2, n_experts=8, keep_host=False, down_fmt="q4k"):
         """benchmark config 5: Mixtral-8x7B-shaped experts (gate/up 14336x4096, down 4096x14336, Q4_K), 16 tokens
         routed top-2 on the device from seeded U[0,1) logits, grouped per-expert SwiGLU; graph-replayed over
         n_sets independent expert sets (> 1.5 GB, past the 256 MB cache). keep_host: also returns host copies of
@@ -623,10 +624,11 @@ def main():
             mats = {"gate": [], "up": [], "down": []}
             for name in ("gate", "up", "down"):
                 n, kk = (4096, 14336) if name == "down" else (14336, 4096)
+                q6 = name == "down" and down_fmt == "q6k"
                 for _ in range(n_experts):
                     wf = torch.randn(n, kk, generator=gen4, device=dev) * 0.02
-                    blocks = ov.quantize_weight(wf, ov.TYPE_Q4_K)
-                    mats[name].append(ov.Q4KWeight(blocks, kk, n))
+                    blocks = ov.quantize_weight(wf, ov.TYPE_Q6_K if q6 else ov.TYPE_Q4_K)
+                    mats[name].append((ov.Q6KWeight if q6 else ov.Q4KWeight)(blocks, kk, n))
                     if host is not None and si == 0:
                         host[name].append(blocks.cpu().numpy().reshape(n, -1))
                     del wf, blocks
@@ -644,15 +646,15 @@ def main():
         g = capture([(lambda m=m: moe_step(m)) for m in sets] * 4)  # 8 steps per graph replay
         us = replay_us(g, 4 * n_sets, 10)
         used = len(set(idx.cpu().numpy().tolist()))
-        wb = used * (2 * weight_bytes(14336, 4096, "q4k") + weight_bytes(4096, 14336, "q4k"))
+        wb = used * (2 * weight_bytes(14336, 4096, "q4k") + weight_bytes(4096, 14336, down_fmt))
         if host is not None:
             host.update(x=xm.cpu().numpy(), idx=idx.cpu().numpy(), w=wts.cpu().numpy(), tokens=tokens,
                         top_k=top_k, weight_bytes=wb)
         del g, sets
         torch.cuda.empty_cache()
-        line = {"what": "benchmark config 5: Mixtral-8x7B experts (Q4_K gate/up/down), 16 tokens, top-2, one MoE "
-                        "step (route + group + quantise in one launch, 2 grouped projections, SwiGLU, the combine "
-                        "folded into the down projection: 4 launches)",
+        line = {"what": "benchmark config 5: Mixtral-8x7B experts (Q4_K gate/up, %s down), 16 tokens, top-2, one "
+                        "MoE step (route + group + quantise in one launch, 2 grouped projections, SwiGLU, the combine "
+                        "folded into the down projection: 4 launches)" % ("Q6_K" if down_fmt == "q6k" else "Q4_K"),
                 "us": round(us, 1), "experts_used": used, "weight_bytes": wb,
                 "GB_s": round(wb / (us * 1e-6) / 1e9, 1), "pct_peak": round(100 * wb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 2),
                 "timing": "HIP graph replay of 8 steps over %d expert sets, per step" % n_sets}
@@ -671,8 +673,9 @@ def main():
                 "us": round(us, 2), "weight_bytes": wb, "GB_s": round(wb / (us * 1e-6) / 1e9, 1),
                 "timing": "HIP graph replay over %d layer copies x 4" % len(copies)}
 
-    if args.profile in ("prefill", "moe", "small", "q8", "heads", "config1"):
-        only = {"prefill": prefill_line, "moe": moe_line, "small": small_batch_line, "q8": q8_line,
+    if args.profile in ("prefill", "moe", "moe_q6k", "small", "q8", "heads", "config1"):
+        only = {"prefill": prefill_line, "moe": moe_line, "moe_q6k": lambda: moe_line(down_fmt="q6k"),
+                "small": small_batch_line, "q8": q8_line,
                 "heads": heads_line,
                 "config1": lambda: gemv_line(4096, 4096, "q4k", 64,
                                              "benchmark config 1: Q4_K 4096x4096 GEMV (quantise in-launch)")}[args.profile]
@@ -730,6 +733,7 @@ def main():
     config3 = prefill_line()
     config4 = model_line()
     config5, moe_host = moe_line(keep_host=not args.no_cpu_baseline)
+    config5_q6k = moe_line(down_fmt="q6k")  # the Q4_K_M layout: Q6_K ffn_down_exps
     ffn = ffn_line()
     q8 = q8_line()
     heads = heads_line()
@@ -767,6 +771,7 @@ def main():
         "config3_prefill_m512": config3,
         "config4_32_layers_lm_head": config4,
         "config5_moe_mixtral_16tok_top2": config5,
+        "config5_moe_q6k_down_experts": config5_q6k,
         "ffn_swiglu_decode": ffn,
         "small_batch_layer": small,
         "q4k_gemv_128256x4096": large_q4k,

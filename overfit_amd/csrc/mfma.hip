@@ -856,18 +856,19 @@ __global__ __launch_bounds__(256) void kquant_mfma_small_kernel(const SArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------ expert stream
-// Grouped (MoE) Q4_K projections with few pairs per expert, on a persistent grid. A unit of work is (expert e,
+// Grouped (MoE) Q4_K / Q6_K projections with few pairs per expert, on a persistent grid. A unit of work is (expert e,
 // matrix, 64-row weight group, 16-pair chunk) and belongs to one workgroup: workgroup b takes units b, b + (workgroups
 // in the launch), ... (experts without pairs skipped) and walks each unit's super-blocks in ascending order, one per
 // step, its four waves in step (wave w owns weight rows 16w .. 16w + 15 of the group). Per step each wave brings its
-// 16 weight rows (16 x 144 bytes) into its own LDS ring slot by DMA, and a quarter of the chunk's A operands (4 pairs
+// 16 weight rows' super-block (Q4_K: 16 x 144 bytes; Q6_K: 16 aligned 224-byte windows holding the 210-byte blocks)
+// into its own LDS ring slot by DMA, and a quarter of the chunk's A operands (4 pairs
 // x 256 activation bytes) and scales into the workgroup's shared slot, so the four waves read the activation once
 // between them; all of it is issued two steps ahead of use and crosses unit boundaries. The step runs the
-// super-block's MFMAs on raw nibbles (Q4KRaw) and the reference's fp32 tail for the results that hold pairs, and adds
+// super-block's MFMAs (Q4_K on raw nibbles, Q4KRaw; Q6_K on the lo/hi operands of Q6KMfma) and the reference's fp32
+// tail for the results that hold pairs, and adds
 // each block value to the lane's running sums: lane
 // (g, r16) owns outputs (MFMA rows 4g + j, weight row r16), so its sum is the reference's sequential sum over the
 // row, with no exchange between waves. The unit's last step stores biasO + sum.
-constexpr int kStreamW = 2304;         // a wave's weights per step: 16 rows x 144 bytes, two 1 KiB DMAs and one of 256
 constexpr int kStreamA = 4096;         // the chunk's A operands per step: 16 pairs x 256 bytes, 1 KiB DMA per wave
 constexpr int kStreamS = 64;           // the chunk's activation scales: 4 per wave
 constexpr int kStreamMaxPairs = 1024;  // the pair -> activation row map is cached in LDS (dynamic, 4 bytes a pair)
@@ -936,12 +937,149 @@ struct Q4KRaw {
     }
 };
 
+// The format side of the expert-stream kernel: a wave's weight DMA per step (pieces of 16 bytes: kPieces per weight
+// row, kRowLds bytes a row in the LDS slot, kWInstr DMA instructions of which the last moves kLastLanes pieces), the
+// swizzle of the shared A slot, and the step's compute from the LDS rings.
+// Q4_K: 144-byte blocks, row starts 16-byte aligned, so a row's block is 9 pieces at super-block offset 144 sb.
+struct StreamQ4K {
+    static constexpr int kPieces = 9;
+    static constexpr int kRowLds = 144;
+    static constexpr int kWInstr = 3;
+    static constexpr int kLastLanes = 16;
+    // scalar offset of super-block sb's pieces in a row
+    __device__ __forceinline__ static uint32_t soff(int sb) { return (uint32_t)sb * kQ4KBytes; }
+    // The MFMA row m of a pair holds its 16-byte pieces XORed with m % 8: rows m and m + 8 then share banks (a two-way
+    // conflict on the reads), but logical pieces i and i + 8 stay 128 bytes apart in every row, so one ds_read2_b64
+    // fetches a sub-block pair (s, s + 4).
+    __device__ __forceinline__ static uint32_t a_swizzle(uint32_t m) { return m & 7u; }
+    // Lane (g, r16) takes activation bytes 32 s + 8 g .. + 7 of sub-block s = 0..7 of its pair (MFMA row r16): half
+    // g % 2 of logical piece 2 s + g / 2, and for sub-block s + 4 the same half 128 bytes further.
+    __device__ __forceinline__ static void a_reads(uint32_t row, int g, int r16, uint32_t (&a_rd)[4]) {
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+            a_rd[t] = row + 16u * ((2u * t + ((uint32_t)g >> 1)) ^ ((uint32_t)r16 & 7u)) + 8u * ((uint32_t)g & 1u);
+    }
+    // wrow: the LDS address of this lane's weight row in the step's slot; abase + a_rd: its A operand pieces; sadr:
+    // its four results' scales. Reads and waits are explicit (see the kernel). Every output is early-clobber: a read's
+    // data may land while later reads of the block still use their address registers.
+    __device__ __forceinline__ static void step(uint32_t wrow, uint32_t abase, const uint32_t (&a_rd)[4], uint32_t sadr,
+                                                int, int g, int live, float (&run)[4]) {
+        u32x4 h, q01, q23, av[4];
+        f32x4 q8s;
+        asm volatile("ds_read_b128 %0, %8\n\t"
+                     "ds_read2_b64 %1, %9 offset1:4\n\t"
+                     "ds_read2_b64 %2, %9 offset0:8 offset1:12\n\t"
+                     "ds_read2_b64 %3, %10 offset1:16\n\t"
+                     "ds_read2_b64 %4, %11 offset1:16\n\t"
+                     "ds_read2_b64 %5, %12 offset1:16\n\t"
+                     "ds_read2_b64 %6, %13 offset1:16\n\t"
+                     "ds_read_b128 %7, %14\n\t"
+                     "s_waitcnt lgkmcnt(0)"
+                     : "=&v"(h), "=&v"(q01), "=&v"(q23), "=&v"(av[0]), "=&v"(av[1]), "=&v"(av[2]), "=&v"(av[3]),
+                       "=&v"(q8s)
+                     : "v"(wrow), "v"(wrow + 16u + 8u * (uint32_t)g), "v"(abase + a_rd[0]), "v"(abase + a_rd[1]),
+                       "v"(abase + a_rd[2]), "v"(abase + a_rd[3]), "v"(sadr)
+                     : "memory");
+        Q4KRaw::accumulate(h, q01, q23, av, q8s, live, run);
+    }
+};
+
+// Q6_K: 210-byte blocks, 2-byte aligned inside a row. With rows 16-byte aligned (super-blocks per row a multiple of 8),
+// super-block sb starts 2 (sb % 8) bytes past a 16-byte boundary in every row, so each row's block is DMA'd as the
+// 14 aligned pieces (224 bytes) from that boundary, and read back from LDS as aligned dwords shifted by 0 or 2 bytes
+// (v_alignbyte_b32). The block then runs as in the other batched kernels: Q6KMfma's lo/hi operands, two
+// v_mfma_i32_16x16x64_i8 per 64-element chunk, the tail d * q8Scale * mainAcc.
+struct StreamQ6K {
+    static constexpr int kPieces = 14;
+    static constexpr int kRowLds = 224;
+    static constexpr int kWInstr = 4;
+    static constexpr int kLastLanes = 32;  // 16 x 14 = 224 pieces = 3 x 64 + 32
+    __device__ __forceinline__ static uint32_t soff(int sb) { return (uint32_t)sb * kQ6KBytes - 2u * (uint32_t)(sb & 7); }
+    // 16-byte reads of one logical piece by the 16 rows of a lane group: XOR with the whole row index, conflict-free.
+    __device__ __forceinline__ static uint32_t a_swizzle(uint32_t m) { return m & 15u; }
+    // Chunk P of lane group g covers elements 128 (g / 2) + 32 P + 16 (g % 2) .. + 15 (Q6KMfma's K order): logical
+    // piece 8 (g / 2) + 2 P + g % 2.
+    __device__ __forceinline__ static void a_reads(uint32_t row, int g, int r16, uint32_t (&a_rd)[4]) {
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+            a_rd[t] = row + 16u * ((8u * ((uint32_t)g >> 1) + 2u * t + ((uint32_t)g & 1u)) ^ ((uint32_t)r16 & 15u));
+    }
+    __device__ __forceinline__ static void step(uint32_t wrow, uint32_t abase, const uint32_t (&a_rd)[4], uint32_t sadr,
+                                                int sb, int g, int live, float (&run)[4]) {
+        // The block starts at wrow + mis; every run the lane reads starts a multiple of 4 bytes after it.
+        const uint32_t mis = 2u * (uint32_t)(sb & 7), sh = mis & 2u;
+        const uint32_t hh = (uint32_t)g >> 1, l0 = 16u * ((uint32_t)g & 1u);
+        const uint32_t blk = wrow + (mis & ~3u);
+        const uint32_t oa = blk + 64u * hh + l0;          // ql[64h + l0 .. +16], then ql[64h + 32 + l0 ..] at + 32
+        const uint32_t oh = blk + 128u + 32u * hh + l0;   // qh[32h + l0 .. +16]
+        const uint32_t os = blk + 192u + 8u * hh;         // sc[8h .. 8h + 8]
+        u32x2 a01, a23, b01, b23, h01, h23, s01;
+        uint32_t a4, b4, h4, s2, dw;
+        u32x4 av[4];
+        f32x4 q8s;
+        asm volatile("ds_read2_b32 %0, %17 offset1:1\n\t"
+                     "ds_read2_b32 %1, %17 offset0:2 offset1:3\n\t"
+                     "ds_read_b32 %2, %17 offset:16\n\t"
+                     "ds_read2_b32 %3, %17 offset0:8 offset1:9\n\t"
+                     "ds_read2_b32 %4, %17 offset0:10 offset1:11\n\t"
+                     "ds_read_b32 %5, %17 offset:48\n\t"
+                     "ds_read2_b32 %6, %18 offset1:1\n\t"
+                     "ds_read2_b32 %7, %18 offset0:2 offset1:3\n\t"
+                     "ds_read_b32 %8, %18 offset:16\n\t"
+                     "ds_read2_b32 %9, %19 offset1:1\n\t"
+                     "ds_read_b32 %10, %19 offset:8\n\t"
+                     "ds_read_b32 %11, %20 offset:208\n\t"
+                     "ds_read_b128 %12, %21\n\t"
+                     "ds_read_b128 %13, %22\n\t"
+                     "ds_read_b128 %14, %23\n\t"
+                     "ds_read_b128 %15, %24\n\t"
+                     "ds_read_b128 %16, %25\n\t"
+                     "s_waitcnt lgkmcnt(0)"
+                     : "=&v"(a01), "=&v"(a23), "=&v"(a4), "=&v"(b01), "=&v"(b23), "=&v"(b4), "=&v"(h01), "=&v"(h23),
+                       "=&v"(h4), "=&v"(s01), "=&v"(s2), "=&v"(dw), "=&v"(av[0]), "=&v"(av[1]), "=&v"(av[2]),
+                       "=&v"(av[3]), "=&v"(q8s)
+                     : "v"(oa), "v"(oh), "v"(os), "v"(blk), "v"(abase + a_rd[0]), "v"(abase + a_rd[1]),
+                       "v"(abase + a_rd[2]), "v"(abase + a_rd[3]), "v"(sadr)
+                     : "memory");
+        Q6KMfma::W w;
+        const uint32_t ra[5] = {a01.x, a01.y, a23.x, a23.y, a4}, rb[5] = {b01.x, b01.y, b23.x, b23.y, b4};
+        const uint32_t rh[5] = {h01.x, h01.y, h23.x, h23.y, h4};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            w.ql[0][i] = __builtin_amdgcn_alignbyte(ra[i + 1], ra[i], sh);
+            w.ql[1][i] = __builtin_amdgcn_alignbyte(rb[i + 1], rb[i], sh);
+            w.qh[i] = __builtin_amdgcn_alignbyte(rh[i + 1], rh[i], sh);
+        }
+        const uint32_t sc0 = __builtin_amdgcn_alignbyte(s01.y, s01.x, sh), sc1 = __builtin_amdgcn_alignbyte(s2, s01.y, sh);
+        w.sc = __builtin_amdgcn_perm(sc1, sc0, (g & 1) ? 0x07050301u : 0x06040200u);
+        w.d = (dw >> (8u * sh)) & 0xffffu;  // d at block byte 208
+        i32x4 op[4][Q6KMfma::kNumMfma];
+        Q6KMfma::operands<0>(w, g, op[0]);
+        Q6KMfma::operands<1>(w, g, op[1]);
+        Q6KMfma::operands<2>(w, g, op[2]);
+        Q6KMfma::operands<3>(w, g, op[3]);
+        i32x4 acc[Q6KMfma::kNumMfma] = {i32x4{0, 0, 0, 0}, i32x4{0, 0, 0, 0}};
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const i32x4 aop = i32x4{(int)av[t].x, (int)av[t].y, (int)av[t].z, (int)av[t].w};
+            acc[0] = mfma16(aop, op[t][0], acc[0]);
+            acc[1] = mfma16(aop, op[t][1], acc[1]);
+        }
+        const float d = Q6KMfma::d_of(w);
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (j < live) run[j] += Q6KMfma::tail(acc, j, d, 0.0f, q8s[j]);
+    }
+};
+
 // D = ring slots: steps q + 1 .. q + D - 1 are in flight while step q is computed.
-template <int D>
-__global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int n_experts, int nmat, int pairs) {
-    static_assert(D >= 3 && 5 * (D - 2) + 3 <= 63, "the wait count below must fit the 6-bit vmcnt field");
+template <class FS, int D>
+__global__ __launch_bounds__(256) void mfma_stream_kernel(const SArgs a, int n_experts, int nmat, int pairs) {
+    constexpr int kWait = (FS::kWInstr + 2) * (D - 2) + FS::kWInstr;
+    static_assert(D >= 3 && kWait <= 63, "the wait count below must fit the 6-bit vmcnt field");
+    constexpr int kSlot = 16 * FS::kRowLds;  // a wave's weights per step
     // The rings are read with explicit LDS instructions after explicit waits (below), so one array serves each.
-    __shared__ __align__(16) uint8_t wring[D][4][kStreamW];
+    __shared__ __align__(16) uint8_t wring[D][4][kSlot];
     __shared__ __align__(16) uint8_t aring[D][kStreamA];
     __shared__ __align__(16) uint8_t sring[D][kStreamS];
     __shared__ int eoff[kMaxExperts + 1];
@@ -964,7 +1102,7 @@ __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int
     const int groups = a.tiles, per_e = groups * nmat, T = n_experts * per_e;
     const int NG = (int)gridDim.x;  // workgroups in the launch
     const uint32_t K = (uint32_t)spr * kQK;
-    const uint32_t row_bytes = (uint32_t)spr * kQ4KBytes;
+    const uint32_t row_bytes = (uint32_t)spr * (uint32_t)(FS::kRowLds == 144 ? kQ4KBytes : kQ6KBytes);
 
     // The schedule: step (unit t, pair chunk n0, super-block sb), the same in every wave of the workgroup. A lead
     // cursor walks it once; each step's fields are kept in a descriptor from the issue of its loads until it is
@@ -984,22 +1122,20 @@ __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int
         asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr) : "memory");
         return __builtin_amdgcn_readfirstlane(v);
     };
-    // Weight DMA pieces of a step (16 rows x 9 pieces of 16 bytes): instruction i = 0, 1, 2 moves pieces 64 i + lane
-    // (16 bytes each; instruction 2 on lanes 0-15 only, pieces 128 .. 143). The super-block's offset in the row goes
-    // in the scalar offset.
-    uint32_t lane_off[3];
+    // Weight DMA pieces of a step (16 rows x kPieces pieces of 16 bytes): instruction i moves pieces 64 i + lane (the
+    // last one on its first kLastLanes lanes only). The super-block's offset in the row goes in the scalar offset.
+    uint32_t lane_off[FS::kWInstr];
 #pragma unroll
-    for (int i = 0; i < 3; i++) {
-        const uint32_t p = 64u * i + (uint32_t)(i == 2 ? (lane & 15) : lane);
-        lane_off[i] = (p / 9u) * row_bytes + 16u * (p % 9u);
+    for (int i = 0; i < FS::kWInstr; i++) {
+        const uint32_t p = 64u * i + (uint32_t)(i == FS::kWInstr - 1 ? (lane & (FS::kLastLanes - 1)) : lane);
+        lane_off[i] = (p / (uint32_t)FS::kPieces) * row_bytes + 16u * (p % (uint32_t)FS::kPieces);
     }
     // Shared A slot: pair p of the chunk (p < 16) at 1024 (p / 4) + 256 (p % 4), written by wave p / 4. The MFMA row
     // of pair p is m(p) = 4 (p % 4) + p / 4 (pair p sits in MFMA row m(p)), and its 16-byte pieces are stored XORed
-    // with m(p) % 8: rows m and m + 8 then share banks (a two-way conflict on the reads), but logical pieces i and
-    // i + 8 stay 128 bytes apart in every row, so one ds_read2_b64 fetches a sub-block pair (s, s + 4).
-    // Wave w's A DMA: lane L moves pair 4w + L / 16, physical piece L % 16 = logical piece (L % 16) ^ (m % 8).
+    // with FS::a_swizzle(m(p)). Wave w's A DMA: lane L moves pair 4w + L / 16 (MFMA row 4 (L / 16) + w), physical
+    // piece L % 16 = logical piece (L % 16) ^ a_swizzle(that row).
     const int a_pair = 4 * wave + (lane >> 4);                       // the pair this lane's A DMA moves
-    const uint32_t a_piece = (uint32_t)((lane & 15) ^ ((4 * (lane >> 4) + wave) & 7));
+    const uint32_t a_piece = (uint32_t)(lane & 15) ^ FS::a_swizzle((uint32_t)(4 * (lane >> 4) + wave));
     const int s_pair = 4 * (lane & 3) + wave;                        // lanes 0-3: the pair of this lane's scale DMA
     const __amdgpu_buffer_rsrc_t qr = make_rsrc(a.q, (uint32_t)a.act_rows * K);
     const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.s, (uint32_t)a.act_rows * (uint32_t)spr * 4u);
@@ -1064,16 +1200,17 @@ __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int
 
     // The lead step's weights go to this wave's ring slot j, its A operands and scales to the shared slot j.
     auto issue_w = [&](const Step& c, int j) {
-        const int soff = c.sb * kQ4KBytes;
+        const int soff = (int)FS::soff(c.sb);
         uint8_t* sl = wring[j][wave];
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(lead_w, (__attribute__((address_space(3))) void*)sl, 16,
-                                                 (int)lane_off[0], soff, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(lead_w, (__attribute__((address_space(3))) void*)(sl + 1024), 16,
-                                                 (int)lane_off[1], soff, 0, 0);
-        // lanes 0-15 only: the DMA writes only active lanes (16 pieces, 256 bytes)
-        if (lane < 16)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(lead_w, (__attribute__((address_space(3))) void*)(sl + 2048), 16,
-                                                     (int)lane_off[2], soff, 0, 0);
+#pragma unroll
+        for (int i = 0; i < FS::kWInstr - 1; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(lead_w, (__attribute__((address_space(3))) void*)(sl + 1024 * i),
+                                                     16, (int)lane_off[i], soff, 0, 0);
+        // the last instruction on its first kLastLanes lanes only (the DMA writes only active lanes)
+        if (lane < FS::kLastLanes)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                lead_w, (__attribute__((address_space(3))) void*)(sl + 1024 * (FS::kWInstr - 1)), 16,
+                (int)lane_off[FS::kWInstr - 1], soff, 0, 0);
     };
     auto issue_a = [&](const Step& c, int j) {
         __builtin_amdgcn_raw_ptr_buffer_load_lds(qr, (__attribute__((address_space(3))) void*)(aring[j] + 1024 * wave),
@@ -1083,16 +1220,10 @@ __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int
             __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (__attribute__((address_space(3))) void*)(sring[j] + 16 * wave),
                                                      4, (int)(lead_s + (uint32_t)c.sb * 4u), 0, 0, 0);
     };
-    // Read side (Q4KRaw): lane (g, r16) takes activation bytes 32 s + 8 g .. + 7 of sub-block s = 0..7 of pair p with
-    // m(p) = r16, i.e. p = 4 (r16 % 4) + r16 / 4, held at 1024 (r16 % 4) + 256 (r16 / 4): half g % 2 of logical piece
-    // 2 s + g / 2, and for sub-block s + 4 the same half 128 bytes further.
+    // Read side: lane (g, r16) reads pair p with m(p) = r16, i.e. p = 4 (r16 % 4) + r16 / 4, held at
+    // 1024 (r16 % 4) + 256 (r16 / 4).
     uint32_t a_rd[4];
-    {
-        const uint32_t row = 1024u * (uint32_t)(r16 & 3) + 256u * (uint32_t)(r16 >> 2);
-#pragma unroll
-        for (int t = 0; t < 4; t++)
-            a_rd[t] = row + 16u * ((2u * t + ((uint32_t)g >> 1)) ^ ((uint32_t)r16 & 7u)) + 8u * ((uint32_t)g & 1u);
-    }
+    FS::a_reads(1024u * (uint32_t)(r16 & 3) + 256u * (uint32_t)(r16 >> 2), g, r16, a_rd);
 
     Step lead;  // the next step whose loads go out
     seek(lead, (int)blockIdx.x);
@@ -1122,34 +1253,19 @@ __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int
         const Step& cur = desc[s];
         desc[w] = lead;
         issue_w(lead, w);
-        // This wave's loads of step q have landed: younger are the next D - 2 steps' five instructions each and the
-        // weights just issued, three (a unit's output stores only add younger ones). The barrier then makes the other
-        // waves' A operands and scales of step q visible, and frees slot w of the shared rings.
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(5 * (D - 2) + 3) : "memory");
+        // This wave's loads of step q have landed: younger are the next D - 2 steps' kWInstr + 2 instructions each and
+        // the weights just issued, kWInstr (a unit's output stores only add younger ones). The barrier then makes the
+        // other waves' A operands and scales of step q visible, and frees slot w of the shared rings.
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kWait) : "memory");
         __builtin_amdgcn_s_barrier();
         issue_a(lead, w);
         advance(lead);
         const uint32_t wrow = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)(wring[s][wave]) +
-                              (uint32_t)r16 * kQ4KBytes;
+                              (uint32_t)r16 * FS::kRowLds;
         const uint32_t abase = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)(aring[s]);
         const uint32_t sadr = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)(sring[s]) + 16u * (uint32_t)g;
-        u32x4 h, q01, q23, av[4];
-        f32x4 q8s;
-        asm volatile("ds_read_b128 %0, %8\n\t"
-                     "ds_read2_b64 %1, %9 offset1:4\n\t"
-                     "ds_read2_b64 %2, %9 offset0:8 offset1:12\n\t"
-                     "ds_read2_b64 %3, %10 offset1:16\n\t"
-                     "ds_read2_b64 %4, %11 offset1:16\n\t"
-                     "ds_read2_b64 %5, %12 offset1:16\n\t"
-                     "ds_read2_b64 %6, %13 offset1:16\n\t"
-                     "ds_read_b128 %7, %14\n\t"
-                     "s_waitcnt lgkmcnt(0)"
-                     : "=v"(h), "=v"(q01), "=v"(q23), "=v"(av[0]), "=v"(av[1]), "=v"(av[2]), "=v"(av[3]), "=v"(q8s)
-                     : "v"(wrow), "v"(wrow + 16u + 8u * (uint32_t)g), "v"(abase + a_rd[0]), "v"(abase + a_rd[1]),
-                       "v"(abase + a_rd[2]), "v"(abase + a_rd[3]), "v"(sadr)
-                     : "memory");
         const int live = min(4, (cur.cnt - cur.n0 + 3) >> 2);  // results j < live hold pairs
-        Q4KRaw::accumulate(h, q01, q23, av, q8s, live, run);
+        FS::step(wrow, abase, a_rd, sadr, cur.sb, g, live, run);
         if (cur.sb == spr - 1) {
             const int o = cur.o0 + r16;
             const float* bias = cur.mat ? a.bias1 : a.bias0;
@@ -1167,7 +1283,7 @@ __global__ __launch_bounds__(256) void q4k_mfma_stream_kernel(const SArgs a, int
                         int tok;
                         float wt;
                         asm volatile("ds_read_b32 %0, %2\n\tds_read_b32 %1, %3\n\ts_waitcnt lgkmcnt(0)"
-                                     : "=v"(tok), "=v"(wt)
+                                     : "=&v"(tok), "=&v"(wt)
                                      : "v"(ta), "v"(wa)
                                      : "memory");
                         const float prod = wt * v;
@@ -1205,10 +1321,11 @@ static hipError_t launch_small(SArgs& sa, int nmat, int experts, hipStream_t st)
 }
 
 // Static LDS of the expert-stream kernel (its dynamic part is the pair map, 4 bytes a pair).
+template <class FS>
 static size_t stream_lds_bytes() {
     static const size_t bytes = [] {
         hipFuncAttributes fa{};
-        return hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(q4k_mfma_stream_kernel<3>)) == hipSuccess
+        return hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(mfma_stream_kernel<FS, 3>)) == hipSuccess
                    ? fa.sharedSizeBytes
                    : (size_t)(160 * 1024);
     }();
@@ -1244,7 +1361,10 @@ bool stream_pair_preferred(int type, int in, int n_rows) {
 static bool mfma_small_streams(int type, const GroupLaunch& L) {
     const int nmat = L.w1 ? 2 : 1;
     const int pairs = L.expert_off ? L.pairs : L.rows;
-    return stream_enabled() && type == 12 && (L.expert_off || stream_dense_ok(nmat, L.n_rows)) && pairs > 0 &&
+    // Q6_K blocks are DMA'd from the 16-byte boundary before them, which is the same in every row when rows are whole
+    // multiples of 16 bytes (super-blocks per row a multiple of 8; Mixtral's 14336 and Llama's 4096 inputs are).
+    const bool fmt = type == 12 || (type == 14 && (L.in / kQK) % 8 == 0);
+    return stream_enabled() && fmt && (L.expert_off || stream_dense_ok(nmat, L.n_rows)) && pairs > 0 &&
            pairs <= kStreamMaxPairs;
 }
 
@@ -1288,9 +1408,15 @@ hipError_t launch_mfma_small(int type, const GroupLaunch& L, hipStream_t st) {
             return v && *v ? atoi(v) : 0;
         }();
         const size_t dyn = (size_t)pairs * sizeof(int) * (L.comb ? 3 : 1);
-        const int per_cu = per_cu_env ? per_cu_env : (stream_lds_bytes() + dyn <= 160 * 1024 / 3 ? 3 : 2);
+        const size_t lds = type == 12 ? stream_lds_bytes<StreamQ4K>() : stream_lds_bytes<StreamQ6K>();
+        const int per_cu = per_cu_env ? per_cu_env : (lds + dyn <= 160 * 1024 / 3 ? 3 : 2);
         const int grid = (int)std::min<long>(units, (long)cus * per_cu);
-        hipLaunchKernelGGL(q4k_mfma_stream_kernel<3>, dim3(grid), dim3(256), dyn, st, sa, L.experts, nmat, pairs);
+        if (type == 12)
+            hipLaunchKernelGGL((mfma_stream_kernel<StreamQ4K, 3>), dim3(grid), dim3(256), dyn, st, sa, L.experts, nmat,
+                               pairs);
+        else
+            hipLaunchKernelGGL((mfma_stream_kernel<StreamQ6K, 3>), dim3(grid), dim3(256), dyn, st, sa, L.experts, nmat,
+                               pairs);
         return hipGetLastError();
     }
     // super-blocks per wave batch (measured on MI355X: 2 beats 4 for every Llama/Mixtral shape)

@@ -82,3 +82,26 @@ def test_kernels_never_bit_cast_a_vector_element():
     for f in os.listdir(csrc):
         text = open(os.path.join(csrc, f)).read()
         assert not pat.search(text), f
+
+
+def test_multi_read_lds_asm_outputs_are_early_clobber():
+    # An inline-asm block that issues several LDS reads before one wait must mark every output early-clobber ("=&v"):
+    # a read's data can land while a later read of the block still needs its address register, and without the
+    # marker the compiler may give both the same VGPR. (The MoE combine's token/weight read once got its weight
+    # address overwritten by the token this way, giving wrong combine weights depending on timing.)
+    import os
+    import re
+
+    csrc = os.path.join(os.path.dirname(overfit_amd.__file__), "csrc")
+    for name in sorted(os.listdir(csrc)):
+        if not name.endswith((".hip", ".h", ".cpp")):
+            continue
+        text = open(os.path.join(csrc, name)).read()
+        for m in re.finditer(r"asm\s+volatile\s*\((.*?)\);", text, re.S):
+            body = m.group(1)
+            template, _, operands = body.partition(":")
+            if template.count("ds_read") < 2:
+                continue
+            outputs = operands.split(":")[0]
+            plain = re.findall(r'"=v"', outputs)
+            assert not plain, f"{name}: multi-read asm block with non-early-clobber outputs: {template[:60]!r}"

@@ -563,6 +563,27 @@ def test_stream_kernel_dense_bit_exact(orc, batched, rows, k, n):
                          "stream up")
 
 
+# Tall Q6_K matrices with rows of a multiple of 8 super-blocks take the stream kernel's Q6_K form: every block DMA'd
+# as the 224 aligned bytes around it (2 (sb % 8) bytes of lead-in), the lo/hi operands built from LDS. Row lengths of 8
+# and 16 super-blocks (every lead-in), 3 .. 37 rows, partial weight groups and pair chunks.
+STREAM_Q6K_SHAPES = [(3, 2048, 12288), (9, 4096, 12290), (16, 2048, 12300), (37, 2048, 12304)]
+
+
+@pytest.mark.parametrize("rows,k,n", STREAM_Q6K_SHAPES)
+def test_stream_kernel_dense_q6k_bit_exact(orc, batched, rows, k, n):
+    case("stream dense q6k", rows, k, n)
+    batched("small")
+    rng = np.random.default_rng(rows * 17 + n)
+    blocks = _kq_blocks(rng, "q6k", n, k)
+    x = normal(rng, (rows, k))
+    bias = normal(rng, n)
+    w = ov.Q6KWeight(blocks, k, n)
+    y = ov.project(w, t(x), t(bias), rows=rows)
+    torch.cuda.synchronize()
+    assert_bit_exact(y.cpu().numpy().reshape(rows, n), orc.q6k_project_batched(x, rows, blocks, k, n, bias),
+                     f"stream q6k {rows}x{k}x{n}")
+
+
 @pytest.mark.parametrize("rows", [2, 3, 4, 5])
 def test_gate_up_pair_rows_boundary_bit_exact(orc, ctx, rows):
     """A gate/up-shaped Q4_K pair tall enough for the expert-stream kernel (6144 rows each: 768 16-row tiles) under
@@ -789,19 +810,22 @@ def test_moe_ffn_matches_oracle(orc, gfmt, dfmt):
     _moe_check(ov.moe_ffn(gw, uw, dw, x, rows, k, idx2, w), ref2, f"{gfmt}/{dfmt} sparse routing")
 
 
-@pytest.mark.parametrize("rows,E,k,dfmt", [(16, 8, 1, "q4k"), (16, 8, 2, "q4k"), (300, 64, 2, "q4k"),
-                                            (16, 8, 2, "q6k"), (40, 8, 1, "q6k")])
-def test_moe_ffn_top2_combine_bit_exact(orc, rows, E, k, dfmt):
-    """Top-1 / top-2 with few pairs per expert: the down launch (the expert-stream kernel for Q4_K, the small-M
-    kernel for Q6_K) adds weight * expert output into y with float atomics instead of a combine launch. y must equal, bit for bit, the reference's in-order combine
+@pytest.mark.parametrize("rows,E,k,dfmt,dff", [(16, 8, 1, "q4k", 512), (16, 8, 2, "q4k", 512),
+                                                (300, 64, 2, "q4k", 512), (16, 8, 2, "q6k", 512), (40, 8, 1, "q6k", 512),
+                                                (16, 8, 2, "q6k", 2048), (40, 8, 1, "q6k", 2048),
+                                                (300, 64, 2, "q6k", 2048)])
+def test_moe_ffn_top2_combine_bit_exact(orc, rows, E, k, dfmt, dff):
+    """Top-1 / top-2 with few pairs per expert: the down launch (the expert-stream kernel for Q4_K and for Q6_K rows of
+    a multiple of 8 super-blocks, else the small-M kernel) adds weight * expert output into y with float atomics
+    instead of a combine launch. y must equal, bit for bit, the reference's in-order combine
     (0 + w0 o0) + w1 o1 (RT/MoeFeedForwardBlock.cs:225-239) of each expert's output, taken here from the one-token
     SwiGLU FFN on the same expert (the same projections and SiLU launch, bit-identical per pair), with an unclaimed
     slot and a repeated index adding nothing, y first filled with NaN (every element written), and a second call
     with fewer tokens into the same buffer (no stale sums). 300 tokens over 64 experts: 600 pairs in the stream
     kernel's pair map, one expert with more than 40 pairs (several 16-pair chunks)."""
-    case("moe top-k combine fold", rows, E, k, dfmt)
+    case("moe top-k combine fold", rows, E, k, dfmt, dff)
     rng = np.random.default_rng(400 + rows + k)
-    dm, dff = 256, 512
+    dm = 256
     gw, uw = ([ov.Q4KWeight(orc.quantize_q4k(normal(rng, shp, 0.05)), shp[1], shp[0]) for _ in range(E)]
               for shp in ((dff, dm), (dff, dm)))
     if dfmt == "q6k":
