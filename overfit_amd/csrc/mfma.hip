@@ -12,7 +12,8 @@
 //        v_mfma_f32_16x16x16_f16 per 16-row sub-tile over the 16 bsums of each row (|bsums| <= 2032 and m <= 63
 //        are exact in fp16, every partial sum is an integer below 2^24, so the fp32 result is minAcc exactly).
 //  Q6_K  unsignedTerm - 32*bsumTerm = sum_e sc_{s(e)} * (q_e - 32) * q8_e. W = sc*(q-32) lies in [-4064, 4096]
-//        (sc = -128 is a legal scale), split as 128*hi + lo (lo in [0,127], hi in [-32,32]); two MFMAs.
+//        (sc = -128 is a legal scale), split as 256*hi + lo with lo the signed low byte of W (in [-128,127]) and
+//        hi = (W + 128) >> 8 (in [-16,16]); two MFMAs, mainAcc = acc_lo + (acc_hi << 8).
 // The regroupings use the Q8_K definition bsums[j] = sum of quants 16j..16j+15 (the quantiser's output); only the
 // tiled Q4_K kernel reads the bsums plane. The fp32 tail of each super-block — q8Scale * (d*mainAcc - dmin*minAcc) and
 // d*q8Scale*mainAcc (RT/Q4KDotKernel.cs:944, RT/Q6KDotKernel.cs:114-115) — is evaluated per (n, o) in the
@@ -86,13 +87,14 @@ __device__ __forceinline__ i32x4 mfma16(i32x4 a, i32x4 b, i32x4 c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
 
-// Two dwords of 16-bit lanes (pe: K bytes 0 and 2, po: K bytes 1 and 3), each value v in [-2^15, 2^15) as two's
-// complement: lo = v & 127 and hi = floor(v / 128) (the low byte of v >> 7, an int8 for |v| <= 2^14) as packed
-// bytes in K order. v_perm_b32 gathers bytes 0 and 2 of each source: selector 0x06020400 = [pe.b0, po.b0, pe.b2,
-// po.b2].
+// Two dwords of 16-bit lanes (pe: K bytes 0 and 2, po: K bytes 1 and 3), each holding u = v + 128 for a value v in
+// [-4064, 4224) (two's complement): lo = the low byte of v as int8 (v mod 256, signed), hi = u >> 8 (the high byte of
+// u), so that v = 256*hi + lo, as packed bytes in K order. v_perm_b32 gathers bytes 0 and 2 of each source (selector
+// 0x06020400 = [pe.b0, po.b0, pe.b2, po.b2]) or bytes 1 and 3 (0x07030501); the low byte of v is the low byte of u
+// with its top bit flipped.
 __device__ __forceinline__ void split_lo_hi(uint32_t pe, uint32_t po, uint32_t& lo, uint32_t& hi) {
-    lo = __builtin_amdgcn_perm(po, pe, 0x06020400u) & 0x7f7f7f7fu;
-    hi = __builtin_amdgcn_perm(po >> 7, pe >> 7, 0x06020400u);
+    lo = __builtin_amdgcn_perm(po, pe, 0x06020400u) ^ 0x80808080u;
+    hi = __builtin_amdgcn_perm(po, pe, 0x07030501u);
 }
 
 // K permutation. The four MFMAs t = 0..3 of a super-block each cover 64 of its 256 elements; lane-group g of
@@ -123,6 +125,16 @@ struct Q4KMfma {
         w.q[0] = ld4(r, off + 16 + 16 * g);
         w.q[1] = ld4(r, off + 16 + 64 + 16 * g);
         return w;
+    }
+    // The min MFMA's B operand for lane group g: m_{2g}, m_{2g}, m_{2g+1}, m_{2g+1} in fp16, from the eight 6-bit
+    // mins (LD/GgmlDequant.cs:64-79 unpacking; lane group g takes sub-blocks 2g and 2g + 1).
+    __device__ __forceinline__ static u32x2 min_operand(const W& w, int g) {
+        const uint32_t m_lo = w.h.z & 0x3f3f3f3fu;
+        const uint32_t m_hi = ((w.h.w >> 4) & 0x0f0f0f0fu) | ((w.h.z >> 2) & 0x30303030u);
+        const uint32_t mg = (g < 2 ? m_lo : m_hi) >> (16 * (g & 1));
+        const uint32_t m0 = __builtin_bit_cast(uint16_t, (_Float16)(mg & 0xffu));
+        const uint32_t m1 = __builtin_bit_cast(uint16_t, (_Float16)((mg >> 8) & 0xffu));
+        return u32x2{m0 * 0x00010001u, m1 * 0x00010001u};
     }
     // Sub-block of MFMA t, lane-group g: js = 4(t&1) + 2(g>>1) + (t>>1) (LD/GgmlDequant.cs:64-79 unpacking).
     template <int T>
@@ -197,11 +209,13 @@ struct Q6KMfma {
         w.d = __builtin_amdgcn_raw_buffer_load_b16(r, (int)(off + 208), 0, 0);
         return w;
     }
+    __device__ __forceinline__ static u32x2 min_operand(const W&, int) { return u32x2{0u, 0u}; }
     template <int P>
     __device__ __forceinline__ static void operands(const W& w, int, i32x4 (&op)[kNumMfma]) {
-        // W = sc * (q - 32) in [-4064, 4096], computed per 16-bit lane modulo 2^16 (two's complement).
+        // W + 128 = sc * q - 32 * sc + 128 (W = sc * (q - 32) in [-4064, 4096]), computed per 16-bit lane modulo
+        // 2^16 (two's complement).
         const uint32_t scp = (uint32_t)(int)(int8_t)((w.sc >> (8 * P)) & 0xffu);
-        const uint32_t sc16 = scp & 0xffffu, bias16 = (0u - 32u * scp) & 0xffffu;
+        const uint32_t sc16 = scp & 0xffffu, bias16 = (128u - 32u * scp) & 0xffffu;
         const u16x2 sc2 = {(unsigned short)sc16, (unsigned short)sc16};
         const u16x2 bias2 = {(unsigned short)bias16, (unsigned short)bias16};
         constexpr uint32_t kNib = (P >> 1) * 4, kBits = 2 * P;
@@ -224,7 +238,7 @@ struct Q6KMfma {
     __device__ __forceinline__ static uint32_t raw_scales(const W& w) { return w.d; }  // fp16 d
     // d * q8Scale * mainAcc   (RT/Q6KDotKernel.cs:114-115)
     __device__ __forceinline__ static float tail(const i32x4 (&acc)[kNumMfma], int i, float d, float, float q8s) {
-        const int main_acc = acc[0][i] + (acc[1][i] << 7);
+        const int main_acc = acc[0][i] + (acc[1][i] << 8);
         return d * q8s * (float)main_acc;
     }
 };
@@ -486,18 +500,7 @@ __global__ __launch_bounds__(256, 2) void kquant_mfma_kernel(const MArgs a) {
             F::template operands<1>(w, g, op[1]);
             F::template operands<2>(w, g, op[2]);
             F::template operands<3>(w, g, op[3]);
-            u32x2 mb = u32x2{0u, 0u};
-            if constexpr (kMinF16) {
-                // the eight 6-bit mins, one byte each (LD/GgmlDequant.cs:64-79 unpacking); lane group g takes
-                // sub-blocks 2g and 2g + 1
-                const uint32_t m_lo = w.h.z & 0x3f3f3f3fu;
-                const uint32_t m_hi = ((w.h.w >> 4) & 0x0f0f0f0fu) | ((w.h.z >> 2) & 0x30303030u);
-                const uint32_t mg = (g < 2 ? m_lo : m_hi) >> (16 * (g & 1));
-                const uint32_t m0 = __builtin_bit_cast(uint16_t, (_Float16)(mg & 0xffu));
-                const uint32_t m1 = __builtin_bit_cast(uint16_t, (_Float16)((mg >> 8) & 0xffu));
-                mb = u32x2{m0 * 0x00010001u, m1 * 0x00010001u};
-            }
-            mma_tail(buf, op, F::d_of(w), F::dmin_of(w), mb);
+            mma_tail(buf, op, F::d_of(w), F::dmin_of(w), F::min_operand(w, g));
         };
         typename F::W wcur = F::load(wr, woff, g);
         stage(0, 0);
