@@ -240,7 +240,7 @@ def main():
                          "config-5 MoE line (Q4_K or Q6_K down experts), the small-batch layer line, the Q8_0 line, the per-head Q8_0 Wo line "
                          "or the config-1 Q4_K 4096x4096 GEMV line")
     ap.add_argument("--pmc", action="store_true",
-                    help="for rocprofv3 --pmc runs: 16 gate/up launches, then 16 plain 64 MiB device copies "
+                    help="for rocprofv3 --pmc runs: 64 gate/up launches, then 16 plain 64 MiB device copies "
                          "(the counter calibration reference)")
     args = ap.parse_args()
 
@@ -284,7 +284,7 @@ def main():
     # Warm up eagerly (allocates any scratch), time K eager steps, then also capture one rotation over the layer
     # copies into a HIP graph on a side stream and time its replays (GPU time without Python launch overhead).
     if args.pmc:
-        for i in range(16):
+        for i in range(64):
             ws = copies[i % len(copies)]
             ctx.project_multi_dev([ws["gate"], ws["up"]], x_in["ffn"], [ys["gate"], ys["up"]])
         torch.cuda.synchronize()
@@ -293,7 +293,7 @@ def main():
         for _ in range(16):
             dst.copy_(src)
         torch.cuda.synchronize()
-        print(json.dumps({"pmc_run": "gate/up x16 then copy 64MiB x16"}), flush=True)
+        print(json.dumps({"pmc_run": "gate/up x64 then copy 64MiB x16"}), flush=True)
         return
 
     side = torch.cuda.Stream()
