@@ -10,17 +10,37 @@
 namespace ovfq {
 
 // ------------------------------------------------------------------------------------------ Q8_K activation
-// Q4KDotKernel.QuantizeActivationQ8K (RT/Q4KDotKernel.cs:71-136): one wave per 256-element super-block, four
-// consecutive elements per lane. absMax is a max (exact in any order); scale = absMax / 127f; inverse =
-// scale > 0 ? 1f / scale : 0f; q = clamp(rint(x * inverse), -127, 127); bsums[g] = sum of the 16 quants of
-// group g (four lanes).
+// Q4KDotKernel.QuantizeActivationQ8K (RT/Q4KDotKernel.cs:71-136): absMax is a max (exact in any order); scale =
+// absMax / 127f; inverse = scale > 0 ? 1f / scale : 0f; q = clamp(rint(x * inverse), -127, 127); bsums[g] = sum
+// of the 16 quants of group g. Four super-blocks per wave, one per 16-lane DPP row, sixteen consecutive elements (one
+// bsum group) per lane: four 16-byte loads and one 16-byte store of quants per lane, the block's absMax by a 4-step
+// DPP row max (a wave per block spent most of its time in the 6 cross-lane exchanges of its max).
 __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float* __restrict__ x, int64_t n_blocks,
                                                             int8_t* __restrict__ q, float* __restrict__ s,
                                                             int16_t* __restrict__ bs) {
     // wave_id() is a readfirstlane value, so the buffer resource below is provably wave-uniform (SGPRs).
-    const int64_t blk = (int64_t)blockIdx.x * 4 + wave_id();
-    if (blk >= n_blocks) return;
-    q8k_quantize_block(x, blk, q, s, bs);
+    const int64_t blk0 = ((int64_t)blockIdx.x * 4 + wave_id()) * 4;
+    if (blk0 >= n_blocks) return;
+    const int lane = threadIdx.x & 63, row = lane >> 4, l16 = lane & 15;
+    const int64_t blk = blk0 + row;
+    // blocks past the end read zeros (the resource ends with the last block) and store nothing
+    const __amdgpu_buffer_rsrc_t xr =
+        make_rsrc(x + blk0 * kQK, rsrc_bytes((uint64_t)n_blocks * kQK * 4, (uint64_t)blk0 * kQK * 4));
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const u32x4 t = ld4(xr, (uint32_t)row * 1024u + (uint32_t)l16 * 64u + (uint32_t)i * 16u);
+        v[4 * i] = as_float(t.x);
+        v[4 * i + 1] = as_float(t.y);
+        v[4 * i + 2] = as_float(t.z);
+        v[4 * i + 3] = as_float(t.w);
+    }
+    const Q8KRow r = q8k_quantize_row16(v);
+    if (blk < n_blocks) {
+        *reinterpret_cast<u32x4*>(q + blk * kQK + l16 * 16) = r.packed;
+        bs[blk * 16 + l16] = (int16_t)r.group_sum;
+        if (l16 == 0) s[blk] = r.scale;
+    }
 }
 
 // ------------------------------------------------------------------------------------------ Q8_0 activation
@@ -322,7 +342,7 @@ hipError_t launch_q5_to_q8_0(const void* gguf, bool q5k, int64_t n_blocks, int8_
 
 hipError_t launch_quantize_q8k(const float* x, int64_t n_blocks, int8_t* q, float* s, int16_t* b, hipStream_t st) {
     if (n_blocks <= 0) return hipSuccess;
-    const int64_t grid = (n_blocks + 3) / 4;
+    const int64_t grid = (n_blocks + 15) / 16;
     hipLaunchKernelGGL(quantize_q8k_kernel, dim3((unsigned)grid), dim3(256), 0, st, x, n_blocks, q, s, b);
     return hipGetLastError();
 }

@@ -67,7 +67,7 @@ def test_batched_kernel_choice_rejects_unknown(ctx):
 
 # ------------------------------------------------------------------------------------------------ quantizers
 
-@pytest.mark.parametrize("rows,k", [(1, 256), (3, 4096), (2, 14336), (7, 512)])
+@pytest.mark.parametrize("rows,k", [(1, 256), (3, 4096), (2, 14336), (7, 512), (5, 256), (512, 4096)])
 def test_quantize_q8k_bit_exact(orc, ctx, rows, k):
     case("quantize_q8k", rows, k)
     rng = np.random.default_rng(rows * 1000 + k)
