@@ -269,11 +269,14 @@ int quantize_into_scratch(ovfq_ctx* c, int type, const float* x_dev, int rows, i
     } else {
         rc = ensure(c, c->act_s, n / 256 * sizeof(float));
         if (rc) return rc;
-        rc = ensure(c, c->act_b, n / 16 * sizeof(int16_t));
+        // the int16 bsums, then the same sums as fp16 (read by the tiled Q4_K kernels)
+        rc = ensure(c, c->act_b, n / 16 * 2 * sizeof(int16_t));
         if (rc) return rc;
-        HIP_TRY(ovfq::launch_quantize_q8k(x_dev, (int64_t)(n / 256), (int8_t*)c->act_q.p, (float*)c->act_s.p,
-                                          (int16_t*)c->act_b.p, c->stream));
-        *act = ovfq::ActQ{(const int8_t*)c->act_q.p, (const float*)c->act_s.p, (const int16_t*)c->act_b.p};
+        int16_t* b = (int16_t*)c->act_b.p;
+        uint16_t* bh = (uint16_t*)(b + n / 16);
+        HIP_TRY(ovfq::launch_quantize_q8k(x_dev, (int64_t)(n / 256), (int8_t*)c->act_q.p, (float*)c->act_s.p, b,
+                                          c->stream, bh));
+        *act = ovfq::ActQ{(const int8_t*)c->act_q.p, (const float*)c->act_s.p, b, bh};
     }
     return OVFQ_OK;
 }

@@ -30,6 +30,7 @@
 // same XCD (blockIdx % 8), so its bytes come from HBM once and from that XCD's L2 for the other activation tiles.
 #include <algorithm>
 #include <cstdlib>
+#include <cstring>
 #include <type_traits>
 #include <utility>
 
@@ -78,7 +79,8 @@ struct MArgs {
     int spr;      // K / 256
     const int8_t* q;
     const float* s;
-    const int16_t* b;  // Q8_K bsums (Q4_K: the min term's activation operand)
+    const int16_t* b;    // Q8_K bsums (Q4_K: the min term's activation operand)
+    const uint16_t* bh;  // the same bsums as fp16 (kernels instantiated with BH read these instead)
     MGroup grp;
 };
 
@@ -304,7 +306,7 @@ struct PreW {
 };
 
 // ------------------------------------------------------------------------------------------ kernel
-template <class F, int NT, bool PRE, bool GRP>
+template <class F, int NT, bool PRE, bool GRP, bool BH = false>
 __global__ __launch_bounds__(256, 2) void kquant_mfma_kernel(const MArgs a) {
     static_assert(!(PRE && GRP), "grouped launches read the GGUF operands");
     constexpr int kSub = NT / 16;
@@ -390,8 +392,9 @@ __global__ __launch_bounds__(256, 2) void kquant_mfma_kernel(const MArgs a) {
     };
     // Q4_K bsums, 32 bytes a tile row, by LDS DMA with the quants: waves w < NT / 32 move rows 32w .. 32w + 31, lane L
     // half L % 2 of row 32w + L / 2.
+    const int16_t* bsrc = BH ? reinterpret_cast<const int16_t*>(a.bh) : a.b;
     const __amdgpu_buffer_rsrc_t br =
-        make_rsrc(a.b + (kMinF16 ? a0 * spr * 16 : 0),
+        make_rsrc(bsrc + (kMinF16 ? a0 * spr * 16 : 0),
                   kMinF16 ? rsrc_bytes((uint64_t)a.m_rows * spr * 32, a0 * spr * 32) : 0u);
     const uint32_t b_src =
         kMinF16 && wave < NT / 32 ? act_row(32u * wave + ((uint32_t)lane >> 1)) * (uint32_t)spr * 32u + 16u * (lane & 1)
@@ -455,8 +458,13 @@ __global__ __launch_bounds__(256, 2) void kquant_mfma_kernel(const MArgs a) {
                         acc[1] = mfma16(aop, op[t][1], acc[1]);
                     }
                     // the row's bsums 4g .. 4g + 3 as fp16 (exact: |b| <= 2048)
-                    const s16x4 bi = *reinterpret_cast<const s16x4*>(&act_b[buf][(s * 16 + r16) * 16 + 4 * g]);
-                    const f16x4 bq = f16x4{(_Float16)bi.x, (_Float16)bi.y, (_Float16)bi.z, (_Float16)bi.w};
+                    f16x4 bq;
+                    if constexpr (BH) {
+                        bq = *reinterpret_cast<const f16x4*>(&act_b[buf][(s * 16 + r16) * 16 + 4 * g]);
+                    } else {
+                        const s16x4 bi = *reinterpret_cast<const s16x4*>(&act_b[buf][(s * 16 + r16) * 16 + 4 * g]);
+                        bq = f16x4{(_Float16)bi.x, (_Float16)bi.y, (_Float16)bi.z, (_Float16)bi.w};
+                    }
                     mn = __builtin_amdgcn_mfma_f32_16x16x16f16(bq, __builtin_bit_cast(f16x4, mb), mn, 0, 0, 0);
                 }
                 if (s > 0) {
@@ -583,6 +591,182 @@ __global__ __launch_bounds__(256, 2) void kquant_mfma_kernel(const MArgs a) {
         }
 }
 
+// ------------------------------------------------------------------------------------------ wide kernel
+// The dense kernel above with 128 activation rows per workgroup, staged through LDS in two 64-row halves: each
+// wave builds its weight operands once per super-block and uses them for 8 sub-tiles instead of 4, which halves the
+// operand build per output, while the two half slots take the LDS of one 64-row double buffer (36.5 KB), so the
+// occupancy stays that of the 64-row kernel. Per super-block: the DMA of the second half is issued, the operands are
+// built, the next super-block's weights are loaded into the registers the build has just read, the first half is
+// computed; a barrier; the DMA of the next super-block's first half is issued into the slot the first half has left,
+// and the second half is computed; a barrier. BH: the activation's bsums are fp16 (the quantiser's second bsum
+// plane), read as the min MFMA's A operand without conversion.
+template <class F, bool BH>
+__global__ __launch_bounds__(256, 4) void kquant_mfma_wide_kernel(const MArgs a) {
+    constexpr int NH = 64;          // activation rows per half
+    constexpr int kSubH = NH / 16;  // sub-tiles per half
+    constexpr int kDma = NH / 16;   // 1 KiB DMA chunks per wave per half
+    constexpr bool kMinF16 = F::kNumMfma == 3;
+    __shared__ __align__(16) uint8_t act[2][NH * 256];
+    __shared__ __align__(16) float act_s[2][NH];
+    __shared__ __align__(16) int16_t act_b[2][kMinF16 ? NH * 16 : 8];
+
+    const int wave = wave_id();
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4, r16 = lane & 15;
+    const int b = blockIdx.x;
+    const int local = b >> 3;
+    const int o_tile = (b & 7) + 8 * (local / a.n_tiles);
+    const int n_tile = local % a.n_tiles;
+    if (o_tile >= a.o_tiles) return;  // uniform over the workgroup
+    int j = 0;
+#pragma unroll
+    for (int t = 1; t < kMaxJobs; t++)
+        if (t < a.njobs && o_tile >= a.job[t].tile0) j = t;
+    const uint8_t* wptr = a.job[j].w;
+    const float* bias = a.job[j].bias;
+    float* y = a.job[j].y;
+    const int n_out = a.job[j].n_out;
+    const int o0 = (o_tile - a.job[j].tile0) * 64 + wave * 16;  // this wave's first weight row
+    const int n0 = n_tile * 2 * NH;
+    const int m_valid = min(2 * NH, a.m_rows - n0);
+    const int spr = a.spr;
+    const uint32_t K = (uint32_t)spr * kQK;
+    const uint32_t row_bytes = (uint32_t)spr * F::kBytes;
+
+    const uint64_t wbase = (uint64_t)o0 * row_bytes;
+    const uint64_t wbase4 = wbase & ~3ull;
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(wptr + wbase4, rsrc_bytes((uint64_t)n_out * row_bytes, wbase4));
+    const uint32_t woff = (uint32_t)(wbase - wbase4) + (uint32_t)r16 * row_bytes;
+    // the tile's activation rows n0 .. n0 + 127; rows past M read zeros (resource-clamped)
+    const uint64_t a0 = (uint64_t)n0;
+    const __amdgpu_buffer_rsrc_t qr = make_rsrc(a.q + a0 * K, rsrc_bytes((uint64_t)a.m_rows * K, a0 * K));
+    const __amdgpu_buffer_rsrc_t sr =
+        make_rsrc(a.s + a0 * spr, rsrc_bytes((uint64_t)a.m_rows * spr * 4, a0 * spr * 4));
+    const int16_t* bsrc = BH ? reinterpret_cast<const int16_t*>(a.bh) : a.b;
+    const __amdgpu_buffer_rsrc_t br =
+        make_rsrc(bsrc + (kMinF16 ? a0 * spr * 16 : 0),
+                  kMinF16 ? rsrc_bytes((uint64_t)a.m_rows * spr * 32, a0 * spr * 32) : 0u);
+    // bsums of half-row r (32 bytes): waves w < 2 move rows 32w .. 32w + 31, lane L half L % 2 of row 32w + L / 2
+    const uint32_t b_src =
+        kMinF16 && wave < NH / 32 ? (32u * wave + ((uint32_t)lane >> 1)) * (uint32_t)spr * 32u + 16u * (lane & 1) : 0u;
+    // DMA chunk c = wave * kDma + i covers LDS bytes [1024c, 1024c + 1024) of a half slot: lane L writes physical slot
+    // L % 16 of half-row 4c + L / 16, which holds logical slot (L % 16) ^ (row % 16).
+    uint32_t dma_src[kDma];
+#pragma unroll
+    for (int i = 0; i < kDma; i++) {
+        const uint32_t row = 4u * (uint32_t)(wave * kDma + i) + ((uint32_t)lane >> 4);
+        dma_src[i] = row * K + 16u * F::src_piece(((uint32_t)lane & 15u) ^ (row & 15u));
+    }
+    const uint32_t s_src = (uint32_t)lane * (uint32_t)spr * 4u;  // wave 0: scale of half-row `lane`
+    const uint32_t half_q = (uint32_t)NH * K, half_s = (uint32_t)NH * spr * 4u, half_b = (uint32_t)NH * spr * 32u;
+    // Reads past the last super-block of a row land in the next row or past the resource: harmless (not used).
+    auto stage = [&](int sb, int h, int buf) {
+#pragma unroll
+        for (int i = 0; i < kDma; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                qr, (__attribute__((address_space(3))) void*)&act[buf][1024 * (wave * kDma + i)], 16,
+                (int)(dma_src[i] + (uint32_t)h * half_q + (uint32_t)sb * kQK), 0, 0, 0);
+        if (wave == 0)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (__attribute__((address_space(3))) void*)&act_s[buf][0], 4,
+                                                     (int)(s_src + (uint32_t)h * half_s + (uint32_t)sb * 4u), 0, 0, 0);
+        if (kMinF16 && wave < NH / 32)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                br, (__attribute__((address_space(3))) void*)&act_b[buf][512 * wave], 16,
+                (int)(b_src + (uint32_t)h * half_b + (uint32_t)sb * 32u), 0, 0, 0);
+    };
+    uint32_t a_off[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) a_off[t] = (uint32_t)r16 * 256u + (((uint32_t)(g ^ r16)) ^ (4u * t)) * 16u;
+
+    float out[2 * kSubH][4];
+#pragma unroll
+    for (int s = 0; s < 2 * kSubH; s++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) out[s][i] = 0.0f;
+
+    // MFMAs and fp32 tails of one half (sub-tiles 4H .. 4H + 3 of the tile): each sub-tile's MFMAs, then its tail.
+    auto mma_tail = [&](auto half, int buf, const i32x4 (&op)[4][F::kNumMfma], float d, float dmin, u32x2 mb) {
+        constexpr int H = decltype(half)::value;
+        const uint8_t* tile = act[buf];
+#pragma unroll
+        for (int s = 0; s < kSubH; s++) {
+            i32x4 acc[F::kNumMfma];
+#pragma unroll
+            for (int k = 0; k < F::kNumMfma; k++) acc[k] = i32x4{0, 0, 0, 0};
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const u32x4 av = *reinterpret_cast<const u32x4*>(tile + s * 4096 + a_off[t]);
+                const i32x4 aop = i32x4{(int)av.x, (int)av.y, (int)av.z, (int)av.w};
+                acc[0] = mfma16(aop, op[t][0], acc[0]);
+                acc[1] = mfma16(aop, op[t][1], acc[1]);
+            }
+            const f32x4 q8s = *reinterpret_cast<const f32x4*>(&act_s[buf][s * 16 + 4 * g]);
+            if constexpr (kMinF16) {
+                f16x4 bq;
+                if constexpr (BH) {
+                    bq = *reinterpret_cast<const f16x4*>(&act_b[buf][(s * 16 + r16) * 16 + 4 * g]);
+                } else {
+                    const s16x4 bi = *reinterpret_cast<const s16x4*>(&act_b[buf][(s * 16 + r16) * 16 + 4 * g]);
+                    bq = f16x4{(_Float16)bi.x, (_Float16)bi.y, (_Float16)bi.z, (_Float16)bi.w};
+                }
+                const f32x4 mn =
+                    __builtin_amdgcn_mfma_f32_16x16x16f16(bq, __builtin_bit_cast(f16x4, mb), f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int main_acc = acc[0][i] + (acc[1][i] << 3);
+                    // q8Scale * (d * mainAcc - dmin * minAcc)   (RT/Q4KDotKernel.cs:944)
+                    out[H * kSubH + s][i] += q8s[i] * (d * (float)main_acc - dmin * mn[i]);
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; i++) out[H * kSubH + s][i] += F::tail(acc, i, d, dmin, q8s[i]);
+            }
+            // the tail stays here: left to itself the compiler sinks the first half's tails past the barrier, with
+            // every sub-tile's accumulators live across it
+            float(&o4)[4] = out[H * kSubH + s];
+            asm volatile("" : "+v"(o4[0]), "+v"(o4[1]), "+v"(o4[2]), "+v"(o4[3]));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    typename F::W w = F::load(wr, woff, g);
+    stage(0, 0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int sb = 0; sb < spr; sb++) {
+        stage(sb, 1, 1);
+        i32x4 op[4][F::kNumMfma];
+        F::template operands<0>(w, g, op[0]);
+        F::template operands<1>(w, g, op[1]);
+        F::template operands<2>(w, g, op[2]);
+        F::template operands<3>(w, g, op[3]);
+        const float d = F::d_of(w), dmin = F::dmin_of(w);
+        const u32x2 mb = F::min_operand(w, g);
+        // the next super-block's weights into the registers just read (past the row: unused)
+        __builtin_amdgcn_sched_barrier(0);
+        w = F::load(wr, woff + (uint32_t)(sb + 1) * F::kBytes, g);
+        mma_tail(std::integral_constant<int, 0>{}, 0, op, d, dmin, mb);
+        __builtin_amdgcn_s_waitcnt(0);  // the second half and the weights have landed; every wave is past slot 0
+        __syncthreads();
+        if (sb + 1 < spr) stage(sb + 1, 0, 0);
+        mma_tail(std::integral_constant<int, 1>{}, 1, op, d, dmin, mb);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+    }
+
+    // y[n][o] = biasO + sum   (RT/Q4KDotKernel.cs:951, RT/Q6KDotKernel.cs:507)
+    const int o = o0 + r16;
+    if (o >= n_out) return;
+    const float bias_o = bias ? bias[o] : 0.0f;
+#pragma unroll
+    for (int s = 0; s < 2 * kSubH; s++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int n = s * 16 + 4 * g + i;
+            if (n < m_valid) y[(size_t)(n0 + n) * n_out + o] = bias_o + out[s][i];
+        }
+}
+
 template <class F, int NT>
 static hipError_t launch_mfma(MArgs& ma, bool pre, hipStream_t st) {
     ma.n_tiles = (ma.m_rows + NT - 1) / NT;
@@ -590,6 +774,11 @@ static hipError_t launch_mfma(MArgs& ma, bool pre, hipStream_t st) {
     if constexpr (F::kNumMfma == 2) {  // only Q6_K weights carry the MFMA-ready copy
         if (pre) {
             hipLaunchKernelGGL((kquant_mfma_kernel<F, NT, true, false>), dim3(grid), dim3(256), 0, st, ma);
+            return hipGetLastError();
+        }
+    } else {
+        if (ma.bh) {  // Q4_K with the quantiser's fp16 bsums
+            hipLaunchKernelGGL((kquant_mfma_kernel<F, NT, false, false, true>), dim3(grid), dim3(256), 0, st, ma);
             return hipGetLastError();
         }
     }
@@ -632,13 +821,22 @@ hipError_t launch_mfma_grouped(int type, const GroupLaunch& L, const int* tiles,
 
 // 128 activation rows per workgroup halve the operand-build cost per output but allow only two workgroups per CU;
 // 64 rows fit four, which hides more latency. Measured on MI355X (Llama-3-8B layer shapes): 64 is faster up to
-// M = 512, 128 from M = 2048.
-static int mfma_tile_rows(int rows) {
+// M = 512, 128 from M = 2048. The wide kernel (128 rows staged in 64-row halves, the LDS of the 64-row kernel, so
+// four workgroups per CU) takes Q4_K launches whose grid has at least 448 workgroups; below that the 64-row kernel's
+// twice-larger grid fills the CUs better. Measured (graph replay with the quantise launch, us, 64-row / 128-row /
+// wide): gate/up 2x14336x4096 at 256 rows 98.7 / 110 / 93.1 and at 512 rows 181 / 184 / 161; q/k/v at 512 rows
+// (384 wide workgroups) 49.2 / 55.7 / 55.4 and at 1024 rows 84.9 / 86.6 / 77.7; o 4096x4096 at 2048 rows 115 / 111 /
+// 99.6. For Q6_K the wide kernel is slower (its operand build is not what bounds the launch: 4096x14336 at 1024
+// rows 250 / 181 / 228). OVFQ_MFMA_TILE_ROWS=64 / 128 / wide forces one.
+constexpr int kWideTile = 1;
+static int mfma_tile_rows(int type, int rows, int o_tiles) {
     static const int forced = [] {
         const char* e = getenv("OVFQ_MFMA_TILE_ROWS");
+        if (e && !strcmp(e, "wide")) return kWideTile;
         return e && *e ? atoi(e) : 0;
     }();
-    if (forced == 64 || forced == 128) return forced;
+    if (forced == 64 || forced == 128 || forced == kWideTile) return forced;
+    if (type == 12 && (long)o_tiles * ((rows + 127) / 128) >= 448) return kWideTile;
     return rows >= 1024 ? 128 : 64;
 }
 
@@ -681,8 +879,20 @@ hipError_t launch_project_mfma(int type, const ProjJob* jobs, int njobs, int in,
     ma.q = act.q;
     ma.s = act.s;
     ma.b = act.b;
+    ma.bh = type == 12 ? act.bh : nullptr;
     if (type == 12 && !ma.b) return hipErrorInvalidValue;  // the Q4_K kernel reads the bsums
-    const int nt = mfma_tile_rows(rows);
+    const int nt = mfma_tile_rows(type, rows, tiles);
+    if (nt == kWideTile && !pre) {
+        ma.n_tiles = (rows + 127) / 128;
+        const int grid = (ma.o_tiles + 7) / 8 * 8 * ma.n_tiles;
+        if (type == 12 && ma.bh)
+            hipLaunchKernelGGL((kquant_mfma_wide_kernel<Q4KMfma, true>), dim3(grid), dim3(256), 0, st, ma);
+        else if (type == 12)
+            hipLaunchKernelGGL((kquant_mfma_wide_kernel<Q4KMfma, false>), dim3(grid), dim3(256), 0, st, ma);
+        else
+            hipLaunchKernelGGL((kquant_mfma_wide_kernel<Q6KMfma, false>), dim3(grid), dim3(256), 0, st, ma);
+        return hipGetLastError();
+    }
     if (type == 12)
         return nt == 128 ? launch_mfma<Q4KMfma, 128>(ma, pre, st) : launch_mfma<Q4KMfma, 64>(ma, pre, st);
     return nt == 128 ? launch_mfma<Q6KMfma, 128>(ma, pre, st) : launch_mfma<Q6KMfma, 64>(ma, pre, st);

@@ -24,9 +24,12 @@ struct ActQ {
     const int8_t* q;
     const float* s;
     const int16_t* b;
+    const uint16_t* bh = nullptr;  // the bsums again as fp16 (the quantiser's optional second plane), or NULL
 };
 
-hipError_t launch_quantize_q8k(const float* x, int64_t n_blocks, int8_t* q, float* s, int16_t* b, hipStream_t st);
+// bh != NULL: the bsums are also written as fp16 (exact: |bsum| <= 16 * 127), the tiled Q4_K kernels' min-term operand.
+hipError_t launch_quantize_q8k(const float* x, int64_t n_blocks, int8_t* q, float* s, int16_t* b, hipStream_t st,
+                               uint16_t* bh = nullptr);
 hipError_t launch_quantize_q8_0(const float* x, int64_t n_blocks, int8_t* q, float* s, hipStream_t st);
 
 // type: 12 (Q4_K) or 14 (Q6_K). `in` % 256 == 0. rows = activation rows (M).

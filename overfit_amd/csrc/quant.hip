@@ -17,7 +17,7 @@ namespace ovfq {
 // DPP row max (a wave per block spent most of its time in the 6 cross-lane exchanges of its max).
 __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float* __restrict__ x, int64_t n_blocks,
                                                             int8_t* __restrict__ q, float* __restrict__ s,
-                                                            int16_t* __restrict__ bs) {
+                                                            int16_t* __restrict__ bs, uint16_t* __restrict__ bh) {
     // wave_id() is a readfirstlane value, so the buffer resource below is provably wave-uniform (SGPRs).
     const int64_t blk0 = ((int64_t)blockIdx.x * 4 + wave_id()) * 4;
     if (blk0 >= n_blocks) return;
@@ -39,6 +39,7 @@ __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float* __restri
     if (blk < n_blocks) {
         *reinterpret_cast<u32x4*>(q + blk * kQK + l16 * 16) = r.packed;
         bs[blk * 16 + l16] = (int16_t)r.group_sum;
+        if (bh) bh[blk * 16 + l16] = __builtin_bit_cast(uint16_t, (_Float16)r.group_sum);
         if (l16 == 0) s[blk] = r.scale;
     }
 }
@@ -340,10 +341,11 @@ hipError_t launch_q5_to_q8_0(const void* gguf, bool q5k, int64_t n_blocks, int8_
     return hipGetLastError();
 }
 
-hipError_t launch_quantize_q8k(const float* x, int64_t n_blocks, int8_t* q, float* s, int16_t* b, hipStream_t st) {
+hipError_t launch_quantize_q8k(const float* x, int64_t n_blocks, int8_t* q, float* s, int16_t* b, hipStream_t st,
+                               uint16_t* bh) {
     if (n_blocks <= 0) return hipSuccess;
     const int64_t grid = (n_blocks + 15) / 16;
-    hipLaunchKernelGGL(quantize_q8k_kernel, dim3((unsigned)grid), dim3(256), 0, st, x, n_blocks, q, s, b);
+    hipLaunchKernelGGL(quantize_q8k_kernel, dim3((unsigned)grid), dim3(256), 0, st, x, n_blocks, q, s, b, bh);
     return hipGetLastError();
 }
 

@@ -243,6 +243,38 @@ def test_kquant_prefill_128_row_tiles(orc, ctx, fmt):
         assert_bit_exact(yd.cpu().numpy().reshape(rows, n), ref, f"{fmt} 1100 rows prepared={prepared}")
 
 
+@pytest.mark.parametrize("rows,k,shapes", [(200, 512, [14300]), (129, 256, [14336]), (300, 256, [9000, 9000])])
+def test_kquant_prefill_wide_tiles(orc, ctx, rows, k, shapes):
+    """Q4_K launches whose 128-row grid reaches 448 workgroups take the wide tiled kernel (128 activation rows per
+    workgroup in two 64-row LDS halves): ragged last activation tiles (200, 129 and 300 rows), a partial last 64-row
+    weight tile, a fused pair, a bias; from the fp32 input (the quantiser's fp16 bsums) and from a prequantised
+    activation whose bsums are not the group sums (the caller's int16 bsums read as the reference's Dot does)."""
+    case("prefill wide tiles", rows, k, shapes)
+    rng = np.random.default_rng(rows * 13 + k + sum(shapes))
+    blocks = [_kq_blocks(rng, "q4k", n, k) for n in shapes]
+    ws = [ov.Q4KWeight(b, k, n) for b, n in zip(blocks, shapes)]
+    x = normal(rng, (rows, k))
+    bias = normal(rng, shapes[-1])
+    biases = [None] * (len(shapes) - 1) + [bias]
+    refs = [orc.q4k_project_batched(x, rows, b, k, n, bb) for b, n, bb in zip(blocks, shapes, biases)]
+    ys = [torch.empty(rows * n, device=DEV) for n in shapes]
+    ctx.project_multi_dev(ws, t(x), ys, [None if bb is None else t(bb) for bb in biases], rows=rows)
+    torch.cuda.synchronize()
+    for i, (y, ref) in enumerate(zip(ys, refs)):
+        assert_bit_exact(y.cpu().numpy().reshape(rows, -1), ref, f"wide tiles rows={rows} job {i}")
+    q, s, b = orc.quantize_q8k(x)
+    b = (b.astype(np.int32) + rng.integers(-9, 10, b.shape)).clip(-2048, 2048).astype(np.int16)
+    L = orc.lib()
+    ref = np.zeros((rows, shapes[0]), np.float32)
+    rc = L.orc_q4k_project_batched_prequantized(rows, orc.P(np.ascontiguousarray(blocks[0], np.uint8)), k,
+                                                 shapes[0], None, orc.P(ref), orc.P(q), orc.P(s), orc.P(b))
+    assert rc == 0
+    y = torch.empty(rows * shapes[0], device=DEV)
+    ctx.project_prequantized_dev(ws[0], t(q), t(s), t(b), y, rows=rows)
+    torch.cuda.synchronize()
+    assert_bit_exact(y.cpu().numpy().reshape(rows, -1), ref, f"wide tiles prequantized shifted bsums rows={rows}")
+
+
 @pytest.mark.parametrize("fmt", ["q4k", "q6k"])
 @pytest.mark.parametrize("rows,k,n", [(32, 256, 64), (70, 512, 200), (128, 4096, 130), (200, 2304, 64)])
 def test_prepared_mfma_prefill_bit_exact(orc, ctx, batched, fmt, rows, k, n):
