@@ -275,6 +275,42 @@ def test_kquant_prefill_wide_tiles(orc, ctx, rows, k, shapes):
     assert_bit_exact(y.cpu().numpy().reshape(rows, -1), ref, f"wide tiles prequantized shifted bsums rows={rows}")
 
 
+@pytest.mark.parametrize("fmt,rows,k,shapes", [("q6k", 200, 768, [260]), ("q6k", 130, 3328, [250]),
+                                               ("q4k", 256, 768, [4096, 1024, 1000]), ("q4k", 500, 1280, [4000])])
+def test_kquant_prefill_pair_kernel(orc, ctx, fmt, rows, k, shapes):
+    """Launches whose 64-row grid leaves each CU one or two tiles take the pair kernel (two waves per 16 weight rows
+    on alternate super-blocks, the odd wave's block values added by the even one in ascending order): an odd number of
+    super-blocks (3, 5: the last has no partner), partial weight and activation tiles, a multi-job launch, a bias; from
+    the fp32 input and, for Q4_K, a prequantised activation whose bsums are not the group sums."""
+    case("prefill pair kernel", fmt, rows, k, shapes)
+    rng = np.random.default_rng(rows * 17 + k + sum(shapes))
+    blocks = [_kq_blocks(rng, fmt, n, k) for n in shapes]
+    Wt = ov.Q4KWeight if fmt == "q4k" else ov.Q6KWeight
+    ws = [Wt(b, k, n) for b, n in zip(blocks, shapes)]
+    x = normal(rng, (rows, k))
+    bias = normal(rng, shapes[-1])
+    biases = [None] * (len(shapes) - 1) + [bias]
+    proj = orc.q4k_project_batched if fmt == "q4k" else orc.q6k_project_batched
+    refs = [proj(x, rows, b, k, n, bb) for b, n, bb in zip(blocks, shapes, biases)]
+    ys = [torch.empty(rows * n, device=DEV) for n in shapes]
+    ctx.project_multi_dev(ws, t(x), ys, [None if bb is None else t(bb) for bb in biases], rows=rows)
+    torch.cuda.synchronize()
+    for i, (y, ref) in enumerate(zip(ys, refs)):
+        assert_bit_exact(y.cpu().numpy().reshape(rows, -1), ref, f"pair kernel {fmt} rows={rows} job {i}")
+    if fmt != "q4k":
+        return
+    q, s, b = orc.quantize_q8k(x)
+    b = (b.astype(np.int32) + rng.integers(-9, 10, b.shape)).clip(-2048, 2048).astype(np.int16)
+    ref = np.zeros((rows, shapes[0]), np.float32)
+    rc = orc.lib().orc_q4k_project_batched_prequantized(rows, orc.P(np.ascontiguousarray(blocks[0], np.uint8)), k,
+                                                         shapes[0], None, orc.P(ref), orc.P(q), orc.P(s), orc.P(b))
+    assert rc == 0
+    y = torch.empty(rows * shapes[0], device=DEV)
+    ctx.project_prequantized_dev(ws[0], t(q), t(s), t(b), y, rows=rows)
+    torch.cuda.synchronize()
+    assert_bit_exact(y.cpu().numpy().reshape(rows, -1), ref, f"pair kernel prequantized shifted bsums rows={rows}")
+
+
 @pytest.mark.parametrize("fmt", ["q4k", "q6k"])
 @pytest.mark.parametrize("rows,k,n", [(32, 256, 64), (70, 512, 200), (128, 4096, 130), (200, 2304, 64)])
 def test_prepared_mfma_prefill_bit_exact(orc, ctx, batched, fmt, rows, k, n):
