@@ -785,9 +785,17 @@ __global__ __launch_bounds__(256, 4) void kquant_mfma_wide_kernel(const MArgs a)
     constexpr int kSubH = NH / 16;  // sub-tiles per half
     constexpr int kDma = NH / 16;   // 1 KiB DMA chunks per wave per half
     constexpr bool kMinF16 = F::kNumMfma == 3;
-    __shared__ __align__(16) uint8_t act[2][NH * 256];
-    __shared__ __align__(16) float act_s[2][NH];
-    __shared__ __align__(16) int16_t act_b[2][kMinF16 ? NH * 16 : 8];
+    // Each slot is its own LDS object: the compiler gives every LDS object an alias scope, so its wait counts can
+    // tell that the DMA into one slot does not write the other one, being read. With one array of two slots it
+    // waited for every DMA in flight before each LDS read, so each half's DMA had landed before the other half was
+    // computed (gate/up at M = 512 157 -> 153 us, at 1024 rows 302 -> 288 us). The 64-row and pair kernels measured
+    // slower with the same change (their Q6_K launches 4-7 %), and keep one array.
+    __shared__ __align__(16) uint8_t act0[NH * 256], act1[NH * 256];
+    __shared__ __align__(16) float act_s0[NH], act_s1[NH];
+    __shared__ __align__(16) int16_t act_b0[kMinF16 ? NH * 16 : 8], act_b1[kMinF16 ? NH * 16 : 8];
+    uint8_t* const act[2] = {act0, act1};
+    float* const act_s[2] = {act_s0, act_s1};
+    int16_t* const act_b[2] = {act_b0, act_b1};
 
     const int wave = wave_id();
     const int lane = threadIdx.x & 63;
