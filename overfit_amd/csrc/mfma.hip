@@ -770,6 +770,224 @@ __global__ __launch_bounds__(512) void kquant_mfma_pair_kernel(const MArgs a) {
         }
 }
 
+// ------------------------------------------------------------------------------------------ pair-wide kernel
+// The pair kernel over 128 activation rows: an 8-wave workgroup owns 64 weight rows x 128 activation rows; waves w
+// and w + 4 share weight rows 16(w & 3) .. + 15 and take the even / odd super-blocks, and each covers all 128 rows
+// in two 64-row halves (as the wide kernel), so every operand build serves 128 rows while a small grid (long inputs,
+// few output rows) still keeps two waves per SIMD. Per super-block pair: the operands are built; a wait and a barrier
+// publish the first halves; the second halves' DMA and the next pair's weights are issued; the first half is
+// computed (the odd waves write their block values to LDS); a barrier; the next pair's first halves are DMA'd, the
+// even waves add the odd values and compute the second half; a barrier; the even waves add the odd second-half
+// values. Each (row, output) is summed in ascending super-block order. The code is specialised per parity so that
+// every slot a wave reads or DMAs is a fixed LDS object (see the wide kernel).
+template <class F, bool BH>
+__global__ __launch_bounds__(512) void kquant_mfma_pairwide_kernel(const MArgs a) {
+    constexpr int NH = 64;
+    constexpr int kSubH = NH / 16;
+    constexpr bool kMinF16 = F::kNumMfma == 3;
+    constexpr int kB = kMinF16 ? NH * 16 : 8;
+    // [parity][half] slots
+    __shared__ __align__(16) uint8_t act00[NH * 256], act01[NH * 256], act10[NH * 256], act11[NH * 256];
+    __shared__ __align__(16) float act_s00[NH], act_s01[NH], act_s10[NH], act_s11[NH];
+    __shared__ __align__(16) int16_t act_b00[kB], act_b01[kB], act_b10[kB], act_b11[kB];
+    // the odd waves' block values of the first / second half, [weight group][sub-tile][lane]
+    __shared__ __align__(16) f32x4 xch0[4][kSubH * 64], xch1[4][kSubH * 64];
+
+    const int wave = wave_id();
+    const int wg = wave & 3, par = wave >> 2;
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4, r16 = lane & 15;
+    const int b = blockIdx.x;
+    const int local = b >> 3;
+    const int o_tile = (b & 7) + 8 * (local / a.n_tiles);
+    const int n_tile = local % a.n_tiles;
+    if (o_tile >= a.o_tiles) return;  // uniform over the workgroup
+    int j = 0;
+#pragma unroll
+    for (int t = 1; t < kMaxJobs; t++)
+        if (t < a.njobs && o_tile >= a.job[t].tile0) j = t;
+    const uint8_t* wptr = a.job[j].w;
+    const float* bias = a.job[j].bias;
+    float* y = a.job[j].y;
+    const int n_out = a.job[j].n_out;
+    const int o0 = (o_tile - a.job[j].tile0) * 64 + wg * 16;  // this wave's first weight row
+    const int n0 = n_tile * 2 * NH;
+    const int m_valid = min(2 * NH, a.m_rows - n0);
+    const int spr = a.spr;
+    const uint32_t K = (uint32_t)spr * kQK;
+    const uint32_t row_bytes = (uint32_t)spr * F::kBytes;
+
+    const uint64_t wbase = (uint64_t)o0 * row_bytes;
+    const uint64_t wbase4 = wbase & ~3ull;
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(wptr + wbase4, rsrc_bytes((uint64_t)n_out * row_bytes, wbase4));
+    const uint32_t woff = (uint32_t)(wbase - wbase4) + (uint32_t)r16 * row_bytes;
+    const uint64_t a0 = (uint64_t)n0;
+    const __amdgpu_buffer_rsrc_t qr = make_rsrc(a.q + a0 * K, rsrc_bytes((uint64_t)a.m_rows * K, a0 * K));
+    const __amdgpu_buffer_rsrc_t sr =
+        make_rsrc(a.s + a0 * spr, rsrc_bytes((uint64_t)a.m_rows * spr * 4, a0 * spr * 4));
+    const int16_t* bsrc = BH ? reinterpret_cast<const int16_t*>(a.bh) : a.b;
+    const __amdgpu_buffer_rsrc_t br =
+        make_rsrc(bsrc + (kMinF16 ? a0 * spr * 16 : 0),
+                  kMinF16 ? rsrc_bytes((uint64_t)a.m_rows * spr * 32, a0 * spr * 32) : 0u);
+    // A half slot of the wave's parity: wave (wg, par) moves its 1 KiB chunks 4wg .. 4wg + 3 (lane L: physical 16-byte
+    // slot L % 16 of half-row 4c + L / 16, holding logical slot (L % 16) ^ (row % 16)), the scales (wg 0: lane L
+    // half-row L) and, for Q4_K, half the bsums (wg < 2: lane L half L % 2 of half-row 32wg + L / 2).
+    uint32_t dma_src[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t row = 4u * (uint32_t)(4 * wg + i) + ((uint32_t)lane >> 4);
+        dma_src[i] = row * K + 16u * F::src_piece(((uint32_t)lane & 15u) ^ (row & 15u));
+    }
+    const uint32_t s_src = (uint32_t)lane * (uint32_t)spr * 4u;
+    const uint32_t b_src = kMinF16 && wg < 2 ? (32u * wg + ((uint32_t)lane >> 1)) * (uint32_t)spr * 32u + 16u * (lane & 1)
+                                             : 0u;
+    const uint32_t half_q = (uint32_t)NH * K, half_s = (uint32_t)NH * spr * 4u, half_b = (uint32_t)NH * spr * 32u;
+    uint32_t a_off[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) a_off[t] = (uint32_t)r16 * 256u + (((uint32_t)(g ^ r16)) ^ (4u * t)) * 16u;
+    const int npair = (spr + 1) / 2;
+
+    float out[2 * kSubH][4];
+#pragma unroll
+    for (int s = 0; s < 2 * kSubH; s++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) out[s][i] = 0.0f;
+
+    auto body = [&](auto pc) {
+        constexpr int P = decltype(pc)::value;  // this wave's parity
+        uint8_t* const act[2] = {P ? act10 : act00, P ? act11 : act01};
+        float* const act_s[2] = {P ? act_s10 : act_s00, P ? act_s11 : act_s01};
+        int16_t* const act_b[2] = {P ? act_b10 : act_b00, P ? act_b11 : act_b01};
+        // half h of super-block pair p (super-block 2p + P; none past the row)
+        auto stage = [&](int p, auto hc) {
+            constexpr int H = decltype(hc)::value;
+            const int sb = 2 * p + P;
+            if (sb >= spr) return;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    qr, (__attribute__((address_space(3))) void*)&act[H][1024 * (4 * wg + i)], 16,
+                    (int)(dma_src[i] + (uint32_t)H * half_q + (uint32_t)sb * kQK), 0, 0, 0);
+            if (wg == 0)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (__attribute__((address_space(3))) void*)&act_s[H][0], 4,
+                                                         (int)(s_src + (uint32_t)H * half_s + (uint32_t)sb * 4u), 0, 0,
+                                                         0);
+            if (kMinF16 && wg < 2)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    br, (__attribute__((address_space(3))) void*)&act_b[H][512 * wg], 16,
+                    (int)(b_src + (uint32_t)H * half_b + (uint32_t)sb * 32u), 0, 0, 0);
+        };
+        // half H of this wave's super-block: the even waves add their block values, the odd ones hand them over
+        auto half = [&](auto hc, const i32x4 (&op)[4][F::kNumMfma], float d, float dmin, u32x2 mb) {
+            constexpr int H = decltype(hc)::value;
+            const uint8_t* tile = act[H];
+            f32x4(&xch)[4][kSubH * 64] = H ? xch1 : xch0;
+#pragma unroll
+            for (int s = 0; s < kSubH; s++) {
+                i32x4 acc[F::kNumMfma];
+#pragma unroll
+                for (int k = 0; k < F::kNumMfma; k++) acc[k] = i32x4{0, 0, 0, 0};
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    const u32x4 av = *reinterpret_cast<const u32x4*>(tile + s * 4096 + a_off[t]);
+                    const i32x4 aop = i32x4{(int)av.x, (int)av.y, (int)av.z, (int)av.w};
+                    acc[0] = mfma16(aop, op[t][0], acc[0]);
+                    acc[1] = mfma16(aop, op[t][1], acc[1]);
+                }
+                const f32x4 q8s = *reinterpret_cast<const f32x4*>(&act_s[H][s * 16 + 4 * g]);
+                f32x4 v;
+                if constexpr (kMinF16) {
+                    f16x4 bq;
+                    if constexpr (BH) {
+                        bq = *reinterpret_cast<const f16x4*>(&act_b[H][(s * 16 + r16) * 16 + 4 * g]);
+                    } else {
+                        const s16x4 bi = *reinterpret_cast<const s16x4*>(&act_b[H][(s * 16 + r16) * 16 + 4 * g]);
+                        bq = f16x4{(_Float16)bi.x, (_Float16)bi.y, (_Float16)bi.z, (_Float16)bi.w};
+                    }
+                    const f32x4 mn = __builtin_amdgcn_mfma_f32_16x16x16f16(bq, __builtin_bit_cast(f16x4, mb),
+                                                                          f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int main_acc = acc[0][i] + (acc[1][i] << 3);
+                        // q8Scale * (d * mainAcc - dmin * minAcc)   (RT/Q4KDotKernel.cs:944)
+                        v[i] = q8s[i] * (d * (float)main_acc - dmin * mn[i]);
+                    }
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; i++) v[i] = F::tail(acc, i, d, dmin, q8s[i]);
+                }
+                if constexpr (P == 0) {
+#pragma unroll
+                    for (int i = 0; i < 4; i++) out[H * kSubH + s][i] += v[i];
+                    // the tail stays here (not sunk past the barrier with the accumulators live)
+                    float(&o4)[4] = out[H * kSubH + s];
+                    asm volatile("" : "+v"(o4[0]), "+v"(o4[1]), "+v"(o4[2]), "+v"(o4[3]));
+                } else {
+                    xch[wg][s * 64 + lane] = v;
+                }
+            }
+        };
+        // the even waves: add the odd waves' values of half H (pair p has an odd super-block)
+        auto take = [&](auto hc, int p) {
+            constexpr int H = decltype(hc)::value;
+            if constexpr (P == 0) {
+                if (2 * p + 1 < spr) {
+                    f32x4(&xch)[4][kSubH * 64] = H ? xch1 : xch0;
+#pragma unroll
+                    for (int s = 0; s < kSubH; s++) {
+                        const f32x4 v = xch[wg][s * 64 + lane];
+#pragma unroll
+                        for (int i = 0; i < 4; i++) out[H * kSubH + s][i] += v[i];
+                    }
+                }
+            }
+        };
+        using H0 = std::integral_constant<int, 0>;
+        using H1 = std::integral_constant<int, 1>;
+        typename F::W w = F::load(wr, woff + (uint32_t)P * F::kBytes, g);
+        stage(0, H0{});
+        for (int p = 0; p < npair; p++) {
+            const bool live = 2 * p + P < spr;  // wave-uniform
+            i32x4 op[4][F::kNumMfma];
+            F::template operands<0>(w, g, op[0]);
+            F::template operands<1>(w, g, op[1]);
+            F::template operands<2>(w, g, op[2]);
+            F::template operands<3>(w, g, op[3]);
+            const float d = F::d_of(w), dmin = F::dmin_of(w);
+            const u32x2 mb = F::min_operand(w, g);
+            __builtin_amdgcn_s_waitcnt(0);  // this wave's share of the first halves has landed
+            __syncthreads();
+            stage(p, H1{});
+            __builtin_amdgcn_sched_barrier(0);
+            w = F::load(wr, woff + (uint32_t)(2 * p + 2 + P) * F::kBytes, g);  // past the row: unused
+            if (live) half(H0{}, op, d, dmin, mb);
+            __builtin_amdgcn_s_waitcnt(0);  // the second halves and the next weights have landed
+            __syncthreads();              // first halves read; the odd first-half values visible
+            if (p + 1 < npair) stage(p + 1, H0{});
+            take(H0{}, p);
+            if (live) half(H1{}, op, d, dmin, mb);
+            __syncthreads();  // second halves read; the odd second-half values visible
+            take(H1{}, p);
+        }
+    };
+    if (par == 0)
+        body(std::integral_constant<int, 0>{});
+    else
+        body(std::integral_constant<int, 1>{});
+
+    // y[n][o] = biasO + sum   (RT/Q4KDotKernel.cs:951, RT/Q6KDotKernel.cs:507): the even waves hold the sums
+    const int o = o0 + r16;
+    if (par != 0 || o >= n_out) return;
+    const float bias_o = bias ? bias[o] : 0.0f;
+#pragma unroll
+    for (int s = 0; s < 2 * kSubH; s++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int n = s * 16 + 4 * g + i;
+            if (n < m_valid) y[(size_t)(n0 + n) * n_out + o] = bias_o + out[s][i];
+        }
+}
+
 // ------------------------------------------------------------------------------------------ wide kernel
 // The dense kernel above with 128 activation rows per workgroup, staged through LDS in two 64-row halves: each
 // wave builds its weight operands once per super-block and uses them for 8 sub-tiles instead of 4, which halves the
@@ -1017,14 +1235,17 @@ hipError_t launch_mfma_grouped(int type, const GroupLaunch& L, const int* tiles,
 // rows 250 / 181 / 228). OVFQ_MFMA_TILE_ROWS=64 / 128 / wide forces one.
 constexpr int kWideTile = 1;
 constexpr int kPairTile = 2;
+constexpr int kPairWideTile = 3;
 static int mfma_tile_rows(int type, int rows, int o_tiles) {
     static const int forced = [] {
         const char* e = getenv("OVFQ_MFMA_TILE_ROWS");
         if (e && !strcmp(e, "wide")) return kWideTile;
         if (e && !strcmp(e, "pair")) return kPairTile;
+        if (e && !strcmp(e, "pairwide")) return kPairWideTile;
         return e && *e ? atoi(e) : 0;
     }();
-    if (forced == 64 || forced == 128 || forced == kWideTile || forced == kPairTile) return forced;
+    if (forced == 64 || forced == 128 || forced == kWideTile || forced == kPairTile || forced == kPairWideTile)
+        return forced;
     if (type == 12 && (long)o_tiles * ((rows + 127) / 128) >= 448) return kWideTile;
     // The pair kernel (two waves per 16 weight rows on alternate super-blocks) where the 64-row grid leaves each CU
     // one or two tiles: Q6_K 4096x14336 at 128 / 256 rows (128 / 256 workgroups) 116 / 118 -> 92 / 93 us, at 512
@@ -1032,6 +1253,11 @@ static int mfma_tile_rows(int type, int rows, int o_tiles) {
     // o 4096x4096 at 512 rows (512) 38.7 -> 37.0, but o at 256 rows (256) 27.4 -> 28.1 and q/k/v at 512 rows (768)
     // 49.4 -> 55.3.
     const long grid64 = (long)o_tiles * ((rows + 63) / 64);
+    // The pair-wide kernel (one 8-wave workgroup per CU: 64 weight rows x 128 activation rows, each wave's operands
+    // built once per 128 rows) for Q6_K where its grid gives about one workgroup per CU: 4096x14336 at 512 rows (256
+    // workgroups) 130.7 -> 112.5 us; at 256 rows (128) 98 -> 105 and at 1024 rows (512, two rounds) 179 -> 210.
+    const long grid128 = (long)o_tiles * ((rows + 127) / 128);
+    if (type == 14 && grid128 >= 192 && grid128 <= 256) return kPairWideTile;
     if (rows < 1024 && (type == 14 ? grid64 <= 256 : grid64 >= 384 && grid64 <= 512)) return kPairTile;
     return rows >= 1024 ? 128 : 64;
 }
@@ -1078,6 +1304,17 @@ hipError_t launch_project_mfma(int type, const ProjJob* jobs, int njobs, int in,
     ma.bh = type == 12 ? act.bh : nullptr;
     if (type == 12 && !ma.b) return hipErrorInvalidValue;  // the Q4_K kernel reads the bsums
     const int nt = mfma_tile_rows(type, rows, tiles);
+    if (nt == kPairWideTile && !pre) {
+        ma.n_tiles = (rows + 127) / 128;
+        const int grid = (ma.o_tiles + 7) / 8 * 8 * ma.n_tiles;
+        if (type == 12 && ma.bh)
+            hipLaunchKernelGGL((kquant_mfma_pairwide_kernel<Q4KMfma, true>), dim3(grid), dim3(512), 0, st, ma);
+        else if (type == 12)
+            hipLaunchKernelGGL((kquant_mfma_pairwide_kernel<Q4KMfma, false>), dim3(grid), dim3(512), 0, st, ma);
+        else
+            hipLaunchKernelGGL((kquant_mfma_pairwide_kernel<Q6KMfma, false>), dim3(grid), dim3(512), 0, st, ma);
+        return hipGetLastError();
+    }
     if (nt == kPairTile && !pre) {
         ma.n_tiles = (rows + 63) / 64;
         const int grid = (ma.o_tiles + 7) / 8 * 8 * ma.n_tiles;

@@ -311,6 +311,27 @@ def test_kquant_prefill_pair_kernel(orc, ctx, fmt, rows, k, shapes):
     assert_bit_exact(y.cpu().numpy().reshape(rows, -1), ref, f"pair kernel prequantized shifted bsums rows={rows}")
 
 
+@pytest.mark.parametrize("rows,k,shapes", [(512, 768, [4096]), (400, 1280, [3000, 1000]), (420, 512, [4000])])
+def test_kquant_prefill_pairwide_kernel(orc, ctx, rows, k, shapes):
+    """Q6_K launches whose 128-row grid gives about one workgroup per CU take the pair-wide kernel (8-wave workgroups
+    on 64 weight rows x 128 activation rows, alternate super-blocks per wave pair, each wave over both 64-row
+    halves, the odd values handed over per half): an odd number of super-blocks (3, 5), ragged activation and weight
+    tiles, a two-job launch, a bias."""
+    case("prefill pair-wide kernel", rows, k, shapes)
+    rng = np.random.default_rng(rows * 19 + k + sum(shapes))
+    blocks = [_kq_blocks(rng, "q6k", n, k) for n in shapes]
+    ws = [ov.Q6KWeight(b, k, n) for b, n in zip(blocks, shapes)]
+    x = normal(rng, (rows, k))
+    bias = normal(rng, shapes[-1])
+    biases = [None] * (len(shapes) - 1) + [bias]
+    refs = [orc.q6k_project_batched(x, rows, b, k, n, bb) for b, n, bb in zip(blocks, shapes, biases)]
+    ys = [torch.empty(rows * n, device=DEV) for n in shapes]
+    ctx.project_multi_dev(ws, t(x), ys, [None if bb is None else t(bb) for bb in biases], rows=rows)
+    torch.cuda.synchronize()
+    for i, (y, ref) in enumerate(zip(ys, refs)):
+        assert_bit_exact(y.cpu().numpy().reshape(rows, -1), ref, f"pair-wide kernel rows={rows} job {i}")
+
+
 @pytest.mark.parametrize("fmt", ["q4k", "q6k"])
 @pytest.mark.parametrize("rows,k,n", [(32, 256, 64), (70, 512, 200), (128, 4096, 130), (200, 2304, 64)])
 def test_prepared_mfma_prefill_bit_exact(orc, ctx, batched, fmt, rows, k, n):
