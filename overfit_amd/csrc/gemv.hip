@@ -15,6 +15,7 @@
 // Dot, and the row's sum over blocks is accumulated in ascending block order by one lane per row, so every
 // output is bit-identical to the reference's sequential loop.
 #include <cstdlib>
+#include <type_traits>
 
 #include "kquant_blocks.h"
 #include "ovfq_device.h"
@@ -74,10 +75,11 @@ __device__ __forceinline__ float ordered_item_sum(float acc, const float* row, i
 // owns elements [16l, 16l+16) of its block, i.e. bsum group l, and writes one 16-byte LDS chunk.
 // `prefetch` issues the first weight item's loads; it runs after the activation loads so that waiting for the
 // activation does not also wait for the weights.
-template <class F, class Prefetch>
+template <class F, int W, class Prefetch>
 __device__ __forceinline__ void stage_activation(const GArgs& a, uint8_t* lq, int16_t* lb, float* ls, int wave,
                                                  int lane, Prefetch prefetch) {
-    constexpr int kPasses = kGemvMaxSpr / 16;
+    constexpr int kPerPass = 4 * W;  // super-blocks per pass: four per wave
+    constexpr int kPasses = (kGemvMaxSpr + kPerPass - 1) / kPerPass;
     const int spr = a.spr;
     const int l16 = lane & 15, row = lane >> 4;
     const int pos = F::lds_pos(16 * l16);
@@ -86,8 +88,8 @@ __device__ __forceinline__ void stage_activation(const GArgs& a, uint8_t* lq, in
         u32x4 xv[kPasses][4];
 #pragma unroll
         for (int p = 0; p < kPasses; p++) {
-            const int sb = p * 16 + wave * 4 + row;
-            if (p * 16 < spr) {
+            const int sb = p * kPerPass + wave * 4 + row;
+            if (p * kPerPass < spr) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) xv[p][i] = ld4(xr, (uint32_t)sb * 1024 + l16 * 64 + i * 16);
             }
@@ -95,8 +97,8 @@ __device__ __forceinline__ void stage_activation(const GArgs& a, uint8_t* lq, in
         prefetch();
 #pragma unroll
         for (int p = 0; p < kPasses; p++) {
-            if (p * 16 >= spr) break;
-            const int sb = p * 16 + wave * 4 + row;
+            if (p * kPerPass >= spr) break;
+            const int sb = p * kPerPass + wave * 4 + row;
             float v[16];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
@@ -120,8 +122,8 @@ __device__ __forceinline__ void stage_activation(const GArgs& a, uint8_t* lq, in
         uint32_t bv[kPasses], sv[kPasses];
 #pragma unroll
         for (int p = 0; p < kPasses; p++) {
-            const int sb = p * 16 + wave * 4 + row;
-            if (p * 16 < spr) {
+            const int sb = p * kPerPass + wave * 4 + row;
+            if (p * kPerPass < spr) {
                 qv[p] = ld4(qr, (uint32_t)sb * kQK + l16 * 16);
                 bv[p] = __builtin_amdgcn_raw_buffer_load_b16(br, (int)((uint32_t)sb * 32 + l16 * 2), 0, 0);
                 sv[p] = ld1(sr, (uint32_t)sb * 4);
@@ -130,8 +132,8 @@ __device__ __forceinline__ void stage_activation(const GArgs& a, uint8_t* lq, in
         prefetch();
 #pragma unroll
         for (int p = 0; p < kPasses; p++) {
-            if (p * 16 >= spr) break;
-            const int sb = p * 16 + wave * 4 + row;
+            if (p * kPerPass >= spr) break;
+            const int sb = p * kPerPass + wave * 4 + row;
             if (sb < spr) {
                 *reinterpret_cast<u32x4*>(lq + sb * kLdsSlot + pos) = qv[p];
                 lb[sb * 16 + l16] = (int16_t)bv[p];
@@ -141,9 +143,10 @@ __device__ __forceinline__ void stage_activation(const GArgs& a, uint8_t* lq, in
     }
 }
 
-// kMulti: the launch has several jobs (fused projections); with one, no job lookup is needed.
-template <class F, int R, bool kMulti>
-__global__ __launch_bounds__(256) void kquant_gemv_kernel(const GArgs a) {
+// kMulti: the launch has several jobs (fused projections); with one, no job lookup is needed. W: waves per
+// workgroup (the activation prologue is paid once per workgroup, its quantisation spread over the W waves).
+template <class F, int R, bool kMulti, int W>
+__global__ __launch_bounds__(64 * W) void kquant_gemv_kernel(const GArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int spr = a.spr;
     uint8_t* lq = smem;
@@ -154,7 +157,7 @@ __global__ __launch_bounds__(256) void kquant_gemv_kernel(const GArgs a) {
     const int lane = threadIdx.x & 63;
     const int q = lane >> 2, t = lane & 3;
     const int nchunks = (spr + 15) >> 4;
-    const int stride = gridDim.x * 4;
+    const int stride = gridDim.x * W;
     const int total = a.total_groups;
     const uint32_t row_bytes = (uint32_t)spr * F::kBytes;
     float* rw = red + wave * R * kRedStride;
@@ -214,12 +217,12 @@ __global__ __launch_bounds__(256) void kquant_gemv_kernel(const GArgs a) {
         it.bias = ld1(bsr, (uint32_t)(row0 + (lane < R ? lane : 0)) * 4);
     };
 
-    int g = blockIdx.x * 4 + wave;
+    int g = blockIdx.x * W + wave;
     int c = 0;
     Item ia, ib;
     // The first item's lookup runs inside the prefetch, after the activation loads have gone out (they, not the
     // weights, bound the start of the first item).
-    stage_activation<F>(a, lq, lb, ls, wave, lane, [&] { load_item(locate(g < total ? g : 0), 0, g < total, ia); });
+    stage_activation<F, W>(a, lq, lb, ls, wave, lane, [&] { load_item(locate(g < total ? g : 0), 0, g < total, ia); });
     __syncthreads();
     if (g >= total) return;
     Cur cj = locate(g);  // job record of row group g, looked up once per row group
@@ -287,6 +290,16 @@ int cu_count() {
     return cus[dev];
 }
 
+template <class F, int R, int W>
+hipError_t launch_gemv_w(const GArgs& ga, int njobs, int wgs, hipStream_t st) {
+    const size_t lds = (size_t)((ga.spr * (kLdsSlot + 36) + 15) & ~15) + W * R * kRedStride * sizeof(float);
+    if (njobs > 1)
+        hipLaunchKernelGGL((kquant_gemv_kernel<F, R, true, W>), dim3(wgs), dim3(64 * W), lds, st, ga);
+    else
+        hipLaunchKernelGGL((kquant_gemv_kernel<F, R, false, W>), dim3(wgs), dim3(64 * W), lds, st, ga);
+    return hipGetLastError();
+}
+
 template <class F, int R>
 hipError_t launch_gemv(GArgs& ga, const ProjJob* jobs, int njobs, hipStream_t st) {
     int groups = 0;
@@ -295,18 +308,26 @@ hipError_t launch_gemv(GArgs& ga, const ProjJob* jobs, int njobs, hipStream_t st
         groups += (jobs[i].n_rows + R - 1) / R;
     }
     ga.total_groups = groups;
-    // Workgroups per CU (measured on MI355X): 2 with two rows per wave (Q4_K rows of up to 16 blocks), else 3.
+    // Waves per workgroup (measured on MI355X, graph replay over weight copies beyond the cache, us, 4 / 8 waves, one
+    // eight-wave workgroup per CU): Q4_K rows longer than 16 blocks (one row per wave) 4096x14336 11.4 / 10.5,
+    // 8192x8192 9.9 / 9.7; the Q6_K 128256x4096 LM head 83.5 / 80.2. Everything else keeps four-wave workgroups:
+    // the Llama-3-8B layer's launches are 1-12 % slower with 8 (also 12 or 16) waves, and so are Q6_K 4096x14336
+    // and 8192x8192.
+    static const int forced_w = env_int("OVFQ_GEMV_WAVES", 0);
+    int W = (std::is_same<F, Q4K>::value && ga.spr > 16) || (std::is_same<F, Q6K>::value && groups >= 65536) ? 8 : 4;
+    if (forced_w == 4 || forced_w == 8) W = forced_w;
+    if (R == 4) W = 4;
+    // Workgroups per CU (measured on MI355X): 2 with two rows per wave (Q4_K rows of up to 16 blocks), else 3;
+    // one eight-wave workgroup.
     static const int forced_wg = env_int("OVFQ_GEMV_WG_PER_CU", 0);
-    const int wg_per_cu = forced_wg > 0 ? forced_wg : (R == 2 ? 2 : 3);
-    int wgs = (groups + 3) / 4;
+    const int wg_per_cu = forced_wg > 0 ? forced_wg : W == 8 ? 1 : (R == 2 ? 2 : 3);
+    int wgs = (groups + W - 1) / W;
     const int cap = cu_count() * wg_per_cu;
     if (wgs > cap) wgs = cap;
-    const size_t lds = (size_t)((ga.spr * (kLdsSlot + 36) + 15) & ~15) + 4 * R * kRedStride * sizeof(float);
-    if (njobs > 1)
-        hipLaunchKernelGGL((kquant_gemv_kernel<F, R, true>), dim3(wgs), dim3(256), lds, st, ga);
-    else
-        hipLaunchKernelGGL((kquant_gemv_kernel<F, R, false>), dim3(wgs), dim3(256), lds, st, ga);
-    return hipGetLastError();
+    if constexpr (R != 4) {
+        if (W == 8) return launch_gemv_w<F, R, 8>(ga, njobs, wgs, st);
+    }
+    return launch_gemv_w<F, R, 4>(ga, njobs, wgs, st);
 }
 
 }  // namespace
@@ -576,10 +597,12 @@ hipError_t launch_gemv_rows_kquant(int type, const ProjJob* jobs, int njobs, int
     return R == 2 ? launch_gemv_rows<Q6K, 2>(ra, jobs, njobs, st) : launch_gemv_rows<Q6K, 1>(ra, jobs, njobs, st);
 }
 
-// Every workgroup of the decode kernel quantises the whole activation; past 32 super-blocks (K > 8192) that
-// prologue costs more than one standalone quantise launch, so long rows are quantised once beforehand.
+// Every workgroup of the decode kernel quantises the whole activation, for every input it takes (up to 64
+// super-blocks): that prologue costs less than a standalone quantise launch (MI355X, config-2 layer step with the
+// 4096x14336 Q6_K down launch quantising its input in-launch 36.97 -> 36.76 us; decode GEMVs at K = 8192-16384
+// 1-8 % faster).
 bool gemv_quantize_inside(int in) {
-    static const int limit = env_int("OVFQ_GEMV_QUANT_INSIDE_MAX_SPR", 32);
+    static const int limit = env_int("OVFQ_GEMV_QUANT_INSIDE_MAX_SPR", kGemvMaxSpr);
     return in / kQK <= limit;
 }
 
