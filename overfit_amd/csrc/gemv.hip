@@ -49,8 +49,10 @@ constexpr int kGemvMaxSpr = 64;  // K <= 16384: the whole Q8_K activation fits i
 // that sums them reads the row with four 16-byte loads).
 constexpr int kRedStride = 20;
 
-// acc + the item's nq block values of LDS row `row`, in ascending block order (from registers: four 16-byte reads).
-__device__ __forceinline__ float ordered_item_sum(float acc, const float* row, int nq) {
+// acc + the item's 16 block values of LDS row `row`, in ascending block order (from registers: four 16-byte reads).
+// A short last chunk stores +0 for the blocks past the row: the running sum starts at +0 and a sum of IEEE additions
+// from +0 is never -0 in round-to-nearest, so each trailing acc + 0 returns acc unchanged (NaN and infinities too).
+__device__ __forceinline__ float ordered_item_sum(float acc, const float* row) {
     float v[16];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -60,14 +62,8 @@ __device__ __forceinline__ float ordered_item_sum(float acc, const float* row, i
         v[4 * i + 2] = x.z;
         v[4 * i + 3] = x.w;
     }
-    if (nq == 16) {  // wave-uniform: every chunk but a row's short last one
 #pragma unroll
-        for (int qq = 0; qq < 16; qq++) acc += v[qq];
-    } else {
-#pragma unroll
-        for (int qq = 0; qq < 16; qq++)
-            if (qq < nq) acc += v[qq];
-    }
+    for (int qq = 0; qq < 16; qq++) acc += v[qq];
     return acc;
 }
 
@@ -178,9 +174,11 @@ __global__ __launch_bounds__(64 * W) void kquant_gemv_kernel(const GArgs a) {
         float* y;
         int n_rows;
         int row0;
+        __amdgpu_buffer_rsrc_t wr;  // the row group's weight bytes (set by bind)
+        uint32_t extra;             // its first row's offset past the 4-byte aligned resource base
     };
     auto locate = [&](int g) -> Cur {
-        Cur c{a.job[0].w, a.job[0].bias, a.job[0].y, a.job[0].n_rows, 0};
+        Cur c{a.job[0].w, a.job[0].bias, a.job[0].y, a.job[0].n_rows, 0, make_rsrc(a.job[0].w, 0u), 0u};
         if constexpr (kMulti) {
 #pragma unroll
             for (int i = 1; i < kMaxJobs; i++) {
@@ -195,22 +193,26 @@ __global__ __launch_bounds__(64 * W) void kquant_gemv_kernel(const GArgs a) {
         c.row0 = (g - c.row0) * R;
         return c;
     };
+    // The weight resource of a row group, made once per row group (a long row's chunks reuse it). It ends with the
+    // row group's last block: quads past the last super-block of a short final chunk then read nothing (instead of
+    // the next row's blocks). No block read uses bytes past its block. Past the end (valid false) it has zero length.
+    auto bind = [&](Cur c, bool valid) -> Cur {
+        const uint64_t base_off = (uint64_t)c.row0 * row_bytes;
+        const uint64_t al = base_off & ~3ull;
+        c.extra = (uint32_t)(base_off & 3ull);
+        const uint64_t end = (uint64_t)min(c.row0 + R, c.n_rows) * row_bytes;
+        c.wr = make_rsrc(c.w + al, valid ? rsrc_bytes(end, al) : 0u);
+        return c;
+    };
     // Issues the loads of item (row group of job record jb, chunk c). The instruction stream is the same whether
     // or not the item exists (past the end the resources have zero length, so the loads return 0 without touching
     // memory): the compiler's wait counts then see a fixed number of younger loads and the prefetch overlaps the
     // current item's math.
     auto load_item = [&](const Cur& jb, int c, bool valid, Item& it) {
         const int row0 = jb.row0;
-        const uint64_t base_off = (uint64_t)row0 * row_bytes;
-        const uint64_t al = base_off & ~3ull;
-        const uint32_t extra = (uint32_t)(base_off & 3ull);
-        // The resource ends with the row group's last block: quads past the last super-block of a short final
-        // chunk then read nothing (instead of the next row's blocks). No block read uses bytes past its block.
-        const uint64_t end = (uint64_t)min(row0 + R, jb.n_rows) * row_bytes;
-        const __amdgpu_buffer_rsrc_t wr = make_rsrc(jb.w + al, valid ? rsrc_bytes(end, al) : 0u);
         const uint32_t sb = (uint32_t)(c * 16 + q);
 #pragma unroll
-        for (int r = 0; r < R; r++) it.w[r] = F::load_w(wr, extra + r * row_bytes + sb * F::kBytes, t);
+        for (int r = 0; r < R; r++) it.w[r] = F::load_w(jb.wr, jb.extra + r * row_bytes + sb * F::kBytes, t);
         const float* bias = jb.bias;
         const bool want_bias = valid && bias != nullptr && c == nchunks - 1;
         const __amdgpu_buffer_rsrc_t bsr = make_rsrc(bias, want_bias ? (uint32_t)jb.n_rows * 4 : 0u);
@@ -222,10 +224,11 @@ __global__ __launch_bounds__(64 * W) void kquant_gemv_kernel(const GArgs a) {
     Item ia, ib;
     // The first item's lookup runs inside the prefetch, after the activation loads have gone out (they, not the
     // weights, bound the start of the first item).
-    stage_activation<F, W>(a, lq, lb, ls, wave, lane, [&] { load_item(locate(g < total ? g : 0), 0, g < total, ia); });
+    stage_activation<F, W>(a, lq, lb, ls, wave, lane,
+                           [&] { load_item(bind(locate(g < total ? g : 0), g < total), 0, g < total, ia); });
     __syncthreads();
     if (g >= total) return;
-    Cur cj = locate(g);  // job record of row group g, looked up once per row group
+    Cur cj = bind(locate(g), true);  // job record of row group g, looked up once per row group
 
     float acc = 0.0f;
     int a_chunk = -1;
@@ -238,8 +241,8 @@ __global__ __launch_bounds__(64 * W) void kquant_gemv_kernel(const GArgs a) {
             ng += stride;
         }
         const bool more = ng < total;
-        Cur nj = cj;
-        if (nc == 0) nj = locate(more ? ng : 0);
+        Cur nj = cj;  // the same row group (and resource) for its next chunk
+        if (nc == 0) nj = bind(locate(more ? ng : 0), more);
         load_item(nj, nc, more, nxt);
         const int sb = c * 16 + q;
         const bool live = sb < spr;
@@ -250,10 +253,10 @@ __global__ __launch_bounds__(64 * W) void kquant_gemv_kernel(const GArgs a) {
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const float v = F::dot(cur.w[r], av, t);
-            if (t == 0 && live) rw[r * kRedStride + q] = v;
+            if (t == 0) rw[r * kRedStride + q] = live ? v : 0.0f;
         }
         wave_sync();
-        if (lane < R) acc = ordered_item_sum(acc, rw + lane * kRedStride, min(16, spr - c * 16));
+        if (lane < R) acc = ordered_item_sum(acc, rw + lane * kRedStride);
         wave_sync();
         if (c == nchunks - 1) {
             if (lane < R && cj.row0 + lane < cj.n_rows) {
@@ -438,6 +441,9 @@ __global__ __launch_bounds__(256) void kquant_gemv_rows_kernel(const RArgs a) {
             if (base == 0) load_item(g, 0, g < total, ia);
 #pragma unroll
             for (int p = 0; p < kPasses; p++) {
+                // passes wholly past the slots quantise nothing (their loads above stay: a fixed load count keeps the
+                // weight prefetch in flight through the compiler's wait counts)
+                if (base + p * 16 >= slots) break;  // wave-uniform
                 const int i = base + p * 16 + wave * 4 + hrow;
                 float v[16];
 #pragma unroll
@@ -513,11 +519,11 @@ __global__ __launch_bounds__(256) void kquant_gemv_rows_kernel(const RArgs a) {
 #pragma unroll
             for (int r = 0; r < R; r++) {
                 const float v = F::dot_p(pw[r], av);
-                if (t == 0 && live) rw[(m * R + r) * kRedStride + q] = v;
+                if (t == 0) rw[(m * R + r) * kRedStride + q] = live ? v : 0.0f;
             }
         }
         wave_sync();
-        if (lane < rows * R) acc = ordered_item_sum(acc, rw + lane * kRedStride, min(16, spr - c * 16));
+        if (lane < rows * R) acc = ordered_item_sum(acc, rw + lane * kRedStride);
         wave_sync();
         if (c == nchunks - 1) {
             const Cur jb = locate(g);
