@@ -174,11 +174,9 @@ __global__ __launch_bounds__(64 * W) void kquant_gemv_kernel(const GArgs a) {
         float* y;
         int n_rows;
         int row0;
-        __amdgpu_buffer_rsrc_t wr;  // the row group's weight bytes (set by bind)
-        uint32_t extra;             // its first row's offset past the 4-byte aligned resource base
     };
     auto locate = [&](int g) -> Cur {
-        Cur c{a.job[0].w, a.job[0].bias, a.job[0].y, a.job[0].n_rows, 0, make_rsrc(a.job[0].w, 0u), 0u};
+        Cur c{a.job[0].w, a.job[0].bias, a.job[0].y, a.job[0].n_rows, 0};
         if constexpr (kMulti) {
 #pragma unroll
             for (int i = 1; i < kMaxJobs; i++) {
@@ -193,29 +191,38 @@ __global__ __launch_bounds__(64 * W) void kquant_gemv_kernel(const GArgs a) {
         c.row0 = (g - c.row0) * R;
         return c;
     };
-    // The weight resource of a row group, made once per row group (a long row's chunks reuse it). It ends with the
-    // row group's last block: quads past the last super-block of a short final chunk then read nothing (instead of
-    // the next row's blocks). No block read uses bytes past its block. Past the end (valid false) it has zero length.
-    auto bind = [&](Cur c, bool valid) -> Cur {
+    // The weight resource of a row group, made once per row group (a long row's chunks reuse it) and kept beside the
+    // job record, not in it (in the record the compiler stopped treating the record's pointers as wave-uniform). It
+    // ends with the row group's last block: quads past the last super-block of a short final chunk then read nothing
+    // (instead of the next row's blocks). No block read uses bytes past its block. Past the end (valid false) it has
+    // zero length.
+    struct WRes {
+        __amdgpu_buffer_rsrc_t r;
+        uint32_t extra;  // the first row's offset past the resource's 4-byte aligned base
+    };
+    auto bind = [&](const Cur& c, bool valid) -> WRes {
         const uint64_t base_off = (uint64_t)c.row0 * row_bytes;
         const uint64_t al = base_off & ~3ull;
-        c.extra = (uint32_t)(base_off & 3ull);
-        const uint64_t end = (uint64_t)min(c.row0 + R, c.n_rows) * row_bytes;
-        c.wr = make_rsrc(c.w + al, valid ? rsrc_bytes(end, al) : 0u);
-        return c;
+        const uint32_t extra = (uint32_t)(base_off & 3ull);
+        // bytes from the aligned base to the group's end: its rows (at most R, a few tens of KB) plus `extra`
+        const uint32_t bytes = (uint32_t)min(R, c.n_rows - c.row0) * row_bytes + extra;
+        return WRes{make_rsrc(c.w + al, valid ? bytes : 0u), extra};
     };
-    // Issues the loads of item (row group of job record jb, chunk c). The instruction stream is the same whether
-    // or not the item exists (past the end the resources have zero length, so the loads return 0 without touching
-    // memory): the compiler's wait counts then see a fixed number of younger loads and the prefetch overlaps the
-    // current item's math.
-    auto load_item = [&](const Cur& jb, int c, bool valid, Item& it) {
+    // Issues the loads of item (row group of job record jb, weight resource wr, chunk c). The instruction stream is
+    // the same whether or not the item exists (past the end the resources have zero length, so the loads return 0
+    // without touching memory): the compiler's wait counts then see a fixed number of younger loads and the prefetch
+    // overlaps the current item's math.
+    auto load_item = [&](const Cur& jb, const WRes& wr, int c, bool valid, Item& it) {
         const int row0 = jb.row0;
         const uint32_t sb = (uint32_t)(c * 16 + q);
 #pragma unroll
-        for (int r = 0; r < R; r++) it.w[r] = F::load_w(jb.wr, jb.extra + r * row_bytes + sb * F::kBytes, t);
+        for (int r = 0; r < R; r++) it.w[r] = F::load_w(wr.r, wr.extra + r * row_bytes + sb * F::kBytes, t);
         const float* bias = jb.bias;
         const bool want_bias = valid && bias != nullptr && c == nchunks - 1;
-        const __amdgpu_buffer_rsrc_t bsr = make_rsrc(bias, want_bias ? (uint32_t)jb.n_rows * 4 : 0u);
+        // (readfirstlane: in the multi-job kernel the compiler kept the job's row count in a vector register and
+        // wrapped this load in a loop over distinct resources)
+        const uint32_t bbytes = (uint32_t)__builtin_amdgcn_readfirstlane(want_bias ? jb.n_rows * 4 : 0);
+        const __amdgpu_buffer_rsrc_t bsr = make_rsrc(bias, bbytes);
         it.bias = ld1(bsr, (uint32_t)(row0 + (lane < R ? lane : 0)) * 4);
     };
 
@@ -224,11 +231,14 @@ __global__ __launch_bounds__(64 * W) void kquant_gemv_kernel(const GArgs a) {
     Item ia, ib;
     // The first item's lookup runs inside the prefetch, after the activation loads have gone out (they, not the
     // weights, bound the start of the first item).
-    stage_activation<F, W>(a, lq, lb, ls, wave, lane,
-                           [&] { load_item(bind(locate(g < total ? g : 0), g < total), 0, g < total, ia); });
+    stage_activation<F, W>(a, lq, lb, ls, wave, lane, [&] {
+        const Cur c0 = locate(g < total ? g : 0);
+        load_item(c0, bind(c0, g < total), 0, g < total, ia);
+    });
     __syncthreads();
     if (g >= total) return;
-    Cur cj = bind(locate(g), true);  // job record of row group g, looked up once per row group
+    Cur cj = locate(g);  // job record of row group g, looked up once per row group
+    WRes cw = bind(cj, true);
 
     float acc = 0.0f;
     int a_chunk = -1;
@@ -242,8 +252,12 @@ __global__ __launch_bounds__(64 * W) void kquant_gemv_kernel(const GArgs a) {
         }
         const bool more = ng < total;
         Cur nj = cj;  // the same row group (and resource) for its next chunk
-        if (nc == 0) nj = bind(locate(more ? ng : 0), more);
-        load_item(nj, nc, more, nxt);
+        WRes nw = cw;
+        if (nc == 0) {
+            nj = locate(more ? ng : 0);
+            nw = bind(nj, more);
+        }
+        load_item(nj, nw, nc, more, nxt);
         const int sb = c * 16 + q;
         const bool live = sb < spr;
         if (c != a_chunk) {
@@ -268,6 +282,7 @@ __global__ __launch_bounds__(64 * W) void kquant_gemv_kernel(const GArgs a) {
         g = ng;
         c = nc;
         cj = nj;
+        cw = nw;
         return more;
     };
     while (step(ia, ib) && step(ib, ia)) {

@@ -68,9 +68,10 @@ struct Q4K {
         // packed words, two bytes at a time.
         const uint32_t sh = (t & 1) * 16;
         const uint32_t A16 = (w.h.y >> sh) & 0xffffu, B16 = (w.h.z >> sh) & 0xffffu, C16 = (w.h.w >> sh) & 0xffffu;
-        const bool upper = t >= 2;
-        const uint32_t sc01 = upper ? ((C16 & 0x0f0fu) | ((A16 >> 2) & 0x3030u)) : (A16 & 0x3f3fu);
-        const uint32_t m01 = upper ? (((C16 >> 4) & 0x0f0fu) | ((B16 >> 2) & 0x3030u)) : (B16 & 0x3f3fu);
+        // sub-blocks 4..7 (t >= 2) or 0..3, chosen by a bit mask: a conditional here became a branch per lane group
+        const uint32_t upper = 0u - ((uint32_t)t >> 1);
+        const uint32_t sc01 = (((C16 & 0x0f0fu) | ((A16 >> 2) & 0x3030u)) & upper) | (A16 & 0x3f3fu & ~upper);
+        const uint32_t m01 = ((((C16 >> 4) & 0x0f0fu) | ((B16 >> 2) & 0x3030u)) & upper) | (B16 & 0x3f3fu & ~upper);
         const uint32_t qw[8] = {w.a.x, w.a.y, w.a.z, w.a.w, w.b.x, w.b.y, w.b.z, w.b.w};
         const uint32_t aw[16] = {a.q[0].x, a.q[0].y, a.q[0].z, a.q[0].w, a.q[1].x, a.q[1].y, a.q[1].z, a.q[1].w,
                                  a.q[2].x, a.q[2].y, a.q[2].z, a.q[2].w, a.q[3].x, a.q[3].y, a.q[3].z, a.q[3].w};
@@ -101,9 +102,9 @@ struct Q4K {
         P p;
         const uint32_t sh = (t & 1) * 16;
         const uint32_t A16 = (w.h.y >> sh) & 0xffffu, B16 = (w.h.z >> sh) & 0xffffu, C16 = (w.h.w >> sh) & 0xffffu;
-        const bool upper = t >= 2;
-        p.sc01 = upper ? ((C16 & 0x0f0fu) | ((A16 >> 2) & 0x3030u)) : (A16 & 0x3f3fu);
-        p.m01 = upper ? (((C16 >> 4) & 0x0f0fu) | ((B16 >> 2) & 0x3030u)) : (B16 & 0x3f3fu);
+        const uint32_t upper = 0u - ((uint32_t)t >> 1);  // as in dot()
+        p.sc01 = (((C16 & 0x0f0fu) | ((A16 >> 2) & 0x3030u)) & upper) | (A16 & 0x3f3fu & ~upper);
+        p.m01 = ((((C16 >> 4) & 0x0f0fu) | ((B16 >> 2) & 0x3030u)) & upper) | (B16 & 0x3f3fu & ~upper);
         const uint32_t qw[8] = {w.a.x, w.a.y, w.a.z, w.a.w, w.b.x, w.b.y, w.b.z, w.b.w};
 #pragma unroll
         for (int k = 0; k < 8; k++) {
