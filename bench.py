@@ -722,7 +722,7 @@ def main():
                                   "(two rocprofv3 --pmc passes, FETCH_SIZE and WRITE_SIZE, calibrated by a 64 MiB "
                                   "device copy; kernel source of commit %s)" % traffic_commit
                                   if traffic is not None else None,
-                "kernel": "kquant_gemv_kernel<Q4K,2,true> (Q8_K quantise + fused gate+up GEMV, 2x14336x4096)",
+                "kernel": "kquant_gemv_kernel<Q4K,2,true,4> (Q8_K quantise + fused gate+up GEMV, 2x14336x4096)",
                 "avg_us": round(gu_avg, 3), "algorithmic_bytes": gu_bytes,
                 "timing": "HIP graph replay of 4x%d launches over %d weight copies, /launch" % (len(copies), len(copies))}
 
