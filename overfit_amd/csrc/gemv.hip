@@ -204,9 +204,10 @@ __global__ __launch_bounds__(64 * W) void kquant_gemv_kernel(const GArgs a) {
         const uint64_t base_off = (uint64_t)c.row0 * row_bytes;
         const uint64_t al = base_off & ~3ull;
         const uint32_t extra = (uint32_t)(base_off & 3ull);
-        // bytes from the aligned base to the group's end: its rows (at most R, a few tens of KB) plus `extra`
-        const uint32_t bytes = (uint32_t)min(R, c.n_rows - c.row0) * row_bytes + extra;
-        return WRes{make_rsrc(c.w + al, valid ? bytes : 0u), extra};
+        // (the length in 64-bit arithmetic: the same value computed in 32 bits made config 1, a 4096x4096 launch of
+        // one item per wave, 5 % slower by a different prologue schedule)
+        const uint64_t end = (uint64_t)min(c.row0 + R, c.n_rows) * row_bytes;
+        return WRes{make_rsrc(c.w + al, valid ? rsrc_bytes(end, al) : 0u), extra};
     };
     // Issues the loads of item (row group of job record jb, weight resource wr, chunk c). The instruction stream is
     // the same whether or not the item exists (past the end the resources have zero length, so the loads return 0
