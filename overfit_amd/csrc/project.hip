@@ -703,138 +703,6 @@ __global__ __launch_bounds__(256, 2) void q8_0_mfma_kernel(const Q8MArgs a) {
     }
 }
 
-// The 64 x 64 tile of the kernel above (T = 4) on eight-wave workgroups with its operands staged by LDS DMA: wave w
-// takes outputs 16 (w % 4) .. + 15 and activation tiles 2 (w / 4) and 2 (w / 4) + 1, so a launch of one 64 x 64
-// tile per workgroup keeps four waves per SIMD instead of two. Per group of four blocks the activation rows (128
-// bytes each), their scales, the workgroup's 64 weight rows and their scales are DMA'd (`buffer_load ... lds`) into
-// one of two slots while the other slot is computed; each slot is its own set of LDS objects, so the compiler's wait
-// before reading one slot leaves the DMA into the other in flight. A row's eight 16-byte pieces sit XOR-swizzled by
-// row % 8 (physical piece p holds logical piece p ^ (row % 8)) against LDS bank conflicts. Per (row, output) the
-// block values are added in ascending block order from +0, as in the kernel above.
-constexpr int kQ8DmaWaves = 8;
-
-__global__ __launch_bounds__(64 * kQ8DmaWaves, 2) void q8_0_mfma_dma_kernel(const Q8MArgs a) {
-    __shared__ __align__(16) uint8_t act0[64 * 128], act1[64 * 128];  // activation rows of the group
-    __shared__ __align__(16) uint8_t wt0[64 * 128], wt1[64 * 128];    // weight rows of the group
-    __shared__ __align__(16) float xs0[64 * 4], xs1[64 * 4];          // activation scales [row][block]
-    __shared__ __align__(16) float ws0[64 * 4], ws1[64 * 4];          // weight scales [row][block]
-    const int wave = wave_id();
-    const int lane = threadIdx.x & 63;
-    const int g = lane >> 4, c16 = lane & 15;
-    const int ow = wave & 3, ah = wave >> 2;
-    const int obase = (int)blockIdx.x * 64;
-    const int m0 = (int)blockIdx.y * 64;
-    const uint32_t K = (uint32_t)a.in, nb = K / 32;
-    const int ng = (int)(nb + 3) / 4;
-    // (readfirstlane: the compiler otherwise clamps these in vector registers and loops each DMA over lanes)
-    const uint32_t wrows = (uint32_t)__builtin_amdgcn_readfirstlane(max(0, min(64, a.n_out - obase)));
-    const uint32_t arows = (uint32_t)__builtin_amdgcn_readfirstlane(min(64, a.rows - m0));
-    // resources end with the tile's last row: rows past the matrix or the batch read zeros
-    const __amdgpu_buffer_rsrc_t qr = make_rsrc(a.q + (uint64_t)m0 * K, arows * K);
-    const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.s + (uint64_t)m0 * nb, arows * nb * 4);
-    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w + (uint64_t)obase * K, wrows * K);
-    const __amdgpu_buffer_rsrc_t wsr = make_rsrc(a.ws + (uint64_t)obase * nb, wrows * nb * 4);
-    // DMA sources. Wave w moves rows 8w .. 8w + 7 of the activation and of the weights (1 KiB each: lane L writes
-    // physical piece L % 8 of row 8w + L / 8), and the scales of rows 16 (w % 4) .. + 15 (lane L: row + L / 4, block
-    // L % 4) of the activation (w < 4) or of the weights (w >= 4).
-    const uint32_t prow = 8u * (uint32_t)wave + ((uint32_t)lane >> 3);
-    const uint32_t piece_src = prow * K + 16u * (((uint32_t)lane & 7u) ^ (prow & 7u));
-    const uint32_t srow = 16u * (uint32_t)ow + ((uint32_t)lane >> 2);
-    const uint32_t scale_src = (srow * nb + ((uint32_t)lane & 3u)) * 4u;
-    const bool scale_act = wave < 4;  // wave-uniform
-    auto stage = [&](auto sc, int k) {
-        constexpr int S = decltype(sc)::value;
-        uint8_t* const act = S ? act1 : act0;
-        uint8_t* const wt = S ? wt1 : wt0;
-        float* const xs = S ? xs1 : xs0;
-        float* const ws = S ? ws1 : ws0;
-        const uint32_t kb = (uint32_t)k * 128u;  // the group's first K byte (4 blocks of 32)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(qr, (__attribute__((address_space(3))) void*)&act[1024 * wave], 16,
-                                                 (int)(piece_src + kb), 0, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (__attribute__((address_space(3))) void*)&wt[1024 * wave], 16,
-                                                 (int)(piece_src + kb), 0, 0, 0);
-        if (scale_act)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (__attribute__((address_space(3))) void*)&xs[64 * ow], 4,
-                                                     (int)(scale_src + (uint32_t)k * 16u), 0, 0, 0);
-        else
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(wsr, (__attribute__((address_space(3))) void*)&ws[64 * ow], 4,
-                                                     (int)(scale_src + (uint32_t)k * 16u), 0, 0, 0);
-    };
-    // byte offset of this lane's 8 bytes of block j in row `row` (lane group g holds K bytes 8g .. 8g + 7 of a block)
-    auto piece = [&](uint32_t row, int j) -> uint32_t {
-        return row * 128u + (((2u * (uint32_t)j + ((uint32_t)g >> 1)) ^ (row & 7u)) * 16u) + 8u * ((uint32_t)g & 1u);
-    };
-    float acc[2][4];
-#pragma unroll
-    for (int t = 0; t < 2; t++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) acc[t][i] = 0.0f;
-    auto compute = [&](auto sc, int k) {
-        constexpr int S = decltype(sc)::value;
-        const uint8_t* const act = S ? act1 : act0;
-        const uint8_t* const wt = S ? wt1 : wt0;
-        const float* const xs = S ? xs1 : xs0;
-        const float* const ws = S ? ws1 : ws0;
-        const int nblk = min(4, (int)nb - 4 * k);  // wave-uniform; only the row's last group is short
-        const uint32_t wrow = 16u * (uint32_t)ow + (uint32_t)c16;
-        const u32x4 wsv = *reinterpret_cast<const u32x4*>(&ws[wrow * 4]);  // the lane's weight row, blocks 0 .. 3
-        u32x2 bw[4];
-#pragma unroll
-        for (int j = 0; j < 4; j++) bw[j] = *reinterpret_cast<const u32x2*>(wt + piece(wrow, j));
-#pragma unroll
-        for (int tt = 0; tt < 2; tt++) {
-            const uint32_t t = 2u * (uint32_t)ah + (uint32_t)tt;
-            u32x2 aw[4];
-#pragma unroll
-            for (int j = 0; j < 4; j++) aw[j] = *reinterpret_cast<const u32x2*>(act + piece(16u * t + (uint32_t)c16, j));
-            u32x4 xv[4];  // scales of activation rows 16t + 4g + i, blocks 0 .. 3
-#pragma unroll
-            for (int i = 0; i < 4; i++) xv[i] = *reinterpret_cast<const u32x4*>(&xs[(16u * t + 4u * g + i) * 4u]);
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                if (j < nblk) {
-                    const long aop = (long)(((uint64_t)aw[j].y << 32) | aw[j].x);
-                    const long bop = (long)(((uint64_t)bw[j].y << 32) | bw[j].x);
-                    const i32x4m d = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, i32x4m{0, 0, 0, 0}, 0, 0, 0);
-                    const float wsc = as_float(j == 0 ? wsv.x : j == 1 ? wsv.y : j == 2 ? wsv.z : wsv.w);
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const uint32_t xw = j == 0 ? xv[i].x : j == 1 ? xv[i].y : j == 2 ? xv[i].z : xv[i].w;
-                        // (wScale * aScale) * blockDot, then the ascending sum
-                        acc[tt][i] += (wsc * as_float(xw)) * (float)d[i];
-                    }
-                }
-            }
-        }
-    };
-    using S0 = std::integral_constant<int, 0>;
-    using S1 = std::integral_constant<int, 1>;
-    stage(S0{}, 0);
-    for (int k = 0; k < ng; k += 2) {
-        __builtin_amdgcn_s_waitcnt(0);  // this wave's DMAs of group k have landed
-        __syncthreads();                // every wave's; and slot 1 is no longer read
-        if (k + 1 < ng) stage(S1{}, k + 1);
-        compute(S0{}, k);
-        if (k + 1 >= ng) break;
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        if (k + 2 < ng) stage(S0{}, k + 2);
-        compute(S1{}, k + 1);
-    }
-    __builtin_amdgcn_s_waitcnt(0);  // no DMA outlives the wave (none is issued after the last wait, but keep it so)
-    const int o = obase + 16 * ow + c16;
-    if (o < a.n_out) {
-        const float bo = a.bias ? a.bias[o] : 0.0f;
-#pragma unroll
-        for (int tt = 0; tt < 2; tt++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int m = m0 + 16 * (2 * ah + tt) + 4 * g + i;
-                if (m < a.rows) a.y[(size_t)m * a.n_out + o] = a.bias ? bo + acc[tt][i] : acc[tt][i];
-            }
-    }
-}
-
 // ------------------------------------------------------------------------------------------ per-head Q8_0 Wo on MFMA
 // The attention output projection of prefill rows with per-head Q8_0 Wo (RT/CachedMultiHeadAttention.cs:600-614,
 // :689-710: BatchedQuantProjection.Dispatch of each head's attention rows through its own Wo_h [d_model][head_dim],
@@ -855,6 +723,195 @@ struct Q8HMArgs {
     const int8_t* q;  // Q8_0 activation [rows][n_heads * head_dim]
     const float* s;
 };
+
+// The 64 x 64 tile (T = 4) of the two kernels above on eight-wave workgroups with the operands staged by LDS DMA:
+// wave w takes outputs 16 (w % 4) .. + 15 and activation tiles 2 (w / 4) and 2 (w / 4) + 1, so a launch of one
+// 64 x 64 tile per workgroup keeps four waves per SIMD instead of two. Per group of four blocks the activation rows
+// (128 bytes each), their scales, the workgroup's 64 weight rows and their scales are DMA'd (`buffer_load ... lds`)
+// into one of two slots while the other slot is computed; each slot is its own set of LDS objects, so the compiler's
+// wait before reading one slot leaves the DMA into the other in flight. A row's eight 16-byte pieces sit
+// XOR-swizzled by row % 8 (physical piece p holds logical piece p ^ (row % 8)) against LDS bank conflicts. Per
+// (row, output) the block values are added in ascending block order from +0; kHeads: the contraction walks the heads
+// (a group never crosses a head, its weight rows come from the head's planes) and each head's value is added to the
+// running output, which starts as bias or zero, in ascending head order, as q8_0_heads_mfma_kernel does.
+constexpr int kQ8DmaWaves = 8;
+
+template <bool kHeads, class Args>
+__global__ __launch_bounds__(64 * kQ8DmaWaves, 2) void q8_0_mfma_dma_kernel(const Args a) {
+    __shared__ __align__(16) uint8_t act0[64 * 128], act1[64 * 128];  // activation rows of the group
+    __shared__ __align__(16) uint8_t wt0[64 * 128], wt1[64 * 128];    // weight rows of the group
+    __shared__ __align__(16) float xs0[64 * 4], xs1[64 * 4];          // activation scales [row][block]
+    __shared__ __align__(16) float ws0[64 * 4], ws1[64 * 4];          // weight scales [row][block]
+    const int wave = wave_id();
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4, c16 = lane & 15;
+    const int ow = wave & 3, ah = wave >> 2;
+    const int obase = (int)blockIdx.x * 64;
+    const int m0 = (int)blockIdx.y * 64;
+    uint32_t K, wk;  // activation row length; weight row length (the head dimension for per-head planes)
+    if constexpr (kHeads) {
+        K = (uint32_t)a.n_heads * (uint32_t)a.head_dim;
+        wk = (uint32_t)a.head_dim;
+    } else {
+        K = (uint32_t)a.in;
+        wk = K;
+    }
+    const uint32_t nb = K / 32, wnb = wk / 32;
+    const int gph = (int)(wnb + 3) / 4;              // groups per weight plane (per head)
+    int ng = gph;  // groups in the contraction
+    if constexpr (kHeads) ng = a.n_heads * gph;
+    // (readfirstlane: the compiler otherwise clamps these in vector registers and loops each DMA over lanes)
+    const uint32_t wrows = (uint32_t)__builtin_amdgcn_readfirstlane(max(0, min(64, a.n_out - obase)));
+    const uint32_t arows = (uint32_t)__builtin_amdgcn_readfirstlane(min(64, a.rows - m0));
+    // resources end with the tile's last row: rows past the matrix or the batch read zeros
+    const __amdgpu_buffer_rsrc_t qr = make_rsrc(a.q + (uint64_t)m0 * K, arows * K);
+    const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.s + (uint64_t)m0 * nb, arows * nb * 4);
+    // DMA sources. Wave w moves rows 8w .. 8w + 7 of the activation and of the weights (1 KiB each: lane L writes
+    // physical piece L % 8 of row 8w + L / 8), and the scales of rows 16 (w % 4) .. + 15 (lane L: row + L / 4, block
+    // L % 4) of the activation (w < 4) or of the weights (w >= 4).
+    const uint32_t prow = 8u * (uint32_t)wave + ((uint32_t)lane >> 3);
+    const uint32_t pcol = 16u * (((uint32_t)lane & 7u) ^ (prow & 7u));
+    const uint32_t srow = 16u * (uint32_t)ow + ((uint32_t)lane >> 2), sblk = (uint32_t)lane & 3u;
+    const bool scale_act = wave < 4;  // wave-uniform
+    // group gi: its head, its first block in the weight plane and in the activation row, its block count
+    struct Grp {
+        int h;
+        uint32_t lb0, b0;
+        int nblk;
+    };
+    auto group_of = [&](int gi) -> Grp {
+        const int h = kHeads ? (gph == 1 ? gi : gi / gph) : 0;
+        const uint32_t lb0 = (uint32_t)(gi - h * gph) * 4u;
+        return Grp{h, lb0, (uint32_t)h * wnb + lb0, min(4, (int)(wnb - lb0))};
+    };
+    auto stage = [&](auto sc, int gi) {
+        constexpr int S = decltype(sc)::value;
+        uint8_t* const act = S ? act1 : act0;
+        uint8_t* const wt = S ? wt1 : wt0;
+        float* const xs = S ? xs1 : xs0;
+        float* const ws = S ? ws1 : ws0;
+        const Grp gr = group_of(gi);
+        const int8_t* wplane;
+        const float* splane;
+        if constexpr (kHeads) {
+            wplane = a.wq[gr.h];
+            splane = a.ws[gr.h];
+        } else {
+            wplane = a.w;
+            splane = a.ws;
+        }
+        // blocks past the plane's last (a short group) read other bytes or zeros, unused
+        const __amdgpu_buffer_rsrc_t wr = make_rsrc(wplane + (uint64_t)obase * wk, wrows * wk);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(qr, (__attribute__((address_space(3))) void*)&act[1024 * wave], 16,
+                                                 (int)(prow * K + gr.b0 * 32u + pcol), 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (__attribute__((address_space(3))) void*)&wt[1024 * wave], 16,
+                                                 (int)(prow * wk + gr.lb0 * 32u + pcol), 0, 0, 0);
+        if (scale_act) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (__attribute__((address_space(3))) void*)&xs[64 * ow], 4,
+                                                     (int)((srow * nb + gr.b0 + sblk) * 4u), 0, 0, 0);
+        } else {
+            const __amdgpu_buffer_rsrc_t wsr = make_rsrc(splane + (uint64_t)obase * wnb, wrows * wnb * 4);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(wsr, (__attribute__((address_space(3))) void*)&ws[64 * ow], 4,
+                                                     (int)((srow * wnb + gr.lb0 + sblk) * 4u), 0, 0, 0);
+        }
+    };
+    // byte offset of this lane's 8 bytes of block j in row `row` (lane group g holds K bytes 8g .. 8g + 7 of a block)
+    auto piece = [&](uint32_t row, int j) -> uint32_t {
+        return row * 128u + (((2u * (uint32_t)j + ((uint32_t)g >> 1)) ^ (row & 7u)) * 16u) + 8u * ((uint32_t)g & 1u);
+    };
+    const int o = obase + 16 * ow + c16;
+    float acc[2][4], tot[2][4];
+    {
+        const float start = (kHeads && a.bias && o < a.n_out) ? a.bias[o] : 0.0f;  // per-head: bias or zero
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                acc[t][i] = 0.0f;
+                tot[t][i] = start;
+            }
+    }
+    auto compute = [&](auto sc, int gi) {
+        constexpr int S = decltype(sc)::value;
+        const uint8_t* const act = S ? act1 : act0;
+        const uint8_t* const wt = S ? wt1 : wt0;
+        const float* const xs = S ? xs1 : xs0;
+        const float* const ws = S ? ws1 : ws0;
+        const Grp gr = group_of(gi);  // nblk < 4 only for a plane's short last group (wave-uniform)
+        const uint32_t wrow = 16u * (uint32_t)ow + (uint32_t)c16;
+        const u32x4 wsv = *reinterpret_cast<const u32x4*>(&ws[wrow * 4]);  // the lane's weight row, blocks 0 .. 3
+        u32x2 bw[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) bw[j] = *reinterpret_cast<const u32x2*>(wt + piece(wrow, j));
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++) {
+            const uint32_t t = 2u * (uint32_t)ah + (uint32_t)tt;
+            u32x2 aw[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) aw[j] = *reinterpret_cast<const u32x2*>(act + piece(16u * t + (uint32_t)c16, j));
+            u32x4 xv[4];  // scales of activation rows 16t + 4g + i, blocks 0 .. 3
+#pragma unroll
+            for (int i = 0; i < 4; i++) xv[i] = *reinterpret_cast<const u32x4*>(&xs[(16u * t + 4u * g + i) * 4u]);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                if (j < gr.nblk) {
+                    const long aop = (long)(((uint64_t)aw[j].y << 32) | aw[j].x);
+                    const long bop = (long)(((uint64_t)bw[j].y << 32) | bw[j].x);
+                    const i32x4m d = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, i32x4m{0, 0, 0, 0}, 0, 0, 0);
+                    const float wsc = as_float(j == 0 ? wsv.x : j == 1 ? wsv.y : j == 2 ? wsv.z : wsv.w);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const uint32_t xw = j == 0 ? xv[i].x : j == 1 ? xv[i].y : j == 2 ? xv[i].z : xv[i].w;
+                        // (wScale * aScale) * blockDot, then the ascending sum
+                        acc[tt][i] += (wsc * as_float(xw)) * (float)d[i];
+                    }
+                }
+            }
+        }
+        if constexpr (kHeads) {
+            if (gr.lb0 + 4u >= wnb) {  // the head's last group: output += head value
+#pragma unroll
+                for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        tot[tt][i] = tot[tt][i] + acc[tt][i];
+                        acc[tt][i] = 0.0f;
+                    }
+            }
+        }
+    };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    stage(S0{}, 0);
+    for (int k = 0; k < ng; k += 2) {
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's DMAs of group k have landed
+        __syncthreads();                // every wave's; and slot 1 is no longer read
+        if (k + 1 < ng) stage(S1{}, k + 1);
+        compute(S0{}, k);
+        if (k + 1 >= ng) break;
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (k + 2 < ng) stage(S0{}, k + 2);
+        compute(S1{}, k + 1);
+    }
+    if (o < a.n_out) {
+        const float bo = (!kHeads && a.bias) ? a.bias[o] : 0.0f;
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int m = m0 + 16 * (2 * ah + tt) + 4 * g + i;
+                if (m >= a.rows) continue;
+                float v;
+                if constexpr (kHeads) {
+                    v = tot[tt][i];
+                } else {
+                    v = a.bias ? bo + acc[tt][i] : acc[tt][i];  // bias[o] + sum; no add at all without a bias
+                }
+                a.y[(size_t)m * a.n_out + o] = v;
+            }
+    }
+}
 
 template <int T, int kW>
 __global__ __launch_bounds__(256, 2) void q8_0_heads_mfma_kernel(const Q8HMArgs a) {
@@ -998,6 +1055,16 @@ bool q8_0_heads_mfma_supported(int n_heads, int head_dim, int rows) {
            K * 64 < (1ull << 31) && K * (uint64_t)rows < (1ull << 31);
 }
 
+// Rows past 32: the eight-wave LDS-DMA kernel (OVFQ_Q8_MFMA_DMA=0 keeps the register-staged four-wave one, for
+// measurements).
+static bool q8_mfma_dma() {
+    static const bool on = [] {
+        const char* v = getenv("OVFQ_Q8_MFMA_DMA");
+        return !(v && *v == '0');
+    }();
+    return on;
+}
+
 hipError_t launch_q8_0_heads_mfma(const int8_t* const* wq, const float* const* ws, int n_heads, int head_dim,
                                   int d_model, int rows, const float* bias, ActQ act, float* y, hipStream_t st) {
     if (!q8_0_heads_mfma_supported(n_heads, head_dim, rows) || !act.q || !act.s) return hipErrorInvalidValue;
@@ -1020,6 +1087,8 @@ hipError_t launch_q8_0_heads_mfma(const int8_t* const* wq, const float* const* w
         hipLaunchKernelGGL((q8_0_heads_mfma_kernel<1, 1>), dim3((d_model + 15) / 16, 1), dim3(64), 0, st, ha);
     else if (T == 2)
         hipLaunchKernelGGL((q8_0_heads_mfma_kernel<2, 4>), grid4, dim3(256), 0, st, ha);
+    else if (q8_mfma_dma())
+        hipLaunchKernelGGL((q8_0_mfma_dma_kernel<true, Q8HMArgs>), grid4, dim3(64 * kQ8DmaWaves), 0, st, ha);
     else
         hipLaunchKernelGGL((q8_0_heads_mfma_kernel<4, 4>), grid4, dim3(256), 0, st, ha);
     return hipGetLastError();
@@ -1028,14 +1097,6 @@ hipError_t launch_q8_0_heads_mfma(const int8_t* const* wq, const float* const* w
 bool q8_0_mfma_supported(int in, int rows) {
     // 32-bit resource offsets: 64 activation rows and 16 weight rows of K bytes, and the whole activation
     return in % 32 == 0 && (uint64_t)in * 64 < (1ull << 31) && (uint64_t)in * (uint64_t)rows < (1ull << 31);
-}
-
-static bool q8_mfma_dma() {
-    static const bool on = [] {
-        const char* v = getenv("OVFQ_Q8_MFMA_DMA");
-        return !(v && *v == '0');
-    }();
-    return on;
 }
 
 hipError_t launch_project_q8_0_mfma(const ProjJob* jobs, int njobs, int in, int rows, ActQ act, hipStream_t st) {
@@ -1057,7 +1118,7 @@ hipError_t launch_project_q8_0_mfma(const ProjJob* jobs, int njobs, int in, int 
         else if (T == 2)
             hipLaunchKernelGGL((q8_0_mfma_kernel<2, 4>), grid4, dim3(256), 0, st, ma);
         else if (q8_mfma_dma())
-            hipLaunchKernelGGL(q8_0_mfma_dma_kernel, grid4, dim3(64 * kQ8DmaWaves), 0, st, ma);
+            hipLaunchKernelGGL((q8_0_mfma_dma_kernel<false, Q8MArgs>), grid4, dim3(64 * kQ8DmaWaves), 0, st, ma);
         else
             hipLaunchKernelGGL((q8_0_mfma_kernel<4, 4>), grid4, dim3(256), 0, st, ma);
         const hipError_t e = hipGetLastError();
