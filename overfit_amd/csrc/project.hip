@@ -1055,8 +1055,10 @@ bool q8_0_heads_mfma_supported(int n_heads, int head_dim, int rows) {
            K * 64 < (1ull << 31) && K * (uint64_t)rows < (1ull << 31);
 }
 
-// Rows past 32: the eight-wave LDS-DMA kernel (OVFQ_Q8_MFMA_DMA=0 keeps the register-staged four-wave one, for
-// measurements).
+// Batches past 16 rows take the eight-wave LDS-DMA kernel (MI355X, Q8_0 4096x4096 with its quantise launch, us,
+// register-staged four-wave kernel / DMA kernel: 17-32 rows 38.7-39.2 / 30.4-30.9, 512 rows 58.7-59.7 / 52.5-52.9;
+// per-head Llama-3-8B Wo at 32 / 64 / 512 rows 46.1 / 64.3 / 73.7 / 35.9 / 36.3 / 54.3). OVFQ_Q8_MFMA_DMA=0 keeps
+// the register-staged kernels, for measurements.
 static bool q8_mfma_dma() {
     static const bool on = [] {
         const char* v = getenv("OVFQ_Q8_MFMA_DMA");
@@ -1085,10 +1087,11 @@ hipError_t launch_q8_0_heads_mfma(const int8_t* const* wq, const float* const* w
     const dim3 grid4((d_model + 63) / 64, (rows + 16 * T - 1) / (16 * T));
     if (T == 1)
         hipLaunchKernelGGL((q8_0_heads_mfma_kernel<1, 1>), dim3((d_model + 15) / 16, 1), dim3(64), 0, st, ha);
+    else if (q8_mfma_dma())
+        hipLaunchKernelGGL((q8_0_mfma_dma_kernel<true, Q8HMArgs>), dim3((d_model + 63) / 64, (rows + 63) / 64),
+                           dim3(64 * kQ8DmaWaves), 0, st, ha);
     else if (T == 2)
         hipLaunchKernelGGL((q8_0_heads_mfma_kernel<2, 4>), grid4, dim3(256), 0, st, ha);
-    else if (q8_mfma_dma())
-        hipLaunchKernelGGL((q8_0_mfma_dma_kernel<true, Q8HMArgs>), grid4, dim3(64 * kQ8DmaWaves), 0, st, ha);
     else
         hipLaunchKernelGGL((q8_0_heads_mfma_kernel<4, 4>), grid4, dim3(256), 0, st, ha);
     return hipGetLastError();
@@ -1115,10 +1118,11 @@ hipError_t launch_project_q8_0_mfma(const ProjJob* jobs, int njobs, int in, int 
         const dim3 grid4((jobs[i].n_rows + 63) / 64, (rows + 16 * T - 1) / (16 * T));
         if (T == 1)
             hipLaunchKernelGGL((q8_0_mfma_kernel<1, 1>), dim3((jobs[i].n_rows + 15) / 16, 1), dim3(64), 0, st, ma);
+        else if (q8_mfma_dma())
+            hipLaunchKernelGGL((q8_0_mfma_dma_kernel<false, Q8MArgs>), dim3((jobs[i].n_rows + 63) / 64, (rows + 63) / 64),
+                               dim3(64 * kQ8DmaWaves), 0, st, ma);
         else if (T == 2)
             hipLaunchKernelGGL((q8_0_mfma_kernel<2, 4>), grid4, dim3(256), 0, st, ma);
-        else if (q8_mfma_dma())
-            hipLaunchKernelGGL((q8_0_mfma_dma_kernel<false, Q8MArgs>), grid4, dim3(64 * kQ8DmaWaves), 0, st, ma);
         else
             hipLaunchKernelGGL((q8_0_mfma_kernel<4, 4>), grid4, dim3(256), 0, st, ma);
         const hipError_t e = hipGetLastError();
