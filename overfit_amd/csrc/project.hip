@@ -294,6 +294,8 @@ struct Q8GArgs {
 constexpr int kQ8GemvMaxIn = 32768;       // LDS copy of the activation rows: 32 KB + 4 KB of scales
 constexpr int kQ8GemvMaxRows = 8;         // activation rows per launch
 constexpr int kQ8GemvQuantMaxIn = 8192;   // in-launch quantisation (every workgroup quantises the whole input)
+constexpr int kQ8Red = 68;                // floats per block-value row: 64 values, 16-byte aligned rows
+typedef float f32x4q __attribute__((ext_vector_type(4)));
 
 template <int R, bool kMulti>
 __global__ __launch_bounds__(256) void q8_0_gemv_kernel(const Q8GArgs a) {
@@ -301,13 +303,13 @@ __global__ __launch_bounds__(256) void q8_0_gemv_kernel(const Q8GArgs a) {
     const int K = a.in, nb = a.nb, M = a.m_rows;
     uint8_t* lq = smem8;                                          // [M][K] activation quants
     float* ls = reinterpret_cast<float*>(smem8 + M * K);          // [M][nb] activation scales
-    float* red = ls + ((M * nb + 3) & ~3);                        // per wave [R][M][65] block values
+    float* red = ls + ((M * nb + 3) & ~3);                        // per wave [R][M][kQ8Red] block values
     const int wave = wave_id();
     const int lane = threadIdx.x & 63;
     const int nchunks = (nb + 63) >> 6;
     const int stride = gridDim.x * 4;
     const int total = a.total_groups;
-    float* rw = red + wave * R * kQ8GemvMaxRows * 65;
+    float* rw = red + wave * R * kQ8GemvMaxRows * kQ8Red;
 
     struct Item {
         u32x4 w[R][2];
@@ -440,14 +442,24 @@ __global__ __launch_bounds__(256) void q8_0_gemv_kernel(const Q8GArgs a) {
                 dot = sdot4(cur.w[r][1].y, x1.y, dot);
                 dot = sdot4(cur.w[r][1].z, x1.z, dot);
                 dot = sdot4(cur.w[r][1].w, x1.w, dot);
-                // (wScale * aScale) * dot
-                if (live) rw[(r * M + m) * 65 + lane] = as_float(cur.ws[r]) * xs * (float)dot;
+                // (wScale * aScale) * dot; +0 for the blocks past the row (a short last chunk)
+                rw[(r * M + m) * kQ8Red + lane] = live ? as_float(cur.ws[r]) * xs * (float)dot : 0.0f;
             }
         }
         wave_sync();
         if (lane < R * M) {  // lane = r * M + m: weight row r, activation row m
-            const int nv = min(64, nb - c * 64);
-            for (int j = 0; j < nv; j++) acc += rw[lane * 65 + j];
+            // the 64 block values in ascending order, read as sixteen 16-byte pieces up front; the running sum starts
+            // at +0 and is never -0, so the trailing +0 of a short chunk leaves it unchanged
+            f32x4q v[16];
+#pragma unroll
+            for (int i = 0; i < 16; i++) v[i] = *reinterpret_cast<const f32x4q*>(rw + lane * kQ8Red + 4 * i);
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                acc += v[i].x;
+                acc += v[i].y;
+                acc += v[i].z;
+                acc += v[i].w;
+            }
         }
         wave_sync();
         if (c == nchunks - 1) {
@@ -501,7 +513,7 @@ hipError_t launch_q8g(Q8GArgs& ga, const ProjJob* jobs, int njobs, hipStream_t s
     const int cap = q8_cu_count() * wg_per_cu;
     if (wgs > cap) wgs = cap;
     const size_t lds = (size_t)ga.m_rows * ga.in + 4 * (size_t)((ga.m_rows * ga.nb + 3) & ~3) +
-                       4 * (size_t)4 * R * kQ8GemvMaxRows * 65;
+                       4 * (size_t)4 * R * kQ8GemvMaxRows * kQ8Red;
     if (njobs > 1)
         hipLaunchKernelGGL((q8_0_gemv_kernel<R, true>), dim3(wgs), dim3(256), lds, st, ga);
     else
